@@ -1,0 +1,374 @@
+#!/usr/bin/env python3
+"""Throughput of the MI355X attention path on one GPU.
+
+Default (no flags): the full-model decode-attention step -- 22 layers, KV
+cache [2048 positions][4 kv heads][64] fp32 per layer, one new token per
+layer (RoPE + append + split-KV attention) -- timed over K steps after W
+warmup steps, with inputs resident in HBM.  To keep the 92.7 MB step out of
+the 256 MB Infinity Cache, steps rotate over 4 copies of the whole cache
+(371 MB).  Prints ONE JSON line:
+
+  value      decode KV GB/s = algorithmic bytes per step / step time, with
+             algorithmic bytes 2048*L + 20480 per (sequence, layer), L = 2048
+  roofline   the split-KV decode kernel's own average duration (HIP events on
+             the engine's stream, every launch), against HBM 8 TB/s
+  prefill    the causal prefill workload (512 tokens, 22 layers): exact causal
+             TFLOP/s against fp32 MFMA 157.3 TFLOP/s
+  cpu_baseline  the reference's own scalar attention() (oracle/_ref) -- or the
+             C restatement when that is not built -- on the host's cores, over
+             a bounded sample of the same workload
+
+Other workloads (--workload): decode_long (16384 context, batch 8, 22 layers),
+decode_ragged (64 sequences, L in [256, 2048], 22 layers), prefill,
+decode_single (one layer, position 127: reported as latency), and copy (the
+device copy kernel, used to calibrate rocprofv3 byte counters).
+"""
+from __future__ import annotations
+
+import argparse
+import importlib
+import json
+import os
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+tla = importlib.import_module("tinyllama-engine_amd")
+W = importlib.import_module("tinyllama-engine_amd.workloads")
+
+HBM_PEAK_GBS = 8000.0
+FP32_MFMA_PEAK_TFLOPS = 157.3
+MALL_BYTES = 256 << 20
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def median(xs):
+    xs = sorted(xs)
+    n = len(xs)
+    return xs[n // 2] if n % 2 else 0.5 * (xs[n // 2 - 1] + xs[n // 2])
+
+
+# ------------------------------------------------------------------ decode --
+
+class DecodeBench:
+    """Inputs for one decode workload resident on the device, with enough
+    rotated copies of the whole KV cache to exceed the Infinity Cache."""
+
+    def __init__(self, eng, case, copies):
+        self.eng, self.case, self.copies = eng, case, copies
+        cfg = eng.cfg
+        self.n_seq = case.n_seq
+        self.seq_stride = cfg.n_layers * cfg.n_ctx * cfg.kv_dim
+        self.kc, self.vc = eng.kv_cache(case.n_seq * copies)
+        self.kc_host_shape = case.kc.shape
+        one = case.kc.nbytes
+        # upload copy 0, replicate on the device
+        tla.lib().tla_memcpy_h2d(eng.h, self.kc.ptr, case.kc.ctypes.data, one)
+        tla.lib().tla_memcpy_h2d(eng.h, self.vc.ptr, case.vc.ctypes.data, one)
+        for c in range(1, copies):
+            eng.copy(self.kc.ptr + c * one, self.kc.ptr, one)
+            eng.copy(self.vc.ptr + c * one, self.vc.ptr, one)
+        self.q, self.k, self.v = eng.array(case.q), eng.array(case.k), eng.array(case.v)
+        self.out = eng.array(case.q.shape)
+        self.bytes_per_copy = one
+        eng.synchronize()
+
+    def step(self, i):
+        c = i % self.copies
+        off = c * self.bytes_per_copy
+        self.eng.decode(self.case.pos, 0, self.case.n_layers, self.out.ptr, self.q.ptr, self.k.ptr,
+                        self.v.ptr, self.kc.ptr + off, self.vc.ptr + off, self.seq_stride)
+
+    def free(self):
+        for a in (self.kc, self.vc, self.q, self.k, self.v, self.out):
+            a.free()
+
+
+def time_steps(eng, step, steps, warmup):
+    for i in range(warmup):
+        step(i)
+    eng.synchronize()
+    eng.event(0)
+    for i in range(steps):
+        step(warmup + i)
+    eng.event(1)
+    eng.synchronize()
+    return eng.elapsed(0, 1) / steps
+
+
+def kernel_avg_ms(eng, step, steps, kernel_id, start=0):
+    eng.profile(True)
+    for i in range(steps):
+        step(start + i)
+    eng.synchronize()
+    total, n = eng.profile_read(kernel_id)
+    eng.profile(False)
+    return total / max(n, 1), n
+
+
+def make_decode_case(workload, n_layers=22):
+    if workload == "decode_model":
+        return W.decode_model(n_layers=n_layers, n_ctx=2048), 2048
+    if workload == "decode_ragged":
+        return W.decode_ragged(n_seq=64, n_layers=n_layers, n_ctx=2048), 2048
+    if workload == "decode_long":
+        # one layer's data from the generator (16384 ctx x 8 seqs, peaked
+        # keys), repeated for every layer: the byte stream per layer is the
+        # same, and host generation stays a few seconds
+        one = W.decode_long(n_seq=8, n_layers=1, n_ctx=16384)
+        rep = lambda a: np.ascontiguousarray(np.repeat(a, n_layers, axis=1))  # noqa: E731
+        case = W.DecodeCase(8, n_layers, 16384, one.pos, rep(one.q), rep(one.k), rep(one.v),
+                            rep(one.kc), rep(one.vc))
+        return case, 16384
+    if workload == "decode_single":
+        return W.decode_single(), 128
+    raise ValueError(workload)
+
+
+def run_decode(workload, steps, warmup, cpu, split=0):
+    n_layers = 1 if workload == "decode_single" else 22
+    case, n_ctx = make_decode_case(workload, n_layers)
+    one_copy = case.kc.nbytes * 2
+    copies = 1 if workload == "decode_single" else max(1, -(-3 * MALL_BYTES // 2 // one_copy))
+    copies = max(copies, 2 if one_copy < MALL_BYTES else 1)
+    log(f"[bench] {workload}: {case.n_seq} seq x {n_layers} layers, ctx {n_ctx}, "
+        f"{copies} rotated cache copies ({copies * one_copy / 1e6:.0f} MB)")
+    eng = tla.Engine(tla.Config.tinyllama(n_layers=n_layers, n_ctx=n_ctx))
+    if split:
+        eng.set_option(tla.OPT_DECODE_SPLIT, split)
+    b = DecodeBench(eng, case, copies)
+    ms = time_steps(eng, b.step, steps, warmup)
+    k_ms, k_n = kernel_avg_ms(eng, b.step, steps, tla.KERNEL_DECODE, start=warmup + steps)
+    c_ms, c_n = kernel_avg_ms(eng, b.step, steps, tla.KERNEL_COMBINE, start=warmup + 2 * steps)
+    algo = case.algorithmic_bytes
+    res = {
+        "workload": workload, "ms_per_step": ms, "algorithmic_bytes": algo,
+        "value": algo / (ms * 1e-3) / 1e9,
+        "decode_kernel_ms": k_ms, "combine_kernel_ms": c_ms if c_n else 0.0,
+        "cache_copies": copies, "mall_resident": copies * one_copy <= MALL_BYTES,
+    }
+    achieved = algo / (k_ms * 1e-3) / 1e9
+    res["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                       "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
+                       "kernel": "decode_split_kernel", "launches": k_n}
+    log(f"[bench] {workload}: {ms * 1e3:.1f} us/step, {res['value']:.0f} GB/s step, "
+        f"decode kernel {k_ms * 1e3:.1f} us -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%})"
+        f", combine {res['combine_kernel_ms'] * 1e3:.1f} us")
+    b.free()
+    eng.close()
+    if cpu:
+        res["cpu_baseline"] = cpu_decode_baseline(case, n_ctx, workload)
+    return res
+
+
+def cpu_threads():
+    return max(1, min(16, os.cpu_count() or 1))
+
+
+def cpu_decode_baseline(case, n_ctx, workload, budget_s=10.0):
+    """Time the reference's attention() (oracle/_ref) or the C restatement on
+    the host over whole steps of the same workload for about budget_s."""
+    import oracle as O
+    kind = "reference" if O.ref_available() else "port"
+    lib = O.ref() if kind == "reference" else None
+    units = case.n_seq * case.n_layers
+    s = O.Shape(n_ctx=n_ctx)
+    q = case.q.reshape(units, -1)
+    k = case.k.reshape(units, -1)
+    v = case.v.reshape(units, -1)
+    kc = case.kc.reshape(units, n_ctx, -1).copy()
+    vc = case.vc.reshape(units, n_ctx, -1).copy()
+    pos = np.repeat(case.pos, case.n_layers).astype(np.int32)
+
+    def measure(threads, budget):
+        times = []
+        t_end = time.perf_counter() + budget
+        while True:
+            t0 = time.perf_counter()
+            O.decode_units_mt(threads, q, k, v, kc, vc, pos, s, rotate=True, lib=lib)
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > t_end and len(times) >= 2:
+                break
+        return median(times), len(times)
+
+    threads = cpu_threads()
+    t1, n1 = measure(1, budget_s * 0.25)
+    tn, nn = measure(threads, budget_s * 0.75)
+    algo = case.algorithmic_bytes
+    log(f"[bench] cpu {kind}: 1 thread {t1 * 1e3:.1f} ms/step, {threads} threads "
+        f"{tn * 1e3:.1f} ms/step")
+    return {"value": round(algo / tn / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": kind,
+            "sample": f"{nn} full steps of {workload} ({case.n_seq} seq x {case.n_layers} layers), "
+                      f"median, {threads} threads; 1 thread: {n1} steps",
+            "single_thread_value": round(algo / t1 / 1e9, 3),
+            "ms_per_step": round(tn * 1e3, 3), "single_thread_ms_per_step": round(t1 * 1e3, 3)}
+
+
+# ----------------------------------------------------------------- prefill --
+
+def run_prefill(steps, warmup, cpu, n_layers=22, n_tok=512):
+    case = W.make_prefill(n_layers=n_layers, n_tok=n_tok)
+    eng = tla.Engine(tla.Config.tinyllama(n_layers=n_layers, n_ctx=n_tok))
+    kc, vc = eng.kv_cache(1)
+    q, k, v = eng.array(case.q), eng.array(case.k), eng.array(case.v)
+    out = eng.array(case.q.shape)
+
+    def step(i):
+        eng.prefill(0, n_tok, 0, n_layers, out.ptr, q.ptr, k.ptr, v.ptr, kc.ptr, vc.ptr)
+
+    ms = time_steps(eng, step, steps, warmup)
+    k_ms, k_n = kernel_avg_ms(eng, step, steps, tla.KERNEL_PREFILL)
+    a_ms, _ = kernel_avg_ms(eng, step, steps, tla.KERNEL_APPEND)
+    flops = case.algorithmic_flops
+    achieved = flops / (k_ms * 1e-3) / 1e12
+    res = {"workload": "prefill", "metric": "prefill-attn TFLOP/s (% MFMA peak)",
+           "value": flops / (ms * 1e-3) / 1e12, "unit": "TFLOP/s", "ms_per_step": ms,
+           "algorithmic_flops": flops, "prefill_kernel_ms": k_ms, "append_kernel_ms": a_ms,
+           "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
+                        "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                        "kernel": "prefill_attention_kernel", "launches": k_n}}
+    log(f"[bench] prefill: {ms * 1e3:.1f} us/step ({res['value']:.1f} TFLOP/s), attention kernel "
+        f"{k_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s ({achieved / FP32_MFMA_PEAK_TFLOPS:.1%}), "
+        f"append {a_ms * 1e3:.1f} us")
+    for a in (kc, vc, q, k, v, out):
+        a.free()
+    eng.close()
+    if cpu:
+        res["cpu_baseline"] = cpu_prefill_baseline(case, n_tok)
+    return res
+
+
+def cpu_prefill_baseline(case, n_tok, budget_s=8.0):
+    """The C restatement of the reference's token-by-token prompt loop, one
+    layer per host thread (the reference's attention() has no threading)."""
+    from concurrent.futures import ThreadPoolExecutor
+
+    import oracle as O
+    s = O.Shape(n_ctx=n_tok, n_layers=1)
+    threads = cpu_threads()
+    times = []
+    t_end = time.perf_counter() + budget_s
+    with ThreadPoolExecutor(threads) as ex:
+        while True:
+            t0 = time.perf_counter()
+
+            def one(layer):
+                kc = np.zeros(n_tok * 256, np.float32)
+                vc = np.zeros_like(kc)
+                O.prefill(case.q[layer], case.k[layer], case.v[layer], kc, vc, 0, 0, s)
+
+            list(ex.map(one, range(case.n_layers)))
+            times.append(time.perf_counter() - t0)
+            if time.perf_counter() > t_end:
+                break
+    t = median(times)
+    log(f"[bench] cpu prefill port: {t * 1e3:.0f} ms/step on {threads} threads")
+    return {"value": round(case.algorithmic_flops / t / 1e12, 5), "unit": "TFLOP/s",
+            "cores": threads, "kind": "port",
+            "sample": f"{len(times)} full prefill steps (512 tokens x {case.n_layers} layers, one "
+                      f"layer per thread), median"}
+
+
+# -------------------------------------------------------------------- copy --
+
+def run_copy(steps, warmup, nbytes=1 << 30):
+    """Device copy kernel over nbytes: the known-size reference for scaling
+    rocprofv3 FETCH_SIZE / WRITE_SIZE."""
+    eng = tla.Engine(tla.Config.tinyllama(n_layers=1, n_ctx=16))
+    a = tla.DeviceArray(eng, (nbytes,), np.uint8)
+    b = tla.DeviceArray(eng, (nbytes,), np.uint8)
+    ms = time_steps(eng, lambda i: eng.copy(b.ptr, a.ptr, nbytes), steps, warmup)
+    log(f"[bench] copy {nbytes >> 20} MiB: {ms * 1e3:.1f} us, {2 * nbytes / ms / 1e6:.0f} GB/s")
+    a.free()
+    b.free()
+    eng.close()
+    return {"workload": "copy", "bytes_read": nbytes, "bytes_written": nbytes, "ms": ms,
+            "value": 2 * nbytes / (ms * 1e-3) / 1e9}
+
+
+# -------------------------------------------------------------------- main --
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--workload", default="decode_model",
+                    choices=["decode_model", "decode_long", "decode_ragged", "decode_single",
+                             "prefill", "copy"])
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-prefill", action="store_true", help="skip the prefill half")
+    ap.add_argument("--split", type=int, default=0, help="decode split length (0 = auto)")
+    ap.add_argument("--extra", action="store_true",
+                    help="also measure decode_long and decode_ragged")
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU only: this build has no multi-GPU path "
+              "(run with --gpus 1)", file=sys.stderr)
+        sys.exit(2)
+    cpu = not args.no_cpu
+
+    if args.workload == "copy":
+        print(json.dumps(run_copy(args.steps, args.warmup)))
+        return
+    if args.workload == "prefill":
+        p = run_prefill(args.steps, args.warmup, cpu)
+        line = {"metric": BASELINE_METRIC, "value": round(p["value"], 3), "unit": "TFLOP/s",
+                "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                "ms_per_step": round(p["ms_per_step"], 4), "higher_is_better": True,
+                "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+                "config": {"workload": "prefill", "n_tok": 512, "n_layers": 22, "n_head": 32,
+                           "n_head_kv": 4, "head_dim": 64, "parallelism": "none"},
+                "roofline": p["roofline"]}
+        if cpu:
+            line["cpu_baseline"] = p["cpu_baseline"]
+        print(json.dumps(line))
+        return
+
+    d = run_decode(args.workload, args.steps, args.warmup, cpu, args.split)
+    cfg = {"decode_model": {"n_seq": 1, "n_layers": 22, "context": 2048},
+           "decode_long": {"n_seq": 8, "n_layers": 22, "context": 16384},
+           "decode_ragged": {"n_seq": 64, "n_layers": 22, "context": "U[256,2048]"},
+           "decode_single": {"n_seq": 1, "n_layers": 1, "context": 128}}[args.workload]
+    line = {"metric": BASELINE_METRIC, "value": round(d["value"], 1), "unit": "GB/s",
+            "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+            "ms_per_step": round(d["ms_per_step"], 5), "higher_is_better": True,
+            "scaling": "weak", "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+            "config": dict({"workload": args.workload, "n_head": 32, "n_head_kv": 4,
+                            "head_dim": 64, "parallelism": "none",
+                            "cache_copies": d["cache_copies"],
+                            "mall_resident": d["mall_resident"]}, **cfg),
+            "roofline": d["roofline"],
+            "kernels_us": {"decode": round(d["decode_kernel_ms"] * 1e3, 2),
+                           "combine": round(d["combine_kernel_ms"] * 1e3, 2)}}
+    if cpu:
+        line["cpu_baseline"] = d["cpu_baseline"]
+    if not args.no_prefill and args.workload == "decode_model":
+        p = run_prefill(max(5, args.steps // 2), max(2, args.warmup // 2), cpu)
+        line["prefill"] = {k: p[k] for k in ("value", "unit", "ms_per_step", "roofline")}
+        line["prefill"]["value"] = round(p["value"], 3)
+        line["prefill"]["config"] = {"workload": "prefill", "n_tok": 512, "n_layers": 22}
+        if cpu:
+            line["prefill"]["cpu_baseline"] = p["cpu_baseline"]
+    if args.extra:
+        line["extra"] = {}
+        for wl in ("decode_long", "decode_ragged"):
+            e = run_decode(wl, args.steps, args.warmup, False)
+            line["extra"][wl] = {"value": round(e["value"], 1), "unit": "GB/s",
+                                 "ms_per_step": round(e["ms_per_step"], 4),
+                                 "roofline": e["roofline"]}
+    print(json.dumps(line))
+
+
+BASELINE_METRIC = "decode-attn KV GB/s (% HBM peak); prefill-attn TFLOP/s (% MFMA peak)"
+
+if __name__ == "__main__":
+    main()

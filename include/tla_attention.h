@@ -1,0 +1,187 @@
+/*
+ * tla_attention.h -- C ABI of the MI355X (gfx950) grouped-query attention
+ * path: RoPE, device-resident KV cache with in-kernel RoPE+append,
+ * split-KV decode attention and causal MFMA prefill attention.
+ *
+ * It replaces the attention block of the reference engine's forward pass
+ * (src/forward.cpp:192-208) and the helpers it calls:
+ *     rope()      src/ops.h:175-176   (src/ops.cpp:1223-1281)
+ *     softmax()   src/ops.h:107       (src/ops.cpp:1072-1091)
+ *     attention() src/ops.h:204-206   (src/ops.cpp:1317-1515)
+ *     RunState key_cache/value_cache  src/run_state.h:93-101, 134-153
+ *
+ * Conventions
+ *   - Every entry point returns int status, TLA_OK (0) on success.  The ABI
+ *     never throws.  tla_last_error() gives a message for the calling
+ *     thread's last failure.  (The reference's ops never validate; its
+ *     callers throw std::runtime_error -- the C++ wrapper in
+ *     tinyllama-engine_amd/host/ turns non-zero codes into exactly that.)
+ *   - Pointers named *_dev are device (HBM) pointers; the library never
+ *     dereferences them on the host.  All compute entry points are
+ *     asynchronous and ordered on the engine's own HIP stream.
+ *   - Layout of one KV cache is the reference's: element (layer, pos, kv_head,
+ *     j) at ((layer * n_ctx + pos) * n_head_kv + kv_head) * head_dim + j,
+ *     fp32.  Several sequences stack with a caller-given seq_stride.
+ *   - Kernels implement head_dim == 64 and n_head / n_head_kv <= 16.
+ *   - One engine is not re-entrant: calls on one engine from several host
+ *     threads must be serialised by the caller.
+ */
+#ifndef TLA_ATTENTION_H
+#define TLA_ATTENTION_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum tla_status {
+    TLA_OK = 0,
+    TLA_ERR_INVALID_ARGUMENT = 1, /* null pointer, bad size, inconsistent shape */
+    TLA_ERR_OUT_OF_RANGE = 2,     /* pos >= n_ctx, layer >= n_layers, ...        */
+    TLA_ERR_UNSUPPORTED = 3,      /* a shape the kernels do not implement        */
+    TLA_ERR_DEVICE = 4,           /* HIP runtime failure                          */
+    TLA_ERR_OUT_OF_MEMORY = 5
+};
+
+/* Flags for tla_decode / tla_prefill. */
+enum tla_flags {
+    /* Apply RoPE to q and to the new k (at each token's position) inside the
+     * kernel, as forward() does with rope() before attention()
+     * (src/forward.cpp:192-206).  Without it q and k are taken as already
+     * rotated, which is attention()'s contract (src/ops.h:185-186). */
+    TLA_ROTATE = 1
+};
+
+/* Shape fields of llama_config_t (src/gguf.h:139-168) that the path uses.
+ * head_dim = n_embd / n_head, as llama_config_t::head_dim(). */
+typedef struct tla_config {
+    int n_layers;
+    int n_embd;
+    int n_head;
+    int n_head_kv;
+    int n_ctx;
+    float rope_freq_base;
+} tla_config;
+
+/* Engine: one device, one HIP stream, the RoPE cos/sin table for
+ * positions [0, n_ctx) and a split-KV workspace.  No reference counterpart
+ * (the reference keeps no device state); it stands in for the
+ * `const llama_config_t& cfg` argument of attention(). */
+typedef struct tla_engine tla_engine;
+
+/* Message for the calling thread's last non-zero status ("" if none). */
+const char* tla_last_error(void);
+
+/* ABI version: bumped on any signature change. */
+int tla_abi_version(void);
+
+int tla_engine_create(const tla_config* cfg, int device, tla_engine** out);
+int tla_engine_destroy(tla_engine* e);
+/* Wait for all work queued on the engine's stream. */
+int tla_synchronize(tla_engine* e);
+
+/* ---- device memory (RunState::allocate / free_buffers,
+ *      src/run_state.h:115-170) ---------------------------------------- */
+/* Zero-filled device allocation of `bytes` bytes. */
+int tla_alloc(tla_engine* e, size_t bytes, void** out_dev);
+int tla_free(tla_engine* e, void* dev);
+/* KV cache for n_seq sequences, each [n_layers][n_ctx][n_head_kv*head_dim]
+ * fp32, zero-filled (src/run_state.h:134-153).  Free with tla_free. */
+int tla_kv_cache_alloc(tla_engine* e, int n_seq, float** key_cache_dev,
+                       float** value_cache_dev);
+/* Blocking copies host<->device and a device copy kernel (device->device,
+ * used e.g. to clone a sequence's cache).  Ordered after queued work. */
+int tla_memcpy_h2d(tla_engine* e, void* dst_dev, const void* src_host, size_t bytes);
+int tla_memcpy_d2h(tla_engine* e, void* dst_host, const void* src_dev, size_t bytes);
+int tla_memcpy_d2d(tla_engine* e, void* dst_dev, const void* src_dev, size_t bytes);
+
+/* ---- operators ------------------------------------------------------ */
+
+/* rope() src/ops.h:175-176, in place on device q [n_head*head_dim] and
+ * k [n_head_kv*head_dim].  Bit-exact with the reference: cos/sin come from
+ * the host's libm with the reference's float expressions, and the rotation
+ * rounds each product and sum separately.  Any pos >= 0 (no n_ctx limit). */
+int tla_rope(tla_engine* e, float* q_dev, float* k_dev, int pos, int head_dim, int n_head,
+             int n_head_kv, float freq_base);
+
+/* softmax() src/ops.h:107, in place on device x[size]. */
+int tla_softmax(tla_engine* e, float* x_dev, int size);
+
+/* attention() src/ops.h:204-206 for one token of one sequence: appends the
+ * (already rotated) k and v at `pos` of `layer`, then writes
+ * out[n_head*head_dim] = softmax(q.K^T / sqrt(head_dim)) V over positions
+ * 0..pos.  key_cache/value_cache are device caches laid out
+ * [n_layers][n_ctx][kv_dim] as RunState's.  `att` is the reference's score
+ * scratch; it is not used (pass NULL or anything). */
+int tla_attention(tla_engine* e, float* out_dev, const float* q_dev, const float* k_dev,
+                  const float* v_dev, float* key_cache_dev, float* value_cache_dev,
+                  float* att, int layer, int pos);
+
+/* The whole attention block of forward() (src/forward.cpp:192-208):
+ * rope(q, k, pos) then attention(...), fused into one launch sequence.
+ * q and k are read unrotated and are left unchanged; the cache receives the
+ * rotated k. */
+int tla_rope_attention(tla_engine* e, float* out_dev, const float* q_dev, const float* k_dev,
+                       const float* v_dev, float* key_cache_dev, float* value_cache_dev,
+                       int layer, int pos);
+
+/* Batched decode: one new token for each of n_seq sequences, for each of the
+ * n_step_layers layers layer0 .. layer0+n_step_layers-1.  Equivalent to
+ * calling attention() (or rope()+attention() with TLA_ROTATE) once per
+ * (sequence, layer) with that sequence's position.
+ *   pos_host  [n_seq]                       host array, 0 <= pos < n_ctx
+ *   q_dev     [n_seq][n_step_layers][n_head][head_dim]
+ *   k/v_dev   [n_seq][n_step_layers][n_head_kv][head_dim]
+ *   out_dev   [n_seq][n_step_layers][n_head][head_dim]
+ *   caches    sequence s, layer l at key_cache_dev + s*seq_stride
+ *             + l*n_ctx*kv_dim (floats); seq_stride >= n_layers*n_ctx*kv_dim
+ *             unless n_seq == 1.
+ * Ragged lengths are supported.  Up to 256 sequences per call. */
+int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_step_layers,
+               int flags, float* out_dev, const float* q_dev, const float* k_dev,
+               const float* v_dev, float* key_cache_dev, float* value_cache_dev,
+               size_t seq_stride);
+
+/* Causal prefill of n_tok prompt tokens at positions pos0 .. pos0+n_tok-1 of
+ * one sequence, for layers layer0 .. layer0+n_step_layers-1.  Equal to the
+ * reference's token-by-token prompt loop (src/generate.cpp:56-59) over the
+ * attention block: every token's k,v are appended to the cache and token t
+ * attends to positions 0 .. pos0+t.  With TLA_ROTATE, q and k are rotated in
+ * the kernel at their own positions.
+ *   q_dev/out_dev [n_step_layers][n_tok][n_head][head_dim]
+ *   k/v_dev       [n_step_layers][n_tok][n_head_kv][head_dim] */
+int tla_prefill(tla_engine* e, int pos0, int n_tok, int layer0, int n_step_layers, int flags,
+                float* out_dev, const float* q_dev, const float* k_dev, const float* v_dev,
+                float* key_cache_dev, float* value_cache_dev);
+
+/* ---- measurement hooks (no reference counterpart) ------------------- */
+enum tla_kernel_id {
+    TLA_KERNEL_DECODE = 0,  /* split-KV decode attention (RoPE+append fused) */
+    TLA_KERNEL_COMBINE = 1, /* split-KV log-sum-exp merge                   */
+    TLA_KERNEL_PREFILL = 2, /* causal MFMA prefill attention                 */
+    TLA_KERNEL_APPEND = 3,  /* prefill RoPE + cache append                   */
+    TLA_KERNEL_COUNT = 4
+};
+/* When enabled, HIP events bracket every launch of each kernel on the
+ * engine's stream; tla_profile_read sums their durations (ms) since the
+ * last reset.  Enabling or disabling resets the sums. */
+int tla_profile_enable(tla_engine* e, int enable);
+int tla_profile_read(tla_engine* e, int kernel_id, double* total_ms, long long* launches);
+
+/* Stream-ordered HIP events for timing whole steps: record into one of 64
+ * slots, then read the elapsed time between two recorded slots. */
+int tla_event_record(tla_engine* e, int slot);
+int tla_event_elapsed(tla_engine* e, int slot_begin, int slot_end, float* ms);
+
+/* Tuning knobs (0 = automatic). */
+enum tla_option {
+    TLA_OPT_DECODE_SPLIT = 0 /* positions per split-KV chunk (multiple of 16) */
+};
+int tla_set_option(tla_engine* e, int option, long long value);
+
+#ifdef __cplusplus
+}  /* extern "C" */
+#endif
+
+#endif /* TLA_ATTENTION_H */

@@ -1,0 +1,198 @@
+"""ctypes loaders for the CPU oracle -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
+this package, as the checker or as the CPU baseline.  The HIP product
+(tinyllama-engine_amd/) never imports or links anything here.
+
+Two libraries:
+  liboracle.so         plain-C restatement of the reference's rope / softmax /
+                       attention (tl_oracle.c, see its header for citations)
+  _ref/libref_ops.so   the reference's own src/ops.cpp, compiled by
+                       oracle/Makefile where /root/reference exists; optional.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+import subprocess
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+ORACLE_SO = os.path.join(HERE, "liboracle.so")
+REF_SO = os.path.join(HERE, "_ref", "libref_ops.so")
+REF_SRC = "/root/reference/src"
+
+_fp = C.POINTER(C.c_float)
+_dp = C.POINTER(C.c_double)
+_ip = C.POINTER(C.c_int)
+
+
+def fptr(a: np.ndarray):
+    assert a.dtype == np.float32 and a.flags["C_CONTIGUOUS"], (a.dtype, a.flags)
+    return a.ctypes.data_as(_fp)
+
+
+def dptr(a: np.ndarray):
+    assert a.dtype == np.float64 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_dp)
+
+
+def iptr(a: np.ndarray):
+    assert a.dtype == np.int32 and a.flags["C_CONTIGUOUS"]
+    return a.ctypes.data_as(_ip)
+
+
+def build(with_ref: bool | None = None) -> None:
+    """Compile liboracle.so, and _ref/libref_ops.so when the reference tree exists."""
+    targets = ["all"]
+    if with_ref is None:
+        with_ref = os.path.isdir(REF_SRC)
+    if with_ref:
+        targets.append("ref")
+    subprocess.run(["make", "-s", "-C", HERE, *targets], check=True)
+
+
+_oracle = None
+_ref = None
+
+
+def oracle() -> C.CDLL:
+    global _oracle
+    if _oracle is None:
+        if not os.path.exists(ORACLE_SO):
+            build(with_ref=False)
+        lib = C.CDLL(ORACLE_SO)
+        lib.oracle_fault.argtypes = [C.c_int]
+        lib.oracle_rope.argtypes = [_fp, _fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
+        lib.oracle_rope_table.argtypes = [_fp, C.c_int, C.c_int, C.c_float]
+        lib.oracle_softmax.argtypes = [_fp, C.c_int]
+        lib.oracle_attention.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, _fp,
+                                         C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+        lib.oracle_attention_f64.argtypes = [_dp, _fp, _fp, _fp, C.c_int, C.c_int,
+                                             C.c_int, C.c_int, C.c_int, C.c_int]
+        lib.oracle_prefill.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, C.c_int, C.c_int,
+                                       C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
+        lib.oracle_decode_units_mt.argtypes = [C.c_int, C.c_int, _fp, _fp, _fp, _fp, _fp, _fp,
+                                               C.c_size_t, _ip, C.c_int, C.c_int, C.c_int,
+                                               C.c_int, C.c_float, C.c_int]
+        lib.oracle_decode_units_mt.restype = C.c_int
+        _oracle = lib
+    return _oracle
+
+
+def ref_available() -> bool:
+    return os.path.exists(REF_SO)
+
+
+def ref() -> C.CDLL:
+    """The compiled reference; raises if oracle/_ref was never built."""
+    global _ref
+    if _ref is None:
+        if not os.path.exists(REF_SO):
+            raise FileNotFoundError(REF_SO)
+        lib = C.CDLL(REF_SO)
+        lib.ref_rope.argtypes = [_fp, _fp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
+        lib.ref_softmax.argtypes = [_fp, C.c_int]
+        lib.ref_attention.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, _fp, C.c_int, C.c_int,
+                                      C.c_int, C.c_int, C.c_int, C.c_int, C.c_int]
+        lib.ref_decode_units_mt.argtypes = [C.c_int, C.c_int, _fp, _fp, _fp, _fp, _fp, _fp,
+                                            C.c_size_t, _ip, C.c_int, C.c_int, C.c_int,
+                                            C.c_int, C.c_float, C.c_int]
+        lib.ref_decode_units_mt.restype = C.c_int
+        _ref = lib
+    return _ref
+
+
+# ---- numpy-level helpers (same calling convention as the reference) -------
+
+class Shape:
+    """TinyLlama attention shape: llama_config_t fields src/gguf.h:139-168."""
+
+    def __init__(self, n_head=32, n_head_kv=4, head_dim=64, n_ctx=2048, n_layers=1,
+                 freq_base=10000.0):
+        self.n_head, self.n_head_kv, self.head_dim = n_head, n_head_kv, head_dim
+        self.n_ctx, self.n_layers, self.freq_base = n_ctx, n_layers, freq_base
+
+    @property
+    def kv_dim(self):
+        return self.n_head_kv * self.head_dim
+
+    @property
+    def q_dim(self):
+        return self.n_head * self.head_dim
+
+
+def rope(q, k, pos, s: Shape, lib=None):
+    """In-place rope on copies; returns (q', k')."""
+    q = np.ascontiguousarray(q, dtype=np.float32).copy()
+    k = np.ascontiguousarray(k, dtype=np.float32).copy()
+    if lib is None:
+        oracle().oracle_rope(fptr(q), fptr(k), pos, s.head_dim, s.n_head, s.n_head_kv, s.freq_base)
+    else:
+        lib.ref_rope(fptr(q), fptr(k), pos, s.head_dim, s.n_head, s.n_head_kv, s.freq_base)
+    return q, k
+
+
+def softmax(x, lib=None):
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    (oracle().oracle_softmax if lib is None else lib.ref_softmax)(fptr(x), x.size)
+    return x
+
+
+def attention(q, k, v, kc, vc, layer, pos, s: Shape, lib=None):
+    """attention() on the given caches (mutated in place: append at pos)."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    out = np.zeros(s.q_dim, np.float32)
+    att = np.zeros(s.n_ctx, np.float32)
+    if lib is None:
+        oracle().oracle_attention(fptr(out), fptr(q), fptr(k), fptr(v), fptr(kc), fptr(vc),
+                                  fptr(att), layer, pos, s.n_head, s.n_head_kv, s.head_dim,
+                                  s.n_ctx)
+    else:
+        lib.ref_attention(fptr(out), fptr(q), fptr(k), fptr(v), fptr(kc), fptr(vc), fptr(att),
+                          layer, pos, s.n_layers, s.n_head, s.n_head_kv, s.head_dim, s.n_ctx)
+    return out
+
+
+def attention_f64(q, kc, vc, layer, pos, s: Shape):
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    out = np.zeros(s.q_dim, np.float64)
+    oracle().oracle_attention_f64(dptr(out), fptr(q), fptr(kc), fptr(vc), layer, pos,
+                                  s.n_head, s.n_head_kv, s.head_dim, s.n_ctx)
+    return out
+
+
+def prefill(q, k, v, kc, vc, layer, pos0, s: Shape):
+    """Token-by-token prompt loop; q [T, q_dim], k/v [T, kv_dim] raw."""
+    q = np.ascontiguousarray(q, dtype=np.float32)
+    k = np.ascontiguousarray(k, dtype=np.float32)
+    v = np.ascontiguousarray(v, dtype=np.float32)
+    t = q.shape[0]
+    out = np.zeros((t, s.q_dim), np.float32)
+    oracle().oracle_prefill(fptr(out), fptr(q), fptr(k), fptr(v), fptr(kc), fptr(vc), layer,
+                            pos0, t, s.n_head, s.n_head_kv, s.head_dim, s.n_ctx, s.freq_base)
+    return out
+
+
+def rope_table(n_pos, head_dim=64, freq_base=10000.0):
+    cs = np.zeros((n_pos, head_dim // 2, 2), np.float32)
+    oracle().oracle_rope_table(fptr(cs), n_pos, head_dim, freq_base)
+    return cs
+
+
+def decode_units_mt(n_threads, q, k, v, kc, vc, pos, s: Shape, rotate=True, lib=None):
+    """n_units independent decode steps; kc/vc [n_units, n_ctx, kv_dim] (mutated)."""
+    n_units = q.shape[0]
+    out = np.zeros((n_units, s.q_dim), np.float32)
+    pos = np.ascontiguousarray(pos, dtype=np.int32)
+    stride = s.n_ctx * s.kv_dim
+    args = (n_threads, n_units, fptr(out), fptr(np.ascontiguousarray(q, np.float32)),
+            fptr(np.ascontiguousarray(k, np.float32)), fptr(np.ascontiguousarray(v, np.float32)),
+            fptr(kc), fptr(vc), stride, iptr(pos), s.n_head, s.n_head_kv, s.head_dim, s.n_ctx,
+            s.freq_base, int(rotate))
+    rc = (oracle().oracle_decode_units_mt if lib is None else lib.ref_decode_units_mt)(*args)
+    assert rc == 0
+    return out

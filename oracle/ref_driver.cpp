@@ -1,0 +1,80 @@
+// extern "C" entry points over the reference engine's own, unmodified ops.cpp
+// (compiled where it lies by oracle/Makefile into oracle/_ref/).  TEST
+// INFRASTRUCTURE ONLY: used to write golden vectors, to check the C oracle
+// live, and as bench.py's "reference" CPU baseline.
+//
+// Wrapped interfaces:
+//   ref_rope       -> rope()       src/ops.h:175-176
+//   ref_softmax    -> softmax()    src/ops.h:107
+//   ref_attention  -> attention()  src/ops.h:204-206, with a llama_config_t
+//                     filled the way src/test_ops.cpp:299-306 fills it
+//   ref_decode_units_mt -> rope()+attention() per (sequence, layer) unit, one
+//                     std::thread per contiguous chunk of units, the pattern of
+//                     parallel_for (src/ops.cpp:67-110).
+#include <cstddef>
+#include <cstring>
+#include <thread>
+#include <vector>
+
+#include "gguf.h"
+#include "ops.h"
+
+static llama_config_t make_cfg(int n_layers, int n_head, int n_head_kv, int head_dim, int n_ctx)
+{
+    llama_config_t cfg;
+    cfg.n_layers = static_cast<std::uint32_t>(n_layers);
+    cfg.n_head = static_cast<std::uint32_t>(n_head);
+    cfg.n_head_kv = static_cast<std::uint32_t>(n_head_kv);
+    cfg.n_embd = static_cast<std::uint32_t>(n_head * head_dim);  // head_dim() = n_embd / n_head
+    cfg.n_ctx = static_cast<std::uint32_t>(n_ctx);
+    return cfg;
+}
+
+extern "C" {
+
+void ref_rope(float* q, float* k, int pos, int head_dim, int n_head, int n_head_kv, float freq_base)
+{
+    rope(q, k, pos, head_dim, n_head, n_head_kv, freq_base);
+}
+
+void ref_softmax(float* x, int size) { softmax(x, size); }
+
+void ref_attention(float* out, const float* q, const float* k, const float* v,
+                   float* key_cache, float* value_cache, float* att, int layer, int pos,
+                   int n_layers, int n_head, int n_head_kv, int head_dim, int n_ctx)
+{
+    const llama_config_t cfg = make_cfg(n_layers, n_head, n_head_kv, head_dim, n_ctx);
+    attention(out, q, k, v, key_cache, value_cache, att, layer, pos, cfg);
+}
+
+int ref_decode_units_mt(int n_threads, int n_units, float* out, const float* q,
+                        const float* k, const float* v, float* key_cache, float* value_cache,
+                        std::size_t unit_cache_stride, const int* pos, int n_head,
+                        int n_head_kv, int head_dim, int n_ctx, float freq_base, int rotate)
+{
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > n_units) n_threads = n_units;
+    const llama_config_t cfg = make_cfg(1, n_head, n_head_kv, head_dim, n_ctx);
+    const int qd = n_head * head_dim, kd = n_head_kv * head_dim;
+    auto work = [&](int u0, int u1) {
+        std::vector<float> qt(qd), kt(kd), att(n_ctx);
+        for (int u = u0; u < u1; ++u) {
+            std::memcpy(qt.data(), q + static_cast<std::size_t>(u) * qd, sizeof(float) * qd);
+            std::memcpy(kt.data(), k + static_cast<std::size_t>(u) * kd, sizeof(float) * kd);
+            if (rotate) rope(qt.data(), kt.data(), pos[u], head_dim, n_head, n_head_kv, freq_base);
+            attention(out + static_cast<std::size_t>(u) * qd, qt.data(), kt.data(),
+                      v + static_cast<std::size_t>(u) * kd,
+                      key_cache + static_cast<std::size_t>(u) * unit_cache_stride,
+                      value_cache + static_cast<std::size_t>(u) * unit_cache_stride, att.data(),
+                      0, pos[u], cfg);
+        }
+    };
+    const int chunk = n_units / n_threads;
+    std::vector<std::thread> pool;
+    for (int t = 0; t + 1 < n_threads; ++t) pool.emplace_back(work, t * chunk, (t + 1) * chunk);
+    work((n_threads - 1) * chunk, n_units);
+    for (auto& th : pool) th.join();
+    return 0;
+}
+
+}  // extern "C"

@@ -1,0 +1,283 @@
+/*
+ * CPU oracle for the grouped-query attention path -- TEST INFRASTRUCTURE ONLY.
+ *
+ * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
+ * load this library, and only as the checker / the CPU baseline.  The HIP
+ * product never links it and never falls back to it.
+ *
+ * It restates, in plain C, the reference engine's scalar ("NAIVE" backend)
+ * semantics so that results can be compared element by element:
+ *
+ *   oracle_rope       <- src/ops.cpp:1223-1281  (rope)
+ *   oracle_softmax    <- src/ops.cpp:1072-1091  (softmax)
+ *   oracle_attention  <- src/ops.cpp:1317-1371 (append) + the naive branches
+ *                        src/ops.cpp:1425-1433 (scores) and 1494-1508 (P.V);
+ *                        KV layout src/run_state.h:93-101, GQA map
+ *                        src/ops.cpp:1329/1383, scale src/ops.cpp:1335
+ *   oracle_prefill    <- the token-by-token prompt loop src/generate.cpp:56-59
+ *                        restricted to the attention block src/forward.cpp:192-208
+ *
+ * Float semantics: every product and sum is rounded separately, as the
+ * reference's x86-64 -O2 build does (no FMA in the baseline ISA).  Build with
+ * -ffp-contract=off; the libm calls (powf/cosf/sinf/expf/sqrtf) are the ones
+ * the reference makes through std::pow/std::cos/std::sin/std::exp/std::sqrt.
+ *
+ * Pinning (how each function is checked independently of itself):
+ *   - golden vectors written in this container from the compiled reference
+ *     (tests/golden/), bit-exact;
+ *   - live comparison with oracle/_ref (the reference's own ops.cpp) where built;
+ *   - closed forms and invariants (rope pair formula, norm preservation,
+ *     softmax sums/limits, pos-0 identity, equal-key averaging, GQA map);
+ *   - fp64 brute force (oracle_attention_f64) and torch SDPA on the CPU.
+ *
+ * oracle_fault() plants deliberate mistakes so the tests can show that each
+ * pin catches a plausible error (a dropped term, a wrong sign or index).
+ */
+#include <math.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <string.h>
+#include <stdlib.h>
+#include <pthread.h>
+
+/* Planted-mistake switch (tests only). 0 = faithful. */
+static int g_fault = 0;
+void oracle_fault(int mode) { g_fault = mode; }
+
+enum {
+    FAULT_NONE = 0,
+    FAULT_ROPE_SIN_SIGN = 1,   /* x0' = x0*c + x1*s                           */
+    FAULT_GQA_MODULO = 2,      /* kvh = qh % n_head_kv instead of qh / ratio  */
+    FAULT_NO_SCALE = 3,        /* drop 1/sqrt(head_dim)                       */
+    FAULT_SKIP_LAST = 4,       /* attend over 0..pos-1 (off by one)           */
+    FAULT_ROPE_PAIR_HALF = 5,  /* rotate (i, i+hd/2) halves, not (2i, 2i+1)   */
+    FAULT_SOFTMAX_NO_MAX = 6,  /* skip the max subtraction                    */
+};
+
+/* ---- rope: src/ops.cpp:1223-1281 ------------------------------------- */
+static void rope_heads(float* x, int n_heads, int pos, int head_dim, float freq_base)
+{
+    const int n_pairs = head_dim / 2;
+    for (int h = 0; h < n_heads; ++h) {
+        float* row = x + (size_t)h * head_dim;
+        for (int i = 0; i < n_pairs; ++i) {
+            /* same float expression as the reference: 1/powf(base, 2i/hd) */
+            float expo = (float)(2 * i) / (float)head_dim;
+            float freq = 1.0f / powf(freq_base, expo);
+            float angle = (float)pos * freq;
+            float c = cosf(angle);
+            float s = sinf(angle);
+            int a = 2 * i, b = 2 * i + 1;
+            if (g_fault == FAULT_ROPE_PAIR_HALF) { a = i; b = i + n_pairs; }
+            float x0 = row[a];
+            float x1 = row[b];
+            float t0 = x0 * c;
+            float t1 = x1 * s;
+            float t2 = x0 * s;
+            float t3 = x1 * c;
+            row[a] = (g_fault == FAULT_ROPE_SIN_SIGN) ? t0 + t1 : t0 - t1;
+            row[b] = t2 + t3;
+        }
+    }
+}
+
+void oracle_rope(float* q, float* k, int pos, int head_dim, int n_head,
+                 int n_head_kv, float freq_base)
+{
+    rope_heads(q, n_head, pos, head_dim, freq_base);
+    rope_heads(k, n_head_kv, pos, head_dim, freq_base);
+}
+
+/* One (cos, sin) pair per (position, pair index), same expressions as above.
+ * Used by tests to check the device RoPE table bit for bit. */
+void oracle_rope_table(float* cs, int n_pos, int head_dim, float freq_base)
+{
+    const int n_pairs = head_dim / 2;
+    for (int p = 0; p < n_pos; ++p)
+        for (int i = 0; i < n_pairs; ++i) {
+            float expo = (float)(2 * i) / (float)head_dim;
+            float freq = 1.0f / powf(freq_base, expo);
+            float angle = (float)p * freq;
+            cs[((size_t)p * n_pairs + i) * 2 + 0] = cosf(angle);
+            cs[((size_t)p * n_pairs + i) * 2 + 1] = sinf(angle);
+        }
+}
+
+/* ---- softmax: src/ops.cpp:1072-1091 ---------------------------------- */
+void oracle_softmax(float* x, int size)
+{
+    float m = x[0];
+    for (int i = 1; i < size; ++i)
+        if (x[i] > m) m = x[i];
+    if (g_fault == FAULT_SOFTMAX_NO_MAX) m = 0.0f;
+    float total = 0.0f;
+    for (int i = 0; i < size; ++i) {
+        float e = expf(x[i] - m);
+        x[i] = e;
+        total += e;
+    }
+    float inv = 1.0f / total;
+    for (int i = 0; i < size; ++i) x[i] *= inv;
+}
+
+/* ---- attention: src/ops.cpp:1317-1515 (naive branches) --------------- */
+static int gqa_kv_head(int qh, int n_head, int n_head_kv)
+{
+    if (g_fault == FAULT_GQA_MODULO) return qh % n_head_kv;
+    return qh / (n_head / n_head_kv);
+}
+
+void oracle_attention(float* out, const float* q, const float* k, const float* v,
+                      float* key_cache, float* value_cache, float* att,
+                      int layer, int pos, int n_head, int n_head_kv, int head_dim,
+                      int n_ctx)
+{
+    const int kv_dim = n_head_kv * head_dim;
+    const float scale = (g_fault == FAULT_NO_SCALE)
+                            ? 1.0f : 1.0f / sqrtf((float)head_dim);
+    /* size_t offsets (the reference uses int, which is equal within its range) */
+    const size_t base = (size_t)layer * (size_t)n_ctx * (size_t)kv_dim;
+
+    memcpy(key_cache + base + (size_t)pos * kv_dim, k, sizeof(float) * kv_dim);
+    memcpy(value_cache + base + (size_t)pos * kv_dim, v, sizeof(float) * kv_dim);
+
+    const int last = (g_fault == FAULT_SKIP_LAST && pos > 0) ? pos - 1 : pos;
+    for (int qh = 0; qh < n_head; ++qh) {
+        const float* qrow = q + (size_t)qh * head_dim;
+        const int kvh = gqa_kv_head(qh, n_head, n_head_kv);
+        for (int p = 0; p <= last; ++p) {
+            const float* krow = key_cache + base + (size_t)p * kv_dim + (size_t)kvh * head_dim;
+            float dot = 0.0f;
+            for (int d = 0; d < head_dim; ++d) dot += qrow[d] * krow[d];
+            att[p] = dot * scale;
+        }
+        oracle_softmax(att, last + 1);
+        float* orow = out + (size_t)qh * head_dim;
+        for (int d = 0; d < head_dim; ++d) orow[d] = 0.0f;
+        for (int p = 0; p <= last; ++p) {
+            const float* vrow = value_cache + base + (size_t)p * kv_dim + (size_t)kvh * head_dim;
+            const float w = att[p];
+            for (int d = 0; d < head_dim; ++d) orow[d] += w * vrow[d];
+        }
+    }
+}
+
+/* ---- fp64 brute force over an already-appended cache ----------------- */
+/* out64[n_head*head_dim] = softmax(q.K^T / sqrt(hd)) V in double precision. */
+void oracle_attention_f64(double* out64, const float* q, const float* key_cache,
+                          const float* value_cache, int layer, int pos, int n_head,
+                          int n_head_kv, int head_dim, int n_ctx)
+{
+    const int kv_dim = n_head_kv * head_dim;
+    const size_t base = (size_t)layer * (size_t)n_ctx * (size_t)kv_dim;
+    const double scale = 1.0 / sqrt((double)head_dim);
+    double* sc = (double*)malloc(sizeof(double) * (size_t)(pos + 1));
+    for (int qh = 0; qh < n_head; ++qh) {
+        const int kvh = qh / (n_head / n_head_kv);
+        double mx = -INFINITY;
+        for (int p = 0; p <= pos; ++p) {
+            const float* krow = key_cache + base + (size_t)p * kv_dim + (size_t)kvh * head_dim;
+            double dot = 0.0;
+            for (int d = 0; d < head_dim; ++d)
+                dot += (double)q[(size_t)qh * head_dim + d] * (double)krow[d];
+            sc[p] = dot * scale;
+            if (sc[p] > mx) mx = sc[p];
+        }
+        double sum = 0.0;
+        for (int p = 0; p <= pos; ++p) { sc[p] = exp(sc[p] - mx); sum += sc[p]; }
+        for (int d = 0; d < head_dim; ++d) {
+            double acc = 0.0;
+            for (int p = 0; p <= pos; ++p)
+                acc += sc[p] * (double)value_cache[base + (size_t)p * kv_dim + (size_t)kvh * head_dim + d];
+            out64[(size_t)qh * head_dim + d] = acc / sum;
+        }
+    }
+    free(sc);
+}
+
+/* ---- prompt prefill as the reference runs it: src/generate.cpp:56-59 -- */
+/* For t = 0..n_tok-1: rope(q_t, k_t, pos0+t); attention(out_t, ..., pos0+t).
+ * q: [n_tok][n_head*hd], k/v: [n_tok][n_head_kv*hd] (raw, not rotated; they
+ * are copied so the caller's inputs stay unchanged), out: [n_tok][n_head*hd]. */
+void oracle_prefill(float* out, const float* q, const float* k, const float* v,
+                    float* key_cache, float* value_cache, int layer, int pos0,
+                    int n_tok, int n_head, int n_head_kv, int head_dim, int n_ctx,
+                    float freq_base)
+{
+    const int qd = n_head * head_dim, kd = n_head_kv * head_dim;
+    float* qt = (float*)malloc(sizeof(float) * (size_t)qd);
+    float* kt = (float*)malloc(sizeof(float) * (size_t)kd);
+    float* att = (float*)malloc(sizeof(float) * (size_t)n_ctx);
+    for (int t = 0; t < n_tok; ++t) {
+        memcpy(qt, q + (size_t)t * qd, sizeof(float) * qd);
+        memcpy(kt, k + (size_t)t * kd, sizeof(float) * kd);
+        oracle_rope(qt, kt, pos0 + t, head_dim, n_head, n_head_kv, freq_base);
+        oracle_attention(out + (size_t)t * qd, qt, kt, v + (size_t)t * kd, key_cache,
+                         value_cache, att, layer, pos0 + t, n_head, n_head_kv,
+                         head_dim, n_ctx);
+    }
+    free(att); free(kt); free(qt);
+}
+
+/* ---- batched decode on several host threads (CPU baseline) ----------- */
+/* A "unit" is one (sequence, layer) decode problem with its own cache
+ * slice.  Units are split across threads in contiguous chunks, the pattern
+ * of the reference's parallel_for (src/ops.cpp:67-110).  Each unit runs
+ * rope + oracle_attention exactly as one forward() layer step does. */
+typedef struct {
+    int u0, u1;
+    float* out; const float* q; const float* k; const float* v;
+    float* kc; float* vc;
+    const int* pos;          /* per unit */
+    size_t unit_cache_stride;/* floats between units' caches */
+    int n_head, n_head_kv, head_dim, n_ctx; float freq_base; int rotate;
+} decode_job;
+
+static void* decode_worker(void* arg)
+{
+    decode_job* j = (decode_job*)arg;
+    const int qd = j->n_head * j->head_dim, kd = j->n_head_kv * j->head_dim;
+    float* qt = (float*)malloc(sizeof(float) * (size_t)qd);
+    float* kt = (float*)malloc(sizeof(float) * (size_t)kd);
+    float* att = (float*)malloc(sizeof(float) * (size_t)j->n_ctx);
+    for (int u = j->u0; u < j->u1; ++u) {
+        memcpy(qt, j->q + (size_t)u * qd, sizeof(float) * qd);
+        memcpy(kt, j->k + (size_t)u * kd, sizeof(float) * kd);
+        if (j->rotate)
+            oracle_rope(qt, kt, j->pos[u], j->head_dim, j->n_head, j->n_head_kv, j->freq_base);
+        oracle_attention(j->out + (size_t)u * qd, qt, kt, j->v + (size_t)u * kd,
+                         j->kc + (size_t)u * j->unit_cache_stride,
+                         j->vc + (size_t)u * j->unit_cache_stride, att, 0, j->pos[u],
+                         j->n_head, j->n_head_kv, j->head_dim, j->n_ctx);
+    }
+    free(att); free(kt); free(qt);
+    return NULL;
+}
+
+int oracle_decode_units_mt(int n_threads, int n_units, float* out, const float* q,
+                           const float* k, const float* v, float* key_cache,
+                           float* value_cache, size_t unit_cache_stride,
+                           const int* pos, int n_head, int n_head_kv, int head_dim,
+                           int n_ctx, float freq_base, int rotate)
+{
+    if (n_threads < 1) n_threads = 1;
+    if (n_threads > n_units) n_threads = n_units;
+    if (n_threads > 256) n_threads = 256;
+    pthread_t tid[256];
+    decode_job jobs[256];
+    const int chunk = n_units / n_threads;
+    for (int t = 0; t < n_threads; ++t) {
+        decode_job* j = &jobs[t];
+        j->u0 = t * chunk;
+        j->u1 = (t == n_threads - 1) ? n_units : (t + 1) * chunk;
+        j->out = out; j->q = q; j->k = k; j->v = v; j->kc = key_cache; j->vc = value_cache;
+        j->pos = pos; j->unit_cache_stride = unit_cache_stride;
+        j->n_head = n_head; j->n_head_kv = n_head_kv; j->head_dim = head_dim;
+        j->n_ctx = n_ctx; j->freq_base = freq_base; j->rotate = rotate;
+    }
+    for (int t = 1; t < n_threads; ++t)
+        if (pthread_create(&tid[t], NULL, decode_worker, &jobs[t]) != 0) return -1;
+    decode_worker(&jobs[0]);
+    for (int t = 1; t < n_threads; ++t) pthread_join(tid[t], NULL);
+    return 0;
+}

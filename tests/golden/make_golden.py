@@ -1,0 +1,197 @@
+"""Write golden vectors for the attention path from the COMPILED REFERENCE.
+
+Runs only in the build container, where /root/reference exists: it builds
+oracle/_ref/libref_ops.so (the reference's own src/ops.cpp, see
+oracle/Makefile) and calls rope / softmax / attention through it.  The
+fixtures it writes (tests/golden/*.npz: inputs where small, seeds plus a
+sha256 of the inputs where not, and the reference's outputs) are what the
+tests compare the oracle and the GPU path with; nothing here runs on the GPU
+box.
+
+    python tests/golden/make_golden.py
+"""
+from __future__ import annotations
+
+import importlib
+import os
+import sys
+
+import numpy as np
+
+ROOT = os.path.abspath(os.path.join(os.path.dirname(__file__), "..", ".."))
+sys.path.insert(0, ROOT)
+
+import oracle as O  # noqa: E402
+
+W = importlib.import_module("tinyllama-engine_amd.workloads")
+OUT = os.path.dirname(os.path.abspath(__file__))
+TL = O.Shape(n_ctx=64, n_layers=2)  # src/test_ops.cpp:299-306 stub config
+
+
+def save(name, **arrays):
+    path = os.path.join(OUT, name)
+    np.savez_compressed(path, **arrays)
+    print(f"wrote {path} ({os.path.getsize(path)} bytes)")
+
+
+def softmax_cases(R):
+    cases = {
+        # src/test_ops.cpp:134-161
+        "t_uniform": np.array([1, 1, 1, 1], np.float32),
+        "t_dominant": np.array([10, 0, 0], np.float32),
+        "t_sum": np.array([2.0, 1.0, 0.1, -1.0, 3.0], np.float32),
+        "t_large": np.array([1000, 1000, 999], np.float32),
+    }
+    g = W.rng(100)
+    for n in (1, 2, 5, 64, 129, 2048, 5000):
+        for scale in (1.0, 10.0):
+            cases[f"r{n}_s{int(scale)}"] = W.normal(g, (n,), scale)
+    out = {}
+    for name, x in cases.items():
+        out["in_" + name] = x
+        out["out_" + name] = O.softmax(x, lib=R)
+    save("softmax.npz", **out)
+
+
+ROPE_POSITIONS = [0, 1, 2, 5, 17, 42, 100, 127, 128, 511, 1000, 2047, 4095, 8191, 16383]
+
+
+def rope_cases(R):
+    s = O.Shape()
+    g = W.rng(101)
+    q = W.normal(g, (s.q_dim,))
+    k = W.normal(g, (s.kv_dim,))
+    qo, ko = [], []
+    for p in ROPE_POSITIONS:
+        a, b = O.rope(q, k, p, s, lib=R)
+        qo.append(a)
+        ko.append(b)
+    # src/test_ops.cpp:530-545: head 0 pair 0 = (3, 4) at pos 1
+    mq = np.zeros(s.q_dim, np.float32)
+    mq[0], mq[1] = 3.0, 4.0
+    mk = np.zeros(s.kv_dim, np.float32)
+    mqo, mko = O.rope(mq, mk, 1, s, lib=R)
+    save("rope.npz", q=q, k=k, positions=np.array(ROPE_POSITIONS, np.int32), q_out=np.stack(qo),
+         k_out=np.stack(ko), manual_q=mq, manual_q_out=mqo, manual_k_out=mko)
+
+
+def testops_attention(R):
+    """Replay src/test_ops.cpp:295-431 (T1-T4) through the reference."""
+    s, hd = TL, 64
+    res = {}
+
+    def fresh():
+        n = s.n_layers * s.n_ctx * s.kv_dim
+        return np.zeros(n, np.float32), np.zeros(n, np.float32)
+
+    # T1: pos 0, q=k=1, v[i] = i % 64
+    kc, vc = fresh()
+    q = np.ones(s.q_dim, np.float32)
+    k = np.ones(s.kv_dim, np.float32)
+    v = (np.arange(s.kv_dim) % hd).astype(np.float32)
+    res["t1_out"] = O.attention(q, k, v, kc, vc, 0, 0, s, lib=R)
+    # T2: two tokens, equal keys, v = 1 then 3
+    kc, vc = fresh()
+    O.attention(q, k, np.ones(s.kv_dim, np.float32), kc, vc, 0, 0, s, lib=R)
+    res["t2_out"] = O.attention(q, k, np.full(s.kv_dim, 3, np.float32), kc, vc, 0, 1, s, lib=R)
+    # T3: 10 tokens of integer patterns
+    kc, vc = fresh()
+    outs, qs, ks, vs = [], [], [], []
+    for p in range(10):
+        qp = ((np.arange(s.q_dim) + p) % 11 - 5).astype(np.float32)
+        kp = ((np.arange(s.kv_dim) + p * 3) % 7 - 3).astype(np.float32)
+        vp = ((np.arange(s.kv_dim) + p * 5) % 9 - 4).astype(np.float32)
+        outs.append(O.attention(qp, kp, vp, kc, vc, 0, p, s, lib=R))
+        qs.append(qp); ks.append(kp); vs.append(vp)
+    res["t3_q"], res["t3_k"], res["t3_v"] = np.stack(qs), np.stack(ks), np.stack(vs)
+    res["t3_out"] = np.stack(outs)
+    res["t3_kc"] = kc.copy()
+    res["t3_vc"] = vc.copy()
+    # T4: GQA map, v head 0 = 10, head 1 = 20
+    kc, vc = fresh()
+    v4 = np.zeros(s.kv_dim, np.float32)
+    v4[:hd] = 10.0
+    v4[hd:2 * hd] = 20.0
+    res["t4_v"] = v4
+    res["t4_out"] = O.attention(q, k, v4, kc, vc, 0, 0, s, lib=R)
+    save("attention_testops.npz", **res)
+
+
+def decode_single(R):
+    """decode_single workload with the reference's real history: rows 0..126
+    are appended token by token with rope at their own positions."""
+    s = O.Shape(n_ctx=128, n_layers=1)
+    g = W.rng("decode_single", 7)
+    n = 128
+    q = W.normal(g, (n, s.q_dim))
+    k = W.normal(g, (n, s.kv_dim))
+    v = W.normal(g, (n, s.kv_dim))
+    kc = np.zeros(s.n_ctx * s.kv_dim, np.float32)
+    vc = np.zeros_like(kc)
+    out = None
+    for p in range(n):
+        qr, kr = O.rope(q[p], k[p], p, s, lib=R)
+        out = O.attention(qr, kr, v[p], kc, vc, 0, p, s, lib=R)
+    save("decode_single.npz", digest=np.array(W.digest(q, k, v)), out=out, kc=kc, vc=vc)
+
+
+def decode_peaked(R):
+    """Reduced decode_long: one sequence, L = 1024, peaked keys."""
+    s = O.Shape(n_ctx=1024, n_layers=1)
+    case = W.make_decode("decode_long", 1, 1, 1024, 1023, kv_std=0.5, peaked_frac=0.01, salt=7)
+    kc = case.kc.reshape(-1).copy()
+    vc = case.vc.reshape(-1).copy()
+    qr, kr = O.rope(case.q[0, 0], case.k[0, 0], 1023, s, lib=R)
+    out = O.attention(qr, kr, case.v[0, 0], kc, vc, 0, 1023, s, lib=R)
+    save("decode_peaked.npz", digest=np.array(W.digest(case.q, case.k, case.v, case.kc, case.vc)),
+         out=out, k_row=kc.reshape(1024, -1)[1023].copy(), v_row=vc.reshape(1024, -1)[1023].copy())
+
+
+def decode_ragged(R):
+    """Three sequences x two layers, ragged positions, rope + attention."""
+    s = O.Shape(n_ctx=64, n_layers=2)
+    pos = [5, 63, 17]
+    case = W.make_decode("decode_ragged", 3, 2, 64, pos, salt=7)
+    outs = np.zeros((3, 2, s.q_dim), np.float32)
+    for si in range(3):
+        kc = case.kc[si].reshape(-1).copy()
+        vc = case.vc[si].reshape(-1).copy()
+        for layer in range(2):
+            qr, kr = O.rope(case.q[si, layer], case.k[si, layer], pos[si], s, lib=R)
+            outs[si, layer] = O.attention(qr, kr, case.v[si, layer], kc, vc, layer, pos[si], s,
+                                          lib=R)
+    save("decode_ragged.npz", digest=np.array(W.digest(case.q, case.k, case.v, case.kc, case.vc)),
+         pos=np.array(pos, np.int32), out=outs)
+
+
+def prefill(R):
+    """40-token prompt into layer 1 of a 2-layer, 64-position cache, token by
+    token as src/generate.cpp:56-59 does."""
+    s = O.Shape(n_ctx=64, n_layers=2)
+    case = W.make_prefill(n_layers=1, n_tok=40, salt=7)
+    kc = np.zeros(s.n_layers * s.n_ctx * s.kv_dim, np.float32)
+    vc = np.zeros_like(kc)
+    outs = []
+    for t in range(40):
+        qr, kr = O.rope(case.q[0, t], case.k[0, t], t, s, lib=R)
+        outs.append(O.attention(qr, kr, case.v[0, t], kc, vc, 1, t, s, lib=R))
+    kcl = kc.reshape(2, 64, -1)[1, :40].copy()
+    vcl = vc.reshape(2, 64, -1)[1, :40].copy()
+    save("prefill.npz", digest=np.array(W.digest(case.q, case.k, case.v)), out=np.stack(outs),
+         kc=kcl, vc=vcl)
+
+
+def main():
+    O.build(with_ref=True)
+    R = O.ref()
+    softmax_cases(R)
+    rope_cases(R)
+    testops_attention(R)
+    decode_single(R)
+    decode_peaked(R)
+    decode_ragged(R)
+    prefill(R)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,214 @@
+"""GPU parity of decode attention (split-KV, RoPE + append fused) through the
+C ABI, against the golden vectors and the oracle on the same seeded inputs.
+Bar: max-abs 1e-4 on outputs, appended cache rows bit-exact."""
+import numpy as np
+import pytest
+
+from conftest import golden
+from helpers import (DECODE_TOL, bits, check_decode, device_arrays, gpu_decode, log, max_err,
+                     oracle_decode)
+
+pytestmark = pytest.mark.gpu
+
+
+def test_decode_single_golden(tla, W, engines):
+    """Position 127 over a cache built token by token by the reference."""
+    g = golden("decode_single.npz")
+    eng = engines(1, 128)
+    rg = W.rng("decode_single", 7)
+    q, k, v = W.normal(rg, (128, 2048)), W.normal(rg, (128, 256)), W.normal(rg, (128, 256))
+    assert W.digest(q, k, v) == str(g["digest"])
+    kc_host = g["kc"].reshape(128, 256).copy()
+    vc_host = g["vc"].reshape(128, 256).copy()
+    kc_host[127] = 0
+    vc_host[127] = 0
+    with device_arrays() as track:
+        kc, vc = eng.kv_cache(1)
+        track(kc), track(vc)
+        kc.upload(kc_host)
+        vc.upload(vc_host)
+        dq, dk, dv = track(eng.array(q[127])), track(eng.array(k[127])), track(eng.array(v[127]))
+        out = track(eng.array((2048,)))
+        eng.rope_attention(out.ptr, dq.ptr, dk.ptr, dv.ptr, kc.ptr, vc.ptr, 0, 127)
+        err = max_err(out.download(), g["out"])
+        log(f"  decode_single vs reference: max-abs {err:.3e}")
+        assert err <= DECODE_TOL
+        assert np.array_equal(bits(kc.download()), bits(g["kc"])), "key cache"
+        assert np.array_equal(bits(vc.download()), bits(g["vc"])), "value cache"
+        # q and k buffers are left unrotated by the fused block
+        assert np.array_equal(dq.download(), q[127])
+
+
+def test_decode_peaked_golden(tla, W, engines):
+    g = golden("decode_peaked.npz")
+    case = W.make_decode("decode_long", 1, 1, 1024, 1023, kv_std=0.5, peaked_frac=0.01, salt=7)
+    assert W.digest(case.q, case.k, case.v, case.kc, case.vc) == str(g["digest"])
+    for split in (0, 16, 48, 1024):
+        got, krow, vrow = gpu_decode(engines(1, 1024), case, split=split)
+        err = max_err(got[0, 0], g["out"])
+        log(f"    vs reference: max-abs {err:.3e}")
+        assert err <= DECODE_TOL
+        assert np.array_equal(bits(krow[0, 0]), bits(g["k_row"]))
+        assert np.array_equal(bits(vrow[0, 0]), bits(g["v_row"]))
+
+
+def test_decode_ragged_golden(tla, W, engines):
+    g = golden("decode_ragged.npz")
+    pos = [int(p) for p in g["pos"]]
+    case = W.make_decode("decode_ragged", 3, 2, 64, pos, salt=7)
+    got, _, _ = gpu_decode(engines(2, 64), case)
+    err = max_err(got, g["out"])
+    log(f"    vs reference: max-abs {err:.3e}")
+    assert err <= DECODE_TOL
+
+
+def test_reference_testops_cases(tla, engines):
+    """src/test_ops.cpp:295-431 through tla_attention (q, k pre-rotated)."""
+    g = golden("attention_testops.npz")
+    eng = engines(2, 64)
+    ones_q, ones_k = np.ones(2048, np.float32), np.ones(256, np.float32)
+    with device_arrays() as track:
+        kc, vc = eng.kv_cache(1)
+        track(kc), track(vc)
+        out = track(eng.array((2048,)))
+
+        def run(qh, kh, vh, pos):
+            dq, dk, dv = eng.array(qh), eng.array(kh), eng.array(vh)
+            eng.attention(out.ptr, dq.ptr, dk.ptr, dv.ptr, kc.ptr, vc.ptr, 0, pos)
+            r = out.download()
+            for a in (dq, dk, dv):
+                a.free()
+            return r
+
+        o = run(ones_q, ones_k, (np.arange(256) % 64).astype(np.float32), 0)
+        assert max_err(o, g["t1_out"]) <= DECODE_TOL
+        assert np.all(np.abs(o[:64] - np.arange(64)) < 1e-3)
+
+        kc.upload(np.zeros(kc.shape, np.float32))
+        vc.upload(np.zeros(vc.shape, np.float32))
+        run(ones_q, ones_k, np.ones(256, np.float32), 0)
+        o = run(ones_q, ones_k, np.full(256, 3, np.float32), 1)
+        assert max_err(o, g["t2_out"]) <= DECODE_TOL and abs(o[0] - 2.0) < 0.01
+
+        kc.upload(np.zeros(kc.shape, np.float32))
+        vc.upload(np.zeros(vc.shape, np.float32))
+        for p in range(10):
+            o = run(g["t3_q"][p], g["t3_k"][p], g["t3_v"][p], p)
+            assert max_err(o, g["t3_out"][p]) <= DECODE_TOL, p
+        assert np.all(np.isfinite(o))
+        assert np.array_equal(bits(kc.download().reshape(-1)), bits(g["t3_kc"]))
+        assert np.array_equal(bits(vc.download().reshape(-1)), bits(g["t3_vc"]))
+
+        kc.upload(np.zeros(kc.shape, np.float32))
+        vc.upload(np.zeros(vc.shape, np.float32))
+        o = run(ones_q, ones_k, g["t4_v"], 0)
+        assert abs(o[0] - 10) < 0.01 and abs(o[8 * 64] - 20) < 0.01
+
+
+@pytest.mark.parametrize("pos", [0, 1, 15, 16, 17, 63, 64, 100, 511, 512, 1000, 2047])
+@pytest.mark.parametrize("split", [0, 16, 64, 208])
+def test_decode_positions_and_splits(O, W, engines, pos, split):
+    case = W.make_decode(11, 1, 2, 2048, pos, salt=pos)
+    check_decode(O, engines(2, 2048), case, split=split)
+
+
+def test_attention_contract_without_rotation(O, W, engines):
+    """tla_decode without TLA_ROTATE = attention(): q, k taken as rotated."""
+    case = W.make_decode(12, 2, 3, 512, [200, 511], salt=1)
+    check_decode(O, engines(3, 512), case, rotate=False)
+
+
+def test_decode_model_full_size(O, W, engines):
+    """22 layers at context 2048 (position 2047), one call."""
+    case = W.decode_model(n_layers=22, n_ctx=2048)
+    check_decode(O, engines(22, 2048), case)
+
+
+def test_decode_ragged_full_size(O, W, engines):
+    """64 sequences, context lengths uniform in [256, 2048], 22 layers."""
+    case = W.decode_ragged(n_seq=64, n_layers=22, n_ctx=2048)
+    check_decode(O, engines(22, 2048), case)
+
+
+def test_decode_long_peaked(O, W, engines):
+    """Context 16384, batch 8, peaked keys (1% of rows x8): online softmax and
+    the split merge; checked against the oracle and against fp64."""
+    case = W.decode_long(n_seq=8, n_layers=2, n_ctx=16384)
+    eng = engines(2, 16384)
+    err = check_decode(O, eng, case)
+    # peaked softmax really is peaked: the largest weight of some head is big
+    got, kc, vc = gpu_decode(eng, W.decode_long(n_seq=1, n_layers=2, n_ctx=16384), keep_cache=True)
+    one = W.decode_long(n_seq=1, n_layers=2, n_ctx=16384)
+    qr, _ = O.rope(one.q[0, 0], one.k[0, 0], 16383, O.Shape())
+    f64 = O.attention_f64(qr, kc[0].reshape(-1), vc[0].reshape(-1), 0, 16383,
+                          O.Shape(n_ctx=16384, n_layers=2))
+    e64 = max_err(got[0, 0], f64)
+    log(f"    vs fp64: {e64:.3e} (vs oracle {err:.3e})")
+    assert e64 <= DECODE_TOL
+
+
+def test_batch_call_equals_per_sequence_calls(O, W, engines):
+    """A ragged batch in one call and the same sequences one at a time."""
+    case = W.make_decode(13, 5, 2, 1024, [3, 1023, 400, 16, 777], salt=3)
+    eng = engines(2, 1024)
+    batch, _, _ = gpu_decode(eng, case)
+    ref, _, _ = oracle_decode(O, case)
+    assert max_err(batch, ref) <= DECODE_TOL
+    for s in range(5):
+        one = W.DecodeCase(1, 2, 1024, case.pos[s:s + 1], case.q[s:s + 1], case.k[s:s + 1],
+                           case.v[s:s + 1], case.kc[s:s + 1], case.vc[s:s + 1])
+        single, _, _ = gpu_decode(eng, one)
+        assert max_err(single[0], ref[s]) <= DECODE_TOL
+
+
+def test_decode_is_deterministic(W, engines):
+    case = W.make_decode(14, 2, 2, 2048, [2047, 999])
+    a, _, _ = gpu_decode(engines(2, 2048), case)
+    b, _, _ = gpu_decode(engines(2, 2048), case)
+    assert np.array_equal(bits(a), bits(b))
+
+
+def test_full_context_properties(tla, W, engines):
+    """Size-independent properties at context 16384: constant V gives that
+    constant; the output is linear in V (same K, same q)."""
+    eng = engines(1, 16384)
+    case = W.make_decode(15, 1, 1, 16384, 16383, kv_std=0.5, peaked_frac=0.01)
+    const = W.DecodeCase(1, 1, 16384, case.pos, case.q, case.k, np.full_like(case.v, 0.75),
+                         case.kc, np.full_like(case.vc, 0.75))
+    got, _, _ = gpu_decode(eng, const)
+    assert np.abs(got - 0.75).max() <= 1e-5
+    v1 = W.normal(W.rng(15, 1), case.vc.shape)
+    n1 = W.normal(W.rng(15, 2), case.v.shape)
+    outs = []
+    for vc, vn in ((case.vc, case.v), (v1, n1), (case.vc + v1, case.v + n1)):
+        c = W.DecodeCase(1, 1, 16384, case.pos, case.q, case.k, vn.astype(np.float32), case.kc,
+                         vc.astype(np.float32))
+        outs.append(gpu_decode(eng, c)[0])
+    assert max_err(outs[0] + outs[1], outs[2]) <= 1e-5
+
+
+def test_out_of_range_is_an_error_and_launches_nothing(tla, W, engines):
+    eng = engines(2, 64)
+    case = W.make_decode(16, 1, 2, 64, 10)
+    with device_arrays() as track:
+        kc, vc = eng.kv_cache(1)
+        track(kc), track(vc)
+        kc.upload(case.kc)
+        q, k, v = track(eng.array(case.q)), track(eng.array(case.k)), track(eng.array(case.v))
+        out = track(eng.array(case.q.shape))
+        before = kc.download()
+        for pos, layer0, nl, code in ((64, 0, 1, tla.TLA_ERR_OUT_OF_RANGE),
+                                      (-1, 0, 1, tla.TLA_ERR_OUT_OF_RANGE),
+                                      (3, 2, 1, tla.TLA_ERR_OUT_OF_RANGE),
+                                      (3, 1, 2, tla.TLA_ERR_OUT_OF_RANGE),
+                                      (3, 0, 0, tla.TLA_ERR_INVALID_ARGUMENT)):
+            with pytest.raises(tla.TlaError) as ei:
+                eng.decode([pos], layer0, nl, out.ptr, q.ptr, k.ptr, v.ptr, kc.ptr, vc.ptr)
+            assert ei.value.code == code, tla.last_error()
+        with pytest.raises(tla.TlaError):
+            eng.decode(np.zeros(257, np.int32), 0, 1, out.ptr, q.ptr, k.ptr, v.ptr, kc.ptr, vc.ptr,
+                       2 * 64 * 256)
+        with pytest.raises(tla.TlaError):  # n_seq > 1 with a too-small seq_stride
+            eng.decode([1, 2], 0, 1, out.ptr, q.ptr, k.ptr, v.ptr, kc.ptr, vc.ptr, 64 * 256)
+        eng.synchronize()
+        assert np.array_equal(bits(kc.download()), bits(before))

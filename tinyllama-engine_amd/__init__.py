@@ -1,0 +1,253 @@
+"""MI355X grouped-query attention path of the TinyLlama engine.
+
+Python view of the C ABI in include/tla_attention.h (libtla.so, built for
+gfx950 by __graft_entry__.build()).  The product is the shared library; this
+module is the ctypes binding the tests and bench.py drive it through.  There
+is no CPU fallback: if libtla.so is missing, importing `lib()` raises.
+
+Interfaces mirrored (reference files):
+    Engine.rope        rope()       src/ops.h:175-176
+    Engine.softmax     softmax()    src/ops.h:107
+    Engine.attention   attention()  src/ops.h:204-206
+    Engine.rope_attention   the block of forward() src/forward.cpp:192-208
+    Engine.decode      batched / multi-layer decode (one attention() per
+                       (sequence, layer))
+    Engine.prefill     the prompt loop src/generate.cpp:56-59, batched
+    Engine.kv_cache    RunState::key_cache / value_cache src/run_state.h:93-101
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libtla.so")
+HOST_LIB_PATH = os.path.join(HERE, "libtla_host.so")
+
+TLA_OK = 0
+TLA_ERR_INVALID_ARGUMENT = 1
+TLA_ERR_OUT_OF_RANGE = 2
+TLA_ERR_UNSUPPORTED = 3
+TLA_ERR_DEVICE = 4
+TLA_ERR_OUT_OF_MEMORY = 5
+TLA_ROTATE = 1
+
+KERNEL_DECODE, KERNEL_COMBINE, KERNEL_PREFILL, KERNEL_APPEND = range(4)
+OPT_DECODE_SPLIT = 0
+
+
+class TlaError(RuntimeError):
+    def __init__(self, code: int, what: str, msg: str):
+        super().__init__(f"{what} failed (status {code}): {msg}")
+        self.code = code
+
+
+class Config(C.Structure):
+    """tla_config: the llama_config_t fields the path uses (src/gguf.h:139-168)."""
+
+    _fields_ = [("n_layers", C.c_int), ("n_embd", C.c_int), ("n_head", C.c_int),
+                ("n_head_kv", C.c_int), ("n_ctx", C.c_int), ("rope_freq_base", C.c_float)]
+
+    @classmethod
+    def tinyllama(cls, n_layers=22, n_ctx=2048):
+        return cls(n_layers, 2048, 32, 4, n_ctx, 10000.0)
+
+    @property
+    def head_dim(self):
+        return self.n_embd // self.n_head
+
+    @property
+    def kv_dim(self):
+        return self.n_head_kv * self.head_dim
+
+
+_vp = C.c_void_p
+_lib = None
+
+# name -> (restype, argtypes); every symbol declared in include/tla_attention.h
+SIGNATURES = {
+    "tla_last_error": (C.c_char_p, []),
+    "tla_abi_version": (C.c_int, []),
+    "tla_engine_create": (C.c_int, [C.POINTER(Config), C.c_int, C.POINTER(_vp)]),
+    "tla_engine_destroy": (C.c_int, [_vp]),
+    "tla_synchronize": (C.c_int, [_vp]),
+    "tla_alloc": (C.c_int, [_vp, C.c_size_t, C.POINTER(_vp)]),
+    "tla_free": (C.c_int, [_vp, _vp]),
+    "tla_kv_cache_alloc": (C.c_int, [_vp, C.c_int, C.POINTER(_vp), C.POINTER(_vp)]),
+    "tla_memcpy_h2d": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+    "tla_memcpy_d2h": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+    "tla_memcpy_d2d": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
+    "tla_rope": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
+    "tla_softmax": (C.c_int, [_vp, _vp, C.c_int]),
+    "tla_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
+    "tla_rope_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
+    "tla_decode": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int,
+                             _vp, _vp, _vp, _vp, _vp, _vp, C.c_size_t]),
+    "tla_prefill": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
+                              _vp, _vp, _vp, _vp, _vp, _vp]),
+    "tla_profile_enable": (C.c_int, [_vp, C.c_int]),
+    "tla_profile_read": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_double),
+                                   C.POINTER(C.c_longlong)]),
+    "tla_event_record": (C.c_int, [_vp, C.c_int]),
+    "tla_event_elapsed": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(C.c_float)]),
+    "tla_set_option": (C.c_int, [_vp, C.c_int, C.c_longlong]),
+}
+
+
+def lib() -> C.CDLL:
+    """Load libtla.so (raises if it was never built -- no fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise FileNotFoundError(
+                f"{LIB_PATH} is missing: build the HIP extension first (__graft_entry__.build())")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in SIGNATURES.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def last_error() -> str:
+    return lib().tla_last_error().decode()
+
+
+def _check(rc: int, what: str):
+    if rc != TLA_OK:
+        raise TlaError(rc, what, last_error())
+
+
+class DeviceArray:
+    """A device allocation with a numpy-like shape and dtype (float32/int32)."""
+
+    def __init__(self, engine: "Engine", shape, dtype=np.float32, ptr=None, owner=True):
+        self.engine = engine
+        self.shape = tuple(int(s) for s in (shape if isinstance(shape, (tuple, list)) else (shape,)))
+        self.dtype = np.dtype(dtype)
+        self.nbytes = int(np.prod(self.shape)) * self.dtype.itemsize
+        self.owner = owner
+        if ptr is None:
+            p = _vp()
+            _check(lib().tla_alloc(engine.h, max(self.nbytes, 4), C.byref(p)), "tla_alloc")
+            ptr = p.value
+        self.ptr = ptr
+
+    def upload(self, host: np.ndarray):
+        host = np.ascontiguousarray(host, dtype=self.dtype)
+        assert host.nbytes == self.nbytes, (host.shape, self.shape)
+        _check(lib().tla_memcpy_h2d(self.engine.h, self.ptr, host.ctypes.data, self.nbytes),
+               "tla_memcpy_h2d")
+        return self
+
+    def download(self) -> np.ndarray:
+        out = np.empty(self.shape, self.dtype)
+        _check(lib().tla_memcpy_d2h(self.engine.h, out.ctypes.data, self.ptr, self.nbytes),
+               "tla_memcpy_d2h")
+        return out
+
+    def at(self, byte_offset: int) -> int:
+        return self.ptr + byte_offset
+
+    def free(self):
+        if self.owner and self.ptr:
+            _check(lib().tla_free(self.engine.h, self.ptr), "tla_free")
+        self.ptr = None
+
+
+class Engine:
+    """One tla_engine: device, stream, RoPE table, split-KV workspace."""
+
+    def __init__(self, cfg: Config, device: int = 0):
+        self.cfg = cfg
+        h = _vp()
+        _check(lib().tla_engine_create(C.byref(cfg), device, C.byref(h)), "tla_engine_create")
+        self.h = h.value
+
+    def close(self):
+        if self.h:
+            lib().tla_engine_destroy(self.h)
+            self.h = None
+
+    def __enter__(self):
+        return self
+
+    def __exit__(self, *exc):
+        self.close()
+
+    # ---- memory -------------------------------------------------------------
+    def array(self, host_or_shape, dtype=np.float32) -> DeviceArray:
+        if isinstance(host_or_shape, np.ndarray):
+            a = DeviceArray(self, host_or_shape.shape, host_or_shape.dtype)
+            return a.upload(host_or_shape)
+        return DeviceArray(self, host_or_shape, dtype)
+
+    def kv_cache(self, n_seq: int = 1):
+        """(key_cache, value_cache) device arrays [n_seq, n_layers, n_ctx, kv_dim], zeroed."""
+        k, v = _vp(), _vp()
+        _check(lib().tla_kv_cache_alloc(self.h, n_seq, C.byref(k), C.byref(v)),
+               "tla_kv_cache_alloc")
+        shape = (n_seq, self.cfg.n_layers, self.cfg.n_ctx, self.cfg.kv_dim)
+        return DeviceArray(self, shape, ptr=k.value), DeviceArray(self, shape, ptr=v.value)
+
+    def copy(self, dst: int, src: int, nbytes: int):
+        _check(lib().tla_memcpy_d2d(self.h, dst, src, nbytes), "tla_memcpy_d2d")
+
+    def synchronize(self):
+        _check(lib().tla_synchronize(self.h), "tla_synchronize")
+
+    # ---- operators --------------------------------------------------------------
+    def rope(self, q: int, k: int, pos: int, head_dim=64, n_head=32, n_head_kv=4,
+             freq_base=10000.0):
+        _check(lib().tla_rope(self.h, q, k, pos, head_dim, n_head, n_head_kv, freq_base),
+               "tla_rope")
+
+    def softmax(self, x: int, size: int):
+        _check(lib().tla_softmax(self.h, x, size), "tla_softmax")
+
+    def attention(self, out: int, q: int, k: int, v: int, key_cache: int, value_cache: int,
+                  layer: int, pos: int, att: int = 0):
+        _check(lib().tla_attention(self.h, out, q, k, v, key_cache, value_cache, att or None,
+                                   layer, pos), "tla_attention")
+
+    def rope_attention(self, out: int, q: int, k: int, v: int, key_cache: int,
+                       value_cache: int, layer: int, pos: int):
+        _check(lib().tla_rope_attention(self.h, out, q, k, v, key_cache, value_cache, layer, pos),
+               "tla_rope_attention")
+
+    def decode(self, pos, layer0: int, n_step_layers: int, out: int, q: int, k: int, v: int,
+               key_cache: int, value_cache: int, seq_stride: int = 0, rotate: bool = True):
+        pos = np.ascontiguousarray(pos, dtype=np.int32).reshape(-1)
+        _check(lib().tla_decode(self.h, int(pos.size), pos.ctypes.data_as(C.POINTER(C.c_int)),
+                                layer0, n_step_layers, TLA_ROTATE if rotate else 0, out, q, k, v,
+                                key_cache, value_cache, seq_stride), "tla_decode")
+
+    def prefill(self, pos0: int, n_tok: int, layer0: int, n_step_layers: int, out: int, q: int,
+                k: int, v: int, key_cache: int, value_cache: int, rotate: bool = True):
+        _check(lib().tla_prefill(self.h, pos0, n_tok, layer0, n_step_layers,
+                                 TLA_ROTATE if rotate else 0, out, q, k, v, key_cache,
+                                 value_cache), "tla_prefill")
+
+    # ---- measurement --------------------------------------------------------------
+    def set_option(self, option: int, value: int):
+        _check(lib().tla_set_option(self.h, option, value), "tla_set_option")
+
+    def profile(self, enable: bool):
+        _check(lib().tla_profile_enable(self.h, int(enable)), "tla_profile_enable")
+
+    def profile_read(self, kernel_id: int):
+        ms, n = C.c_double(), C.c_longlong()
+        _check(lib().tla_profile_read(self.h, kernel_id, C.byref(ms), C.byref(n)),
+               "tla_profile_read")
+        return ms.value, n.value
+
+    def event(self, slot: int):
+        _check(lib().tla_event_record(self.h, slot), "tla_event_record")
+
+    def elapsed(self, a: int, b: int) -> float:
+        ms = C.c_float()
+        _check(lib().tla_event_elapsed(self.h, a, b, C.byref(ms)), "tla_event_elapsed")
+        return ms.value

@@ -1,0 +1,625 @@
+// C ABI of libtla.so: engine lifetime, device memory, argument validation
+// and launch planning.  Kernels live in decode.hip, prefill.hip and
+// small_ops.hip.
+#include <algorithm>
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+#include <string>
+#include <utility>
+#include <vector>
+
+#include "tla_internal.h"
+
+using namespace tla;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...)
+{
+    char buf[512];
+    va_list ap;
+    va_start(ap, fmt);
+    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    va_end(ap);
+    g_last_error = buf;
+    return code;
+}
+
+int ok()
+{
+    return TLA_OK;
+}
+
+#define TLA_HIP(call)                                                                         \
+    do {                                                                                      \
+        const hipError_t err_ = (call);                                                       \
+        if (err_ != hipSuccess)                                                               \
+            return fail(err_ == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE, \
+                        "%s failed: %s", #call, hipGetErrorString(err_));                     \
+    } while (0)
+
+// cos/sin table with the reference's float expressions (src/ops.cpp:1244-1251):
+//   freq  = 1.0f / powf(base, (float)(2i) / (float)head_dim)
+//   angle = (float)pos * freq;  c = cosf(angle);  s = sinf(angle)
+// Contraction off so that nothing is fused; the libm is the host's, as the
+// reference's.
+void rope_cos_sin(float2* out, int pos, int head_dim, float freq_base)
+{
+#pragma clang fp contract(off)
+    const int pairs = head_dim / 2;
+    for (int i = 0; i < pairs; ++i) {
+        const float expo = static_cast<float>(2 * i) / static_cast<float>(head_dim);
+        const float freq = 1.0f / std::pow(freq_base, expo);
+        const float angle = static_cast<float>(pos) * freq;
+        out[i].x = std::cos(angle);
+        out[i].y = std::sin(angle);
+    }
+}
+
+void rope_table_host(std::vector<float2>& tab, int n_pos, int head_dim, float freq_base)
+{
+#pragma clang fp contract(off)
+    const int pairs = head_dim / 2;
+    std::vector<float> freq(pairs);
+    for (int i = 0; i < pairs; ++i) {
+        const float expo = static_cast<float>(2 * i) / static_cast<float>(head_dim);
+        freq[i] = 1.0f / std::pow(freq_base, expo);
+    }
+    tab.resize(static_cast<size_t>(n_pos) * pairs);
+    for (int p = 0; p < n_pos; ++p)
+        for (int i = 0; i < pairs; ++i) {
+            const float angle = static_cast<float>(p) * freq[i];
+            tab[static_cast<size_t>(p) * pairs + i] = make_float2(std::cos(angle), std::sin(angle));
+        }
+}
+
+constexpr int kEventSlots = 64;
+
+}  // namespace
+
+struct tla_engine {
+    tla_config cfg{};
+    int device = 0;
+    int head_dim = 0;
+    int kv_dim = 0;
+    int gqa = 0;
+    hipStream_t stream = nullptr;
+    float2* rope = nullptr;  // [n_ctx][head_dim/2]
+    void* ws = nullptr;      // split-KV partials
+    size_t ws_bytes = 0;
+    long long opt_split = 0;
+
+    bool prof = false;
+    std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_pending[TLA_KERNEL_COUNT];
+    double prof_ms[TLA_KERNEL_COUNT] = {};
+    long long prof_n[TLA_KERNEL_COUNT] = {};
+    std::vector<hipEvent_t> event_pool;
+
+    hipEvent_t slots[kEventSlots] = {};
+};
+
+namespace {
+
+int set_device(tla_engine* e)
+{
+    TLA_HIP(hipSetDevice(e->device));
+    return TLA_OK;
+}
+
+int take_event(tla_engine* e, hipEvent_t* ev)
+{
+    if (!e->event_pool.empty()) {
+        *ev = e->event_pool.back();
+        e->event_pool.pop_back();
+        return TLA_OK;
+    }
+    TLA_HIP(hipEventCreate(ev));
+    return TLA_OK;
+}
+
+// Settle finished profiling events into the per-kernel sums.
+int prof_collect(tla_engine* e)
+{
+    for (int k = 0; k < TLA_KERNEL_COUNT; ++k) {
+        for (auto& pr : e->prof_pending[k]) {
+            TLA_HIP(hipEventSynchronize(pr.second));
+            float ms = 0.f;
+            TLA_HIP(hipEventElapsedTime(&ms, pr.first, pr.second));
+            e->prof_ms[k] += ms;
+            e->prof_n[k] += 1;
+            e->event_pool.push_back(pr.first);
+            e->event_pool.push_back(pr.second);
+        }
+        e->prof_pending[k].clear();
+    }
+    return TLA_OK;
+}
+
+// Launch `fn` on the engine stream, bracketed by events when profiling.
+template <class Fn>
+int launch(tla_engine* e, int kernel_id, const char* what, Fn&& fn)
+{
+    hipEvent_t a = nullptr, b = nullptr;
+    if (e->prof) {
+        if (int rc = take_event(e, &a)) return rc;
+        if (int rc = take_event(e, &b)) return rc;
+        TLA_HIP(hipEventRecord(a, e->stream));
+    }
+    const hipError_t err = fn();
+    if (err != hipSuccess)
+        return fail(TLA_ERR_DEVICE, "%s launch failed: %s", what, hipGetErrorString(err));
+    if (e->prof) {
+        TLA_HIP(hipEventRecord(b, e->stream));
+        e->prof_pending[kernel_id].emplace_back(a, b);
+        // Keep the pending list bounded for long profiled runs.
+        if (e->prof_pending[kernel_id].size() > 4096)
+            if (int rc = prof_collect(e)) return rc;
+    }
+    return TLA_OK;
+}
+
+int ensure_ws(tla_engine* e, size_t bytes)
+{
+    if (bytes <= e->ws_bytes) return TLA_OK;
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    if (e->ws) TLA_HIP(hipFree(e->ws));
+    e->ws = nullptr;
+    e->ws_bytes = 0;
+    const size_t rounded = (bytes + (1u << 20) - 1) & ~static_cast<size_t>((1u << 20) - 1);
+    TLA_HIP(hipMalloc(&e->ws, rounded));
+    e->ws_bytes = rounded;
+    return TLA_OK;
+}
+
+int check_engine(const tla_engine* e)
+{
+    if (!e) return fail(TLA_ERR_INVALID_ARGUMENT, "engine is NULL");
+    return TLA_OK;
+}
+
+float scale_log2(int head_dim)
+{
+    // scores are q.k / sqrt(head_dim) (src/ops.cpp:1335); softmax runs in base 2.
+    return static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
+}
+
+// Positions per split-KV chunk: enough workgroups to fill 256 CUs several
+// times over, long enough that the per-split partial (8.4 KB for 32 heads)
+// stays a few percent of the KV bytes a split streams.
+int plan_split(long long total_positions, long long opt)
+{
+    if (opt > 0) {
+        long long s = (opt + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
+        return static_cast<int>(std::min<long long>(std::max<long long>(s, kDecodeTile), 1 << 24));
+    }
+    long long s = (total_positions + 2559) / 2560;
+    s = (s + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
+    return static_cast<int>(std::min<long long>(std::max<long long>(s, 64), 512));
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* tla_last_error(void)
+{
+    return g_last_error.c_str();
+}
+
+int tla_abi_version(void)
+{
+    return 1;
+}
+
+int tla_engine_create(const tla_config* cfg, int device, tla_engine** out)
+{
+    if (!cfg || !out) return fail(TLA_ERR_INVALID_ARGUMENT, "cfg and out must not be NULL");
+    *out = nullptr;
+    if (cfg->n_layers < 1 || cfg->n_head < 1 || cfg->n_head_kv < 1 || cfg->n_embd < 1 || cfg->n_ctx < 1)
+        return fail(TLA_ERR_INVALID_ARGUMENT,
+                    "n_layers, n_head, n_head_kv, n_embd and n_ctx must be >= 1");
+    if (cfg->n_embd % cfg->n_head != 0)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "n_embd (%d) is not a multiple of n_head (%d)",
+                    cfg->n_embd, cfg->n_head);
+    if (cfg->n_head % cfg->n_head_kv != 0)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "n_head (%d) is not a multiple of n_head_kv (%d)",
+                    cfg->n_head, cfg->n_head_kv);
+    if (!(cfg->rope_freq_base > 0.0f) || !std::isfinite(cfg->rope_freq_base))
+        return fail(TLA_ERR_INVALID_ARGUMENT, "rope_freq_base must be finite and > 0");
+    const int head_dim = cfg->n_embd / cfg->n_head;
+    const int gqa = cfg->n_head / cfg->n_head_kv;
+    if (head_dim != kHeadDim)
+        return fail(TLA_ERR_UNSUPPORTED, "head_dim %d: kernels implement head_dim 64", head_dim);
+    if (gqa > kMaxGqa)
+        return fail(TLA_ERR_UNSUPPORTED, "n_head/n_head_kv = %d > %d", gqa, kMaxGqa);
+    if (cfg->n_ctx > (1 << 24)) return fail(TLA_ERR_UNSUPPORTED, "n_ctx %d > 2^24", cfg->n_ctx);
+    if (device < 0) return fail(TLA_ERR_INVALID_ARGUMENT, "device %d < 0", device);
+
+    int n_dev = 0;
+    TLA_HIP(hipGetDeviceCount(&n_dev));
+    if (device >= n_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "device %d of %d", device, n_dev);
+
+    tla_engine* e = new tla_engine;
+    e->cfg = *cfg;
+    e->device = device;
+    e->head_dim = head_dim;
+    e->kv_dim = cfg->n_head_kv * head_dim;
+    e->gqa = gqa;
+
+    auto bail = [&](int rc) {
+        tla_engine_destroy(e);
+        return rc;
+    };
+    if (int rc = set_device(e)) return bail(rc);
+    {
+        const hipError_t err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
+        if (err != hipSuccess)
+            return bail(fail(TLA_ERR_DEVICE, "hipStreamCreate: %s", hipGetErrorString(err)));
+    }
+    std::vector<float2> tab;
+    rope_table_host(tab, cfg->n_ctx, head_dim, cfg->rope_freq_base);
+    const size_t tab_bytes = tab.size() * sizeof(float2);
+    hipError_t err = hipMalloc(&e->rope, tab_bytes);
+    if (err == hipSuccess) err = hipMemcpy(e->rope, tab.data(), tab_bytes, hipMemcpyHostToDevice);
+    if (err != hipSuccess)
+        return bail(fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE,
+                         "rope table: %s", hipGetErrorString(err)));
+    *out = e;
+    return ok();
+}
+
+int tla_engine_destroy(tla_engine* e)
+{
+    if (!e) return TLA_OK;
+    (void)hipSetDevice(e->device);
+    if (e->stream) (void)hipStreamSynchronize(e->stream);
+    for (auto& v : e->prof_pending)
+        for (auto& pr : v) {
+            (void)hipEventDestroy(pr.first);
+            (void)hipEventDestroy(pr.second);
+        }
+    for (hipEvent_t ev : e->event_pool) (void)hipEventDestroy(ev);
+    for (hipEvent_t ev : e->slots)
+        if (ev) (void)hipEventDestroy(ev);
+    if (e->ws) (void)hipFree(e->ws);
+    if (e->rope) (void)hipFree(e->rope);
+    if (e->stream) (void)hipStreamDestroy(e->stream);
+    delete e;
+    return TLA_OK;
+}
+
+int tla_synchronize(tla_engine* e)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (int rc = set_device(e)) return rc;
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    return ok();
+}
+
+int tla_alloc(tla_engine* e, size_t bytes, void** out_dev)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!out_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "out_dev is NULL");
+    *out_dev = nullptr;
+    if (bytes == 0) return fail(TLA_ERR_INVALID_ARGUMENT, "zero-byte allocation");
+    if (int rc = set_device(e)) return rc;
+    void* p = nullptr;
+    TLA_HIP(hipMalloc(&p, bytes));
+    hipError_t err = hipMemsetAsync(p, 0, bytes, e->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
+    if (err != hipSuccess) {
+        (void)hipFree(p);
+        return fail(TLA_ERR_DEVICE, "zero fill: %s", hipGetErrorString(err));
+    }
+    *out_dev = p;
+    return ok();
+}
+
+int tla_free(tla_engine* e, void* dev)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!dev) return TLA_OK;
+    if (int rc = set_device(e)) return rc;
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    TLA_HIP(hipFree(dev));
+    return ok();
+}
+
+int tla_kv_cache_alloc(tla_engine* e, int n_seq, float** key_cache_dev, float** value_cache_dev)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!key_cache_dev || !value_cache_dev)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "output pointers must not be NULL");
+    if (n_seq < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_seq %d < 1", n_seq);
+    const size_t bytes = static_cast<size_t>(n_seq) * e->cfg.n_layers * e->cfg.n_ctx * e->kv_dim *
+                         sizeof(float);
+    void* k = nullptr;
+    void* v = nullptr;
+    if (int rc = tla_alloc(e, bytes, &k)) return rc;
+    if (int rc = tla_alloc(e, bytes, &v)) {
+        tla_free(e, k);
+        return rc;
+    }
+    *key_cache_dev = static_cast<float*>(k);
+    *value_cache_dev = static_cast<float*>(v);
+    return ok();
+}
+
+int tla_memcpy_h2d(tla_engine* e, void* dst_dev, const void* src_host, size_t bytes)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (bytes == 0) return TLA_OK;
+    if (!dst_dev || !src_host) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (int rc = set_device(e)) return rc;
+    TLA_HIP(hipMemcpyAsync(dst_dev, src_host, bytes, hipMemcpyHostToDevice, e->stream));
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    return ok();
+}
+
+int tla_memcpy_d2h(tla_engine* e, void* dst_host, const void* src_dev, size_t bytes)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (bytes == 0) return TLA_OK;
+    if (!dst_host || !src_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (int rc = set_device(e)) return rc;
+    TLA_HIP(hipMemcpyAsync(dst_host, src_dev, bytes, hipMemcpyDeviceToHost, e->stream));
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    return ok();
+}
+
+int tla_memcpy_d2d(tla_engine* e, void* dst_dev, const void* src_dev, size_t bytes)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (bytes == 0) return TLA_OK;
+    if (!dst_dev || !src_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (int rc = set_device(e)) return rc;
+    const hipError_t err = launch_copy(dst_dev, src_dev, bytes, e->stream);
+    if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "copy launch: %s", hipGetErrorString(err));
+    return ok();
+}
+
+int tla_rope(tla_engine* e, float* q_dev, float* k_dev, int pos, int head_dim, int n_head,
+             int n_head_kv, float freq_base)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!q_dev || !k_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "q and k must not be NULL");
+    if (pos < 0) return fail(TLA_ERR_OUT_OF_RANGE, "pos %d < 0", pos);
+    if (head_dim < 2 || head_dim % 2 != 0 || head_dim / 2 > kMaxRopePairs)
+        return fail(TLA_ERR_UNSUPPORTED, "head_dim %d (even, <= %d)", head_dim, 2 * kMaxRopePairs);
+    if (n_head < 0 || n_head_kv < 0 || n_head + n_head_kv < 1)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "head counts %d, %d", n_head, n_head_kv);
+    if (int rc = set_device(e)) return rc;
+    RopeParams p{};
+    p.q = q_dev;
+    p.k = k_dev;
+    p.n_head = n_head;
+    p.n_head_kv = n_head_kv;
+    p.head_dim = head_dim;
+    rope_cos_sin(p.cs, pos, head_dim, freq_base);
+    const hipError_t err = launch_rope(p, e->stream);
+    if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "rope launch: %s", hipGetErrorString(err));
+    return ok();
+}
+
+int tla_softmax(tla_engine* e, float* x_dev, int size)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!x_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "x is NULL");
+    if (size < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "size %d < 1", size);
+    if (int rc = set_device(e)) return rc;
+    const hipError_t err = launch_softmax(x_dev, size, e->stream);
+    if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "softmax launch: %s", hipGetErrorString(err));
+    return ok();
+}
+
+int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_step_layers,
+               int flags, float* out_dev, const float* q_dev, const float* k_dev,
+               const float* v_dev, float* key_cache_dev, float* value_cache_dev,
+               size_t seq_stride)
+{
+    if (int rc = check_engine(e)) return rc;
+    const tla_config& c = e->cfg;
+    if (n_seq < 1 || n_seq > kMaxSeqPerLaunch)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "n_seq %d not in [1, %d]", n_seq, kMaxSeqPerLaunch);
+    if (!pos_host) return fail(TLA_ERR_INVALID_ARGUMENT, "pos is NULL");
+    if (!out_dev || !q_dev || !k_dev || !v_dev || !key_cache_dev || !value_cache_dev)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (flags & ~TLA_ROTATE) return fail(TLA_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
+    if (n_step_layers < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_step_layers %d < 1", n_step_layers);
+    if (layer0 < 0 || layer0 + n_step_layers > c.n_layers)
+        return fail(TLA_ERR_OUT_OF_RANGE, "layers [%d, %d) outside [0, %d)", layer0,
+                    layer0 + n_step_layers, c.n_layers);
+    const long long layer_stride = static_cast<long long>(c.n_ctx) * e->kv_dim;
+    if (n_seq > 1 && seq_stride < static_cast<size_t>(layer_stride) * c.n_layers)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "seq_stride %zu < n_layers*n_ctx*kv_dim", seq_stride);
+
+    DecodeParams p{};
+    long long total_positions = 0;
+    int max_len = 0;
+    for (int s = 0; s < n_seq; ++s) {
+        const int pos = pos_host[s];
+        if (pos < 0 || pos >= c.n_ctx)
+            return fail(TLA_ERR_OUT_OF_RANGE, "pos[%d] = %d outside [0, n_ctx=%d)", s, pos, c.n_ctx);
+        p.pos[s] = pos;
+        total_positions += static_cast<long long>(pos + 1) * n_step_layers;
+        max_len = std::max(max_len, pos + 1);
+    }
+    const int split_len = plan_split(total_positions, e->opt_split);
+    p.split_prefix[0] = 0;
+    int max_splits = 1;
+    for (int s = 0; s < n_seq; ++s) {
+        const int ns = (p.pos[s] + 1 + split_len - 1) / split_len;
+        p.split_prefix[s + 1] = p.split_prefix[s] + ns;
+        max_splits = std::max(max_splits, ns);
+    }
+    if (static_cast<long long>(p.split_prefix[n_seq]) * n_step_layers > 0x7fffffffLL)
+        return fail(TLA_ERR_UNSUPPORTED, "too many workgroups");
+    if (int rc = set_device(e)) return rc;
+
+    const long long units = static_cast<long long>(n_seq) * n_step_layers;
+    if (max_splits > 1) {
+        const size_t o_bytes = static_cast<size_t>(units) * c.n_head * max_splits * kHeadDim * sizeof(float);
+        const size_t ml_bytes = static_cast<size_t>(units) * c.n_head * max_splits * sizeof(float2);
+        if (int rc = ensure_ws(e, o_bytes + ml_bytes)) return rc;
+        p.part_o = static_cast<float*>(e->ws);
+        p.part_ml = reinterpret_cast<float2*>(static_cast<char*>(e->ws) + o_bytes);
+    }
+    p.q = q_dev;
+    p.k = k_dev;
+    p.v = v_dev;
+    p.out = out_dev;
+    p.kc = key_cache_dev;
+    p.vc = value_cache_dev;
+    p.rope = e->rope;
+    p.seq_stride = static_cast<long long>(seq_stride);
+    p.layer_stride = layer_stride;
+    p.n_seq = n_seq;
+    p.n_lb = n_step_layers;
+    p.layer0 = layer0;
+    p.n_head = c.n_head;
+    p.n_head_kv = c.n_head_kv;
+    p.gqa = e->gqa;
+    p.split_len = split_len;
+    p.max_splits = max_splits;
+    p.total_splits = p.split_prefix[n_seq];
+    p.rotate = (flags & TLA_ROTATE) ? 1 : 0;
+    p.scale_log2 = scale_log2(e->head_dim);
+
+    if (int rc = launch(e, TLA_KERNEL_DECODE, "decode", [&] { return launch_decode(p, e->stream); }))
+        return rc;
+    if (max_splits > 1)
+        if (int rc = launch(e, TLA_KERNEL_COMBINE, "combine",
+                            [&] { return launch_decode_combine(p, e->stream); }))
+            return rc;
+    return ok();
+}
+
+int tla_attention(tla_engine* e, float* out_dev, const float* q_dev, const float* k_dev,
+                  const float* v_dev, float* key_cache_dev, float* value_cache_dev, float* att,
+                  int layer, int pos)
+{
+    (void)att;
+    return tla_decode(e, 1, &pos, layer, 1, 0, out_dev, q_dev, k_dev, v_dev, key_cache_dev,
+                      value_cache_dev, 0);
+}
+
+int tla_rope_attention(tla_engine* e, float* out_dev, const float* q_dev, const float* k_dev,
+                       const float* v_dev, float* key_cache_dev, float* value_cache_dev, int layer,
+                       int pos)
+{
+    return tla_decode(e, 1, &pos, layer, 1, TLA_ROTATE, out_dev, q_dev, k_dev, v_dev,
+                      key_cache_dev, value_cache_dev, 0);
+}
+
+int tla_prefill(tla_engine* e, int pos0, int n_tok, int layer0, int n_step_layers, int flags,
+                float* out_dev, const float* q_dev, const float* k_dev, const float* v_dev,
+                float* key_cache_dev, float* value_cache_dev)
+{
+    if (int rc = check_engine(e)) return rc;
+    const tla_config& c = e->cfg;
+    if (!out_dev || !q_dev || !k_dev || !v_dev || !key_cache_dev || !value_cache_dev)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (flags & ~TLA_ROTATE) return fail(TLA_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
+    if (n_tok < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_tok %d < 1", n_tok);
+    if (pos0 < 0 || static_cast<long long>(pos0) + n_tok > c.n_ctx)
+        return fail(TLA_ERR_OUT_OF_RANGE, "positions [%d, %lld) outside [0, n_ctx=%d)", pos0,
+                    static_cast<long long>(pos0) + n_tok, c.n_ctx);
+    if (n_step_layers < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_step_layers %d < 1", n_step_layers);
+    if (layer0 < 0 || layer0 + n_step_layers > c.n_layers)
+        return fail(TLA_ERR_OUT_OF_RANGE, "layers [%d, %d) outside [0, %d)", layer0,
+                    layer0 + n_step_layers, c.n_layers);
+    if (int rc = set_device(e)) return rc;
+    PrefillParams p{};
+    p.q = q_dev;
+    p.k = k_dev;
+    p.v = v_dev;
+    p.out = out_dev;
+    p.kc = key_cache_dev;
+    p.vc = value_cache_dev;
+    p.rope = e->rope;
+    p.layer_stride = static_cast<long long>(c.n_ctx) * e->kv_dim;
+    p.n_lb = n_step_layers;
+    p.layer0 = layer0;
+    p.pos0 = pos0;
+    p.n_tok = n_tok;
+    p.n_head = c.n_head;
+    p.n_head_kv = c.n_head_kv;
+    p.gqa = e->gqa;
+    p.rotate = (flags & TLA_ROTATE) ? 1 : 0;
+    p.scale_log2 = scale_log2(e->head_dim);
+    if (int rc = launch(e, TLA_KERNEL_APPEND, "prefill append",
+                        [&] { return launch_prefill_append(p, e->stream); }))
+        return rc;
+    if (int rc = launch(e, TLA_KERNEL_PREFILL, "prefill attention",
+                        [&] { return launch_prefill_attention(p, e->stream); }))
+        return rc;
+    return ok();
+}
+
+int tla_profile_enable(tla_engine* e, int enable)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (int rc = set_device(e)) return rc;
+    if (int rc = prof_collect(e)) return rc;
+    for (int k = 0; k < TLA_KERNEL_COUNT; ++k) {
+        e->prof_ms[k] = 0.0;
+        e->prof_n[k] = 0;
+    }
+    e->prof = enable != 0;
+    return ok();
+}
+
+int tla_profile_read(tla_engine* e, int kernel_id, double* total_ms, long long* launches)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (kernel_id < 0 || kernel_id >= TLA_KERNEL_COUNT)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "kernel id %d", kernel_id);
+    if (!total_ms || !launches) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL output");
+    if (int rc = set_device(e)) return rc;
+    if (int rc = prof_collect(e)) return rc;
+    *total_ms = e->prof_ms[kernel_id];
+    *launches = e->prof_n[kernel_id];
+    return ok();
+}
+
+int tla_event_record(tla_engine* e, int slot)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (slot < 0 || slot >= kEventSlots) return fail(TLA_ERR_INVALID_ARGUMENT, "slot %d", slot);
+    if (int rc = set_device(e)) return rc;
+    if (!e->slots[slot]) TLA_HIP(hipEventCreate(&e->slots[slot]));
+    TLA_HIP(hipEventRecord(e->slots[slot], e->stream));
+    return ok();
+}
+
+int tla_event_elapsed(tla_engine* e, int slot_begin, int slot_end, float* ms)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!ms) return fail(TLA_ERR_INVALID_ARGUMENT, "ms is NULL");
+    if (slot_begin < 0 || slot_begin >= kEventSlots || slot_end < 0 || slot_end >= kEventSlots ||
+        !e->slots[slot_begin] || !e->slots[slot_end])
+        return fail(TLA_ERR_INVALID_ARGUMENT, "slots %d, %d not recorded", slot_begin, slot_end);
+    if (int rc = set_device(e)) return rc;
+    TLA_HIP(hipEventSynchronize(e->slots[slot_end]));
+    TLA_HIP(hipEventElapsedTime(ms, e->slots[slot_begin], e->slots[slot_end]));
+    return ok();
+}
+
+int tla_set_option(tla_engine* e, int option, long long value)
+{
+    if (int rc = check_engine(e)) return rc;
+    switch (option) {
+    case TLA_OPT_DECODE_SPLIT:
+        if (value < 0) return fail(TLA_ERR_INVALID_ARGUMENT, "split %lld < 0", value);
+        e->opt_split = value;
+        return ok();
+    default:
+        return fail(TLA_ERR_INVALID_ARGUMENT, "unknown option %d", option);
+    }
+}
+
+}  // extern "C"

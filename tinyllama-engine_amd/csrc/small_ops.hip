@@ -1,0 +1,129 @@
+// Stand-alone device ops: rope (src/ops.cpp:1223-1281), softmax
+// (src/ops.cpp:1072-1091) and a vectorised device copy.
+#include "rope_math.h"
+#include "tla_internal.h"
+
+namespace tla {
+namespace {
+
+// One thread per rotated pair; q heads first, then k heads, as the
+// reference's two loops (src/ops.cpp:1229-1280).  cos/sin for this position
+// arrive in the kernel arguments, computed on the host (engine.hip).
+__global__ __launch_bounds__(256) void rope_kernel(const RopeParams p)
+{
+    const int pairs = p.head_dim / 2;
+    const int idx = blockIdx.x * 256 + threadIdx.x;
+    if (idx >= (p.n_head + p.n_head_kv) * pairs) return;
+    const int h = idx / pairs;
+    const int i = idx - h * pairs;
+    float* row = (h < p.n_head) ? p.q + (long long)h * p.head_dim
+                                : p.k + (long long)(h - p.n_head) * p.head_dim;
+    const float2 cs = p.cs[i];
+    const float x0 = row[2 * i];
+    const float x1 = row[2 * i + 1];
+    row[2 * i] = rot_lo(x0, x1, cs.x, cs.y);
+    row[2 * i + 1] = rot_hi(x0, x1, cs.x, cs.y);
+}
+
+__device__ __forceinline__ float wave_max(float v)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v = fmaxf(v, __shfl_xor(v, m));
+    return v;
+}
+
+__device__ __forceinline__ float wave_sum(float v)
+{
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+// softmax in place: max, exp(x - max), sum, multiply by 1/sum (the same
+// three steps and the same final multiply as src/ops.cpp:1072-1091).
+__global__ __launch_bounds__(1024) void softmax_kernel(float* x, int n)
+{
+    __shared__ float red[16];
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+
+    float m = -INFINITY;
+    for (int i = tid; i < n; i += 1024) m = fmaxf(m, x[i]);
+    m = wave_max(m);
+    if (lane == 0) red[wave] = m;
+    __syncthreads();
+    m = red[0];
+    for (int w = 1; w < 16; ++w) m = fmaxf(m, red[w]);
+    __syncthreads();
+
+    float s = 0.f;
+    for (int i = tid; i < n; i += 1024) {
+        const float e = expf(x[i] - m);
+        x[i] = e;
+        s += e;
+    }
+    s = wave_sum(s);
+    if (lane == 0) red[wave] = s;
+    __syncthreads();
+    s = 0.f;
+    for (int w = 0; w < 16; ++w) s += red[w];
+    const float inv = 1.0f / s;
+    for (int i = tid; i < n; i += 1024) x[i] *= inv;
+}
+
+__global__ __launch_bounds__(256) void copy16_kernel(float4* __restrict__ dst,
+                                                     const float4* __restrict__ src, long long n16)
+{
+    const long long stride = (long long)gridDim.x * 256;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride) dst[i] = src[i];
+}
+
+__global__ __launch_bounds__(256) void copy1_kernel(unsigned char* __restrict__ dst,
+                                                    const unsigned char* __restrict__ src, long long n)
+{
+    const long long stride = (long long)gridDim.x * 256;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) dst[i] = src[i];
+}
+
+}  // namespace
+
+hipError_t launch_rope(const RopeParams& p, hipStream_t s)
+{
+    const int total = (p.n_head + p.n_head_kv) * (p.head_dim / 2);
+    hipLaunchKernelGGL(rope_kernel, dim3((total + 255) / 256), dim3(256), 0, s, p);
+    return hipGetLastError();
+}
+
+hipError_t launch_softmax(float* x, int size, hipStream_t s)
+{
+    hipLaunchKernelGGL(softmax_kernel, dim3(1), dim3(1024), 0, s, x, size);
+    return hipGetLastError();
+}
+
+hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s)
+{
+    if (bytes == 0) return hipSuccess;
+    const bool aligned = ((reinterpret_cast<uintptr_t>(dst) | reinterpret_cast<uintptr_t>(src)) & 15) == 0;
+    const long long n16 = aligned ? (long long)(bytes / 16) : 0;
+    if (n16 > 0) {
+        long long blocks = (n16 + 255) / 256;
+        if (blocks > 256 * 64) blocks = 256 * 64;
+        hipLaunchKernelGGL(copy16_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                           static_cast<float4*>(dst), static_cast<const float4*>(src), n16);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const size_t done = (size_t)n16 * 16;
+    if (done < bytes) {
+        const long long rest = (long long)(bytes - done);
+        long long blocks = (rest + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(copy1_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                           static_cast<unsigned char*>(dst) + done,
+                           static_cast<const unsigned char*>(src) + done, rest);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
+
+}  // namespace tla

@@ -1,0 +1,89 @@
+// Internal declarations shared by the HIP sources of libtla.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstddef>
+#include <cstdint>
+
+#include "tla_attention.h"
+
+namespace tla {
+
+constexpr int kHeadDim = 64;        // head_dim the kernels implement
+constexpr int kPairs = kHeadDim / 2;
+constexpr int kMaxGqa = 16;         // q heads per kv head (MFMA N = 16)
+constexpr int kMaxSeqPerLaunch = 256;
+constexpr int kDecodeTile = 16;     // positions per decode MFMA tile
+constexpr int kMaxRopePairs = 128;  // tla_rope: head_dim <= 256
+
+// ---- decode ------------------------------------------------------------
+// One "unit" = one (sequence, layer) decode problem.  unit = seq * n_lb + lb.
+struct DecodeParams {
+    const float* q;      // [n_seq][n_lb][n_head][64]
+    const float* k;      // [n_seq][n_lb][n_head_kv][64] new keys
+    const float* v;      // [n_seq][n_lb][n_head_kv][64] new values
+    float* out;          // [n_seq][n_lb][n_head][64]
+    float* kc;           // cache base (seq 0, layer 0)
+    float* vc;
+    const float2* rope;  // [n_ctx][32] (cos, sin)
+    float* part_o;       // [unit][n_head][max_splits][64] unnormalised partial O
+    float2* part_ml;     // [unit][n_head][max_splits] (running max in log2 units, sum)
+    long long seq_stride;    // floats
+    long long layer_stride;  // floats = n_ctx * kv_dim
+    int n_seq;
+    int n_lb;
+    int layer0;
+    int n_head;
+    int n_head_kv;
+    int gqa;
+    int split_len;     // positions per split, multiple of kDecodeTile
+    int max_splits;    // split stride in part_o / part_ml
+    int total_splits;  // split_prefix[n_seq]
+    int rotate;
+    float scale_log2;  // log2(e) / sqrt(head_dim)
+    int pos[kMaxSeqPerLaunch];
+    int split_prefix[kMaxSeqPerLaunch + 1];
+};
+
+hipError_t launch_decode(const DecodeParams& p, hipStream_t s);
+hipError_t launch_decode_combine(const DecodeParams& p, hipStream_t s);
+
+// ---- prefill -------------------------------------------------------------
+struct PrefillParams {
+    const float* q;   // [n_lb][n_tok][n_head][64]
+    const float* k;   // [n_lb][n_tok][n_head_kv][64]
+    const float* v;
+    float* out;       // [n_lb][n_tok][n_head][64]
+    float* kc;        // cache base of the sequence (layer 0)
+    float* vc;
+    const float2* rope;
+    long long layer_stride;  // floats
+    int n_lb;
+    int layer0;
+    int pos0;
+    int n_tok;
+    int n_head;
+    int n_head_kv;
+    int gqa;
+    int rotate;
+    float scale_log2;
+};
+
+hipError_t launch_prefill_append(const PrefillParams& p, hipStream_t s);
+hipError_t launch_prefill_attention(const PrefillParams& p, hipStream_t s);
+
+// ---- small ops -------------------------------------------------------------
+struct RopeParams {
+    float* q;
+    float* k;
+    int n_head;
+    int n_head_kv;
+    int head_dim;
+    float2 cs[kMaxRopePairs];
+};
+hipError_t launch_rope(const RopeParams& p, hipStream_t s);
+hipError_t launch_softmax(float* x, int size, hipStream_t s);
+hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
+
+}  // namespace tla

@@ -1,0 +1,153 @@
+"""Seeded synthetic inputs and work counts for the attention path.
+
+Shapes are TinyLlama's (n_head 32, n_head_kv 4, head_dim 64, RoPE theta 1e4).
+Inputs come from numpy's PCG64 generator (`standard_normal`, float32), seeded
+from a fixed base and the workload id, so the host side of a test, the
+golden-vector script and bench.py all see the same numbers.
+
+Workloads (one new token per (sequence, layer) unless stated):
+    decode_single   1 layer, position 127, cache rows 0..126 filled
+    decode_model    22 layers, context 2048 (position 2047)
+    decode_ragged   64 sequences, positions uniform in [255, 2047], 22 layers
+    prefill         512-token prompt, 22 layers, RoPE in-kernel
+    decode_long     16384 context, batch 8, 22 layers, K,V ~ N(0, 0.5^2) with
+                    1% of (position, kv head) key rows scaled x8
+"""
+from __future__ import annotations
+
+import hashlib
+
+import numpy as np
+
+SEED_BASE = 0x7A11A
+
+N_HEAD, N_HEAD_KV, HEAD_DIM = 32, 4, 64
+Q_DIM, KV_DIM = N_HEAD * HEAD_DIM, N_HEAD_KV * HEAD_DIM
+FREQ_BASE = 10000.0
+
+WORKLOAD_IDS = {"decode_single": 1, "decode_model": 2, "decode_ragged": 3, "prefill": 4,
+                "decode_long": 5}
+
+
+def rng(workload: str | int, salt: int = 0) -> np.random.Generator:
+    wid = WORKLOAD_IDS[workload] if isinstance(workload, str) else int(workload)
+    return np.random.default_rng([SEED_BASE, wid, salt])
+
+
+def normal(g: np.random.Generator, shape, std: float = 1.0) -> np.ndarray:
+    x = g.standard_normal(int(np.prod(shape)), dtype=np.float32).reshape(shape)
+    if std != 1.0:
+        x *= np.float32(std)
+    return x
+
+
+def digest(*arrays: np.ndarray) -> str:
+    h = hashlib.sha256()
+    for a in arrays:
+        h.update(np.ascontiguousarray(a).tobytes())
+    return h.hexdigest()
+
+
+# ---- algorithmic work --------------------------------------------------------
+
+def decode_bytes(length: int, n_head=N_HEAD, n_head_kv=N_HEAD_KV, head_dim=HEAD_DIM) -> int:
+    """HBM bytes one (sequence, layer) decode step must move at L = pos+1.
+
+    K and V read once (not once per q head) + q in + out + new k,v in +
+    appended k,v out.  For TinyLlama: 2048*L + 20480.
+    """
+    kv = n_head_kv * head_dim * 4
+    qd = n_head * head_dim * 4
+    return 2 * length * kv + 2 * qd + 4 * kv
+
+
+def prefill_flops(n_tok: int, n_head=N_HEAD, head_dim=HEAD_DIM, pos0: int = 0) -> int:
+    """Exact causal flops of QK^T plus PV: token t sees pos0+t+1 keys."""
+    keys = n_tok * pos0 + n_tok * (n_tok + 1) // 2
+    return 2 * 2 * n_head * head_dim * keys
+
+
+# ---- decode inputs -----------------------------------------------------------
+
+class DecodeCase:
+    """Host arrays for n_seq sequences x n_layers layers, one new token each.
+
+    cache rows 0..pos-1 of every (sequence, layer) are filled; row pos and
+    later are zero (the new token is appended at pos).
+    """
+
+    def __init__(self, n_seq, n_layers, n_ctx, pos, q, k, v, kc, vc):
+        self.n_seq, self.n_layers, self.n_ctx = n_seq, n_layers, n_ctx
+        self.pos = np.asarray(pos, np.int32)
+        self.q, self.k, self.v = q, k, v   # [n_seq, n_layers, heads*64]
+        self.kc, self.vc = kc, vc          # [n_seq, n_layers, n_ctx, 256]
+
+    @property
+    def algorithmic_bytes(self) -> int:
+        return int(sum(decode_bytes(int(p) + 1) for p in self.pos) * self.n_layers)
+
+
+def make_decode(workload: str | int, n_seq: int, n_layers: int, n_ctx: int, pos,
+                kv_std: float = 1.0, peaked_frac: float = 0.0, peaked_scale: float = 8.0,
+                salt: int = 0) -> DecodeCase:
+    g = rng(workload, salt)
+    pos = np.broadcast_to(np.asarray(pos, np.int32), (n_seq,)).copy()
+    q = normal(g, (n_seq, n_layers, Q_DIM))
+    k = normal(g, (n_seq, n_layers, KV_DIM))
+    v = normal(g, (n_seq, n_layers, KV_DIM))
+    kc = np.zeros((n_seq, n_layers, n_ctx, KV_DIM), np.float32)
+    vc = np.zeros_like(kc)
+    for s in range(n_seq):
+        n = int(pos[s])
+        if n == 0:
+            continue
+        kc[s, :, :n] = normal(g, (n_layers, n, KV_DIM), kv_std)
+        vc[s, :, :n] = normal(g, (n_layers, n, KV_DIM), kv_std)
+        if peaked_frac > 0:
+            rows = kc[s, :, :n].reshape(n_layers, n, N_HEAD_KV, HEAD_DIM)
+            hit = g.random((n_layers, n, N_HEAD_KV)) < peaked_frac
+            rows[hit] *= np.float32(peaked_scale)
+    return DecodeCase(n_seq, n_layers, n_ctx, pos, q, k, v, kc, vc)
+
+
+def decode_single() -> DecodeCase:
+    return make_decode("decode_single", 1, 1, 128, 127)
+
+
+def decode_model(n_layers: int = 22, n_ctx: int = 2048, salt: int = 0) -> DecodeCase:
+    return make_decode("decode_model", 1, n_layers, n_ctx, n_ctx - 1, salt=salt)
+
+
+def ragged_positions(n_seq: int = 64, lo: int = 256, hi: int = 2048) -> np.ndarray:
+    """Context lengths uniform in [lo, hi] from the seed; returns pos = L - 1."""
+    g = rng("decode_ragged", 1000)
+    return (g.integers(lo, hi + 1, size=n_seq) - 1).astype(np.int32)
+
+
+def decode_ragged(n_seq: int = 64, n_layers: int = 22, n_ctx: int = 2048) -> DecodeCase:
+    return make_decode("decode_ragged", n_seq, n_layers, n_ctx, ragged_positions(n_seq))
+
+
+def decode_long(n_seq: int = 8, n_layers: int = 22, n_ctx: int = 16384) -> DecodeCase:
+    return make_decode("decode_long", n_seq, n_layers, n_ctx, n_ctx - 1, kv_std=0.5,
+                       peaked_frac=0.01)
+
+
+# ---- prefill inputs -------------------------------------------------------------
+
+class PrefillCase:
+    def __init__(self, n_layers, n_tok, pos0, q, k, v):
+        self.n_layers, self.n_tok, self.pos0 = n_layers, n_tok, pos0
+        self.q, self.k, self.v = q, k, v   # [n_layers, n_tok, dim]
+
+    @property
+    def algorithmic_flops(self) -> int:
+        return prefill_flops(self.n_tok, pos0=self.pos0) * self.n_layers
+
+
+def make_prefill(n_layers: int = 22, n_tok: int = 512, pos0: int = 0, salt: int = 0) -> PrefillCase:
+    g = rng("prefill", salt)
+    q = normal(g, (n_layers, n_tok, Q_DIM))
+    k = normal(g, (n_layers, n_tok, KV_DIM))
+    v = normal(g, (n_layers, n_tok, KV_DIM))
+    return PrefillCase(n_layers, n_tok, pos0, q, k, v)
