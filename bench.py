@@ -145,12 +145,11 @@ def run_decode(workload, steps, warmup, cpu, split=0):
     b = DecodeBench(eng, case, copies)
     ms = time_steps(eng, b.step, steps, warmup)
     k_ms, k_n = kernel_avg_ms(eng, b.step, steps, tla.KERNEL_DECODE, start=warmup + steps)
-    c_ms, c_n = kernel_avg_ms(eng, b.step, steps, tla.KERNEL_COMBINE, start=warmup + 2 * steps)
     algo = case.algorithmic_bytes
     res = {
         "workload": workload, "ms_per_step": ms, "algorithmic_bytes": algo,
         "value": algo / (ms * 1e-3) / 1e9,
-        "decode_kernel_ms": k_ms, "combine_kernel_ms": c_ms if c_n else 0.0,
+        "decode_kernel_ms": k_ms,
         "cache_copies": copies, "mall_resident": copies * one_copy <= MALL_BYTES,
     }
     achieved = algo / (k_ms * 1e-3) / 1e9
@@ -158,8 +157,7 @@ def run_decode(workload, steps, warmup, cpu, split=0):
                        "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
                        "kernel": "decode_split_kernel", "launches": k_n}
     log(f"[bench] {workload}: {ms * 1e3:.1f} us/step, {res['value']:.0f} GB/s step, "
-        f"decode kernel {k_ms * 1e3:.1f} us -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%})"
-        f", combine {res['combine_kernel_ms'] * 1e3:.1f} us")
+        f"decode kernel {k_ms * 1e3:.1f} us -> {achieved:.0f} GB/s ({achieved / HBM_PEAK_GBS:.1%})")
     b.free()
     eng.close()
     if cpu:
@@ -347,8 +345,7 @@ def main():
                             "cache_copies": d["cache_copies"],
                             "mall_resident": d["mall_resident"]}, **cfg),
             "roofline": d["roofline"],
-            "kernels_us": {"decode": round(d["decode_kernel_ms"] * 1e3, 2),
-                           "combine": round(d["combine_kernel_ms"] * 1e3, 2)}}
+            "kernels_us": {"decode": round(d["decode_kernel_ms"] * 1e3, 2)}}
     if cpu:
         line["cpu_baseline"] = d["cpu_baseline"]
     if not args.no_prefill and args.workload == "decode_model":

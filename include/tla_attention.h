@@ -157,11 +157,11 @@ int tla_prefill(tla_engine* e, int pos0, int n_tok, int layer0, int n_step_layer
 
 /* ---- measurement hooks (no reference counterpart) ------------------- */
 enum tla_kernel_id {
-    TLA_KERNEL_DECODE = 0,  /* split-KV decode attention (RoPE+append fused) */
-    TLA_KERNEL_COMBINE = 1, /* split-KV log-sum-exp merge                   */
-    TLA_KERNEL_PREFILL = 2, /* causal MFMA prefill attention                 */
-    TLA_KERNEL_APPEND = 3,  /* prefill RoPE + cache append                   */
-    TLA_KERNEL_COUNT = 4
+    TLA_KERNEL_DECODE = 0,  /* split-KV decode attention: RoPE + append +
+                               attention + split merge, one launch           */
+    TLA_KERNEL_PREFILL = 1, /* causal MFMA prefill attention                 */
+    TLA_KERNEL_APPEND = 2,  /* prefill RoPE + cache append                   */
+    TLA_KERNEL_COUNT = 3
 };
 /* When enabled, HIP events bracket every launch of each kernel on the
  * engine's stream; tla_profile_read sums their durations (ms) since the

@@ -33,8 +33,8 @@ def test_decode_single_golden(tla, W, engines):
         err = max_err(out.download(), g["out"])
         log(f"  decode_single vs reference: max-abs {err:.3e}")
         assert err <= DECODE_TOL
-        assert np.array_equal(bits(kc.download()), bits(g["kc"])), "key cache"
-        assert np.array_equal(bits(vc.download()), bits(g["vc"])), "value cache"
+        assert np.array_equal(bits(kc.download().reshape(-1)), bits(g["kc"])), "key cache"
+        assert np.array_equal(bits(vc.download().reshape(-1)), bits(g["vc"])), "value cache"
         # q and k buffers are left unrotated by the fused block
         assert np.array_equal(dq.download(), q[127])
 
@@ -131,20 +131,34 @@ def test_decode_ragged_full_size(O, W, engines):
 
 
 def test_decode_long_peaked(O, W, engines):
-    """Context 16384, batch 8, peaked keys (1% of rows x8): online softmax and
-    the split merge; checked against the oracle and against fp64."""
+    """Context 16384, batch 8, peaked keys (1% of key rows x8): online softmax
+    and the split merge.  Here the reference's own fp32 result drifts up to
+    ~2.2e-4 from the exact (fp64) value -- its sequential accumulation of
+    16384 weighted rows (src/ops.cpp:1500-1508) -- so the bound is stated
+    against fp64: the GPU must be within 1e-4 of fp64 and no further from the
+    reference than 1e-4 plus the reference's own error."""
     case = W.decode_long(n_seq=8, n_layers=2, n_ctx=16384)
-    eng = engines(2, 16384)
-    err = check_decode(O, eng, case)
-    # peaked softmax really is peaked: the largest weight of some head is big
-    got, kc, vc = gpu_decode(eng, W.decode_long(n_seq=1, n_layers=2, n_ctx=16384), keep_cache=True)
-    one = W.decode_long(n_seq=1, n_layers=2, n_ctx=16384)
-    qr, _ = O.rope(one.q[0, 0], one.k[0, 0], 16383, O.Shape())
-    f64 = O.attention_f64(qr, kc[0].reshape(-1), vc[0].reshape(-1), 0, 16383,
-                          O.Shape(n_ctx=16384, n_layers=2))
-    e64 = max_err(got[0, 0], f64)
-    log(f"    vs fp64: {e64:.3e} (vs oracle {err:.3e})")
-    assert e64 <= DECODE_TOL
+    got, kc, vc = gpu_decode(engines(2, 16384), case, keep_cache=True)
+    ref, rkc, rvc = oracle_decode(O, case, keep_cache=True)
+    assert np.array_equal(bits(kc[:, :, 16383]), bits(rkc[:, :, 16383])), "appended keys"
+    assert np.array_equal(bits(vc[:, :, 16383]), bits(rvc[:, :, 16383])), "appended values"
+    s = O.Shape(n_ctx=16384)
+    worst_gpu, worst_ref, worst_pair = 0.0, 0.0, 0.0
+    for si in range(8):
+        for layer in range(2):
+            qr, _ = O.rope(case.q[si, layer], case.k[si, layer], 16383, s)
+            f64 = O.attention_f64(qr, rkc[si, layer].reshape(-1), rvc[si, layer].reshape(-1), 0,
+                                  16383, s)
+            e_gpu = np.abs(got[si, layer] - f64)
+            e_ref = np.abs(ref[si, layer] - f64)
+            e_pair = np.abs(got[si, layer].astype(np.float64) - ref[si, layer])
+            assert np.all(e_pair <= 1e-4 + e_ref), (si, layer)
+            worst_gpu = max(worst_gpu, e_gpu.max())
+            worst_ref = max(worst_ref, e_ref.max())
+            worst_pair = max(worst_pair, e_pair.max())
+    log(f"    GPU vs fp64 {worst_gpu:.2e}; reference vs fp64 {worst_ref:.2e}; "
+        f"GPU vs reference {worst_pair:.2e}")
+    assert worst_gpu <= DECODE_TOL
 
 
 def test_batch_call_equals_per_sequence_calls(O, W, engines):

@@ -83,6 +83,9 @@ def test_softmax_against_reference_golden(engines):
 
 
 def test_softmax_long_vectors(O, engines):
+    """Long vectors (vocabulary-sized): the reference sums exp() sequentially
+    in fp32 (src/ops.cpp:1080-1084), whose own error grows with n, so the GPU
+    is held to 1e-6 of fp64 and to 1e-6 plus the reference's error of it."""
     eng = engines(1, 64)
     rg = np.random.default_rng(23)
     for n in (1, 1023, 1024, 1025, 32000, 100003):
@@ -90,9 +93,14 @@ def test_softmax_long_vectors(O, engines):
         with device_arrays() as track:
             d = track(eng.array(x))
             eng.softmax(d.ptr, n)
-            err = max_err(d.download(), O.softmax(x))
-        log(f"  softmax n={n}: max-abs {err:.2e}")
-        assert err <= 1e-6
+            y = d.download()
+        f64 = np.exp(x.astype(np.float64) - x.max())
+        f64 /= f64.sum()
+        ref = O.softmax(x)
+        e_gpu, e_ref = np.abs(y - f64), np.abs(ref - f64)
+        log(f"  softmax n={n}: GPU vs fp64 {e_gpu.max():.2e}, reference vs fp64 {e_ref.max():.2e}")
+        assert e_gpu.max() <= 1e-6
+        assert np.all(np.abs(y.astype(np.float64) - ref) <= 1e-6 + e_ref)
 
 
 def test_device_copy_any_size_and_alignment(tla, engines):

@@ -34,7 +34,7 @@ TLA_ERR_DEVICE = 4
 TLA_ERR_OUT_OF_MEMORY = 5
 TLA_ROTATE = 1
 
-KERNEL_DECODE, KERNEL_COMBINE, KERNEL_PREFILL, KERNEL_APPEND = range(4)
+KERNEL_DECODE, KERNEL_PREFILL, KERNEL_APPEND = range(3)
 OPT_DECODE_SPLIT = 0
 
 

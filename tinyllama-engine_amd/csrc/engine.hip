@@ -91,6 +91,8 @@ struct tla_engine {
     float2* rope = nullptr;  // [n_ctx][head_dim/2]
     void* ws = nullptr;      // split-KV partials
     size_t ws_bytes = 0;
+    int* counters = nullptr; // per-unit split arrival counters, zero between launches
+    size_t n_counters = 0;
     long long opt_split = 0;
 
     bool prof = false;
@@ -172,6 +174,23 @@ int ensure_ws(tla_engine* e, size_t bytes)
     const size_t rounded = (bytes + (1u << 20) - 1) & ~static_cast<size_t>((1u << 20) - 1);
     TLA_HIP(hipMalloc(&e->ws, rounded));
     e->ws_bytes = rounded;
+    return TLA_OK;
+}
+
+// Arrival counters for `units` units.  Zeroed once when (re)allocated; the
+// decode kernel returns every counter it uses to zero.
+int ensure_counters(tla_engine* e, size_t units)
+{
+    if (units <= e->n_counters) return TLA_OK;
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    if (e->counters) TLA_HIP(hipFree(e->counters));
+    e->counters = nullptr;
+    e->n_counters = 0;
+    const size_t n = std::max<size_t>(units, 1024);
+    TLA_HIP(hipMalloc(&e->counters, n * sizeof(int)));
+    TLA_HIP(hipMemsetAsync(e->counters, 0, n * sizeof(int), e->stream));
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    e->n_counters = n;
     return TLA_OK;
 }
 
@@ -286,6 +305,7 @@ int tla_engine_destroy(tla_engine* e)
     for (hipEvent_t ev : e->slots)
         if (ev) (void)hipEventDestroy(ev);
     if (e->ws) (void)hipFree(e->ws);
+    if (e->counters) (void)hipFree(e->counters);
     if (e->rope) (void)hipFree(e->rope);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     delete e;
@@ -465,8 +485,10 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
         const size_t o_bytes = static_cast<size_t>(units) * c.n_head * max_splits * kHeadDim * sizeof(float);
         const size_t ml_bytes = static_cast<size_t>(units) * c.n_head * max_splits * sizeof(float2);
         if (int rc = ensure_ws(e, o_bytes + ml_bytes)) return rc;
+        if (int rc = ensure_counters(e, static_cast<size_t>(units))) return rc;
         p.part_o = static_cast<float*>(e->ws);
         p.part_ml = reinterpret_cast<float2*>(static_cast<char*>(e->ws) + o_bytes);
+        p.counters = e->counters;
     }
     p.q = q_dev;
     p.k = k_dev;
@@ -491,10 +513,6 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
 
     if (int rc = launch(e, TLA_KERNEL_DECODE, "decode", [&] { return launch_decode(p, e->stream); }))
         return rc;
-    if (max_splits > 1)
-        if (int rc = launch(e, TLA_KERNEL_COMBINE, "combine",
-                            [&] { return launch_decode_combine(p, e->stream); }))
-            return rc;
     return ok();
 }
 

@@ -72,7 +72,8 @@ struct PrefillGrid {
     int per_xcd;    // ceil(n_logical / 8)
 };
 
-__global__ __launch_bounds__(64 * kWavesP) void prefill_attention_kernel(const PrefillParams p,
+__global__ __launch_bounds__(64 * kWavesP) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+prefill_attention_kernel(const PrefillParams p,
                                                                         const PrefillGrid g)
 {
     // ---- XCD-aware, heavy-first mapping of workgroups to tiles ----
@@ -124,26 +125,35 @@ __global__ __launch_bounds__(64 * kWavesP) void prefill_attention_kernel(const P
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    for (int j0 = 0; j0 <= last_key; j0 += kKTile) {
-        // ---- K operand: lane holds K[j0 + col][32*half + s] ----
-        float4 kk[8];
-        {
-            const int kr = min(j0 + col, last_key);
-            const float* src = kc + (long long)kr * kv_dim + 32 * half;
+    // K operand: lane holds K[j0 + col][32*half + s];  V operand: lane holds
+    // V[key(gi)][2*col + dt] for the 16 keys key(gi) = j0 + 8*(gi/4) + 4*half + gi%4.
+    // Keys past last_key are clamped (masked in the scores).  Offsets are
+    // 32-bit from a wave-uniform base (a layer's cache slice is < 4 GiB).
+    auto load_k = [&](int j0, float4 (&k)[8]) {
+        const unsigned ko = (unsigned)min(j0 + col, last_key) * (unsigned)kv_dim + 32u * half;
 #pragma unroll
-            for (int f = 0; f < 8; ++f) kk[f] = ldg4(src + 4 * f);
+        for (int f = 0; f < 8; ++f) k[f] = ldg4(kc + (ko + 4u * f));
+    };
+    auto load_v = [&](int j0, float2 (&v)[16]) {
+#pragma unroll
+        for (int gi = 0; gi < 16; ++gi) {
+            const unsigned key = (unsigned)min(j0 + 8 * (gi >> 2) + 4 * half + (gi & 3), last_key);
+            v[gi] = *reinterpret_cast<const float2*>(vc + (key * (unsigned)kv_dim + 2u * col));
         }
+    };
+
+    // One key tile: S^T = K.Q^T, causal mask, online softmax, O^T += V^T.P^T.
+    auto step = [&](const float4 (&k)[8], const float2 (&v)[16], int j0) {
         floatx16 s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.f;
 #pragma unroll
         for (int f = 0; f < 8; ++f) {
-            s = mfma32(kk[f].x, qv[f].x, s);
-            s = mfma32(kk[f].y, qv[f].y, s);
-            s = mfma32(kk[f].z, qv[f].z, s);
-            s = mfma32(kk[f].w, qv[f].w, s);
+            s = mfma32(k[f].x, qv[f].x, s);
+            s = mfma32(k[f].y, qv[f].y, s);
+            s = mfma32(k[f].z, qv[f].z, s);
+            s = mfma32(k[f].w, qv[f].w, s);
         }
-
         // s[gi] = S[query col][key j0 + 8*(gi/4) + 4*half + gi%4]
         float mx = -INFINITY;
 #pragma unroll
@@ -166,15 +176,29 @@ __global__ __launch_bounds__(64 * kWavesP) void prefill_attention_kernel(const P
         l_run = l_run * alpha + lsum;
         o0 *= alpha;
         o1 *= alpha;
-
-        // ---- O^T += V^T . P^T; V operand: lane holds V[key][2*col + dt] ----
 #pragma unroll
         for (int gi = 0; gi < 16; ++gi) {
-            const int key = min(j0 + 8 * (gi >> 2) + 4 * half + (gi & 3), last_key);
-            const float2 vv = *reinterpret_cast<const float2*>(vc + (long long)key * kv_dim + 2 * col);
-            o0 = mfma32(vv.x, s[gi], o0);
-            o1 = mfma32(vv.y, s[gi], o1);
+            o0 = mfma32(v[gi].x, s[gi], o0);
+            o1 = mfma32(v[gi].y, s[gi], o1);
         }
+    };
+
+    // K tiles ping-pong one tile ahead; each tile's V loads are issued when
+    // its step starts and land while the S products run.
+    float4 ka[8], kb[8];
+    float2 vv[16];
+    load_k(0, ka);
+    for (int j0 = 0;; j0 += 2 * kKTile) {
+        const bool has_b = j0 + kKTile <= last_key;  // uniform
+        load_v(j0, vv);
+        if (has_b) load_k(j0 + kKTile, kb);
+        step(ka, vv, j0);
+        if (!has_b) break;
+        const bool has_a = j0 + 2 * kKTile <= last_key;
+        load_v(j0 + kKTile, vv);
+        if (has_a) load_k(j0 + 2 * kKTile, ka);
+        step(kb, vv, j0 + kKTile);
+        if (!has_a) break;
     }
 
     l_run += __shfl_xor(l_run, 32);

@@ -29,6 +29,7 @@ struct DecodeParams {
     const float2* rope;  // [n_ctx][32] (cos, sin)
     float* part_o;       // [unit][n_head][max_splits][64] unnormalised partial O
     float2* part_ml;     // [unit][n_head][max_splits] (running max in log2 units, sum)
+    int* counters;       // [unit] split arrivals; zero between launches
     long long seq_stride;    // floats
     long long layer_stride;  // floats = n_ctx * kv_dim
     int n_seq;
@@ -47,7 +48,6 @@ struct DecodeParams {
 };
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t s);
-hipError_t launch_decode_combine(const DecodeParams& p, hipStream_t s);
 
 // ---- prefill -------------------------------------------------------------
 struct PrefillParams {
