@@ -226,3 +226,34 @@ def test_out_of_range_is_an_error_and_launches_nothing(tla, W, engines):
             eng.decode([1, 2], 0, 1, out.ptr, q.ptr, k.ptr, v.ptr, kc.ptr, vc.ptr, 64 * 256)
         eng.synchronize()
         assert np.array_equal(bits(kc.download()), bits(before))
+
+
+def test_split_merge_is_stable_under_repetition(O, W, engines, tla):
+    """The cross-workgroup merge (per-unit arrival counter, device-scope
+    partials) on a many-split problem, 200 calls in a row: every output must be
+    bit-identical to the first and within tolerance of the oracle."""
+    case = W.make_decode(17, 4, 22, 2048, [2047, 1000, 517, 64], salt=1)
+    eng = engines(22, 2048)
+    ref, _, _ = oracle_decode(O, case)
+    with device_arrays() as track:
+        kc, vc = eng.kv_cache(4)
+        track(kc), track(vc)
+        kc.upload(case.kc)
+        vc.upload(case.vc)
+        q, k, v = track(eng.array(case.q)), track(eng.array(case.k)), track(eng.array(case.v))
+        out = track(eng.array(case.q.shape))
+        stride = 22 * 2048 * 256
+        for split in (16, 48):
+            eng.set_option(tla.OPT_DECODE_SPLIT, split)
+            first = None
+            for it in range(200):
+                eng.decode(case.pos, 0, 22, out.ptr, q.ptr, k.ptr, v.ptr, kc.ptr, vc.ptr, stride)
+                got = out.download()
+                if first is None:
+                    first = got
+                    err = max_err(got, ref)
+                    log(f"  split {split}: max-abs {err:.3e}")
+                    assert err <= DECODE_TOL
+                else:
+                    assert np.array_equal(bits(got), bits(first)), f"split {split} call {it}"
+        eng.set_option(tla.OPT_DECODE_SPLIT, 0)

@@ -52,6 +52,25 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c)
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
+// Split partials cross workgroups (and XCDs, each with its own L2) inside one
+// launch.  They are stored and loaded with agent-scope relaxed atomics, which
+// go to the device-coherent level instead of a non-coherent L2 copy, so no
+// cache-wide writeback/invalidate (what an agent-scope fence costs) is needed.
+__device__ __forceinline__ void st_dev(float* p, float v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float ld_dev(const float* p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float4 ld_dev4(const float* p)
+{
+    return make_float4(ld_dev(p), ld_dev(p + 1), ld_dev(p + 2), ld_dev(p + 3));
+}
+
 struct Tile {
     float4 k[4];  // K row (p0 + hsub), dims 16t + 4grp + c
     float4 v[4];  // V row (p0 + 4grp + r), dims 4hsub + c
@@ -75,10 +94,11 @@ __device__ void merge_unit(const DecodeParams& p, int unit, int nsplit)
 #pragma unroll
             for (int j = 0; j < kChunk; ++j) {
                 if (s0 + j < nsplit) {
-                    ml[j] = p.part_ml[base + s0 + j];
+                    const float* mlp = reinterpret_cast<const float*>(p.part_ml + base + s0 + j);
+                    ml[j] = make_float2(ld_dev(mlp), ld_dev(mlp + 1));
                     const float* src = p.part_o + (base + s0 + j) * kHeadDim + 8 * c;
-                    x0[j] = ldg4(src);
-                    x1[j] = ldg4(src + 4);
+                    x0[j] = ld_dev4(src);
+                    x1[j] = ld_dev4(src + 4);
                 } else {
                     ml[j] = make_float2(-INFINITY, 0.f);
                     x0[j] = x1[j] = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -285,23 +305,30 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
                 float* po = p.part_o + idx * kHeadDim + 16 * grp;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    stg4(po + 4 * i, make_float4(o[0][i], o[1][i], o[2][i], o[3][i]));
-                if (grp == 0) p.part_ml[idx] = make_float2(m_run, l_run);
+#pragma unroll
+                    for (int dt = 0; dt < 4; ++dt) st_dev(po + 4 * i + dt, o[dt][i]);
+                if (grp == 0) {
+                    float* mlp = reinterpret_cast<float*>(p.part_ml + idx);
+                    st_dev(mlp, m_run);
+                    st_dev(mlp + 1, l_run);
+                }
             }
         }
     }
 
     if (nsplit == 1) return;  // uniform per workgroup
-    // Release the partials, count this split in; the last one merges.
-    __threadfence();
+    // Wait until this wave's partial stores are acknowledged at device scope,
+    // then count the split in; the workgroup that completes the count merges.
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     if (threadIdx.x == 0)
-        s_last = (atomicAdd(p.counters + unit, 1) == nsplit * (int)gridDim.y - 1);
+        s_last = __hip_atomic_fetch_add(p.counters + unit, 1, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT) == nsplit * (int)gridDim.y - 1;
     __syncthreads();
     if (!s_last) return;
-    __threadfence();  // acquire the other splits' partials
     merge_unit(p, unit, nsplit);
-    if (threadIdx.x == 0) p.counters[unit] = 0;
+    if (threadIdx.x == 0)
+        __hip_atomic_store(p.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
