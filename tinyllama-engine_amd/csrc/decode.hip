@@ -76,55 +76,69 @@ struct Tile {
     float4 v[4];  // V row (p0 + 4grp + r), dims 4hsub + c
 };
 
-// Merge the n_split partials of one unit: out = sum_s O_s w_s / sum_s l_s w_s
-// with w_s = 2^(m_s - max m).  256 threads: thread -> (head, 8-float chunk).
-// Splits are merged online in chunks of 8 whose loads are all issued before
-// any is used, so a unit costs one memory round trip per 8 splits.
-__device__ void merge_unit(const DecodeParams& p, int unit, int nsplit)
+// Partial layout, per (unit, split, kv head) slot: the wave's 16 O
+// accumulator registers dumped in lane order (o[r][lane], r = 4*i + dt holds
+// O[head][16*grp + 4*i + dt] of lane (hsub, grp)), then m[16] and l[16] per
+// head.  Every store and load instruction touches 256 (or 64) contiguous bytes.
+constexpr int kPartFloats = 16 * 64 + 32;
+
+__device__ __forceinline__ long long part_slot(const DecodeParams& p, int unit, int split, int kvh)
+{
+    return ((long long)unit * p.max_splits + split) * p.n_head_kv + kvh;
+}
+
+// Merge the n_split partials of one unit, one wave per kv head, each lane
+// merging the same 16 values it would have produced: out = sum_s O_s w_s /
+// sum_s l_s w_s with w_s = 2^(m_s - max m).  Online over chunks of 8 splits
+// whose loads are all issued before any is used.
+__device__ void merge_unit(const DecodeParams& p, int unit, int nsplit, int kvh, int lane)
 {
     constexpr int kChunk = 8;
-    const int c = threadIdx.x & 7;
-    for (int h = threadIdx.x >> 3; h < p.n_head; h += 32) {
-        const long long base = ((long long)unit * p.n_head + h) * p.max_splits;
-        float m = -INFINITY, l = 0.f;
-        float4 a0 = make_float4(0.f, 0.f, 0.f, 0.f), a1 = a0;
-        for (int s0 = 0; s0 < nsplit; s0 += kChunk) {
-            float2 ml[kChunk];
-            float4 x0[kChunk], x1[kChunk];
+    const int hsub = lane & 15, grp = lane >> 4;
+    float m = -INFINITY, l = 0.f;
+    float acc[16];
 #pragma unroll
-            for (int j = 0; j < kChunk; ++j) {
-                if (s0 + j < nsplit) {
-                    const float* mlp = reinterpret_cast<const float*>(p.part_ml + base + s0 + j);
-                    ml[j] = make_float2(ld_dev(mlp), ld_dev(mlp + 1));
-                    const float* src = p.part_o + (base + s0 + j) * kHeadDim + 8 * c;
-                    x0[j] = ld_dev4(src);
-                    x1[j] = ld_dev4(src + 4);
-                } else {
-                    ml[j] = make_float2(-INFINITY, 0.f);
-                    x0[j] = x1[j] = make_float4(0.f, 0.f, 0.f, 0.f);
-                }
-            }
-            float mc = m;
+    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    for (int s0 = 0; s0 < nsplit; s0 += kChunk) {
+        float ms[kChunk], ls[kChunk], x[kChunk][16];
 #pragma unroll
-            for (int j = 0; j < kChunk; ++j) mc = fmaxf(mc, ml[j].x);
-            const float r = __builtin_amdgcn_exp2f(m - mc);  // 0 on the first chunk
-            m = mc;
-            l *= r;
-            a0.x *= r; a0.y *= r; a0.z *= r; a0.w *= r;
-            a1.x *= r; a1.y *= r; a1.z *= r; a1.w *= r;
+        for (int j = 0; j < kChunk; ++j) {
+            if (s0 + j < nsplit) {
+                const float* part = p.part + part_slot(p, unit, s0 + j, kvh) * kPartFloats;
 #pragma unroll
-            for (int j = 0; j < kChunk; ++j) {
-                const float w = __builtin_amdgcn_exp2f(ml[j].x - m);
-                l += ml[j].y * w;
-                a0.x += x0[j].x * w; a0.y += x0[j].y * w; a0.z += x0[j].z * w; a0.w += x0[j].w * w;
-                a1.x += x1[j].x * w; a1.y += x1[j].y * w; a1.z += x1[j].z * w; a1.w += x1[j].w * w;
+                for (int r = 0; r < 16; ++r) x[j][r] = ld_dev(part + r * 64 + lane);
+                ms[j] = ld_dev(part + 1024 + hsub);
+                ls[j] = ld_dev(part + 1040 + hsub);
+            } else {
+                ms[j] = -INFINITY;
+                ls[j] = 0.f;
+#pragma unroll
+                for (int r = 0; r < 16; ++r) x[j][r] = 0.f;
             }
         }
-        const float inv = 1.0f / l;
-        float* dst = p.out + ((long long)unit * p.n_head + h) * kHeadDim + 8 * c;
-        stg4(dst, make_float4(a0.x * inv, a0.y * inv, a0.z * inv, a0.w * inv));
-        stg4(dst + 4, make_float4(a1.x * inv, a1.y * inv, a1.z * inv, a1.w * inv));
+        float mc = m;
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) mc = fmaxf(mc, ms[j]);
+        const float sc = __builtin_amdgcn_exp2f(m - mc);  // 0 on the first chunk
+        m = mc;
+        l *= sc;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) acc[r] *= sc;
+#pragma unroll
+        for (int j = 0; j < kChunk; ++j) {
+            const float w = __builtin_amdgcn_exp2f(ms[j] - m);
+            l += ls[j] * w;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) acc[r] += x[j][r] * w;
+        }
     }
+    if (hsub >= p.gqa) return;
+    const float inv = 1.0f / l;
+    float* orow = p.out + ((long long)unit * p.n_head + kvh * p.gqa + hsub) * kHeadDim + 16 * grp;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        stg4(orow + 4 * i, make_float4(acc[4 * i] * inv, acc[4 * i + 1] * inv, acc[4 * i + 2] * inv,
+                                       acc[4 * i + 3] * inv));
 }
 
 __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeParams p)
@@ -132,7 +146,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     __shared__ int s_last;
     __shared__ float4 s_new[kWaves][32];  // appended k row (16 float4) | v row (16 float4)
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave index made explicitly scalar so cache bases stay in SGPRs
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int kvh = blockIdx.y * kWaves + wave;
     const bool active = kvh < p.n_head_kv;  // uniform per wave
 
@@ -204,54 +219,33 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
         }
 
         // Rows past `end` are masked; they load row `begin` (always valid).
-        // Offsets are 32-bit (a unit's cache slice is < 4 GiB) from a
+        // Byte offsets are 32-bit (a unit's cache slice is < 4 GiB) from a
         // wave-uniform base.
         auto load_tile = [&](int p0, Tile& tl) {
             int r = p0 + hsub;
             if (r >= end) r = begin;
-            const unsigned ko = (unsigned)r * kv_dim + 4u * grp;
+            const unsigned ko = ((unsigned)r * kv_dim + 4u * grp) * 4u;  // bytes
 #pragma unroll
-            for (int t = 0; t < 4; ++t) tl.k[t] = ldg4(kc + ko + 16u * t);
+            for (int t = 0; t < 4; ++t) tl.k[t] = ldg4_at(kc, ko + 64u * t);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 int row = p0 + 4 * grp + i;
                 if (row >= end) row = begin;
-                tl.v[i] = ldg4(vc + ((unsigned)row * kv_dim + 4u * hsub));
+                tl.v[i] = ldg4_at(vc, ((unsigned)row * kv_dim + 4u * hsub) * 4u);
             }
         };
 
-        Tile cur;
-        load_tile(begin, cur);
-        for (int p0 = begin; p0 < end; p0 += kDecodeTile) {
-            const bool more = p0 + kDecodeTile < end;  // uniform
-            Tile nxt;
-            if (more) load_tile(p0 + kDecodeTile, nxt);
-
-            if (has_new && !more) {
-                // Last tile of the appending split: position `pos` comes from
-                // the row kept in LDS, not from the cache row just written.
-                if (min(p0 + hsub, end - 1) == pos || (p0 + hsub >= end && begin == pos)) {
-#pragma unroll
-                    for (int t = 0; t < 4; ++t) cur.k[t] = s_new[wave][4 * t + grp];
-                }
-#pragma unroll
-                for (int i = 0; i < 4; ++i) {
-                    const int row = p0 + 4 * grp + i;
-                    if (row == pos || (row >= end && begin == pos)) cur.v[i] = s_new[wave][16 + hsub];
-                }
-            }
-
-            // ---- S^T = K . Q^T ----
+        // One tile: S^T = K.Q^T, online softmax, O^T += V^T.P^T.
+        auto step = [&](const Tile& tl, int p0) {
             floatx4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                s = mfma16(cur.k[t].x, qv[t].x, s);
-                s = mfma16(cur.k[t].y, qv[t].y, s);
-                s = mfma16(cur.k[t].z, qv[t].z, s);
-                s = mfma16(cur.k[t].w, qv[t].w, s);
+                s = mfma16(tl.k[t].x, qv[t].x, s);
+                s = mfma16(tl.k[t].y, qv[t].y, s);
+                s = mfma16(tl.k[t].z, qv[t].z, s);
+                s = mfma16(tl.k[t].w, qv[t].w, s);
             }
-
-            // ---- online softmax (per head = lane & 15) ----
+            // s[r] = S[position p0 + 4grp + r][head hsub]
             float sc[4];
             float mx = -INFINITY;
 #pragma unroll
@@ -275,16 +269,55 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
             l_run = l_run * alpha + lsum;
 #pragma unroll
             for (int i = 0; i < 4; ++i) o[i] *= alpha;
-
-            // ---- O^T += V^T . P^T ----
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                o[0] = mfma16(cur.v[r].x, ps[r], o[0]);
-                o[1] = mfma16(cur.v[r].y, ps[r], o[1]);
-                o[2] = mfma16(cur.v[r].z, ps[r], o[2]);
-                o[3] = mfma16(cur.v[r].w, ps[r], o[3]);
+                o[0] = mfma16(tl.v[r].x, ps[r], o[0]);
+                o[1] = mfma16(tl.v[r].y, ps[r], o[1]);
+                o[2] = mfma16(tl.v[r].z, ps[r], o[2]);
+                o[3] = mfma16(tl.v[r].w, ps[r], o[3]);
             }
-            if (more) cur = nxt;
+        };
+
+        // The appending split's last tile holds `pos`; that row comes from
+        // LDS (the copy kept at append), not from the cache row just written.
+        // Rows loaded for masked lanes (>= end) are `begin`, also replaced
+        // when begin == pos.
+        auto substitute = [&](Tile& tl, int p0) {
+            if (p0 + hsub >= pos) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) tl.k[t] = s_new[wave][4 * t + grp];
+            }
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int row = p0 + 4 * grp + i;
+                if (row == pos || (row >= end && begin == pos)) tl.v[i] = s_new[wave][16 + hsub];
+            }
+        };
+
+        // Two tiles ping-pong: the next tile's loads are in flight while the
+        // current one is computed.  The special last tile is peeled so that
+        // the loop body has no divergent branches.
+        const int n_tiles = (end - begin + kDecodeTile - 1) / kDecodeTile;
+        const int n_main = has_new ? n_tiles - 1 : n_tiles;
+        Tile ta, tb;
+        load_tile(begin, ta);
+        int t = 0;
+        for (; t + 1 < n_main; t += 2) {
+            load_tile(begin + (t + 1) * kDecodeTile, tb);
+            step(ta, begin + t * kDecodeTile);
+            if (t + 2 < n_tiles) load_tile(begin + (t + 2) * kDecodeTile, ta);
+            step(tb, begin + (t + 1) * kDecodeTile);
+        }
+        if (t < n_main) {
+            if (t + 1 < n_tiles) load_tile(begin + (t + 1) * kDecodeTile, tb);
+            step(ta, begin + t * kDecodeTile);
+            if (has_new) {
+                substitute(tb, begin + (t + 1) * kDecodeTile);
+                step(tb, begin + (t + 1) * kDecodeTile);
+            }
+        } else if (has_new) {
+            substitute(ta, begin + t * kDecodeTile);
+            step(ta, begin + t * kDecodeTile);
         }
 
         // Row sums: each lane group summed different positions of the same head.
@@ -292,26 +325,22 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
         l_run += __shfl_xor(l_run, 32);
 
         // o[dt][i] = O[head hsub][d = 16*grp + 4*i + dt]
-        if (head_ok) {
-            if (nsplit == 1) {
+        if (nsplit == 1) {
+            if (head_ok) {
                 const float inv = 1.0f / l_run;
                 float* orow = p.out + ((long long)unit * p.n_head + qh) * kHeadDim + 16 * grp;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
                     stg4(orow + 4 * i,
                          make_float4(o[0][i] * inv, o[1][i] * inv, o[2][i] * inv, o[3][i] * inv));
-            } else {
-                const long long idx = ((long long)unit * p.n_head + qh) * p.max_splits + split;
-                float* po = p.part_o + idx * kHeadDim + 16 * grp;
+            }
+        } else {
+            float* part = p.part + part_slot(p, unit, split, kvh) * kPartFloats;
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-#pragma unroll
-                    for (int dt = 0; dt < 4; ++dt) st_dev(po + 4 * i + dt, o[dt][i]);
-                if (grp == 0) {
-                    float* mlp = reinterpret_cast<float*>(p.part_ml + idx);
-                    st_dev(mlp, m_run);
-                    st_dev(mlp + 1, l_run);
-                }
+            for (int r = 0; r < 16; ++r) st_dev(part + r * 64 + lane, o[r & 3][r >> 2]);
+            if (grp == 0) {
+                st_dev(part + 1024 + hsub, m_run);
+                st_dev(part + 1040 + hsub, l_run);
             }
         }
     }
@@ -326,9 +355,9 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
                                         __HIP_MEMORY_SCOPE_AGENT) == nsplit * (int)gridDim.y - 1;
     __syncthreads();
     if (!s_last) return;
-    merge_unit(p, unit, nsplit);
-    if (threadIdx.x == 0)
+    if (threadIdx.x == 0)  // every split has arrived: ready for the next launch
         __hip_atomic_store(p.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (active) merge_unit(p, unit, nsplit, kvh, lane);
 }
 
 }  // namespace

@@ -482,12 +482,12 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
 
     const long long units = static_cast<long long>(n_seq) * n_step_layers;
     if (max_splits > 1) {
-        const size_t o_bytes = static_cast<size_t>(units) * c.n_head * max_splits * kHeadDim * sizeof(float);
-        const size_t ml_bytes = static_cast<size_t>(units) * c.n_head * max_splits * sizeof(float2);
-        if (int rc = ensure_ws(e, o_bytes + ml_bytes)) return rc;
+        // per (unit, split, kv head): 16x64 accumulator floats + 16 maxima + 16 sums
+        const size_t bytes = static_cast<size_t>(units) * max_splits * c.n_head_kv *
+                             (16 * 64 + 32) * sizeof(float);
+        if (int rc = ensure_ws(e, bytes)) return rc;
         if (int rc = ensure_counters(e, static_cast<size_t>(units))) return rc;
-        p.part_o = static_cast<float*>(e->ws);
-        p.part_ml = reinterpret_cast<float2*>(static_cast<char*>(e->ws) + o_bytes);
+        p.part = static_cast<float*>(e->ws);
         p.counters = e->counters;
     }
     p.q = q_dev;

@@ -88,7 +88,7 @@ prefill_attention_kernel(const PrefillParams p,
     const int lb = pair / p.n_head_kv;
     const int kvh = pair - lb * p.n_head_kv;
 
-    const int wave = threadIdx.x >> 6;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
     const int lane = threadIdx.x & 63;
     const int hq = hg * kWavesP + wave;
     if (hq >= p.gqa) return;  // uniform per wave
@@ -127,18 +127,18 @@ prefill_attention_kernel(const PrefillParams p,
 
     // K operand: lane holds K[j0 + col][32*half + s];  V operand: lane holds
     // V[key(gi)][2*col + dt] for the 16 keys key(gi) = j0 + 8*(gi/4) + 4*half + gi%4.
-    // Keys past last_key are clamped (masked in the scores).  Offsets are
-    // 32-bit from a wave-uniform base (a layer's cache slice is < 4 GiB).
+    // Keys past last_key are clamped (masked in the scores).  Byte offsets
+    // are 32-bit from a wave-uniform base (a layer's cache slice is < 4 GiB).
     auto load_k = [&](int j0, float4 (&k)[8]) {
-        const unsigned ko = (unsigned)min(j0 + col, last_key) * (unsigned)kv_dim + 32u * half;
+        const unsigned ko = ((unsigned)min(j0 + col, last_key) * (unsigned)kv_dim + 32u * half) * 4u;
 #pragma unroll
-        for (int f = 0; f < 8; ++f) k[f] = ldg4(kc + (ko + 4u * f));
+        for (int f = 0; f < 8; ++f) k[f] = ldg4_at(kc, ko + 16u * f);
     };
     auto load_v = [&](int j0, float2 (&v)[16]) {
 #pragma unroll
         for (int gi = 0; gi < 16; ++gi) {
             const unsigned key = (unsigned)min(j0 + 8 * (gi >> 2) + 4 * half + (gi & 3), last_key);
-            v[gi] = *reinterpret_cast<const float2*>(vc + (key * (unsigned)kv_dim + 2u * col));
+            v[gi] = ldg2_at(vc, (key * (unsigned)kv_dim + 2u * col) * 4u);
         }
     };
 

@@ -42,6 +42,18 @@ __device__ __forceinline__ float4 ldg4(const float* p)
     return *reinterpret_cast<const float4*>(p);
 }
 
+// 16-byte load at a 32-bit byte offset from a (wave-uniform) base: lets the
+// compiler use the scalar-base + 32-bit-offset addressing form.
+__device__ __forceinline__ float4 ldg4_at(const float* base, unsigned byte_off)
+{
+    return *reinterpret_cast<const float4*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+
+__device__ __forceinline__ float2 ldg2_at(const float* base, unsigned byte_off)
+{
+    return *reinterpret_cast<const float2*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+
 __device__ __forceinline__ void stg4(float* p, float4 v)
 {
     *reinterpret_cast<float4*>(p) = v;

@@ -27,8 +27,7 @@ struct DecodeParams {
     float* kc;           // cache base (seq 0, layer 0)
     float* vc;
     const float2* rope;  // [n_ctx][32] (cos, sin)
-    float* part_o;       // [unit][n_head][max_splits][64] unnormalised partial O
-    float2* part_ml;     // [unit][n_head][max_splits] (running max in log2 units, sum)
+    float* part;         // split partials, [unit][max_splits][n_head_kv][16*64 + 32]
     int* counters;       // [unit] split arrivals; zero between launches
     long long seq_stride;    // floats
     long long layer_stride;  // floats = n_ctx * kv_dim
