@@ -76,15 +76,18 @@ struct Tile {
     float4 v[4];  // V row (p0 + 4grp + r), dims 4hsub + c
 };
 
-// Partial layout, per (unit, split, kv head) slot: the wave's 16 O
-// accumulator registers dumped in lane order (o[r][lane], r = 4*i + dt holds
-// O[head][16*grp + 4*i + dt] of lane (hsub, grp)), then m[16] and l[16] per
-// head.  Every store and load instruction touches 256 (or 64) contiguous bytes.
-constexpr int kPartFloats = 16 * 64 + 32;
+// Partial layout, per (unit, split, kv head) slot, for the gqa real heads
+// only (MFMA columns gqa..15 are padding): o[r][grp][hsub] with
+// r = 4*i + dt holding O[head hsub][16*grp + 4*i + dt], then m[hsub] and
+// l[hsub].  A store or load instruction covers 4*gqa contiguous floats.
+__device__ __forceinline__ int part_floats(int gqa)
+{
+    return 66 * gqa;
+}
 
 __device__ __forceinline__ long long part_slot(const DecodeParams& p, int unit, int split, int kvh)
 {
-    return ((long long)unit * p.max_splits + split) * p.n_head_kv + kvh;
+    return (((long long)unit * p.max_splits + split) * p.n_head_kv + kvh) * part_floats(p.gqa);
 }
 
 // Merge the n_split partials of one unit, one wave per kv head, each lane
@@ -93,8 +96,10 @@ __device__ __forceinline__ long long part_slot(const DecodeParams& p, int unit, 
 // whose loads are all issued before any is used.
 __device__ void merge_unit(const DecodeParams& p, int unit, int nsplit, int kvh, int lane)
 {
-    constexpr int kChunk = 8;
+    constexpr int kChunk = 4;
     const int hsub = lane & 15, grp = lane >> 4;
+    if (hsub >= p.gqa) return;  // padding columns hold no partials
+    const int g4 = 4 * p.gqa, li = grp * p.gqa + hsub, mo = 64 * p.gqa;
     float m = -INFINITY, l = 0.f;
     float acc[16];
 #pragma unroll
@@ -104,11 +109,12 @@ __device__ void merge_unit(const DecodeParams& p, int unit, int nsplit, int kvh,
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
             if (s0 + j < nsplit) {
-                const float* part = p.part + part_slot(p, unit, s0 + j, kvh) * kPartFloats;
+                const float* part = p.part + part_slot(p, unit, s0 + j, kvh);
+                const float* q = part + li;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) x[j][r] = ld_dev(part + r * 64 + lane);
-                ms[j] = ld_dev(part + 1024 + hsub);
-                ls[j] = ld_dev(part + 1040 + hsub);
+                for (int r = 0; r < 16; ++r, q += g4) x[j][r] = ld_dev(q);
+                ms[j] = ld_dev(part + mo + hsub);
+                ls[j] = ld_dev(part + mo + p.gqa + hsub);
             } else {
                 ms[j] = -INFINITY;
                 ls[j] = 0.f;
@@ -132,7 +138,6 @@ __device__ void merge_unit(const DecodeParams& p, int unit, int nsplit, int kvh,
             for (int r = 0; r < 16; ++r) acc[r] += x[j][r] * w;
         }
     }
-    if (hsub >= p.gqa) return;
     const float inv = 1.0f / l;
     float* orow = p.out + ((long long)unit * p.n_head + kvh * p.gqa + hsub) * kHeadDim + 16 * grp;
 #pragma unroll
@@ -334,13 +339,15 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
                     stg4(orow + 4 * i,
                          make_float4(o[0][i] * inv, o[1][i] * inv, o[2][i] * inv, o[3][i] * inv));
             }
-        } else {
-            float* part = p.part + part_slot(p, unit, split, kvh) * kPartFloats;
+        } else if (head_ok) {
+            float* part = p.part + part_slot(p, unit, split, kvh);
+            const int g4 = 4 * p.gqa;
+            float* q = part + grp * p.gqa + hsub;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) st_dev(part + r * 64 + lane, o[r & 3][r >> 2]);
+            for (int r = 0; r < 16; ++r, q += g4) st_dev(q, o[r & 3][r >> 2]);
             if (grp == 0) {
-                st_dev(part + 1024 + hsub, m_run);
-                st_dev(part + 1040 + hsub, l_run);
+                st_dev(part + 64 * p.gqa + hsub, m_run);
+                st_dev(part + 65 * p.gqa + hsub, l_run);
             }
         }
     }

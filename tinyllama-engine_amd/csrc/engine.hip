@@ -206,18 +206,19 @@ float scale_log2(int head_dim)
     return static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
 }
 
-// Positions per split-KV chunk: enough workgroups to fill 256 CUs several
-// times over, long enough that the per-split partial (8.4 KB for 32 heads)
-// stays a few percent of the KV bytes a split streams.
+// Positions per split-KV chunk.  Measured on MI355X: splits long enough that
+// about 240 workgroups (one per CU) cover the whole batch, between 64 and
+// 2048 positions -- short splits multiply the partials the merge must read
+// back, long ones leave CUs idle on small batches.
 int plan_split(long long total_positions, long long opt)
 {
     if (opt > 0) {
         long long s = (opt + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
         return static_cast<int>(std::min<long long>(std::max<long long>(s, kDecodeTile), 1 << 24));
     }
-    long long s = (total_positions + 2559) / 2560;
+    long long s = (total_positions + 239) / 240;
     s = (s + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
-    return static_cast<int>(std::min<long long>(std::max<long long>(s, 64), 512));
+    return static_cast<int>(std::min<long long>(std::max<long long>(s, 64), 2048));
 }
 
 }  // namespace
@@ -482,9 +483,9 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
 
     const long long units = static_cast<long long>(n_seq) * n_step_layers;
     if (max_splits > 1) {
-        // per (unit, split, kv head): 16x64 accumulator floats + 16 maxima + 16 sums
-        const size_t bytes = static_cast<size_t>(units) * max_splits * c.n_head_kv *
-                             (16 * 64 + 32) * sizeof(float);
+        // per (unit, split, kv head): 64 output floats + max + sum for each real head
+        const size_t bytes = static_cast<size_t>(units) * max_splits * c.n_head_kv * 66 *
+                             e->gqa * sizeof(float);
         if (int rc = ensure_ws(e, bytes)) return rc;
         if (int rc = ensure_counters(e, static_cast<size_t>(units))) return rc;
         p.part = static_cast<float*>(e->ws);

@@ -27,7 +27,7 @@ struct DecodeParams {
     float* kc;           // cache base (seq 0, layer 0)
     float* vc;
     const float2* rope;  // [n_ctx][32] (cos, sin)
-    float* part;         // split partials, [unit][max_splits][n_head_kv][16*64 + 32]
+    float* part;         // split partials, [unit][max_splits][n_head_kv][66 * gqa]
     int* counters;       // [unit] split arrivals; zero between launches
     long long seq_stride;    // floats
     long long layer_stride;  // floats = n_ctx * kv_dim
