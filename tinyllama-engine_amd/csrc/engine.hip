@@ -209,14 +209,16 @@ float scale_log2(int head_dim)
 // Positions per split-KV chunk.  Measured on MI355X: splits long enough that
 // about 240 workgroups (one per CU) cover the whole batch, between 64 and
 // 2048 positions -- short splits multiply the partials the merge must read
-// back, long ones leave CUs idle on small batches.
-int plan_split(long long total_positions, long long opt)
+// back, long ones leave CUs idle on small batches -- and at most half the
+// longest sequence, so ragged batches spread their long sequences.
+int plan_split(long long total_positions, int max_len, long long opt)
 {
     if (opt > 0) {
         long long s = (opt + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
         return static_cast<int>(std::min<long long>(std::max<long long>(s, kDecodeTile), 1 << 24));
     }
     long long s = (total_positions + 239) / 240;
+    s = std::min<long long>(s, (max_len + 1) / 2);
     s = (s + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
     return static_cast<int>(std::min<long long>(std::max<long long>(s, 64), 2048));
 }
@@ -469,7 +471,7 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
         total_positions += static_cast<long long>(pos + 1) * n_step_layers;
         max_len = std::max(max_len, pos + 1);
     }
-    const int split_len = plan_split(total_positions, e->opt_split);
+    const int split_len = plan_split(total_positions, max_len, e->opt_split);
     p.split_prefix[0] = 0;
     int max_splits = 1;
     for (int s = 0; s < n_seq; ++s) {
