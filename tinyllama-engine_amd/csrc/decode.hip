@@ -53,22 +53,16 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c)
 }
 
 // Split partials cross workgroups (and XCDs, each with its own L2) inside one
-// launch.  They are stored and loaded with agent-scope relaxed atomics, which
-// go to the device-coherent level instead of a non-coherent L2 copy, so no
-// cache-wide writeback/invalidate (what an agent-scope fence costs) is needed.
-__device__ __forceinline__ void st_dev(float* p, float v)
-{
-    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
+// launch.  They are written and read with device-scope (sc1) buffer accesses,
+// which go to the device-coherent level instead of a non-coherent L2 copy,
+// so no cache-wide writeback/invalidate (what an agent-scope fence costs) is
+// needed.  16-byte accesses keep each request a whole vector.
+constexpr int kDeviceScope = 16;             // cache-policy bit SC1: device scope
+constexpr int kRawBufferWord3 = 0x00020000;  // untyped 32-bit buffer (gfx9 family)
 
-__device__ __forceinline__ float ld_dev(const float* p)
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(float* base, int bytes)
 {
-    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-__device__ __forceinline__ float4 ld_dev4(const float* p)
-{
-    return make_float4(ld_dev(p), ld_dev(p + 1), ld_dev(p + 2), ld_dev(p + 3));
+    return __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, kRawBufferWord3);
 }
 
 struct Tile {
@@ -77,9 +71,10 @@ struct Tile {
 };
 
 // Partial layout, per (unit, split, kv head) slot, for the gqa real heads
-// only (MFMA columns gqa..15 are padding): o[r][grp][hsub] with
-// r = 4*i + dt holding O[head hsub][16*grp + 4*i + dt], then m[hsub] and
-// l[hsub].  A store or load instruction covers 4*gqa contiguous floats.
+// only (MFMA columns gqa..15 are padding): for i = 0..3, the float4
+// O[head hsub][16*grp + 4*i .. +3] of lane li = grp*gqa + hsub at float
+// offset (i*4*gqa + li)*4; then m[hsub] at 64*gqa and l[hsub] at 65*gqa.
+// One 16-byte store (or load) instruction covers 4*gqa contiguous float4s.
 __device__ __forceinline__ int part_floats(int gqa)
 {
     return 66 * gqa;
@@ -96,30 +91,35 @@ __device__ __forceinline__ long long part_slot(const DecodeParams& p, int unit, 
 // whose loads are all issued before any is used.
 __device__ void merge_unit(const DecodeParams& p, int unit, int nsplit, int kvh, int lane)
 {
-    constexpr int kChunk = 4;
+    constexpr int kChunk = 8;
     const int hsub = lane & 15, grp = lane >> 4;
     if (hsub >= p.gqa) return;  // padding columns hold no partials
-    const int g4 = 4 * p.gqa, li = grp * p.gqa + hsub, mo = 64 * p.gqa;
+    const int li = grp * p.gqa + hsub;
+    const int slot_bytes = part_floats(p.gqa) * 4;
     float m = -INFINITY, l = 0.f;
-    float acc[16];
+    floatx4 acc[4];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) acc[r] = 0.f;
+    for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < nsplit; s0 += kChunk) {
-        float ms[kChunk], ls[kChunk], x[kChunk][16];
+        float ms[kChunk], ls[kChunk];
+        floatx4 x[kChunk][4];
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
             if (s0 + j < nsplit) {
-                const float* part = p.part + part_slot(p, unit, s0 + j, kvh);
-                const float* q = part + li;
+                const auto rs = part_rsrc(p.part + part_slot(p, unit, s0 + j, kvh), slot_bytes);
 #pragma unroll
-                for (int r = 0; r < 16; ++r, q += g4) x[j][r] = ld_dev(q);
-                ms[j] = ld_dev(part + mo + hsub);
-                ls[j] = ld_dev(part + mo + p.gqa + hsub);
+                for (int i = 0; i < 4; ++i)
+                    x[j][i] = __builtin_amdgcn_raw_buffer_load_b128(
+                        rs, (i * 4 * p.gqa + li) * 16, 0, kDeviceScope);
+                ms[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (64 * p.gqa + hsub) * 4, 0,
+                                                             kDeviceScope);
+                ls[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (65 * p.gqa + hsub) * 4, 0,
+                                                             kDeviceScope);
             } else {
                 ms[j] = -INFINITY;
                 ls[j] = 0.f;
 #pragma unroll
-                for (int r = 0; r < 16; ++r) x[j][r] = 0.f;
+                for (int i = 0; i < 4; ++i) x[j][i] = floatx4{0.f, 0.f, 0.f, 0.f};
             }
         }
         float mc = m;
@@ -129,21 +129,21 @@ __device__ void merge_unit(const DecodeParams& p, int unit, int nsplit, int kvh,
         m = mc;
         l *= sc;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) acc[r] *= sc;
+        for (int i = 0; i < 4; ++i) acc[i] *= sc;
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
             const float w = __builtin_amdgcn_exp2f(ms[j] - m);
             l += ls[j] * w;
 #pragma unroll
-            for (int r = 0; r < 16; ++r) acc[r] += x[j][r] * w;
+            for (int i = 0; i < 4; ++i) acc[i] += x[j][i] * w;
         }
     }
     const float inv = 1.0f / l;
     float* orow = p.out + ((long long)unit * p.n_head + kvh * p.gqa + hsub) * kHeadDim + 16 * grp;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
-        stg4(orow + 4 * i, make_float4(acc[4 * i] * inv, acc[4 * i + 1] * inv, acc[4 * i + 2] * inv,
-                                       acc[4 * i + 3] * inv));
+        stg4(orow + 4 * i, make_float4(acc[i][0] * inv, acc[i][1] * inv, acc[i][2] * inv,
+                                       acc[i][3] * inv));
 }
 
 __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeParams p)
@@ -340,14 +340,17 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
                          make_float4(o[0][i] * inv, o[1][i] * inv, o[2][i] * inv, o[3][i] * inv));
             }
         } else if (head_ok) {
-            float* part = p.part + part_slot(p, unit, split, kvh);
-            const int g4 = 4 * p.gqa;
-            float* q = part + grp * p.gqa + hsub;
+            const auto rs = part_rsrc(p.part + part_slot(p, unit, split, kvh), part_floats(p.gqa) * 4);
+            const int li = grp * p.gqa + hsub;
 #pragma unroll
-            for (int r = 0; r < 16; ++r, q += g4) st_dev(q, o[r & 3][r >> 2]);
+            for (int i = 0; i < 4; ++i)
+                __builtin_amdgcn_raw_buffer_store_b128(floatx4{o[0][i], o[1][i], o[2][i], o[3][i]},
+                                                       rs, (i * 4 * p.gqa + li) * 16, 0, kDeviceScope);
             if (grp == 0) {
-                st_dev(part + 64 * p.gqa + hsub, m_run);
-                st_dev(part + 65 * p.gqa + hsub, l_run);
+                __builtin_amdgcn_raw_buffer_store_b32(m_run, rs, (64 * p.gqa + hsub) * 4, 0,
+                                                      kDeviceScope);
+                __builtin_amdgcn_raw_buffer_store_b32(l_run, rs, (65 * p.gqa + hsub) * 4, 0,
+                                                      kDeviceScope);
             }
         }
     }
