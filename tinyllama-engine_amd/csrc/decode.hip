@@ -65,6 +65,33 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t part_rsrc(float* base, int byt
     return __builtin_amdgcn_make_buffer_rsrc(base, 0, bytes, kRawBufferWord3);
 }
 
+// The buffer builtins move raw 32-bit words: bit-cast, never value-convert.
+typedef unsigned uintx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void st_dev4(floatx4 v, __amdgpu_buffer_rsrc_t rs, int byte_off)
+{
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(uintx4, v), rs, byte_off, 0,
+                                           kDeviceScope);
+}
+
+__device__ __forceinline__ void st_dev1(float v, __amdgpu_buffer_rsrc_t rs, int byte_off)
+{
+    __builtin_amdgcn_raw_buffer_store_b32(__builtin_bit_cast(unsigned, v), rs, byte_off, 0,
+                                          kDeviceScope);
+}
+
+__device__ __forceinline__ floatx4 ld_dev4(__amdgpu_buffer_rsrc_t rs, int byte_off)
+{
+    return __builtin_bit_cast(floatx4,
+                              __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, kDeviceScope));
+}
+
+__device__ __forceinline__ float ld_dev1(__amdgpu_buffer_rsrc_t rs, int byte_off)
+{
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_raw_buffer_load_b32(rs, byte_off, 0, kDeviceScope));
+}
+
 struct Tile {
     float4 k[4];  // K row (p0 + hsub), dims 16t + 4grp + c
     float4 v[4];  // V row (p0 + 4grp + r), dims 4hsub + c
@@ -108,13 +135,9 @@ __device__ void merge_unit(const DecodeParams& p, int unit, int nsplit, int kvh,
             if (s0 + j < nsplit) {
                 const auto rs = part_rsrc(p.part + part_slot(p, unit, s0 + j, kvh), slot_bytes);
 #pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    x[j][i] = __builtin_amdgcn_raw_buffer_load_b128(
-                        rs, (i * 4 * p.gqa + li) * 16, 0, kDeviceScope);
-                ms[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (64 * p.gqa + hsub) * 4, 0,
-                                                             kDeviceScope);
-                ls[j] = __builtin_amdgcn_raw_buffer_load_b32(rs, (65 * p.gqa + hsub) * 4, 0,
-                                                             kDeviceScope);
+                for (int i = 0; i < 4; ++i) x[j][i] = ld_dev4(rs, (i * 4 * p.gqa + li) * 16);
+                ms[j] = ld_dev1(rs, (64 * p.gqa + hsub) * 4);
+                ls[j] = ld_dev1(rs, (65 * p.gqa + hsub) * 4);
             } else {
                 ms[j] = -INFINITY;
                 ls[j] = 0.f;
@@ -344,13 +367,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
             const int li = grp * p.gqa + hsub;
 #pragma unroll
             for (int i = 0; i < 4; ++i)
-                __builtin_amdgcn_raw_buffer_store_b128(floatx4{o[0][i], o[1][i], o[2][i], o[3][i]},
-                                                       rs, (i * 4 * p.gqa + li) * 16, 0, kDeviceScope);
+                st_dev4(floatx4{o[0][i], o[1][i], o[2][i], o[3][i]}, rs, (i * 4 * p.gqa + li) * 16);
             if (grp == 0) {
-                __builtin_amdgcn_raw_buffer_store_b32(m_run, rs, (64 * p.gqa + hsub) * 4, 0,
-                                                      kDeviceScope);
-                __builtin_amdgcn_raw_buffer_store_b32(l_run, rs, (65 * p.gqa + hsub) * 4, 0,
-                                                      kDeviceScope);
+                st_dev1(m_run, rs, (64 * p.gqa + hsub) * 4);
+                st_dev1(l_run, rs, (65 * p.gqa + hsub) * 4);
             }
         }
     }
