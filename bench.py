@@ -5,13 +5,15 @@ Default (no flags): the full-model decode-attention step -- 22 layers, KV
 cache [2048 positions][4 kv heads][64] fp32 per layer, one new token per
 layer (RoPE + append + split-KV attention) -- timed over K steps after W
 warmup steps, with inputs resident in HBM.  To keep the 92.7 MB step out of
-the 256 MB Infinity Cache, steps rotate over 4 copies of the whole cache
-(371 MB).  Prints ONE JSON line:
+the 256 MB Infinity Cache, steps rotate over 5 copies of the whole cache
+(461 MB).  Prints ONE JSON line:
 
   value      decode KV GB/s = algorithmic bytes per step / step time, with
              algorithmic bytes 2048*L + 20480 per (sequence, layer), L = 2048
-  roofline   the split-KV decode kernel's own average duration (HIP events on
-             the engine's stream, every launch), against HBM 8 TB/s
+  roofline   the decode kernel against HBM 8 TB/s: a step is one launch, so
+             HIP events around the K timed steps on the engine's stream give
+             its average duration; `traffic` is the HBM bytes per launch
+             measured with rocprofv3 and recorded under profiles/
   prefill    the causal prefill workload (512 tokens, 22 layers): exact causal
              TFLOP/s against fp32 MFMA 157.3 TFLOP/s
   cpu_baseline  the reference's own scalar attention() (oracle/_ref) -- or the
@@ -29,6 +31,7 @@ import argparse
 import importlib
 import json
 import os
+import re
 import sys
 import time
 
@@ -46,6 +49,17 @@ MALL_BYTES = 256 << 20
 
 def log(msg):
     print(msg, file=sys.stderr, flush=True)
+
+
+def profiled_traffic(kernel, workload):
+    """HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x2.0 +
+    WRITE_SIZE x1.0, scaled by the copy-kernel calibration) and recorded in
+    profiles/<kernel>__<workload>.md, or None when not profiled."""
+    path = os.path.join(ROOT, "profiles", f"{kernel}__{workload}.md")
+    if not os.path.exists(path):
+        return None
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)\s*$", open(path).read(), re.M)
+    return int(m.group(1)) if m else None
 
 
 def median(xs):
@@ -158,8 +172,10 @@ def run_decode(workload, steps, warmup, cpu, split=0):
     }
     achieved = algo / (ms * 1e-3) / 1e9
     res["roofline"] = {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
-                       "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": None,
-                       "kernel": "decode_split_kernel", "launches": steps}
+                       "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4),
+                       "traffic": profiled_traffic("decode_split_kernel", workload),
+                       "algorithmic_bytes": algo, "kernel": "decode_split_kernel",
+                       "launches": steps}
     log(f"[bench] {workload}: {ms * 1e3:.1f} us/step = decode kernel -> {achieved:.0f} GB/s "
         f"({achieved / HBM_PEAK_GBS:.1%}); per-launch events {ev_ms * 1e3:.1f} us")
     b.free()
@@ -234,7 +250,9 @@ def run_prefill(steps, warmup, cpu, n_layers=22, n_tok=512):
            "algorithmic_flops": flops, "prefill_kernel_ms": k_ms, "append_kernel_ms": a_ms,
            "roofline": {"bound": "mfma", "achieved": round(achieved, 2),
                         "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
-                        "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4), "traffic": None,
+                        "frac": round(achieved / FP32_MFMA_PEAK_TFLOPS, 4),
+                        "traffic": profiled_traffic("prefill_attention_kernel", "prefill"),
+                        "algorithmic_flops": flops,
                         "kernel": "prefill_attention_kernel", "launches": k_n}}
     log(f"[bench] prefill: {ms * 1e3:.1f} us/step ({res['value']:.1f} TFLOP/s), attention kernel "
         f"{k_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s ({achieved / FP32_MFMA_PEAK_TFLOPS:.1%}), "
