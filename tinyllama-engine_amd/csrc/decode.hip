@@ -45,7 +45,9 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kWaves = 4;  // waves per workgroup, one kv head each
+constexpr int kKvWaves = 4;               // kv heads per workgroup
+constexpr int kSub = 2;                   // position halves per kv head
+constexpr int kWaves = kKvWaves * kSub;   // waves per workgroup
 
 __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c)
 {
@@ -112,27 +114,37 @@ __device__ __forceinline__ long long part_slot(const DecodeParams& p, int unit, 
     return (((long long)unit * p.max_splits + split) * p.n_head_kv + kvh) * part_floats(p.gqa);
 }
 
-// Merge the n_split partials of one unit, one wave per kv head, each lane
-// merging the same 16 values it would have produced: out = sum_s O_s w_s /
-// sum_s l_s w_s with w_s = 2^(m_s - max m).  Online over chunks of 8 splits
-// whose loads are all issued before any is used.
-__device__ void merge_unit(const DecodeParams& p, int unit, int nsplit, int kvh, int lane)
+// Running state of one lane: O[head hsub][16*grp + 4*i + c] in acc[i][c],
+// the head's running max (log2 units) and sum.
+struct Partial {
+    floatx4 acc[4];
+    float m;
+    float l;
+};
+
+// Online merge of the partials of splits [s_lo, s_hi) of one unit for one kv
+// head, each lane merging the same 16 values it produces in the main loop:
+// O = sum_s O_s w_s, l = sum_s l_s w_s with w_s = 2^(m_s - max m).  Chunks of
+// 8 splits whose loads are all issued before any is used.
+__device__ Partial merge_range(const DecodeParams& p, int unit, int s_lo, int s_hi, int kvh,
+                               int lane)
 {
     constexpr int kChunk = 8;
     const int hsub = lane & 15, grp = lane >> 4;
-    if (hsub >= p.gqa) return;  // padding columns hold no partials
     const int li = grp * p.gqa + hsub;
     const int slot_bytes = part_floats(p.gqa) * 4;
-    float m = -INFINITY, l = 0.f;
-    floatx4 acc[4];
+    Partial r;
+    r.m = -INFINITY;
+    r.l = 0.f;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-    for (int s0 = 0; s0 < nsplit; s0 += kChunk) {
+    for (int i = 0; i < 4; ++i) r.acc[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+    if (hsub >= p.gqa) return r;  // padding columns hold no partials
+    for (int s0 = s_lo; s0 < s_hi; s0 += kChunk) {
         float ms[kChunk], ls[kChunk];
         floatx4 x[kChunk][4];
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
-            if (s0 + j < nsplit) {
+            if (s0 + j < s_hi) {
                 const auto rs = part_rsrc(p.part + part_slot(p, unit, s0 + j, kvh), slot_bytes);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) x[j][i] = ld_dev4(rs, (i * 4 * p.gqa + li) * 16);
@@ -145,38 +157,66 @@ __device__ void merge_unit(const DecodeParams& p, int unit, int nsplit, int kvh,
                 for (int i = 0; i < 4; ++i) x[j][i] = floatx4{0.f, 0.f, 0.f, 0.f};
             }
         }
-        float mc = m;
+        float mc = r.m;
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) mc = fmaxf(mc, ms[j]);
-        const float sc = __builtin_amdgcn_exp2f(m - mc);  // 0 on the first chunk
-        m = mc;
-        l *= sc;
+        const float sc = __builtin_amdgcn_exp2f(r.m - mc);  // 0 on the first chunk
+        r.m = mc;
+        r.l *= sc;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] *= sc;
+        for (int i = 0; i < 4; ++i) r.acc[i] *= sc;
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
-            const float w = __builtin_amdgcn_exp2f(ms[j] - m);
-            l += ls[j] * w;
+            const float w = __builtin_amdgcn_exp2f(ms[j] - r.m);
+            r.l += ls[j] * w;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) acc[i] += x[j][i] * w;
+            for (int i = 0; i < 4; ++i) r.acc[i] += x[j][i] * w;
         }
     }
-    const float inv = 1.0f / l;
-    float* orow = p.out + ((long long)unit * p.n_head + kvh * p.gqa + hsub) * kHeadDim + 16 * grp;
+    return r;
+}
+
+// Combine the state of the wave one position-half above (in LDS) into this
+// wave's: the two halves of a kv head meet here.  Either side may be empty
+// (m = -inf, l = 0, acc = 0) but not both.
+struct HalfExchange {
+    floatx4 acc[kKvWaves][4][64];
+    float m[kKvWaves][16];
+    float l[kKvWaves][16];
+};
+
+__device__ __forceinline__ void put_half(HalfExchange& x, int slot, int lane, const Partial& r)
+{
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        stg4(orow + 4 * i, make_float4(acc[i][0] * inv, acc[i][1] * inv, acc[i][2] * inv,
-                                       acc[i][3] * inv));
+    for (int i = 0; i < 4; ++i) x.acc[slot][i][lane] = r.acc[i];
+    if (lane < 16) {
+        x.m[slot][lane] = r.m;
+        x.l[slot][lane] = r.l;
+    }
+}
+
+__device__ __forceinline__ void add_half(const HalfExchange& x, int slot, int lane, Partial& r)
+{
+    const float m1 = x.m[slot][lane & 15], l1 = x.l[slot][lane & 15];
+    const float mm = fmaxf(r.m, m1);
+    const float a0 = __builtin_amdgcn_exp2f(r.m - mm), a1 = __builtin_amdgcn_exp2f(m1 - mm);
+    r.m = mm;
+    r.l = r.l * a0 + l1 * a1;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.acc[i] = r.acc[i] * a0 + x.acc[slot][i][lane] * a1;
 }
 
 __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeParams p)
 {
     __shared__ int s_last;
     __shared__ float4 s_new[kWaves][32];  // appended k row (16 float4) | v row (16 float4)
+    __shared__ HalfExchange s_half;
     const int lane = threadIdx.x & 63;
     // wave index made explicitly scalar so cache bases stay in SGPRs
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int kvh = blockIdx.y * kWaves + wave;
+    const int slot = wave % kKvWaves;  // kv head within the workgroup
+    const int sub = wave / kKvWaves;   // which half of the split's positions
+    const int kvh = blockIdx.y * kKvWaves + slot;
     const bool active = kvh < p.n_head_kv;  // uniform per wave
 
     // blockIdx.x -> (layer step lb, sequence, split)
@@ -194,9 +234,15 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     const int unit = seq * p.n_lb + lb;
     const int layer = p.layer0 + lb;
 
-    const int begin = split * p.split_len;
-    const int end = min(pos + 1, begin + p.split_len);  // exclusive, > begin
-    const bool has_new = (pos >= begin) && (pos < end);  // this split appends; pos = end-1
+    // The split's tiles are cut in two halves (the first half rounded up);
+    // this wave takes positions [begin, end) of its half, possibly none.
+    const int split_begin = split * p.split_len;
+    const int split_end = min(pos + 1, split_begin + p.split_len);  // exclusive
+    const int half_tiles = ((split_end - split_begin + kDecodeTile - 1) / kDecodeTile + 1) / 2;
+    const int begin = sub == 0 ? split_begin : split_begin + half_tiles * kDecodeTile;
+    const int end = sub == 0 ? min(split_end, split_begin + half_tiles * kDecodeTile) : split_end;
+    const bool has_rows = begin < end;                   // uniform per wave
+    const bool has_new = (pos >= begin) && (pos < end);  // this half appends; pos = end-1
 
     const int hsub = lane & 15;  // q head within the group / K row within the tile
     const int grp = lane >> 4;   // 0..3
@@ -232,7 +278,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    if (active) {
+    if (active && has_rows) {
         // B operand of S^T: lane holds q[head hsub][16t + 4grp + c], rotated
         // with the pairs 8t + 2grp + {0,1} of the table row for `pos`.
         float4 qv[4];
@@ -351,26 +397,36 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
         // Row sums: each lane group summed different positions of the same head.
         l_run += __shfl_xor(l_run, 16);
         l_run += __shfl_xor(l_run, 32);
+    }
 
-        // o[dt][i] = O[head hsub][d = 16*grp + 4*i + dt]
+    // The two halves of each kv head meet in LDS; the first half continues.
+    Partial r;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) r.acc[i] = o[i];
+    r.m = m_run;
+    r.l = l_run;
+    if (active && sub == 1) put_half(s_half, slot, lane, r);
+    __syncthreads();
+    if (active && sub == 0) {
+        add_half(s_half, slot, lane, r);
+        // r.acc[i][c] = O[head hsub][d = 16*grp + 4*i + c]
         if (nsplit == 1) {
             if (head_ok) {
-                const float inv = 1.0f / l_run;
+                const float inv = 1.0f / r.l;
                 float* orow = p.out + ((long long)unit * p.n_head + qh) * kHeadDim + 16 * grp;
 #pragma unroll
                 for (int i = 0; i < 4; ++i)
-                    stg4(orow + 4 * i,
-                         make_float4(o[0][i] * inv, o[1][i] * inv, o[2][i] * inv, o[3][i] * inv));
+                    stg4(orow + 4 * i, make_float4(r.acc[i][0] * inv, r.acc[i][1] * inv,
+                                                   r.acc[i][2] * inv, r.acc[i][3] * inv));
             }
         } else if (head_ok) {
             const auto rs = part_rsrc(p.part + part_slot(p, unit, split, kvh), part_floats(p.gqa) * 4);
             const int li = grp * p.gqa + hsub;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-                st_dev4(floatx4{o[0][i], o[1][i], o[2][i], o[3][i]}, rs, (i * 4 * p.gqa + li) * 16);
+            for (int i = 0; i < 4; ++i) st_dev4(r.acc[i], rs, (i * 4 * p.gqa + li) * 16);
             if (grp == 0) {
-                st_dev1(m_run, rs, (64 * p.gqa + hsub) * 4);
-                st_dev1(l_run, rs, (65 * p.gqa + hsub) * 4);
+                st_dev1(r.m, rs, (64 * p.gqa + hsub) * 4);
+                st_dev1(r.l, rs, (65 * p.gqa + hsub) * 4);
             }
         }
     }
@@ -387,14 +443,27 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     if (!s_last) return;
     if (threadIdx.x == 0)  // every split has arrived: ready for the next launch
         __hip_atomic_store(p.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (active) merge_unit(p, unit, nsplit, kvh, lane);
+    // Both halves of each kv head merge half of the splits, then meet in LDS.
+    const int s_mid = (nsplit + 1) / 2;
+    Partial mr;
+    if (active) mr = merge_range(p, unit, sub == 0 ? 0 : s_mid, sub == 0 ? s_mid : nsplit, kvh, lane);
+    if (active && sub == 1) put_half(s_half, slot, lane, mr);
+    __syncthreads();
+    if (!active || sub != 0 || !head_ok) return;
+    add_half(s_half, slot, lane, mr);
+    const float inv = 1.0f / mr.l;
+    float* orow = p.out + ((long long)unit * p.n_head + qh) * kHeadDim + 16 * grp;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+        stg4(orow + 4 * i, make_float4(mr.acc[i][0] * inv, mr.acc[i][1] * inv, mr.acc[i][2] * inv,
+                                       mr.acc[i][3] * inv));
 }
 
 }  // namespace
 
 hipError_t launch_decode(const DecodeParams& p, hipStream_t s)
 {
-    dim3 grid(p.total_splits * p.n_lb, (p.n_head_kv + kWaves - 1) / kWaves);
+    dim3 grid(p.total_splits * p.n_lb, (p.n_head_kv + kKvWaves - 1) / kKvWaves);
     hipLaunchKernelGGL(decode_split_kernel, grid, dim3(64 * kWaves), 0, s, p);
     return hipGetLastError();
 }
