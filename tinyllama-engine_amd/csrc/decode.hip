@@ -400,9 +400,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     }
 
     // The two halves of each kv head meet in LDS; the first half continues.
+    // o[dt][i] = O[head hsub][16*grp + 4*i + dt]  ->  r.acc[i][dt]
     Partial r;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) r.acc[i] = o[i];
+    for (int i = 0; i < 4; ++i) r.acc[i] = floatx4{o[0][i], o[1][i], o[2][i], o[3][i]};
     r.m = m_run;
     r.l = l_run;
     if (active && sub == 1) put_half(s_half, slot, lane, r);
