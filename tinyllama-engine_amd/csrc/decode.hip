@@ -206,7 +206,9 @@ __device__ __forceinline__ void add_half(const HalfExchange& x, int slot, int la
     for (int i = 0; i < 4; ++i) r.acc[i] = r.acc[i] * a0 + x.acc[slot][i][lane] * a1;
 }
 
-__global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeParams p)
+template <int kMaxSeq>
+__global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeParams p,
+                                                                   const DecodeSeqs<kMaxSeq> b)
 {
     __shared__ int s_last;
     __shared__ float4 s_new[kWaves][32];  // appended k row (16 float4) | v row (16 float4)
@@ -225,12 +227,12 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     int lo = 0, hi = p.n_seq - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (p.split_prefix[mid] <= rem) lo = mid; else hi = mid - 1;
+        if (b.split_prefix[mid] <= rem) lo = mid; else hi = mid - 1;
     }
     const int seq = lo;
-    const int split = rem - p.split_prefix[seq];
-    const int nsplit = p.split_prefix[seq + 1] - p.split_prefix[seq];
-    const int pos = p.pos[seq];
+    const int split = rem - b.split_prefix[seq];
+    const int nsplit = b.split_prefix[seq + 1] - b.split_prefix[seq];
+    const int pos = b.pos[seq];
     const int unit = seq * p.n_lb + lb;
     const int layer = p.layer0 + lb;
 
@@ -462,10 +464,19 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
 
 }  // namespace
 
-hipError_t launch_decode(const DecodeParams& p, hipStream_t s)
+hipError_t launch_decode(const DecodeParams& p, const DecodeSeqs<kMaxSeqPerLaunch>& seqs,
+                         hipStream_t s)
 {
     dim3 grid(p.total_splits * p.n_lb, (p.n_head_kv + kKvWaves - 1) / kKvWaves);
-    hipLaunchKernelGGL(decode_split_kernel, grid, dim3(64 * kWaves), 0, s, p);
+    if (p.n_seq <= 8) {
+        DecodeSeqs<8> small{};
+        for (int i = 0; i < p.n_seq; ++i) small.pos[i] = seqs.pos[i];
+        for (int i = 0; i <= p.n_seq; ++i) small.split_prefix[i] = seqs.split_prefix[i];
+        hipLaunchKernelGGL(decode_split_kernel<8>, grid, dim3(64 * kWaves), 0, s, p, small);
+    } else {
+        hipLaunchKernelGGL(decode_split_kernel<kMaxSeqPerLaunch>, grid, dim3(64 * kWaves), 0, s, p,
+                           seqs);
+    }
     return hipGetLastError();
 }
 

@@ -461,25 +461,26 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
         return fail(TLA_ERR_INVALID_ARGUMENT, "seq_stride %zu < n_layers*n_ctx*kv_dim", seq_stride);
 
     DecodeParams p{};
+    DecodeSeqs<kMaxSeqPerLaunch> seqs{};
     long long total_positions = 0;
     int max_len = 0;
     for (int s = 0; s < n_seq; ++s) {
         const int pos = pos_host[s];
         if (pos < 0 || pos >= c.n_ctx)
             return fail(TLA_ERR_OUT_OF_RANGE, "pos[%d] = %d outside [0, n_ctx=%d)", s, pos, c.n_ctx);
-        p.pos[s] = pos;
+        seqs.pos[s] = pos;
         total_positions += static_cast<long long>(pos + 1) * n_step_layers;
         max_len = std::max(max_len, pos + 1);
     }
     const int split_len = plan_split(total_positions, max_len, e->opt_split);
-    p.split_prefix[0] = 0;
+    seqs.split_prefix[0] = 0;
     int max_splits = 1;
     for (int s = 0; s < n_seq; ++s) {
-        const int ns = (p.pos[s] + 1 + split_len - 1) / split_len;
-        p.split_prefix[s + 1] = p.split_prefix[s] + ns;
+        const int ns = (seqs.pos[s] + 1 + split_len - 1) / split_len;
+        seqs.split_prefix[s + 1] = seqs.split_prefix[s] + ns;
         max_splits = std::max(max_splits, ns);
     }
-    if (static_cast<long long>(p.split_prefix[n_seq]) * n_step_layers > 0x7fffffffLL)
+    if (static_cast<long long>(seqs.split_prefix[n_seq]) * n_step_layers > 0x7fffffffLL)
         return fail(TLA_ERR_UNSUPPORTED, "too many workgroups");
     if (int rc = set_device(e)) return rc;
 
@@ -510,11 +511,12 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
     p.gqa = e->gqa;
     p.split_len = split_len;
     p.max_splits = max_splits;
-    p.total_splits = p.split_prefix[n_seq];
+    p.total_splits = seqs.split_prefix[n_seq];
     p.rotate = (flags & TLA_ROTATE) ? 1 : 0;
     p.scale_log2 = scale_log2(e->head_dim);
 
-    if (int rc = launch(e, TLA_KERNEL_DECODE, "decode", [&] { return launch_decode(p, e->stream); }))
+    if (int rc = launch(e, TLA_KERNEL_DECODE, "decode",
+                        [&] { return launch_decode(p, seqs, e->stream); }))
         return rc;
     return ok();
 }

@@ -42,11 +42,20 @@ struct DecodeParams {
     int total_splits;  // split_prefix[n_seq]
     int rotate;
     float scale_log2;  // log2(e) / sqrt(head_dim)
-    int pos[kMaxSeqPerLaunch];
-    int split_prefix[kMaxSeqPerLaunch + 1];
 };
 
-hipError_t launch_decode(const DecodeParams& p, hipStream_t s);
+// Per-sequence positions and split offsets of one launch, passed by value in
+// the kernel arguments.  The kernel is instantiated for up to 8 and up to
+// 256 sequences so small batches do not pay for a 2 KiB argument block
+// (about 1 us per launch).
+template <int kMaxSeq>
+struct DecodeSeqs {
+    int pos[kMaxSeq];
+    int split_prefix[kMaxSeq + 1];  // cumulative splits per sequence
+};
+
+hipError_t launch_decode(const DecodeParams& p, const DecodeSeqs<kMaxSeqPerLaunch>& seqs,
+                         hipStream_t s);
 
 // ---- prefill -------------------------------------------------------------
 struct PrefillParams {
