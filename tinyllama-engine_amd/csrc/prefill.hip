@@ -72,14 +72,19 @@ struct PrefillGrid {
     int per_xcd;    // ceil(n_logical / 8)
 };
 
-__global__ __launch_bounds__(64 * kWavesP) __attribute__((amdgpu_waves_per_eu(2, 2))) void
-prefill_attention_kernel(const PrefillParams p,
-                                                                        const PrefillGrid g)
+constexpr int kRowPad = 68;  // LDS row stride (floats): 64 + 4 keeps operand reads conflict-free
+
+__global__ __launch_bounds__(64 * kWavesP) __attribute__((amdgpu_waves_per_eu(3, 3))) void
+prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
 {
+    // K and V tiles of 32 keys, shared by the 4 waves, double-buffered.
+    __shared__ float sk[2][kKTile][kRowPad];
+    __shared__ float sv[2][kKTile][kRowPad];
+
     // ---- XCD-aware, heavy-first mapping of workgroups to tiles ----
     const int bid = blockIdx.x;
     const int logical = (bid % kXcds) * g.per_xcd + bid / kXcds;
-    if (logical >= g.n_logical) return;
+    if (logical >= g.n_logical) return;  // whole workgroup
     const int per_pair = g.n_qt * g.n_hg;
     const int pair = logical / per_pair;  // (lb, kvh)
     const int r = logical - pair * per_pair;
@@ -91,8 +96,8 @@ prefill_attention_kernel(const PrefillParams p,
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
     const int lane = threadIdx.x & 63;
     const int hq = hg * kWavesP + wave;
-    if (hq >= p.gqa) return;  // uniform per wave
-    const int qh = kvh * p.gqa + hq;
+    const bool computes = hq < p.gqa;  // uniform per wave; others only load tiles
+    const int qh = kvh * p.gqa + (computes ? hq : 0);
 
     const int col = lane & 31;  // query row within the tile
     const int half = lane >> 5; // which 32 of the 64 dims (Q/K) / key sub-block
@@ -105,6 +110,28 @@ prefill_attention_kernel(const PrefillParams p,
     const long long layer_off = (long long)(p.layer0 + lb) * p.layer_stride + (long long)kvh * kHeadDim;
     const float* kc = p.kc + layer_off;
     const float* vc = p.vc + layer_off;
+
+    // ---- cooperative tile load: thread -> rows (t/16, t/16 + 16), float4 t%16.
+    // Keys past last_key are clamped (masked in the scores).  Byte offsets are
+    // 32-bit from a uniform base (a layer's cache slice is < 4 GiB).
+    const int lrow = threadIdx.x >> 4, lc4 = threadIdx.x & 15;
+    float4 stage[4];  // K row lrow, K row lrow+16, V row lrow, V row lrow+16
+    auto gload = [&](int j0) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            const unsigned key = (unsigned)min(j0 + lrow + 16 * h, last_key);
+            const unsigned off = (key * (unsigned)kv_dim + 4u * lc4) * 4u;
+            stage[h] = ldg4_at(kc, off);
+            stage[2 + h] = ldg4_at(vc, off);
+        }
+    };
+    auto lstore = [&](int buf) {
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            *reinterpret_cast<float4*>(&sk[buf][lrow + 16 * h][4 * lc4]) = stage[h];
+            *reinterpret_cast<float4*>(&sv[buf][lrow + 16 * h][4 * lc4]) = stage[2 + h];
+        }
+    };
 
     // ---- Q^T operand: lane holds q[row][32*half + s], s = 0..31 ----
     float4 qv[8];
@@ -125,34 +152,21 @@ prefill_attention_kernel(const PrefillParams p,
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    // K operand: lane holds K[j0 + col][32*half + s];  V operand: lane holds
-    // V[key(gi)][2*col + dt] for the 16 keys key(gi) = j0 + 8*(gi/4) + 4*half + gi%4.
-    // Keys past last_key are clamped (masked in the scores).  Byte offsets
-    // are 32-bit from a wave-uniform base (a layer's cache slice is < 4 GiB).
-    auto load_k = [&](int j0, float4 (&k)[8]) {
-        const unsigned ko = ((unsigned)min(j0 + col, last_key) * (unsigned)kv_dim + 32u * half) * 4u;
-#pragma unroll
-        for (int f = 0; f < 8; ++f) k[f] = ldg4_at(kc, ko + 16u * f);
-    };
-    auto load_v = [&](int j0, float2 (&v)[16]) {
-#pragma unroll
-        for (int gi = 0; gi < 16; ++gi) {
-            const unsigned key = (unsigned)min(j0 + 8 * (gi >> 2) + 4 * half + (gi & 3), last_key);
-            v[gi] = ldg2_at(vc, (key * (unsigned)kv_dim + 2u * col) * 4u);
-        }
-    };
-
-    // One key tile: S^T = K.Q^T, causal mask, online softmax, O^T += V^T.P^T.
-    auto step = [&](const float4 (&k)[8], const float2 (&v)[16], int j0) {
+    // One key tile from LDS buffer `buf`: S^T = K.Q^T (K operand: lane holds
+    // K[j0 + col][32*half + s]), causal mask, online softmax, O^T += V^T.P^T
+    // (V operand: lane holds V[key(gi)][2*col + dt], key(gi) = 8*(gi/4) + 4*half + gi%4).
+    auto step = [&](int buf, int j0) {
+        const float* krow = &sk[buf][col][32 * half];
         floatx16 s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.f;
 #pragma unroll
         for (int f = 0; f < 8; ++f) {
-            s = mfma32(k[f].x, qv[f].x, s);
-            s = mfma32(k[f].y, qv[f].y, s);
-            s = mfma32(k[f].z, qv[f].z, s);
-            s = mfma32(k[f].w, qv[f].w, s);
+            const float4 kk = *reinterpret_cast<const float4*>(krow + 4 * f);
+            s = mfma32(kk.x, qv[f].x, s);
+            s = mfma32(kk.y, qv[f].y, s);
+            s = mfma32(kk.z, qv[f].z, s);
+            s = mfma32(kk.w, qv[f].w, s);
         }
         // s[gi] = S[query col][key j0 + 8*(gi/4) + 4*half + gi%4]
         float mx = -INFINITY;
@@ -178,29 +192,29 @@ prefill_attention_kernel(const PrefillParams p,
         o1 *= alpha;
 #pragma unroll
         for (int gi = 0; gi < 16; ++gi) {
-            o0 = mfma32(v[gi].x, s[gi], o0);
-            o1 = mfma32(v[gi].y, s[gi], o1);
+            const int kin = 8 * (gi >> 2) + 4 * half + (gi & 3);
+            const float2 vv = *reinterpret_cast<const float2*>(&sv[buf][kin][2 * col]);
+            o0 = mfma32(vv.x, s[gi], o0);
+            o1 = mfma32(vv.y, s[gi], o1);
         }
     };
 
-    // K tiles ping-pong one tile ahead; each tile's V loads are issued when
-    // its step starts and land while the S products run.
-    float4 ka[8], kb[8];
-    float2 vv[16];
-    load_k(0, ka);
-    for (int j0 = 0;; j0 += 2 * kKTile) {
-        const bool has_b = j0 + kKTile <= last_key;  // uniform
-        load_v(j0, vv);
-        if (has_b) load_k(j0 + kKTile, kb);
-        step(ka, vv, j0);
-        if (!has_b) break;
-        const bool has_a = j0 + 2 * kKTile <= last_key;
-        load_v(j0 + kKTile, vv);
-        if (has_a) load_k(j0 + 2 * kKTile, ka);
-        step(kb, vv, j0 + kKTile);
-        if (!has_a) break;
+    // Tile j is computed from LDS while tile j+1's global loads are in flight;
+    // they land in the other buffer before the barrier that ends the step.
+    gload(0);
+    lstore(0);
+    __syncthreads();
+    int buf = 0;
+    for (int j0 = 0; j0 <= last_key; j0 += kKTile) {
+        const bool more = j0 + kKTile <= last_key;  // uniform
+        if (more) gload(j0 + kKTile);
+        if (computes) step(buf, j0);
+        if (more) lstore(buf ^ 1);
+        __syncthreads();
+        buf ^= 1;
     }
 
+    if (!computes) return;
     l_run += __shfl_xor(l_run, 32);
     if (i0 + col >= p.n_tok) return;
     const float inv = 1.0f / l_run;
