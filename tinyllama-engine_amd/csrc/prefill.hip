@@ -22,8 +22,9 @@
 //
 // Scheduling: key/value tiles of one (layer, kv head) are read by all its
 //   query tiles and q heads, so those workgroups are placed on one XCD
-//   (workgroup i runs on XCD i % 8) to share that XCD's L2, and within a
-//   (layer, kv head) the query tiles with the most key tiles go first.
+//   (workgroup i runs on XCD i % 8) to share that XCD's L2, and each XCD
+//   starts the query tiles with the most key tiles first, across all of its
+//   (layer, kv head) pairs, so the last workgroups to start are short ones.
 #include "rope_math.h"
 #include "tla_internal.h"
 
@@ -66,10 +67,10 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(const PrefillParams
 }
 
 struct PrefillGrid {
-    int n_qt;       // query tiles
-    int n_hg;       // head groups of 4 waves per kv head
-    int n_logical;  // n_lb * n_head_kv * n_hg * n_qt
-    int per_xcd;    // ceil(n_logical / 8)
+    int n_qt;     // query tiles
+    int n_hg;     // head groups of 4 waves per kv head
+    int n_pairs;  // n_lb * n_head_kv
+    int per_xcd;  // workgroup slots per XCD: ceil(n_pairs / 8) * n_hg * n_qt
 };
 
 constexpr int kRowPad = 68;  // LDS row stride (floats): 64 + 4 keeps operand reads conflict-free
@@ -82,14 +83,19 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     __shared__ float sv[2][kKTile][kRowPad];
 
     // ---- XCD-aware, heavy-first mapping of workgroups to tiles ----
-    const int bid = blockIdx.x;
-    const int logical = (bid % kXcds) * g.per_xcd + bid / kXcds;
-    if (logical >= g.n_logical) return;  // whole workgroup
-    const int per_pair = g.n_qt * g.n_hg;
-    const int pair = logical / per_pair;  // (lb, kvh)
-    const int r = logical - pair * per_pair;
-    const int qt = g.n_qt - 1 - r / g.n_hg;
-    const int hg = r % g.n_hg;
+    // Workgroup b runs on XCD b % 8 and XCDs start their workgroups in order
+    // of b / 8.  (layer, kv head) pair i belongs to XCD i % 8, so all query
+    // tiles of a pair share one L2; within an XCD, query tiles are handed out
+    // longest first (most key tiles) across all its pairs.
+    const int xcd = blockIdx.x % kXcds;
+    const int slot = blockIdx.x / kXcds;
+    const int xcd_pairs = (g.n_pairs - xcd + kXcds - 1) / kXcds;
+    const int per_rank = xcd_pairs * g.n_hg;
+    if (slot >= per_rank * g.n_qt) return;  // whole workgroup
+    const int qt = g.n_qt - 1 - slot / per_rank;
+    const int rem = slot - (slot / per_rank) * per_rank;
+    const int pair = xcd + kXcds * (rem / g.n_hg);  // (lb, kvh)
+    const int hg = rem % g.n_hg;
     const int lb = pair / p.n_head_kv;
     const int kvh = pair - lb * p.n_head_kv;
 
@@ -105,35 +111,34 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     const int trow = min(i0 + col, p.n_tok - 1);  // clamped token index
     const int qpos = p.pos0 + i0 + col;           // this row's position
     const int last_key = p.pos0 + min(i0 + kQTile - 1, p.n_tok - 1);
+    const int n_kt = last_key / kKTile + 1;  // key tiles covering 0..last_key
+    // Tiles below (pos0 + i0 + 1) / 32 end at or before the tile's first query
+    // position: no key in them is masked for any row.
+    const int n_plain = min((p.pos0 + i0 + 1) / kKTile, n_kt - 1);
 
     const int kv_dim = p.n_head_kv * kHeadDim;
     const long long layer_off = (long long)(p.layer0 + lb) * p.layer_stride + (long long)kvh * kHeadDim;
     const float* kc = p.kc + layer_off;
     const float* vc = p.vc + layer_off;
 
-    // ---- cooperative tile load: thread -> rows (t/16, t/16 + 16), float4 t%16.
-    // Keys past last_key are clamped (masked in the scores).  Byte offsets are
-    // 32-bit from a uniform base (a layer's cache slice is < 4 GiB).
+    // ---- cooperative tile loads: thread -> rows t/16 and t/16 + 16, float4 t%16.
+    // Keys past last_key are clamped to it (masked in the scores, or never
+    // used).  Byte offsets are 32-bit from a uniform base (one layer's cache
+    // slice is < 4 GiB).
     const int lrow = threadIdx.x >> 4, lc4 = threadIdx.x & 15;
-    float4 stage[4];  // K row lrow, K row lrow+16, V row lrow, V row lrow+16
-    auto gload = [&](int j0) {
+    auto gload = [&](const float* base, int tile, float4* dst) {
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-            const unsigned key = (unsigned)min(j0 + lrow + 16 * h, last_key);
-            const unsigned off = (key * (unsigned)kv_dim + 4u * lc4) * 4u;
-            stage[h] = ldg4_at(kc, off);
-            stage[2 + h] = ldg4_at(vc, off);
+            const unsigned key = (unsigned)min(tile * kKTile + lrow + 16 * h, last_key);
+            dst[h] = ldg4_at(base, (key * (unsigned)kv_dim + 4u * lc4) * 4u);
         }
     };
-    auto lstore = [&](int buf) {
+    auto lstore = [&](float (*buf)[kRowPad], const float4* src) {
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            *reinterpret_cast<float4*>(&sk[buf][lrow + 16 * h][4 * lc4]) = stage[h];
-            *reinterpret_cast<float4*>(&sv[buf][lrow + 16 * h][4 * lc4]) = stage[2 + h];
-        }
+        for (int h = 0; h < 2; ++h) *reinterpret_cast<float4*>(&buf[lrow + 16 * h][4 * lc4]) = src[h];
     };
 
-    // ---- Q^T operand: lane holds q[row][32*half + s], s = 0..31 ----
+    // ---- Q^T operand: lane holds q[row][32*half + s] * scale * log2(e) ----
     float4 qv[8];
     {
         const float* qrow = p.q + (((long long)lb * p.n_tok + trow) * p.n_head + qh) * kHeadDim + 32 * half;
@@ -142,7 +147,8 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
         for (int f = 0; f < 8; ++f) {
             float4 x = ldg4(qrow + 4 * f);
             if (p.rotate) x = rotate4(x, ldg4(tab + 2 * (16 * half + 2 * f)));
-            qv[f] = x;
+            qv[f] = make_float4(x.x * p.scale_log2, x.y * p.scale_log2, x.z * p.scale_log2,
+                                x.w * p.scale_log2);
         }
     }
 
@@ -152,11 +158,10 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    // One key tile from LDS buffer `buf`: S^T = K.Q^T (K operand: lane holds
-    // K[j0 + col][32*half + s]), causal mask, online softmax, O^T += V^T.P^T
-    // (V operand: lane holds V[key(gi)][2*col + dt], key(gi) = 8*(gi/4) + 4*half + gi%4).
-    auto step = [&](int buf, int j0) {
-        const float* krow = &sk[buf][col][32 * half];
+    // S^T = K.Q^T for the tile in K buffer b (K operand: lane holds
+    // K[col][32*half + s]).  s[gi] = S[query col][key 8*(gi/4) + 4*half + gi%4].
+    auto scores = [&](int b) {
+        const float* krow = &sk[b][col][32 * half];
         floatx16 s;
 #pragma unroll
         for (int i = 0; i < 16; ++i) s[i] = 0.f;
@@ -168,15 +173,20 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
             s = mfma32(kk.z, qv[f].z, s);
             s = mfma32(kk.w, qv[f].w, s);
         }
-        // s[gi] = S[query col][key j0 + 8*(gi/4) + 4*half + gi%4]
-        float mx = -INFINITY;
+        return s;
+    };
+    // Online softmax of one tile's scores (log2 units) into P, in place.
+    auto softmax = [&](floatx16& s, int j0, bool masked) {
+        if (masked) {
 #pragma unroll
-        for (int gi = 0; gi < 16; ++gi) {
-            const int key = j0 + 8 * (gi >> 2) + 4 * half + (gi & 3);
-            const float x = (key <= qpos && key <= last_key) ? s[gi] * p.scale_log2 : -INFINITY;
-            s[gi] = x;
-            mx = fmaxf(mx, x);
+            for (int gi = 0; gi < 16; ++gi) {
+                const int key = j0 + 8 * (gi >> 2) + 4 * half + (gi & 3);
+                s[gi] = (key <= qpos && key <= last_key) ? s[gi] : -INFINITY;
+            }
         }
+        float mx = s[0];
+#pragma unroll
+        for (int gi = 1; gi < 16; ++gi) mx = fmaxf(mx, s[gi]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
         const float m_new = fmaxf(m_run, mx);
         const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
@@ -190,28 +200,68 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
         l_run = l_run * alpha + lsum;
         o0 *= alpha;
         o1 *= alpha;
+    };
+    // O^T += V^T.P^T for the tile in V buffer b (V operand: lane holds
+    // V[8*(gi/4) + 4*half + gi%4][2*col + dt]).
+    auto accumulate = [&](const floatx16& s, int b) {
 #pragma unroll
         for (int gi = 0; gi < 16; ++gi) {
             const int kin = 8 * (gi >> 2) + 4 * half + (gi & 3);
-            const float2 vv = *reinterpret_cast<const float2*>(&sv[buf][kin][2 * col]);
+            const float2 vv = *reinterpret_cast<const float2*>(&sv[b][kin][2 * col]);
             o0 = mfma32(vv.x, s[gi], o0);
             o1 = mfma32(vv.y, s[gi], o1);
         }
     };
 
-    // Tile j is computed from LDS while tile j+1's global loads are in flight;
-    // they land in the other buffer before the barrier that ends the step.
-    gload(0);
-    lstore(0);
+    // Software pipeline over key tiles j: step j computes the scores of tile
+    // j+1 (MFMA) while the softmax of tile j (VALU) runs, then P.V of tile j.
+    // At the start of step j the LDS holds K[j+1] and V[j]; the step stores
+    // K[j+2] and V[j+1], loaded from global memory one step earlier, into the
+    // buffers of K[j] and V[j-1], and issues the loads of K[j+3] and V[j+2].
+    float4 ld_k[2], ld_v[2];
+    gload(kc, 0, ld_k);
+    gload(vc, 0, ld_v);
+    lstore(sk[0], ld_k);
+    lstore(sv[0], ld_v);
+    gload(kc, 1, ld_k);
+    gload(vc, 1, ld_v);
+    lstore(sk[1], ld_k);
+    gload(kc, 2, ld_k);
     __syncthreads();
-    int buf = 0;
-    for (int j0 = 0; j0 <= last_key; j0 += kKTile) {
-        const bool more = j0 + kKTile <= last_key;  // uniform
-        if (more) gload(j0 + kKTile);
-        if (computes) step(buf, j0);
-        if (more) lstore(buf ^ 1);
+    floatx16 s_cur;
+    if (computes) s_cur = scores(0);
+    __syncthreads();  // K[0]'s buffer is overwritten in step 0
+
+    int j = 0;
+    for (; j < n_plain; ++j) {
+        if (computes) {
+            const floatx16 s_next = scores((j + 1) & 1);
+            softmax(s_cur, j * kKTile, false);
+            accumulate(s_cur, j & 1);
+            s_cur = s_next;
+        }
+        lstore(sk[j & 1], ld_k);
+        lstore(sv[(j + 1) & 1], ld_v);
+        gload(kc, j + 3, ld_k);
+        gload(vc, j + 2, ld_v);
         __syncthreads();
-        buf ^= 1;
+    }
+    for (; j < n_kt; ++j) {  // at most two tiles reach the diagonal
+        const bool more = j + 1 < n_kt;  // uniform
+        if (computes) {
+            floatx16 s_next;
+            if (more) s_next = scores((j + 1) & 1);
+            softmax(s_cur, j * kKTile, true);
+            accumulate(s_cur, j & 1);
+            s_cur = s_next;
+        }
+        if (more) {
+            lstore(sk[j & 1], ld_k);
+            lstore(sv[(j + 1) & 1], ld_v);
+            gload(kc, j + 3, ld_k);
+            gload(vc, j + 2, ld_v);
+            __syncthreads();
+        }
     }
 
     if (!computes) return;
@@ -244,8 +294,8 @@ hipError_t launch_prefill_attention(const PrefillParams& p, hipStream_t s)
     PrefillGrid g;
     g.n_qt = (p.n_tok + kQTile - 1) / kQTile;
     g.n_hg = (p.gqa + kWavesP - 1) / kWavesP;
-    g.n_logical = p.n_lb * p.n_head_kv * g.n_hg * g.n_qt;
-    g.per_xcd = (g.n_logical + kXcds - 1) / kXcds;
+    g.n_pairs = p.n_lb * p.n_head_kv;
+    g.per_xcd = (g.n_pairs + kXcds - 1) / kXcds * g.n_hg * g.n_qt;
     hipLaunchKernelGGL(prefill_attention_kernel, dim3(g.per_xcd * kXcds), dim3(64 * kWavesP), 0, s,
                        p, g);
     return hipGetLastError();
