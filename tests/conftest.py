@@ -55,13 +55,15 @@ def faulty_oracle(O):
 
 @pytest.fixture(scope="session")
 def engines(tla):
-    """Cache of GPU engines keyed by (n_layers, n_ctx); closed at session end."""
+    """Cache of GPU engines keyed by (n_layers, n_ctx, n_head, n_head_kv);
+    closed at session end.  Heads default to TinyLlama's 32 / 4 (head_dim 64)."""
     made = {}
 
-    def get(n_layers, n_ctx):
-        key = (n_layers, n_ctx)
+    def get(n_layers, n_ctx, n_head=32, n_head_kv=4):
+        key = (n_layers, n_ctx, n_head, n_head_kv)
         if key not in made:
-            made[key] = tla.Engine(tla.Config.tinyllama(n_layers=n_layers, n_ctx=n_ctx))
+            cfg = tla.Config(n_layers, n_head * 64, n_head, n_head_kv, n_ctx, 10000.0)
+            made[key] = tla.Engine(cfg)
         return made[key]
 
     yield get

@@ -91,9 +91,9 @@ def oracle_decode(O, case, rotate=True, keep_cache=False):
     kc = case.kc.reshape(units, case.n_ctx, kv_dim).copy()
     vc = case.vc.reshape(units, case.n_ctx, kv_dim).copy()
     pos = np.repeat(case.pos, case.n_layers).astype(np.int32)
+    shape = O.Shape(n_head=case.n_head, n_head_kv=case.n_head_kv, n_ctx=case.n_ctx)
     out = O.decode_units_mt(ORACLE_THREADS, case.q.reshape(units, -1), case.k.reshape(units, -1),
-                            case.v.reshape(units, -1), kc, vc, pos, O.Shape(n_ctx=case.n_ctx),
-                            rotate=rotate)
+                            case.v.reshape(units, -1), kc, vc, pos, shape, rotate=rotate)
     out = out.reshape(case.n_seq, case.n_layers, -1)
     if keep_cache:
         return out, kc.reshape(case.kc.shape), vc.reshape(case.vc.shape)

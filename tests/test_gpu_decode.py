@@ -112,6 +112,16 @@ def test_decode_positions_and_splits(O, W, engines, pos, split):
     check_decode(O, engines(2, 2048), case, split=split)
 
 
+@pytest.mark.parametrize("n_head,n_head_kv", [(32, 8), (32, 2), (16, 1), (24, 6), (64, 4), (12, 12)])
+@pytest.mark.parametrize("split", [0, 64])
+def test_decode_other_head_shapes(O, W, engines, n_head, n_head_kv, split):
+    """GQA ratios 1..16, more than one workgroup of kv heads per split (grid
+    y > 1) and groups with idle waves; several splits per sequence."""
+    case = W.make_decode(13, 2, 2, 1024, [1023, 300], salt=n_head * 100 + n_head_kv,
+                         n_head=n_head, n_head_kv=n_head_kv)
+    check_decode(O, engines(2, 1024, n_head, n_head_kv), case, split=split)
+
+
 def test_attention_contract_without_rotation(O, W, engines):
     """tla_decode without TLA_ROTATE = attention(): q, k taken as rotated."""
     case = W.make_decode(12, 2, 3, 512, [200, 511], salt=1)

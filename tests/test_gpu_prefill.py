@@ -15,10 +15,11 @@ pytestmark = pytest.mark.gpu
 
 def gpu_prefill(eng, case, layer0=0, chunks=None, kc_init=None, vc_init=None, rotate=True):
     """Run `case` (n_layers x n_tok) at positions pos0.. in the given chunks;
-    returns (out [n_layers, n_tok, 2048], key cache, value cache)."""
+    returns (out [n_layers, n_tok, q_dim], key cache, value cache)."""
     nl, nt = case.n_layers, case.n_tok
+    q_dim = case.q.shape[-1]
     chunks = chunks or [nt]
-    outs = np.zeros((nl, nt, 2048), np.float32)
+    outs = np.zeros((nl, nt, q_dim), np.float32)
     with device_arrays() as track:
         kc, vc = eng.kv_cache(1)
         track(kc), track(vc)
@@ -30,7 +31,7 @@ def gpu_prefill(eng, case, layer0=0, chunks=None, kc_init=None, vc_init=None, ro
             q = track(eng.array(np.ascontiguousarray(case.q[:, t0:t0 + c])))
             k = track(eng.array(np.ascontiguousarray(case.k[:, t0:t0 + c])))
             v = track(eng.array(np.ascontiguousarray(case.v[:, t0:t0 + c])))
-            out = track(eng.array((nl, c, 2048)))
+            out = track(eng.array((nl, c, q_dim)))
             log(f"  tla_prefill pos0={case.pos0 + t0} n_tok={c} layers={layer0}..{layer0 + nl - 1}")
             eng.prefill(case.pos0 + t0, c, layer0, nl, out.ptr, q.ptr, k.ptr, v.ptr, kc.ptr, vc.ptr,
                         rotate=rotate)
@@ -40,9 +41,10 @@ def gpu_prefill(eng, case, layer0=0, chunks=None, kc_init=None, vc_init=None, ro
 
 
 def oracle_prefill(O, case, n_layers_total, n_ctx, layer0=0, kc=None, vc=None):
-    s = O.Shape(n_ctx=n_ctx, n_layers=n_layers_total)
+    s = O.Shape(n_head=case.n_head, n_head_kv=case.n_head_kv, n_ctx=n_ctx,
+                n_layers=n_layers_total)
     if kc is None:
-        kc = np.zeros(n_layers_total * n_ctx * 256, np.float32)
+        kc = np.zeros(n_layers_total * n_ctx * s.kv_dim, np.float32)
         vc = np.zeros_like(kc)
     outs = [None] * case.n_layers
 
@@ -158,3 +160,19 @@ def test_prefill_range_errors(tla, W, engines):
             with pytest.raises(tla.TlaError) as ei:
                 eng.prefill(pos0, n, l0, nl, buf.ptr, buf.ptr, buf.ptr, buf.ptr, kc.ptr, vc.ptr)
             assert ei.value.code == code
+
+
+@pytest.mark.parametrize("n_head,n_head_kv", [(32, 8), (32, 2), (16, 1), (24, 6), (64, 4), (12, 12)])
+def test_prefill_other_head_shapes(O, W, engines, n_head, n_head_kv):
+    """GQA ratios 1..16 and kv head counts that leave workgroup waves idle."""
+    n_ctx = 256
+    case = W.make_prefill(n_layers=2, n_tok=77, pos0=0, salt=n_head * 100 + n_head_kv,
+                          n_head=n_head, n_head_kv=n_head_kv)
+    eng = engines(2, n_ctx, n_head, n_head_kv)
+    got, gkc, gvc = gpu_prefill(eng, case)
+    ref, rkc, rvc = oracle_prefill(O, case, 2, n_ctx)
+    err = max_err(got, ref)
+    log(f"    heads {n_head}/{n_head_kv}: max-abs error {err:.3e}")
+    assert err <= PREFILL_TOL
+    assert np.array_equal(bits(gkc.reshape(-1)), bits(rkc.reshape(-1)))
+    assert np.array_equal(bits(gvc.reshape(-1)), bits(rvc.reshape(-1)))

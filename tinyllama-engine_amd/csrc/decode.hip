@@ -45,7 +45,7 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kKvWaves = 4;               // kv heads per workgroup
+constexpr int kKvWaves = kDecodeKvGroup;  // kv heads per workgroup
 constexpr int kSub = 2;                   // position halves per kv head
 constexpr int kWaves = kKvWaves * kSub;   // waves per workgroup
 
@@ -122,12 +122,24 @@ struct Partial {
     float l;
 };
 
-// Online merge of the partials of splits [s_lo, s_hi) of one unit for one kv
-// head, each lane merging the same 16 values it produces in the main loop:
-// O = sum_s O_s w_s, l = sum_s l_s w_s with w_s = 2^(m_s - max m).  Chunks of
-// 8 splits whose loads are all issued before any is used.
-__device__ Partial merge_range(const DecodeParams& p, int unit, int s_lo, int s_hi, int kvh,
-                               int lane)
+// Combine the state of the wave one position-half above (in LDS) into this
+// wave's: the two halves of a kv head meet here.  Either side may be empty
+// (m = -inf, l = 0, acc = 0) but not both.
+struct HalfExchange {
+    floatx4 acc[kKvWaves][4][64];
+    float m[kKvWaves][16];
+    float l[kKvWaves][16];
+};
+
+// Online merge of the partials of splits [s_lo, s_hi) of one unit for one
+// kv head, each lane merging the same 16 values it produces in the main
+// loop: O = sum_s O_s w_s, l = sum_s l_s w_s with w_s = 2^(m_s - max m).
+// Split `own` (the merging workgroup's) is read from `mine` in LDS, every
+// other from the workspace, so the order of the sums does not depend on
+// which workgroup merges.  Chunks of 8 splits whose loads are all issued
+// before any is used.
+__device__ Partial merge_range(const DecodeParams& p, int unit, int s_lo, int s_hi, int own,
+                               const HalfExchange& mine, int slot, int kvh, int lane)
 {
     constexpr int kChunk = 8;
     const int hsub = lane & 15, grp = lane >> 4;
@@ -142,14 +154,23 @@ __device__ Partial merge_range(const DecodeParams& p, int unit, int s_lo, int s_
     for (int s0 = s_lo; s0 < s_hi; s0 += kChunk) {
         float ms[kChunk], ls[kChunk];
         floatx4 x[kChunk][4];
+        auto read = [&](int j) {
+            const auto rs = part_rsrc(p.part + part_slot(p, unit, s0 + j, kvh), slot_bytes);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[j][i] = ld_dev4(rs, (i * 4 * p.gqa + li) * 16);
+            ms[j] = ld_dev1(rs, (64 * p.gqa + hsub) * 4);
+            ls[j] = ld_dev1(rs, (65 * p.gqa + hsub) * 4);
+        };
+        auto use = [&](int j) { return s0 + j < s_hi && s0 + j != own; };
 #pragma unroll
         for (int j = 0; j < kChunk; ++j) {
-            if (s0 + j < s_hi) {
-                const auto rs = part_rsrc(p.part + part_slot(p, unit, s0 + j, kvh), slot_bytes);
+            if (use(j)) {
+                read(j);
+            } else if (s0 + j < s_hi) {  // s0 + j == own
 #pragma unroll
-                for (int i = 0; i < 4; ++i) x[j][i] = ld_dev4(rs, (i * 4 * p.gqa + li) * 16);
-                ms[j] = ld_dev1(rs, (64 * p.gqa + hsub) * 4);
-                ls[j] = ld_dev1(rs, (65 * p.gqa + hsub) * 4);
+                for (int i = 0; i < 4; ++i) x[j][i] = mine.acc[slot][i][lane];
+                ms[j] = mine.m[slot][hsub];
+                ls[j] = mine.l[slot][hsub];
             } else {
                 ms[j] = -INFINITY;
                 ls[j] = 0.f;
@@ -175,15 +196,6 @@ __device__ Partial merge_range(const DecodeParams& p, int unit, int s_lo, int s_
     }
     return r;
 }
-
-// Combine the state of the wave one position-half above (in LDS) into this
-// wave's: the two halves of a kv head meet here.  Either side may be empty
-// (m = -inf, l = 0, acc = 0) but not both.
-struct HalfExchange {
-    floatx4 acc[kKvWaves][4][64];
-    float m[kKvWaves][16];
-    float l[kKvWaves][16];
-};
 
 __device__ __forceinline__ void put_half(HalfExchange& x, int slot, int lane, const Partial& r)
 {
@@ -211,8 +223,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
                                                                    const DecodeSeqs<kMaxSeq> b)
 {
     __shared__ int s_last;
-    __shared__ float4 s_new[kWaves][32];  // appended k row (16 float4) | v row (16 float4)
+    __shared__ float4 s_new[kKvWaves][32];  // appended k row (16 float4) | v row (16 float4)
+    __shared__ int s_claim[kKvWaves];       // next unclaimed tile, per kv head
     __shared__ HalfExchange s_half;
+    __shared__ HalfExchange s_mine;  // this split's partial, for the merge
     const int lane = threadIdx.x & 63;
     // wave index made explicitly scalar so cache bases stay in SGPRs
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -236,15 +250,16 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     const int unit = seq * p.n_lb + lb;
     const int layer = p.layer0 + lb;
 
-    // The split's tiles are cut in two halves (the first half rounded up);
-    // this wave takes positions [begin, end) of its half, possibly none.
-    const int split_begin = split * p.split_len;
-    const int split_end = min(pos + 1, split_begin + p.split_len);  // exclusive
-    const int half_tiles = ((split_end - split_begin + kDecodeTile - 1) / kDecodeTile + 1) / 2;
-    const int begin = sub == 0 ? split_begin : split_begin + half_tiles * kDecodeTile;
-    const int end = sub == 0 ? min(split_end, split_begin + half_tiles * kDecodeTile) : split_end;
-    const bool has_rows = begin < end;                   // uniform per wave
-    const bool has_new = (pos >= begin) && (pos < end);  // this half appends; pos = end-1
+    // The split's positions [begin, end) are cut into tiles of 16.  The two
+    // waves of a kv head share them: each starts on tiles sub and 2 + sub,
+    // then claims the next unprocessed tile from a counter in LDS, so the
+    // wave that the SIMD serves first takes more tiles and both finish
+    // together.
+    const int begin = split * p.split_len;
+    const int end = min(pos + 1, begin + p.split_len);  // exclusive
+    const int n_tiles = (end - begin + kDecodeTile - 1) / kDecodeTile;
+    const bool appends = pos < end;  // this split holds `pos`: its last tile does
+    const int special = appends ? n_tiles - 1 : n_tiles;
 
     const int hsub = lane & 15;  // q head within the group / K row within the tile
     const int grp = lane >> 4;   // 0..3
@@ -259,19 +274,21 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     float* const vc = p.vc + cache_off;
     const float* const tab = reinterpret_cast<const float*>(p.rope + (long long)pos * kPairs);
 
-    // Append (attention() step 1, src/ops.cpp:1370-1371): 16 lanes write the
-    // (rotated) k row and the v row to the cache and keep a copy in LDS for
-    // this split's last tile.
-    if (active && has_new && lane < 16) {
+    // Append (attention() step 1, src/ops.cpp:1370-1371): 16 lanes of the
+    // first wave of the kv head write the (rotated) k row and the v row to
+    // the cache and keep a copy in LDS for the split's last tile.
+    if (active && appends && sub == 0 && lane < 16) {
         const long long row = ((long long)unit * p.n_head_kv + kvh) * kHeadDim + 4 * lane;
-        float4 kx = ldg4(p.k + row);
-        if (p.rotate) kx = rotate4(kx, ldg4(tab + 4 * lane));
+        const float4 k_in = ldg4(p.k + row);
+        const float4 cs = ldg4(tab + 4 * lane);  // loaded either way: no branch before the loads
         const float4 vx = ldg4(p.v + row);
+        const float4 kx = p.rotate ? rotate4(k_in, cs) : k_in;
         stg4(kc + (long long)pos * kv_dim + 4 * lane, kx);
         stg4(vc + (long long)pos * kv_dim + 4 * lane, vx);
-        s_new[wave][lane] = kx;
-        s_new[wave][16 + lane] = vx;
+        s_new[slot][lane] = kx;
+        s_new[slot][16 + lane] = vx;
     }
+    if (threadIdx.x < kKvWaves) s_claim[threadIdx.x] = kSub * 2;  // tiles 0..3 are pre-assigned
     __syncthreads();
 
     floatx4 o[4];
@@ -280,24 +297,26 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    if (active && has_rows) {
+    if (active) {
         // B operand of S^T: lane holds q[head hsub][16t + 4grp + c], rotated
         // with the pairs 8t + 2grp + {0,1} of the table row for `pos`.
-        float4 qv[4];
+        // The q and table loads, then the first two tiles' loads, are all
+        // issued before q is rotated (below).
+        float4 qv[4], qcs[4];
         {
             const float* qrow = p.q + ((long long)unit * p.n_head + (head_ok ? qh : 0)) * kHeadDim;
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
-                float4 x = ldg4(qrow + 16 * t + 4 * grp);
-                if (p.rotate) x = rotate4(x, ldg4(tab + 2 * (8 * t + 2 * grp)));
-                qv[t] = head_ok ? x : make_float4(0.f, 0.f, 0.f, 0.f);
+                qv[t] = ldg4(qrow + 16 * t + 4 * grp);
+                qcs[t] = ldg4(tab + 2 * (8 * t + 2 * grp));
             }
         }
 
         // Rows past `end` are masked; they load row `begin` (always valid).
         // Byte offsets are 32-bit (a unit's cache slice is < 4 GiB) from a
         // wave-uniform base.
-        auto load_tile = [&](int p0, Tile& tl) {
+        auto load_tile = [&](int tile, Tile& tl) {
+            const int p0 = begin + tile * kDecodeTile;
             int r = p0 + hsub;
             if (r >= end) r = begin;
             const unsigned ko = ((unsigned)r * kv_dim + 4u * grp) * 4u;  // bytes
@@ -312,7 +331,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
         };
 
         // One tile: S^T = K.Q^T, online softmax, O^T += V^T.P^T.
-        auto step = [&](const Tile& tl, int p0) {
+        auto step = [&](const Tile& tl, int tile) {
+            const int p0 = begin + tile * kDecodeTile;
             floatx4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int t = 0; t < 4; ++t) {
@@ -355,46 +375,63 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
         };
 
         // The appending split's last tile holds `pos`; that row comes from
-        // LDS (the copy kept at append), not from the cache row just written.
-        // Rows loaded for masked lanes (>= end) are `begin`, also replaced
-        // when begin == pos.
-        auto substitute = [&](Tile& tl, int p0) {
+        // LDS (the copy kept at append), not from the cache, which the
+        // append may not have reached when the tile was loaded.  Rows loaded
+        // for masked lanes (>= end) are `begin`, also replaced when
+        // begin == pos.
+        auto substitute = [&](Tile& tl, int tile) {
+            const int p0 = begin + tile * kDecodeTile;
             if (p0 + hsub >= pos) {
 #pragma unroll
-                for (int t = 0; t < 4; ++t) tl.k[t] = s_new[wave][4 * t + grp];
+                for (int t = 0; t < 4; ++t) tl.k[t] = s_new[slot][4 * t + grp];
             }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const int row = p0 + 4 * grp + i;
-                if (row == pos || (row >= end && begin == pos)) tl.v[i] = s_new[wave][16 + hsub];
+                if (row == pos || (row >= end && begin == pos)) tl.v[i] = s_new[slot][16 + hsub];
             }
         };
+        auto process = [&](Tile& tl, int tile) {
+            if (tile == special) substitute(tl, tile);  // uniform branch
+            step(tl, tile);
+        };
+        // Claims are wave-uniform: lane 0 bumps the counter, every lane
+        // reads lane 0's value.
+        auto claim = [&]() {
+            int c = 0;
+            if (lane == 0) c = atomicAdd(&s_claim[slot], 1);
+            return __builtin_amdgcn_readfirstlane(c);
+        };
 
-        // Two tiles ping-pong: the next tile's loads are in flight while the
-        // current one is computed.  The special last tile is peeled so that
-        // the loop body has no divergent branches.
-        const int n_tiles = (end - begin + kDecodeTile - 1) / kDecodeTile;
-        const int n_main = has_new ? n_tiles - 1 : n_tiles;
+        // Two tiles in flight: while one is computed the other is loading.
+        // Claims only grow, so once the older of the two is past the end,
+        // so is every later one.  Loads are unconditional, so that the
+        // count of loads in flight is the same on every path and waiting
+        // for one tile never waits for the other: a claim past the end
+        // reloads a tile already loaded (a cache hit) and is not used.
+        int ca = sub, cb = kSub + sub;
         Tile ta, tb;
-        load_tile(begin, ta);
-        int t = 0;
-        for (; t + 1 < n_main; t += 2) {
-            load_tile(begin + (t + 1) * kDecodeTile, tb);
-            step(ta, begin + t * kDecodeTile);
-            if (t + 2 < n_tiles) load_tile(begin + (t + 2) * kDecodeTile, ta);
-            step(tb, begin + (t + 1) * kDecodeTile);
+        load_tile(min(ca, n_tiles - 1), ta);
+        __builtin_amdgcn_sched_barrier(0);  // all of ta's loads before tb's
+        load_tile(min(cb, n_tiles - 1), tb);
+        if (p.rotate) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) qv[t] = rotate4(qv[t], qcs[t]);
         }
-        if (t < n_main) {
-            if (t + 1 < n_tiles) load_tile(begin + (t + 1) * kDecodeTile, tb);
-            step(ta, begin + t * kDecodeTile);
-            if (has_new) {
-                substitute(tb, begin + (t + 1) * kDecodeTile);
-                step(tb, begin + (t + 1) * kDecodeTile);
-            }
-        } else if (has_new) {
-            substitute(ta, begin + t * kDecodeTile);
-            step(ta, begin + t * kDecodeTile);
+        if (!head_ok) {
+#pragma unroll
+            for (int t = 0; t < 4; ++t) qv[t] = make_float4(0.f, 0.f, 0.f, 0.f);
         }
+        do {
+            if (ca < n_tiles) process(ta, ca);  // uniform branches: the loads stay outside
+            const int na = claim();
+            load_tile(na < n_tiles ? na : min(ca, n_tiles - 1), ta);
+            if (cb < n_tiles) process(tb, cb);
+            const int nb = claim();
+            load_tile(nb < n_tiles ? nb : min(cb, n_tiles - 1), tb);
+            ca = na;
+            cb = nb;
+        } while (ca < n_tiles);
 
         // Row sums: each lane group summed different positions of the same head.
         l_run += __shfl_xor(l_run, 16);
@@ -422,34 +459,44 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
                     stg4(orow + 4 * i, make_float4(r.acc[i][0] * inv, r.acc[i][1] * inv,
                                                    r.acc[i][2] * inv, r.acc[i][3] * inv));
             }
-        } else if (head_ok) {
-            const auto rs = part_rsrc(p.part + part_slot(p, unit, split, kvh), part_floats(p.gqa) * 4);
-            const int li = grp * p.gqa + hsub;
+        } else {
+            // The partial goes to the workspace for whichever workgroup merges
+            // and to LDS in case it is this one.
+            put_half(s_mine, slot, lane, r);
+            if (head_ok) {
+                const auto rs =
+                    part_rsrc(p.part + part_slot(p, unit, split, kvh), part_floats(p.gqa) * 4);
+                const int li = grp * p.gqa + hsub;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) st_dev4(r.acc[i], rs, (i * 4 * p.gqa + li) * 16);
-            if (grp == 0) {
-                st_dev1(r.m, rs, (64 * p.gqa + hsub) * 4);
-                st_dev1(r.l, rs, (65 * p.gqa + hsub) * 4);
+                for (int i = 0; i < 4; ++i) st_dev4(r.acc[i], rs, (i * 4 * p.gqa + li) * 16);
+                if (grp == 0) {
+                    st_dev1(r.m, rs, (64 * p.gqa + hsub) * 4);
+                    st_dev1(r.l, rs, (65 * p.gqa + hsub) * 4);
+                }
             }
         }
     }
 
     if (nsplit == 1) return;  // uniform per workgroup
     // Wait until this wave's partial stores are acknowledged at device scope,
-    // then count the split in; the workgroup that completes the count merges.
+    // then count the split in; the workgroup that completes the count of its
+    // (unit, kv head group) merges.
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    int* const counter = p.counters + (long long)unit * gridDim.y + blockIdx.y;
     if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(p.counters + unit, 1, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT) == nsplit * (int)gridDim.y - 1;
+        s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
+                 nsplit - 1;
     __syncthreads();
     if (!s_last) return;
     if (threadIdx.x == 0)  // every split has arrived: ready for the next launch
-        __hip_atomic_store(p.counters + unit, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     // Both halves of each kv head merge half of the splits, then meet in LDS.
     const int s_mid = (nsplit + 1) / 2;
     Partial mr;
-    if (active) mr = merge_range(p, unit, sub == 0 ? 0 : s_mid, sub == 0 ? s_mid : nsplit, kvh, lane);
+    if (active)
+        mr = merge_range(p, unit, sub == 0 ? 0 : s_mid, sub == 0 ? s_mid : nsplit, split, s_mine,
+                         slot, kvh, lane);
     if (active && sub == 1) put_half(s_half, slot, lane, mr);
     __syncthreads();
     if (!active || sub != 0 || !head_ok) return;

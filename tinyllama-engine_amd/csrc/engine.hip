@@ -177,8 +177,8 @@ int ensure_ws(tla_engine* e, size_t bytes)
     return TLA_OK;
 }
 
-// Arrival counters for `units` units.  Zeroed once when (re)allocated; the
-// decode kernel returns every counter it uses to zero.
+// Arrival counters for `units` (unit, kv head group) pairs.  Zeroed once
+// when (re)allocated; the decode kernel returns every counter it uses to zero.
 int ensure_counters(tla_engine* e, size_t units)
 {
     if (units <= e->n_counters) return TLA_OK;
@@ -490,7 +490,8 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
         const size_t bytes = static_cast<size_t>(units) * max_splits * c.n_head_kv * 66 *
                              e->gqa * sizeof(float);
         if (int rc = ensure_ws(e, bytes)) return rc;
-        if (int rc = ensure_counters(e, static_cast<size_t>(units))) return rc;
+        const long long groups = (c.n_head_kv + kDecodeKvGroup - 1) / kDecodeKvGroup;
+        if (int rc = ensure_counters(e, static_cast<size_t>(units * groups))) return rc;
         p.part = static_cast<float*>(e->ws);
         p.counters = e->counters;
     }

@@ -55,11 +55,10 @@ __global__ __launch_bounds__(256) void prefill_append_kernel(const PrefillParams
     const int t = (int)(lt % p.n_tok);
     const int lb = (int)(lt / p.n_tok);
     const int pos = p.pos0 + t;
-    float4 kx = ldg4(p.k + row * kHeadDim + 4 * c4);
-    if (p.rotate) {
-        const float* tab = reinterpret_cast<const float*>(p.rope + (long long)pos * kPairs);
-        kx = rotate4(kx, ldg4(tab + 4 * c4));
-    }
+    const float* tab = reinterpret_cast<const float*>(p.rope + (long long)pos * kPairs);
+    const float4 k_in = ldg4(p.k + row * kHeadDim + 4 * c4);
+    const float4 cs = ldg4(tab + 4 * c4);  // loaded either way: no branch before the loads
+    const float4 kx = p.rotate ? rotate4(k_in, cs) : k_in;
     const long long dst = (long long)(p.layer0 + lb) * p.layer_stride +
                           ((long long)pos * p.n_head_kv + kvh) * kHeadDim + 4 * c4;
     stg4(p.kc + dst, kx);
@@ -143,10 +142,16 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     {
         const float* qrow = p.q + (((long long)lb * p.n_tok + trow) * p.n_head + qh) * kHeadDim + 32 * half;
         const float* tab = reinterpret_cast<const float*>(p.rope + (long long)(p.pos0 + trow) * kPairs);
+        // All sixteen loads are issued before any is used.
+        float4 cs[8];
 #pragma unroll
         for (int f = 0; f < 8; ++f) {
-            float4 x = ldg4(qrow + 4 * f);
-            if (p.rotate) x = rotate4(x, ldg4(tab + 2 * (16 * half + 2 * f)));
+            qv[f] = ldg4(qrow + 4 * f);
+            cs[f] = ldg4(tab + 2 * (16 * half + 2 * f));
+        }
+#pragma unroll
+        for (int f = 0; f < 8; ++f) {
+            const float4 x = p.rotate ? rotate4(qv[f], cs[f]) : qv[f];
             qv[f] = make_float4(x.x * p.scale_log2, x.y * p.scale_log2, x.z * p.scale_log2,
                                 x.w * p.scale_log2);
         }
@@ -249,7 +254,7 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     for (; j < n_kt; ++j) {  // at most two tiles reach the diagonal
         const bool more = j + 1 < n_kt;  // uniform
         if (computes) {
-            floatx16 s_next;
+            floatx16 s_next = {};  // unused after the last tile
             if (more) s_next = scores((j + 1) & 1);
             softmax(s_cur, j * kKTile, true);
             accumulate(s_cur, j & 1);

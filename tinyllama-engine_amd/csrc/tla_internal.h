@@ -15,6 +15,7 @@ constexpr int kPairs = kHeadDim / 2;
 constexpr int kMaxGqa = 16;         // q heads per kv head (MFMA N = 16)
 constexpr int kMaxSeqPerLaunch = 256;
 constexpr int kDecodeTile = 16;     // positions per decode MFMA tile
+constexpr int kDecodeKvGroup = 4;   // kv heads per decode workgroup (grid y = groups)
 constexpr int kMaxRopePairs = 128;  // tla_rope: head_dim <= 256
 
 // ---- decode ------------------------------------------------------------
@@ -28,7 +29,7 @@ struct DecodeParams {
     float* vc;
     const float2* rope;  // [n_ctx][32] (cos, sin)
     float* part;         // split partials, [unit][max_splits][n_head_kv][66 * gqa]
-    int* counters;       // [unit] split arrivals; zero between launches
+    int* counters;       // [unit][kv head group] split arrivals; zero between launches
     long long seq_stride;    // floats
     long long layer_stride;  // floats = n_ctx * kv_dim
     int n_seq;
@@ -38,7 +39,7 @@ struct DecodeParams {
     int n_head_kv;
     int gqa;
     int split_len;     // positions per split, multiple of kDecodeTile
-    int max_splits;    // split stride in part_o / part_ml
+    int max_splits;    // split stride in `part`
     int total_splits;  // split_prefix[n_seq]
     int rotate;
     float scale_log2;  // log2(e) / sqrt(head_dim)

@@ -76,11 +76,13 @@ class DecodeCase:
     later are zero (the new token is appended at pos).
     """
 
-    def __init__(self, n_seq, n_layers, n_ctx, pos, q, k, v, kc, vc):
+    def __init__(self, n_seq, n_layers, n_ctx, pos, q, k, v, kc, vc, n_head=N_HEAD,
+                 n_head_kv=N_HEAD_KV):
         self.n_seq, self.n_layers, self.n_ctx = n_seq, n_layers, n_ctx
+        self.n_head, self.n_head_kv = n_head, n_head_kv
         self.pos = np.asarray(pos, np.int32)
         self.q, self.k, self.v = q, k, v   # [n_seq, n_layers, heads*64]
-        self.kc, self.vc = kc, vc          # [n_seq, n_layers, n_ctx, 256]
+        self.kc, self.vc = kc, vc          # [n_seq, n_layers, n_ctx, kv heads*64]
 
     @property
     def algorithmic_bytes(self) -> int:
@@ -89,25 +91,26 @@ class DecodeCase:
 
 def make_decode(workload: str | int, n_seq: int, n_layers: int, n_ctx: int, pos,
                 kv_std: float = 1.0, peaked_frac: float = 0.0, peaked_scale: float = 8.0,
-                salt: int = 0) -> DecodeCase:
+                salt: int = 0, n_head: int = N_HEAD, n_head_kv: int = N_HEAD_KV) -> DecodeCase:
     g = rng(workload, salt)
+    q_dim, kv_dim = n_head * HEAD_DIM, n_head_kv * HEAD_DIM
     pos = np.broadcast_to(np.asarray(pos, np.int32), (n_seq,)).copy()
-    q = normal(g, (n_seq, n_layers, Q_DIM))
-    k = normal(g, (n_seq, n_layers, KV_DIM))
-    v = normal(g, (n_seq, n_layers, KV_DIM))
-    kc = np.zeros((n_seq, n_layers, n_ctx, KV_DIM), np.float32)
+    q = normal(g, (n_seq, n_layers, q_dim))
+    k = normal(g, (n_seq, n_layers, kv_dim))
+    v = normal(g, (n_seq, n_layers, kv_dim))
+    kc = np.zeros((n_seq, n_layers, n_ctx, kv_dim), np.float32)
     vc = np.zeros_like(kc)
     for s in range(n_seq):
         n = int(pos[s])
         if n == 0:
             continue
-        kc[s, :, :n] = normal(g, (n_layers, n, KV_DIM), kv_std)
-        vc[s, :, :n] = normal(g, (n_layers, n, KV_DIM), kv_std)
+        kc[s, :, :n] = normal(g, (n_layers, n, kv_dim), kv_std)
+        vc[s, :, :n] = normal(g, (n_layers, n, kv_dim), kv_std)
         if peaked_frac > 0:
-            rows = kc[s, :, :n].reshape(n_layers, n, N_HEAD_KV, HEAD_DIM)
-            hit = g.random((n_layers, n, N_HEAD_KV)) < peaked_frac
+            rows = kc[s, :, :n].reshape(n_layers, n, n_head_kv, HEAD_DIM)
+            hit = g.random((n_layers, n, n_head_kv)) < peaked_frac
             rows[hit] *= np.float32(peaked_scale)
-    return DecodeCase(n_seq, n_layers, n_ctx, pos, q, k, v, kc, vc)
+    return DecodeCase(n_seq, n_layers, n_ctx, pos, q, k, v, kc, vc, n_head, n_head_kv)
 
 
 def decode_single() -> DecodeCase:
@@ -136,18 +139,20 @@ def decode_long(n_seq: int = 8, n_layers: int = 22, n_ctx: int = 16384) -> Decod
 # ---- prefill inputs -------------------------------------------------------------
 
 class PrefillCase:
-    def __init__(self, n_layers, n_tok, pos0, q, k, v):
+    def __init__(self, n_layers, n_tok, pos0, q, k, v, n_head=N_HEAD, n_head_kv=N_HEAD_KV):
         self.n_layers, self.n_tok, self.pos0 = n_layers, n_tok, pos0
+        self.n_head, self.n_head_kv = n_head, n_head_kv
         self.q, self.k, self.v = q, k, v   # [n_layers, n_tok, dim]
 
     @property
     def algorithmic_flops(self) -> int:
-        return prefill_flops(self.n_tok, pos0=self.pos0) * self.n_layers
+        return prefill_flops(self.n_tok, n_head=self.n_head, pos0=self.pos0) * self.n_layers
 
 
-def make_prefill(n_layers: int = 22, n_tok: int = 512, pos0: int = 0, salt: int = 0) -> PrefillCase:
+def make_prefill(n_layers: int = 22, n_tok: int = 512, pos0: int = 0, salt: int = 0,
+                 n_head: int = N_HEAD, n_head_kv: int = N_HEAD_KV) -> PrefillCase:
     g = rng("prefill", salt)
-    q = normal(g, (n_layers, n_tok, Q_DIM))
-    k = normal(g, (n_layers, n_tok, KV_DIM))
-    v = normal(g, (n_layers, n_tok, KV_DIM))
-    return PrefillCase(n_layers, n_tok, pos0, q, k, v)
+    q = normal(g, (n_layers, n_tok, n_head * HEAD_DIM))
+    k = normal(g, (n_layers, n_tok, n_head_kv * HEAD_DIM))
+    v = normal(g, (n_layers, n_tok, n_head_kv * HEAD_DIM))
+    return PrefillCase(n_layers, n_tok, pos0, q, k, v, n_head, n_head_kv)
