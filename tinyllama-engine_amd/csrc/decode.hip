@@ -8,13 +8,14 @@
 //
 // Work decomposition.  A "unit" is one (sequence, layer).  Its positions
 // 0..pos are cut into splits of split_len positions.  One workgroup = one
-// (unit, split) and holds 4 waves, one per kv head, so a workgroup streams
-// whole 1 KiB position rows of K and of V.  Each wave keeps the gqa (= 8)
-// q heads of its kv head in registers and walks its split in tiles of 16
-// positions:
+// (unit, split, group of 4 kv heads) and holds 8 waves: two per kv head,
+// which interleave the split's tiles of 16 positions (wave `sub` takes
+// tiles sub, sub + 2, ...).  The workgroup thus streams whole 1 KiB position
+// rows of K and of V.  Each wave keeps the gqa (<= 16) q heads of its kv
+// head in registers and, per tile:
 //
 //   S^T[16 pos][16 heads] = K[16 pos][64] . Q^T[64][16 heads]
-//                           16 x v_mfma_f32_16x16x4f32, heads 8..15 zero
+//                           16 x v_mfma_f32_16x16x4f32, heads gqa..15 zero
 //   online softmax per head (running max in log2 units, running sum)
 //   O^T[64 d][16 heads]  += V^T[64 d][16 pos] . P^T[16 pos][16 heads]
 //                           16 x v_mfma_f32_16x16x4f32
@@ -24,18 +25,22 @@
 // is directly the B operand of the P.V products, and K and V are loaded
 // from HBM straight into A-operand registers with 16-byte loads.  Each
 // lane loads 64 B of a K row and 4 x 16 B of V rows per tile; a wave's
-// loads cover 16 full 256 B head rows of K and of V.  No LDS is needed.
-// The next tile's loads are issued before the current tile is computed.
+// loads cover 16 full 256 B head rows of K and of V.  No LDS staging is
+// needed.  Two tiles are in flight per wave: the next tile's loads are
+// issued before the current tile is computed, and q and the first two
+// tiles are requested together at the start.
 //
 // The split that contains `pos` also appends the new token: it writes the
 // (rotated) k row and the v row to the cache, and uses the same register
 // values for position `pos` in its own tile, so it never reads back the
 // row it has just written.
 //
-// Merge.  With one split, the wave writes `out` directly.  With several,
-// each split writes its unnormalised O and (running max, sum) to the
-// workspace, then bumps the unit's arrival counter; the workgroup that
-// arrives last merges all splits of the unit with log-sum-exp weights and
+// Merge.  The two waves of a kv head combine in LDS.  With one split, the
+// result goes to `out` directly.  With several, each split writes its
+// unnormalised O and (running max, sum) to the workspace, waits for the
+// stores, then bumps the arrival counter of its (unit, kv head group); the
+// workgroup that arrives last merges all splits of the unit with
+// log-sum-exp weights, in split order (its own partial from LDS), and
 // resets the counter to zero for the next launch.  One launch per step.
 #include "rope_math.h"
 #include "tla_internal.h"
@@ -224,7 +229,6 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
 {
     __shared__ int s_last;
     __shared__ float4 s_new[kKvWaves][32];  // appended k row (16 float4) | v row (16 float4)
-    __shared__ int s_claim[kKvWaves];       // next unclaimed tile, per kv head
     __shared__ HalfExchange s_half;
     __shared__ HalfExchange s_mine;  // this split's partial, for the merge
     const int lane = threadIdx.x & 63;
@@ -251,10 +255,9 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     const int layer = p.layer0 + lb;
 
     // The split's positions [begin, end) are cut into tiles of 16.  The two
-    // waves of a kv head share them: each starts on tiles sub and 2 + sub,
-    // then claims the next unprocessed tile from a counter in LDS, so the
-    // wave that the SIMD serves first takes more tiles and both finish
-    // together.
+    // waves of a kv head interleave them, wave `sub` taking tiles sub,
+    // sub + 2, sub + 4, ...: a fixed assignment, so results do not depend
+    // on timing.
     const int begin = split * p.split_len;
     const int end = min(pos + 1, begin + p.split_len);  // exclusive
     const int n_tiles = (end - begin + kDecodeTile - 1) / kDecodeTile;
@@ -288,7 +291,6 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
         s_new[slot][lane] = kx;
         s_new[slot][16 + lane] = vx;
     }
-    if (threadIdx.x < kKvWaves) s_claim[threadIdx.x] = kSub * 2;  // tiles 0..3 are pre-assigned
     __syncthreads();
 
     floatx4 o[4];
@@ -395,20 +397,13 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
             if (tile == special) substitute(tl, tile);  // uniform branch
             step(tl, tile);
         };
-        // Claims are wave-uniform: lane 0 bumps the counter, every lane
-        // reads lane 0's value.
-        auto claim = [&]() {
-            int c = 0;
-            if (lane == 0) c = atomicAdd(&s_claim[slot], 1);
-            return __builtin_amdgcn_readfirstlane(c);
-        };
 
         // Two tiles in flight: while one is computed the other is loading.
-        // Claims only grow, so once the older of the two is past the end,
-        // so is every later one.  Loads are unconditional, so that the
-        // count of loads in flight is the same on every path and waiting
-        // for one tile never waits for the other: a claim past the end
-        // reloads a tile already loaded (a cache hit) and is not used.
+        // Loads are unconditional, so that the count of loads in flight is
+        // the same on every path and waiting for one tile never waits for
+        // the other: a tile index past the end reloads a tile already
+        // loaded (a cache hit) and is not used.
+        constexpr int kStride = 2 * kSub;  // tiles between a wave's ta and its next ta
         int ca = sub, cb = kSub + sub;
         Tile ta, tb;
         load_tile(min(ca, n_tiles - 1), ta);
@@ -424,10 +419,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
         }
         do {
             if (ca < n_tiles) process(ta, ca);  // uniform branches: the loads stay outside
-            const int na = claim();
+            const int na = ca + kStride;
             load_tile(na < n_tiles ? na : min(ca, n_tiles - 1), ta);
             if (cb < n_tiles) process(tb, cb);
-            const int nb = claim();
+            const int nb = cb + kStride;
             load_tile(nb < n_tiles ? nb : min(cb, n_tiles - 1), tb);
             ca = na;
             cb = nb;
