@@ -208,9 +208,10 @@ float scale_log2(int head_dim)
 
 // Positions per split-KV chunk.  Measured on MI355X: splits long enough that
 // about 240 workgroups (one per CU) cover the whole batch, between 64 and
-// 2048 positions -- short splits multiply the partials the merge must read
-// back, long ones leave CUs idle on small batches -- and at most half the
-// longest sequence, so ragged batches spread their long sequences.
+// 4096 positions -- short splits multiply the partials the merge must read
+// back and each workgroup's fixed start and merge costs, long ones leave CUs
+// idle on small batches -- and at most half the longest sequence, so ragged
+// batches spread their long sequences.
 int plan_split(long long total_positions, int max_len, long long opt)
 {
     if (opt > 0) {
@@ -220,7 +221,7 @@ int plan_split(long long total_positions, int max_len, long long opt)
     long long s = (total_positions + 239) / 240;
     s = std::min<long long>(s, (max_len + 1) / 2);
     s = (s + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
-    return static_cast<int>(std::min<long long>(std::max<long long>(s, 64), 2048));
+    return static_cast<int>(std::min<long long>(std::max<long long>(s, 64), 4096));
 }
 
 }  // namespace
