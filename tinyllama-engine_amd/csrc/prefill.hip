@@ -14,7 +14,8 @@
 // prefill_attention_kernel: one workgroup = 4 waves = 4 q heads of one kv
 //   head, over one tile of 32 query tokens.  Each wave:
 //     S^T[32 keys][32 queries] = K[32][64] . Q^T[64][32]   32 x mfma_f32_32x32x2f32
-//     causal mask, online softmax per query row
+//     causal mask, online softmax per query row (the running max moves
+//       only when it grows by more than 2^8, so most tiles skip rescaling O)
 //     O^T[64 d][32 queries]   += V^T[64][32] . P^T[32][32] 32 x mfma_f32_32x32x2f32
 //   The S accumulator layout (lane l: query l%32, keys 8*(g/4)+4*(l/32)+g%4)
 //   is the B operand of the P.V product as is, so P never leaves registers.
@@ -72,6 +73,7 @@ struct PrefillGrid {
     int per_xcd;  // workgroup slots per XCD: ceil(n_pairs / 8) * n_hg * n_qt
 };
 
+constexpr float kRescaleSlack = 8.f;  // log2 units
 constexpr int kRowPad = 68;  // LDS row stride (floats): 64 + 4 keeps operand reads conflict-free
 
 __global__ __launch_bounds__(64 * kWavesP) __attribute__((amdgpu_waves_per_eu(3, 3))) void
@@ -193,18 +195,25 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
 #pragma unroll
         for (int gi = 1; gi < 16; ++gi) mx = fmaxf(mx, s[gi]);
         mx = fmaxf(mx, __shfl_xor(mx, 32));
-        const float m_new = fmaxf(m_run, mx);
-        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-        m_run = m_new;
+        // The running max only moves when some row's tile max exceeds it by
+        // more than 2^8: probabilities then stay <= 256 and the sums in fp32
+        // range, and most tiles skip the rescale of O.  The result is the
+        // same softmax: O and l share whatever max they were scaled by.
+        if (__any(mx > m_run + kRescaleSlack)) {
+            const float m_new = fmaxf(m_run, mx);
+            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
+            m_run = m_new;
+            l_run *= alpha;
+            o0 *= alpha;
+            o1 *= alpha;
+        }
         float lsum = 0.f;
 #pragma unroll
         for (int gi = 0; gi < 16; ++gi) {
-            s[gi] = __builtin_amdgcn_exp2f(s[gi] - m_new);
+            s[gi] = __builtin_amdgcn_exp2f(s[gi] - m_run);
             lsum += s[gi];
         }
-        l_run = l_run * alpha + lsum;
-        o0 *= alpha;
-        o1 *= alpha;
+        l_run += lsum;
     };
     // O^T += V^T.P^T for the tile in V buffer b (V operand: lane holds
     // V[8*(gi/4) + 4*half + gi%4][2*col + dt]).
