@@ -22,8 +22,10 @@ the 256 MB Infinity Cache, steps rotate over 5 copies of the whole cache
 
 Other workloads (--workload): decode_long (16384 context, batch 8, 22 layers),
 decode_ragged (64 sequences, L in [256, 2048], 22 layers), prefill,
-decode_single (one layer, position 127: reported as latency), and copy (the
-device copy kernel, used to calibrate rocprofv3 byte counters).
+decode_single (one layer, position 127: reported as latency), copy (the
+device copy kernel, used to calibrate rocprofv3 byte counters) and read (a
+plain library reduction over 6 GiB: what HBM delivers to a read stream, the
+practical ceiling the decode figures sit under).
 """
 from __future__ import annotations
 
@@ -313,6 +315,27 @@ def run_copy(steps, warmup, nbytes=1 << 30):
             "value": 2 * nbytes / (ms * 1e-3) / 1e9}
 
 
+def run_read(steps, warmup, nbytes=6 << 30):
+    """HBM read ceiling: torch's sum over an nbytes float32 tensor (a library
+    streaming reduction, nothing of this build), timed with events on torch's
+    current stream, which is where it runs."""
+    import torch
+    x = torch.ones(nbytes // 4, dtype=torch.float32, device="cuda")
+    for _ in range(warmup):
+        x.sum()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(steps):
+        x.sum()
+    b.record()
+    b.synchronize()
+    ms = a.elapsed_time(b) / steps
+    log(f"[bench] read {nbytes >> 20} MiB (torch sum): {ms * 1e3:.1f} us, {nbytes / ms / 1e6:.0f} GB/s")
+    del x
+    return {"workload": "read", "bytes_read": nbytes, "ms": ms, "value": nbytes / (ms * 1e-3) / 1e9}
+
+
 # -------------------------------------------------------------------- main --
 
 def main():
@@ -322,7 +345,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode_model",
                     choices=["decode_model", "decode_long", "decode_ragged", "decode_single",
-                             "prefill", "copy"])
+                             "prefill", "copy", "read"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill half")
     ap.add_argument("--split", type=int, default=0, help="decode split length (0 = auto)")
@@ -338,6 +361,9 @@ def main():
 
     if args.workload == "copy":
         print(json.dumps(run_copy(args.steps, args.warmup)))
+        return
+    if args.workload == "read":
+        print(json.dumps(run_read(args.steps, args.warmup)))
         return
     if args.workload == "prefill":
         p = run_prefill(args.steps, args.warmup, cpu)
