@@ -239,18 +239,20 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     const int kvh = blockIdx.y * kKvWaves + slot;
     const bool active = kvh < p.n_head_kv;  // uniform per wave
 
-    // blockIdx.x -> (layer step lb, sequence, split)
-    const int lb = blockIdx.x / p.total_splits;
-    const int rem = blockIdx.x - lb * p.total_splits;
+    // blockIdx.x -> (sequence rank, split, layer step lb), layers innermost.
+    // Ranks run longest sequence first, so workgroups start roughly longest
+    // first and the last ones to start are short.
+    const int lb = blockIdx.x % p.n_lb;
+    const int rem = blockIdx.x / p.n_lb;
     int lo = 0, hi = p.n_seq - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
         if (b.split_prefix[mid] <= rem) lo = mid; else hi = mid - 1;
     }
-    const int seq = lo;
-    const int split = rem - b.split_prefix[seq];
-    const int nsplit = b.split_prefix[seq + 1] - b.split_prefix[seq];
-    const int pos = b.pos[seq];
+    const int split = rem - b.split_prefix[lo];
+    const int nsplit = b.split_prefix[lo + 1] - b.split_prefix[lo];
+    const int pos = b.pos[lo];
+    const int seq = b.seq_id[lo];
     const int unit = seq * p.n_lb + lb;
     const int layer = p.layer0 + lb;
 
@@ -512,7 +514,10 @@ hipError_t launch_decode(const DecodeParams& p, const DecodeSeqs<kMaxSeqPerLaunc
     dim3 grid(p.total_splits * p.n_lb, (p.n_head_kv + kKvWaves - 1) / kKvWaves);
     if (p.n_seq <= 8) {
         DecodeSeqs<8> small{};
-        for (int i = 0; i < p.n_seq; ++i) small.pos[i] = seqs.pos[i];
+        for (int i = 0; i < p.n_seq; ++i) {
+            small.pos[i] = seqs.pos[i];
+            small.seq_id[i] = seqs.seq_id[i];
+        }
         for (int i = 0; i <= p.n_seq; ++i) small.split_prefix[i] = seqs.split_prefix[i];
         hipLaunchKernelGGL(decode_split_kernel<8>, grid, dim3(64 * kWaves), 0, s, p, small);
     } else {

@@ -469,16 +469,21 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
         const int pos = pos_host[s];
         if (pos < 0 || pos >= c.n_ctx)
             return fail(TLA_ERR_OUT_OF_RANGE, "pos[%d] = %d outside [0, n_ctx=%d)", s, pos, c.n_ctx);
-        seqs.pos[s] = pos;
+        seqs.seq_id[s] = s;
         total_positions += static_cast<long long>(pos + 1) * n_step_layers;
         max_len = std::max(max_len, pos + 1);
     }
+    // Longest sequences first (ties in caller order): their workgroups start
+    // first, so the last round of workgroups is the shortest.
+    std::stable_sort(seqs.seq_id, seqs.seq_id + n_seq,
+                     [&](int a, int b) { return pos_host[a] > pos_host[b]; });
+    for (int r = 0; r < n_seq; ++r) seqs.pos[r] = pos_host[seqs.seq_id[r]];
     const int split_len = plan_split(total_positions, max_len, e->opt_split);
     seqs.split_prefix[0] = 0;
     int max_splits = 1;
-    for (int s = 0; s < n_seq; ++s) {
-        const int ns = (seqs.pos[s] + 1 + split_len - 1) / split_len;
-        seqs.split_prefix[s + 1] = seqs.split_prefix[s] + ns;
+    for (int r = 0; r < n_seq; ++r) {
+        const int ns = (seqs.pos[r] + 1 + split_len - 1) / split_len;
+        seqs.split_prefix[r + 1] = seqs.split_prefix[r] + ns;
         max_splits = std::max(max_splits, ns);
     }
     if (static_cast<long long>(seqs.split_prefix[n_seq]) * n_step_layers > 0x7fffffffLL)

@@ -46,13 +46,15 @@ struct DecodeParams {
 };
 
 // Per-sequence positions and split offsets of one launch, passed by value in
-// the kernel arguments.  The kernel is instantiated for up to 8 and up to
-// 256 sequences so small batches do not pay for a 2 KiB argument block
-// (about 1 us per launch).
+// the kernel arguments.  Sequences appear by rank, longest first; seq_id maps
+// a rank to the caller's sequence index.  The kernel is instantiated for up
+// to 8 and up to 256 sequences so small batches do not pay for a 3 KiB
+// argument block (about 1 us per launch).
 template <int kMaxSeq>
 struct DecodeSeqs {
-    int pos[kMaxSeq];
-    int split_prefix[kMaxSeq + 1];  // cumulative splits per sequence
+    int pos[kMaxSeq];               // by rank
+    int seq_id[kMaxSeq];            // rank -> sequence index
+    int split_prefix[kMaxSeq + 1];  // cumulative splits, by rank
 };
 
 hipError_t launch_decode(const DecodeParams& p, const DecodeSeqs<kMaxSeqPerLaunch>& seqs,
