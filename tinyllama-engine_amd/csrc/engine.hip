@@ -210,8 +210,9 @@ float scale_log2(int head_dim)
 // about 240 workgroups (one per CU) cover the whole batch, between 64 and
 // 4096 positions -- short splits multiply the partials the merge must read
 // back and each workgroup's fixed start and merge costs, long ones leave CUs
-// idle on small batches -- and at most half the longest sequence, so ragged
-// batches spread their long sequences.
+// idle on small batches.  A batch big enough for several rounds of
+// workgroups takes whole sequences (up to 4096 positions) per workgroup:
+// sequences are dispatched longest first, so the last round is short.
 int plan_split(long long total_positions, int max_len, long long opt)
 {
     if (opt > 0) {
@@ -219,7 +220,7 @@ int plan_split(long long total_positions, int max_len, long long opt)
         return static_cast<int>(std::min<long long>(std::max<long long>(s, kDecodeTile), 1 << 24));
     }
     long long s = (total_positions + 239) / 240;
-    s = std::min<long long>(s, (max_len + 1) / 2);
+    s = std::min<long long>(s, max_len);
     s = (s + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
     return static_cast<int>(std::min<long long>(std::max<long long>(s, 64), 4096));
 }
