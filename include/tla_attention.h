@@ -155,13 +155,59 @@ int tla_prefill(tla_engine* e, int pos0, int n_tok, int layer0, int n_step_layer
                 float* out_dev, const float* q_dev, const float* k_dev, const float* v_dev,
                 float* key_cache_dev, float* value_cache_dev);
 
+/* ---- projections either side of the attention block ------------------ */
+
+/* Weight formats: the reference's ggml_type ids (src/gguf.h:23-32) and block
+ * layouts (src/gguf.h:56-135).  Weights are row-major [rows][cols] in the
+ * GGUF byte layout, on the device, 16-byte aligned. */
+enum tla_weight_type {
+    TLA_W_F32 = 0,
+    TLA_W_F16 = 1,
+    TLA_W_Q4_0 = 2,
+    TLA_W_Q8_0 = 8,
+    TLA_W_Q6_K = 14
+};
+
+/* matmul() src/ops.h:64-66: out[rows] = W[rows][cols] . x[cols], device
+ * pointers.  cols must be a multiple of 64 (of 256 for Q6_K) and at most
+ * 15360 (x is staged in 60 KiB of LDS); other shapes return
+ * TLA_ERR_UNSUPPORTED.  fp32 accumulation; equal
+ * to the reference to fp32 rounding (the sums are grouped differently). */
+int tla_matmul(tla_engine* e, float* out_dev, const void* w_dev, const float* x_dev, int rows,
+               int cols, int type);
+
+/* rmsnorm() src/ops.h:95-96: out = x / sqrt(mean(x^2) + eps) * weight. */
+int tla_rmsnorm(tla_engine* e, float* out_dev, const float* x_dev, const float* weight_dev,
+                int size, float eps);
+
+/* vec_add() src/ops.h:143: out[i] += x[i]. */
+int tla_vec_add(tla_engine* e, float* out_dev, const float* x_dev, int size);
+
+/* The input half of the attention block for n_seq sequences
+ * (src/forward.cpp:180-190): xb = rmsnorm(x, norm_w, eps) (skipped when
+ * norm_w is NULL), q = Wq.xb, k = Wk.xb, v = Wv.xb, in one launch per 8
+ * sequences (fewer when 8 x n_embd floats exceed 60 KiB).  x, q [n_seq][n_embd];
+ * k, v [n_seq][kv_dim]; Wq [n_embd][n_embd],
+ * Wk, Wv [kv_dim][n_embd], all of one type.  q and k leave unrotated, ready
+ * for tla_decode with TLA_ROTATE (RoPE and the cache append are its
+ * prologue). */
+int tla_attn_qkv(tla_engine* e, int n_seq, float* q_dev, float* k_dev, float* v_dev,
+                 const float* x_dev, const float* norm_w_dev, float eps, const void* wq_dev,
+                 const void* wk_dev, const void* wv_dev, int type);
+
+/* The output half (src/forward.cpp:210-213): x += Wo . xb2 for n_seq
+ * sequences, x and xb2 [n_seq][n_embd], Wo [n_embd][n_embd]. */
+int tla_attn_out(tla_engine* e, int n_seq, float* x_dev, const void* wo_dev,
+                 const float* xb2_dev, int type);
+
 /* ---- measurement hooks (no reference counterpart) ------------------- */
 enum tla_kernel_id {
     TLA_KERNEL_DECODE = 0,  /* split-KV decode attention: RoPE + append +
                                attention + split merge, one launch           */
     TLA_KERNEL_PREFILL = 1, /* causal MFMA prefill attention                 */
     TLA_KERNEL_APPEND = 2,  /* prefill RoPE + cache append                   */
-    TLA_KERNEL_COUNT = 3
+    TLA_KERNEL_GEMV = 3,    /* projections: matmul / attn_qkv / attn_out     */
+    TLA_KERNEL_COUNT = 4
 };
 /* When enabled, HIP events bracket every launch of each kernel on the
  * engine's stream; tla_profile_read sums their durations (ms) since the

@@ -77,6 +77,14 @@ def oracle() -> C.CDLL:
                                                C.c_size_t, _ip, C.c_int, C.c_int, C.c_int,
                                                C.c_int, C.c_float, C.c_int]
         lib.oracle_decode_units_mt.restype = C.c_int
+        lib.oracle_fp16_to_f32.argtypes = [C.c_uint16]
+        lib.oracle_fp16_to_f32.restype = C.c_float
+        lib.oracle_row_bytes.argtypes = [C.c_int, C.c_int]
+        lib.oracle_row_bytes.restype = C.c_longlong
+        lib.oracle_matmul.argtypes = [_fp, C.c_void_p, _fp, C.c_int, C.c_int, C.c_int]
+        lib.oracle_matmul.restype = C.c_int
+        lib.oracle_rmsnorm.argtypes = [_fp, _fp, _fp, C.c_int, C.c_float]
+        lib.oracle_vec_add.argtypes = [_fp, _fp, C.c_int]
         _oracle = lib
     return _oracle
 
@@ -100,6 +108,11 @@ def ref() -> C.CDLL:
                                             C.c_size_t, _ip, C.c_int, C.c_int, C.c_int,
                                             C.c_int, C.c_float, C.c_int]
         lib.ref_decode_units_mt.restype = C.c_int
+        lib.ref_matmul.argtypes = [_fp, C.c_void_p, _fp, C.c_int, C.c_int, C.c_int]
+        lib.ref_rmsnorm.argtypes = [_fp, _fp, _fp, C.c_int, C.c_float]
+        lib.ref_vec_add.argtypes = [_fp, _fp, C.c_int]
+        lib.ref_fp16_to_f32.argtypes = [C.c_uint16]
+        lib.ref_fp16_to_f32.restype = C.c_float
         _ref = lib
     return _ref
 
@@ -195,4 +208,44 @@ def decode_units_mt(n_threads, q, k, v, kc, vc, pos, s: Shape, rotate=True, lib=
             s.freq_base, int(rotate))
     rc = (oracle().oracle_decode_units_mt if lib is None else lib.ref_decode_units_mt)(*args)
     assert rc == 0
+    return out
+
+
+# ---- projections either side of the attention block -----------------------
+# Weight type ids are the reference's ggml_type values (src/gguf.h:23-32).
+F32, F16, Q4_0, Q8_0, Q6_K = 0, 1, 2, 8, 14
+BLOCK = {F32: 1, F16: 1, Q4_0: 32, Q8_0: 32, Q6_K: 256}
+
+
+def row_bytes(wtype: int, cols: int) -> int:
+    return int(oracle().oracle_row_bytes(wtype, cols))
+
+
+def matmul(W: np.ndarray, x: np.ndarray, rows: int, cols: int, wtype: int, lib=None) -> np.ndarray:
+    """out[rows] = W . x with W the raw bytes (uint8) of a [rows][cols] matrix
+    of type wtype; lib=ref() runs the reference's own matmul()."""
+    W = np.ascontiguousarray(W, dtype=np.uint8)
+    assert W.size == rows * row_bytes(wtype, cols)
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(rows, np.float32)
+    if lib is None:
+        assert oracle().oracle_matmul(fptr(out), W.ctypes.data, fptr(x), rows, cols, wtype) == 0
+    else:
+        lib.ref_matmul(fptr(out), W.ctypes.data, fptr(x), rows, cols, wtype)
+    return out
+
+
+def rmsnorm(x: np.ndarray, w: np.ndarray, eps: float, lib=None) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    out = np.zeros_like(x)
+    (oracle().oracle_rmsnorm if lib is None else lib.ref_rmsnorm)(fptr(out), fptr(x), fptr(w),
+                                                                   x.size, eps)
+    return out
+
+
+def vec_add(out: np.ndarray, x: np.ndarray, lib=None) -> np.ndarray:
+    out = np.ascontiguousarray(out, dtype=np.float32).copy()
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    (oracle().oracle_vec_add if lib is None else lib.ref_vec_add)(fptr(out), fptr(x), out.size)
     return out

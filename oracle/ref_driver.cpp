@@ -11,6 +11,10 @@
 //   ref_decode_units_mt -> rope()+attention() per (sequence, layer) unit, one
 //                     std::thread per contiguous chunk of units, the pattern of
 //                     parallel_for (src/ops.cpp:67-110).
+//   ref_matmul     -> matmul()     src/ops.h:64 (type = ggml_type id)
+//   ref_rmsnorm    -> rmsnorm()    src/ops.h:95
+//   ref_vec_add    -> vec_add()    src/ops.h:143
+//   ref_fp16_to_f32 -> fp16_to_f32() src/ops.h:39
 #include <cstddef>
 #include <cstring>
 #include <thread>
@@ -76,5 +80,19 @@ int ref_decode_units_mt(int n_threads, int n_units, float* out, const float* q,
     for (auto& th : pool) th.join();
     return 0;
 }
+
+void ref_matmul(float* out, const void* W, const float* x, int rows, int cols, int type)
+{
+    matmul(out, W, x, rows, cols, static_cast<ggml_type>(type));
+}
+
+void ref_rmsnorm(float* out, const float* x, const float* weight, int size, float eps)
+{
+    rmsnorm(out, x, weight, size, eps);
+}
+
+void ref_vec_add(float* out, const float* x, int size) { vec_add(out, x, size); }
+
+float ref_fp16_to_f32(unsigned short h) { return fp16_to_f32(h); }
 
 }  // extern "C"

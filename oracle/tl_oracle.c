@@ -16,6 +16,12 @@
  *                        src/ops.cpp:1329/1383, scale src/ops.cpp:1335
  *   oracle_prefill    <- the token-by-token prompt loop src/generate.cpp:56-59
  *                        restricted to the attention block src/forward.cpp:192-208
+ *   oracle_fp16_to_f32 <- src/ops.cpp:119-156
+ *   oracle_matmul     <- matmul() src/ops.cpp:959-983 and the naive branches of
+ *                        matmul_f32/f16/q8_0/q4_0/q6_k src/ops.cpp:178-957;
+ *                        block layouts src/gguf.h:56-135
+ *   oracle_rmsnorm    <- src/ops.cpp:1003-1055 (naive branch)
+ *   oracle_vec_add    <- src/ops.cpp:1165-1184 (naive branch)
  *
  * Float semantics: every product and sum is rounded separately, as the
  * reference's x86-64 -O2 build does (no FMA in the baseline ISA).  Build with
@@ -52,6 +58,9 @@ enum {
     FAULT_SKIP_LAST = 4,       /* attend over 0..pos-1 (off by one)           */
     FAULT_ROPE_PAIR_HALF = 5,  /* rotate (i, i+hd/2) halves, not (2i, 2i+1)   */
     FAULT_SOFTMAX_NO_MAX = 6,  /* skip the max subtraction                    */
+    FAULT_Q4_NIBBLE_ORDER = 7, /* low nibble -> element 2j, high -> 2j+1      */
+    FAULT_Q6K_QH_SHIFT = 8,    /* upper 2 bits taken from the wrong qh pair   */
+    FAULT_RMS_NO_MEAN = 9,     /* sum of squares not divided by size          */
 };
 
 /* ---- rope: src/ops.cpp:1223-1281 ------------------------------------- */
@@ -280,4 +289,148 @@ int oracle_decode_units_mt(int n_threads, int n_units, float* out, const float* 
     decode_worker(&jobs[0]);
     for (int t = 1; t < n_threads; ++t) pthread_join(tid[t], NULL);
     return 0;
+}
+
+
+/* ---- weights: src/gguf.h:23-32 (type ids), 56-135 (block layouts) ------ */
+enum { T_F32 = 0, T_F16 = 1, T_Q4_0 = 2, T_Q8_0 = 8, T_Q6_K = 14 };
+
+/* src/ops.cpp:119-156: exact widening of an IEEE half (subnormals normalised,
+ * NaN made quiet). */
+float oracle_fp16_to_f32(uint16_t h)
+{
+    const uint32_t sign = ((uint32_t)h & 0x8000u) << 16;
+    uint32_t e = ((uint32_t)h >> 10) & 0x1Fu;
+    uint32_t m = (uint32_t)h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0) {
+        if (m == 0) {
+            bits = sign;
+        } else {
+            int ex = -14;
+            while ((m & 0x400u) == 0) { m <<= 1; --ex; }
+            bits = sign | ((uint32_t)(ex + 127) << 23) | ((m & 0x3FFu) << 13);
+        }
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13) | (m ? 0x00400000u : 0u);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+static uint16_t rd16(const uint8_t* p) { return (uint16_t)(p[0] | (p[1] << 8)); }
+
+/* One output row of the reference's naive matmul for each type: a single fp32
+ * accumulator over the row in the reference's order.  Q8_0 and Q4_0 sum each
+ * block of 32 first and add scale * block_sum; Q6_K adds every product
+ * d*scale*q*x to the row sum directly. */
+static float row_dot(const uint8_t* row, const float* x, int cols, int type)
+{
+    float sum = 0.0f;
+    if (type == T_F32) {
+        const float* w = (const float*)row;
+        for (int j = 0; j < cols; ++j) sum += w[j] * x[j];
+    } else if (type == T_F16) {
+        for (int j = 0; j < cols; ++j) sum += oracle_fp16_to_f32(rd16(row + 2 * j)) * x[j];
+    } else if (type == T_Q8_0) {
+        for (int b = 0; b < cols / 32; ++b) {
+            const uint8_t* blk = row + 34 * b;
+            const float scale = oracle_fp16_to_f32(rd16(blk));
+            const int8_t* qs = (const int8_t*)(blk + 2);
+            const float* xb = x + 32 * b;
+            float bs = 0.0f;
+            for (int j = 0; j < 32; ++j) bs += (float)qs[j] * xb[j];
+            sum += scale * bs;
+        }
+    } else if (type == T_Q4_0) {
+        for (int b = 0; b < cols / 32; ++b) {
+            const uint8_t* blk = row + 18 * b;
+            const float scale = oracle_fp16_to_f32(rd16(blk));
+            const uint8_t* qs = blk + 2;
+            const float* xb = x + 32 * b;
+            float bs = 0.0f;
+            for (int j = 0; j < 16; ++j) {
+                const int lo = (int)(qs[j] & 0x0F) - 8, hi = (int)(qs[j] >> 4) - 8;
+                if (g_fault == FAULT_Q4_NIBBLE_ORDER) {
+                    bs += (float)lo * xb[2 * j];
+                    bs += (float)hi * xb[2 * j + 1];
+                } else {
+                    bs += (float)lo * xb[j];
+                    bs += (float)hi * xb[j + 16];
+                }
+            }
+            sum += scale * bs;
+        }
+    } else if (type == T_Q6_K) {
+        /* super-block of 256: ql[128] qh[64] scales[16] d (210 bytes) */
+        for (int b = 0; b < cols / 256; ++b) {
+            const uint8_t* blk = row + 210 * b;
+            const uint8_t* ql0 = blk;
+            const uint8_t* qh0 = blk + 128;
+            const int8_t* sc0 = (const int8_t*)(blk + 192);
+            const float d = oracle_fp16_to_f32(rd16(blk + 208));
+            const float* xb = x + 256 * b;
+            for (int half = 0; half < 2; ++half) {
+                const uint8_t* ql = ql0 + 64 * half;
+                const uint8_t* qh = qh0 + 32 * half;
+                const int8_t* sc = sc0 + 8 * half;
+                const float* xh = xb + 128 * half;
+                for (int l = 0; l < 32; ++l) {
+                    const int is = l / 16;
+                    const int s2 = g_fault == FAULT_Q6K_QH_SHIFT ? 4 : 2;
+                    const int s4 = g_fault == FAULT_Q6K_QH_SHIFT ? 2 : 4;
+                    const int q1 = ((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                    const int q2 = ((ql[l + 32] & 0x0F) | (((qh[l] >> s2) & 3) << 4)) - 32;
+                    const int q3 = ((ql[l] >> 4) | (((qh[l] >> s4) & 3) << 4)) - 32;
+                    const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                    sum += d * (float)sc[is + 0] * (float)q1 * xh[l + 0];
+                    sum += d * (float)sc[is + 2] * (float)q2 * xh[l + 32];
+                    sum += d * (float)sc[is + 4] * (float)q3 * xh[l + 64];
+                    sum += d * (float)sc[is + 6] * (float)q4 * xh[l + 96];
+                }
+            }
+        }
+    }
+    return sum;
+}
+
+/* Bytes of one row of `cols` weights of `type`; 0 for an unknown type. */
+long long oracle_row_bytes(int type, int cols)
+{
+    switch (type) {
+    case T_F32: return 4LL * cols;
+    case T_F16: return 2LL * cols;
+    case T_Q8_0: return 34LL * (cols / 32);
+    case T_Q4_0: return 18LL * (cols / 32);
+    case T_Q6_K: return 210LL * (cols / 256);
+    default: return 0;
+    }
+}
+
+/* out[rows] = W[rows][cols] . x[cols]; returns -1 for an unknown type. */
+int oracle_matmul(float* out, const void* W, const float* x, int rows, int cols, int type)
+{
+    const long long rb = oracle_row_bytes(type, cols);
+    if (rb == 0) return -1;
+    for (int i = 0; i < rows; ++i) out[i] = row_dot((const uint8_t*)W + rb * i, x, cols, type);
+    return 0;
+}
+
+/* src/ops.cpp:1003-1055 naive branch. */
+void oracle_rmsnorm(float* out, const float* x, const float* weight, int size, float eps)
+{
+    float ss = 0.0f;
+    for (int i = 0; i < size; ++i) ss += x[i] * x[i];
+    const float ms = g_fault == FAULT_RMS_NO_MEAN ? ss : ss / (float)size;
+    const float rms = 1.0f / sqrtf(ms + eps);
+    for (int i = 0; i < size; ++i) out[i] = x[i] * rms * weight[i];
+}
+
+/* src/ops.cpp:1165-1184 naive branch. */
+void oracle_vec_add(float* out, const float* x, int size)
+{
+    for (int i = 0; i < size; ++i) out[i] += x[i];
 }

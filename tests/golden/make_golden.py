@@ -8,7 +8,7 @@ sha256 of the inputs where not, and the reference's outputs) are what the
 tests compare the oracle and the GPU path with; nothing here runs on the GPU
 box.
 
-    python tests/golden/make_golden.py
+    python tests/golden/make_golden.py [section ...]   (default: all)
 """
 from __future__ import annotations
 
@@ -181,17 +181,43 @@ def prefill(R):
          kc=kcl, vc=vcl)
 
 
-def main():
+def projections(R):
+    """matmul() in every weight format (src/ops.cpp:959-983) on seeded
+    matrices whose raw bytes are stored, rmsnorm() (src/ops.cpp:1003-1055) and
+    fp16_to_f32() (src/ops.cpp:119-156) over all 65536 half patterns."""
+    arrays = {}
+    rg = np.random.default_rng(11)
+    for t in (W.W_F32, W.W_F16, W.W_Q4_0, W.W_Q8_0, W.W_Q6_K):
+        rows, cols = 6, 512
+        raw = W.make_weights(t, rows, cols, salt=2)
+        x = rg.standard_normal(cols).astype(np.float32)
+        name = W.W_NAMES[t]
+        arrays[f"{name}_w"] = raw
+        arrays[f"{name}_x"] = x
+        arrays[f"{name}_out"] = O.matmul(raw, x, rows, cols, t, lib=R)
+    for i, (n, eps) in enumerate(((2048, 1e-5), (7, 1e-6), (256, 0.0))):
+        x = (rg.standard_normal(n) * (1 + i)).astype(np.float32)
+        w = rg.uniform(0.5, 1.5, n).astype(np.float32)
+        arrays[f"rms{i}_x"], arrays[f"rms{i}_w"] = x, w
+        arrays[f"rms{i}_eps"] = np.float32(eps)
+        arrays[f"rms{i}_out"] = O.rmsnorm(x, w, eps, lib=R)
+    halves = np.arange(65536, dtype=np.uint32)
+    arrays["fp16_bits"] = np.array([np.float32(R.ref_fp16_to_f32(int(h))) for h in halves],
+                                   np.float32).view(np.uint32)
+    save("projections.npz", **arrays)
+
+
+SECTIONS = {"softmax": softmax_cases, "rope": rope_cases, "attention": testops_attention,
+            "decode_single": decode_single, "decode_peaked": decode_peaked,
+            "decode_ragged": decode_ragged, "prefill": prefill, "projections": projections}
+
+
+def main(names):
     O.build(with_ref=True)
     R = O.ref()
-    softmax_cases(R)
-    rope_cases(R)
-    testops_attention(R)
-    decode_single(R)
-    decode_peaked(R)
-    decode_ragged(R)
-    prefill(R)
+    for n in names or SECTIONS:
+        SECTIONS[n](R)
 
 
 if __name__ == "__main__":
-    main()
+    main(sys.argv[1:])

@@ -1,0 +1,210 @@
+"""GPU parity of the projections either side of the attention block, through
+the C ABI: matmul() in the five weight formats (src/ops.cpp:959-983),
+rmsnorm() (src/ops.cpp:1003-1055), vec_add() (src/ops.cpp:1165-1184), the
+fused input half (rmsnorm + Wq/Wk/Wv, src/forward.cpp:180-190) and output half
+(Wo + residual, src/forward.cpp:210-213), and the whole attention block of a
+layer on the device, token by token, against the oracle.
+
+Tolerance (fp32 accumulation in a different order than the reference's
+sequential loops): per output row, |gpu - fp64| <= 1e-5 * sum_j |w_ij x_j| and
+|gpu - oracle| <= 2e-5 * the same sum; rmsnorm within 1e-6 relative; vec_add
+bit-exact; the chained block within max(1e-4, 5e-6 * max|x|) of the oracle's
+chain, x being the residual stream."""
+import numpy as np
+import pytest
+
+import quant_ref as Q
+from helpers import bits, device_arrays, log
+
+pytestmark = pytest.mark.gpu
+
+TYPES = [(Q.F32, "f32"), (Q.F16, "f16"), (Q.Q4_0, "q4_0"), (Q.Q8_0, "q8_0"), (Q.Q6_K, "q6_k")]
+ROW_TOL, ORACLE_TOL = 1e-5, 2e-5
+# The residual stream of the chained block grows to |x| ~ 1e3 under random
+# weights; its error is bounded relative to that magnitude.
+CHAIN_REL_TOL = 5e-6
+
+
+def gpu_matmul(eng, raw, x, rows, cols, t):
+    with device_arrays() as track:
+        w = track(eng.array(np.ascontiguousarray(raw, np.uint8)))
+        xd = track(eng.array(np.ascontiguousarray(x, np.float32)))
+        out = track(eng.array((rows,)))
+        eng.matmul(out.ptr, w.ptr, xd.ptr, rows, cols, t)
+        return out.download()
+
+
+def check_rows(got, ora, raw, x, t, rows, cols, what):
+    ref, scale = Q.matmul_f64(raw, x, t, rows, cols)
+    scale = scale + 1e-30
+    e64 = float(np.max(np.abs(got - ref) / scale))
+    eor = float(np.max(np.abs(got - ora) / scale))
+    log(f"    {what}: |gpu-fp64|/sum|wx| {e64:.2e}, |gpu-oracle|/sum|wx| {eor:.2e}")
+    assert e64 <= ROW_TOL, what
+    assert eor <= ORACLE_TOL, what
+
+
+SHAPES = [(1, 64), (3, 128), (64, 512), (256, 2048), (2048, 2048), (300, 5632), (37, 4096)]
+
+
+@pytest.mark.parametrize("t,name", TYPES)
+@pytest.mark.parametrize("rows,cols", SHAPES)
+def test_matmul_parity(O, W, engines, t, name, rows, cols):
+    if t == Q.Q6_K and cols % 256:
+        pytest.skip("Q6_K rows are whole 256-weight super-blocks")
+    raw = W.make_weights(t, rows, cols, salt=rows + cols)
+    x = np.random.default_rng(rows * cols).standard_normal(cols).astype(np.float32)
+    log(f"  tla_matmul {name} {rows}x{cols}")
+    got = gpu_matmul(engines(1, 64), raw, x, rows, cols, t)
+    check_rows(got, O.matmul(raw, x, rows, cols, t), raw, x, t, rows, cols, f"{name} {rows}x{cols}")
+
+
+def pad64(raw, x, rows, cols, t):
+    """A reference known-answer case widened to a multiple of 64 columns with
+    zero weights (zero scale for the block formats) and zero inputs."""
+    if cols % 64 == 0:
+        return raw, x, cols
+    c2 = (cols + 63) // 64 * 64
+    rb, rb2 = Q_row_bytes(t, cols), Q_row_bytes(t, c2)
+    out = np.zeros((rows, rb2), np.uint8)
+    out[:, :rb] = np.asarray(raw, np.uint8).reshape(rows, rb)
+    xp = np.zeros(c2, np.float32)
+    xp[:cols] = x
+    return out.reshape(-1), xp, c2
+
+
+def Q_row_bytes(t, cols):
+    return {Q.F32: 4 * cols, Q.F16: 2 * cols, Q.Q8_0: 34 * (cols // 32), Q.Q4_0: 18 * (cols // 32),
+            Q.Q6_K: 210 * (cols // 256)}[t]
+
+
+def test_reference_known_answers_on_gpu(engines):
+    """src/test_ops.cpp:42-90 and 638-853, on the device."""
+    from test_oracle_proj import reference_matmul_cases
+    eng = engines(1, 64)
+    for name, raw, x, rows, cols, t, expect, tol in reference_matmul_cases():
+        raw2, x2, c2 = pad64(raw, x, rows, cols, t)
+        got = gpu_matmul(eng, raw2, x2, rows, c2, t)
+        log(f"  {name}: {got}")
+        assert np.abs(got - np.asarray(expect, np.float32)).max() <= tol, name
+
+
+def test_rmsnorm_and_vec_add(O, engines):
+    eng = engines(1, 64)
+    rg = np.random.default_rng(4)
+    for n in (1, 7, 256, 2048, 5632):
+        x = (rg.standard_normal(n) * 3).astype(np.float32)
+        w = rg.uniform(0.5, 1.5, n).astype(np.float32)
+        with device_arrays() as track:
+            xd, wd, od = track(eng.array(x)), track(eng.array(w)), track(eng.array((n,)))
+            eng.rmsnorm(od.ptr, xd.ptr, wd.ptr, n, 1e-5)
+            got = od.download()
+            ref = O.rmsnorm(x, w, 1e-5)
+            assert np.max(np.abs(got - ref) / (np.abs(ref) + 1e-30)) <= 1e-6, n
+            y = rg.standard_normal(n).astype(np.float32)
+            yd = track(eng.array(y))
+            eng.vec_add(yd.ptr, xd.ptr, n)
+            assert np.array_equal(bits(yd.download()), bits(O.vec_add(y, x))), n
+
+
+def tiny_block_weights(W, t, embd, kv, salt):
+    return (W.make_weights(t, embd, embd, salt=salt), W.make_weights(t, kv, embd, salt=salt + 1),
+            W.make_weights(t, kv, embd, salt=salt + 2), W.make_weights(t, embd, embd, salt=salt + 3))
+
+
+@pytest.mark.parametrize("t,name", TYPES)
+@pytest.mark.parametrize("n_seq", [1, 3, 8, 11])
+def test_attn_qkv_and_out(O, W, engines, t, name, n_seq):
+    """The fused input half (rmsnorm, Wq, Wk, Wv) and output half (x += Wo.xb2)
+    for n_seq sequences, against the oracle's rmsnorm and matmul."""
+    eng = engines(1, 64)
+    embd, kv = 2048, 256
+    wq, wk, wv, wo = tiny_block_weights(W, t, embd, kv, 100 + n_seq)
+    rg = np.random.default_rng(n_seq)
+    x = rg.standard_normal((n_seq, embd)).astype(np.float32)
+    nw = rg.uniform(0.5, 1.5, embd).astype(np.float32)
+    xb2 = rg.standard_normal((n_seq, embd)).astype(np.float32)
+    with device_arrays() as track:
+        d = {k: track(eng.array(v)) for k, v in
+             (("wq", wq), ("wk", wk), ("wv", wv), ("wo", wo), ("x", x), ("nw", nw), ("xb2", xb2))}
+        q, k, v = track(eng.array((n_seq, embd))), track(eng.array((n_seq, kv))), track(eng.array((n_seq, kv)))
+        for norm in (True, False):
+            log(f"  tla_attn_qkv {name} n_seq={n_seq} norm={norm}")
+            eng.attn_qkv(n_seq, q.ptr, k.ptr, v.ptr, d["x"].ptr, d["nw"].ptr if norm else None,
+                         1e-5, d["wq"].ptr, d["wk"].ptr, d["wv"].ptr, t)
+            gq, gk, gv = q.download(), k.download(), v.download()
+            for s in range(n_seq):
+                xb = O.rmsnorm(x[s], nw, 1e-5) if norm else x[s]
+                for got, raw, rows in ((gq[s], wq, embd), (gk[s], wk, kv), (gv[s], wv, kv)):
+                    check_rows(got, O.matmul(raw, xb, rows, embd, t), raw, xb, t, rows, embd,
+                               f"{name} seq {s} rows {rows}")
+        log(f"  tla_attn_out {name} n_seq={n_seq}")
+        eng.attn_out(n_seq, d["x"].ptr, d["wo"].ptr, d["xb2"].ptr, t)
+        gx = d["x"].download()
+        for s in range(n_seq):
+            want = O.vec_add(x[s], O.matmul(wo, xb2[s], embd, embd, t))
+            _, scale = Q.matmul_f64(wo, xb2[s], t, embd, embd)
+            assert np.max(np.abs(gx[s] - want) / (scale + np.abs(x[s]) + 1e-30)) <= ORACLE_TOL, s
+
+
+@pytest.mark.parametrize("t,name", [(Q.Q8_0, "q8_0"), (Q.F16, "f16"), (Q.Q4_0, "q4_0")])
+def test_attention_block_on_device_token_by_token(O, W, engines, t, name):
+    """One layer's attention block entirely on the device for 40 tokens
+    (src/forward.cpp:180-213): rmsnorm + QKV (tla_attn_qkv), RoPE + append +
+    attention (tla_decode), Wo + residual (tla_attn_out); the residual stream
+    x carries over between tokens.  The oracle runs the reference's sequence
+    of ops on the host."""
+    n_ctx, embd, kv = 128, 2048, 256
+    eng = engines(1, n_ctx)
+    wq, wk, wv, wo = tiny_block_weights(W, t, embd, kv, 900)
+    rg = np.random.default_rng(77)
+    nw = rg.uniform(0.5, 1.5, embd).astype(np.float32)
+    s = O.Shape(n_ctx=n_ctx, n_layers=1)
+    kc_ref = np.zeros(n_ctx * kv, np.float32)
+    vc_ref = np.zeros_like(kc_ref)
+    x_ref = rg.standard_normal(embd).astype(np.float32)
+    worst = 0.0
+    with device_arrays() as track:
+        d = {k: track(eng.array(v)) for k, v in
+             (("wq", wq), ("wk", wk), ("wv", wv), ("wo", wo), ("nw", nw), ("x", x_ref))}
+        kc, vc = eng.kv_cache(1)
+        track(kc), track(vc)
+        q, k, v = track(eng.array((embd,))), track(eng.array((kv,))), track(eng.array((kv,)))
+        att = track(eng.array((embd,)))
+        for pos in range(40):
+            eng.attn_qkv(1, q.ptr, k.ptr, v.ptr, d["x"].ptr, d["nw"].ptr, 1e-5, d["wq"].ptr,
+                         d["wk"].ptr, d["wv"].ptr, t)
+            eng.decode(np.array([pos], np.int32), 0, 1, att.ptr, q.ptr, k.ptr, v.ptr, kc.ptr,
+                       vc.ptr, 0, True)
+            eng.attn_out(1, d["x"].ptr, d["wo"].ptr, att.ptr, t)
+            # oracle: the reference's forward() attention half, op by op
+            xb = O.rmsnorm(x_ref, nw, 1e-5)
+            qh = O.matmul(wq, xb, embd, embd, t)
+            kh = O.matmul(wk, xb, kv, embd, t)
+            vh = O.matmul(wv, xb, kv, embd, t)
+            qh, kh = O.rope(qh, kh, pos, s)
+            out = O.attention(qh, kh, vh, kc_ref, vc_ref, 0, pos, s)
+            x_ref = O.vec_add(x_ref, O.matmul(wo, out, embd, embd, t))
+            err = float(np.abs(d["x"].download() - x_ref).max())
+            bound = max(1e-4, CHAIN_REL_TOL * float(np.abs(x_ref).max()))
+            worst = max(worst, err / bound)
+            assert err <= bound, (pos, err, bound)
+    log(f"    {name}: worst error / bound over 40 tokens {worst:.2f}")
+
+
+def test_projection_errors(tla, W, engines):
+    eng = engines(1, 64)
+    raw = W.make_weights(Q.Q8_0, 4, 96, salt=1)  # 96 columns: 3 blocks per row
+    with device_arrays() as track:
+        w = track(eng.array(raw))
+        x = track(eng.array(np.ones(96, np.float32)))
+        out = track(eng.array((4,)))
+        with pytest.raises(tla.TlaError) as e:
+            eng.matmul(out.ptr, w.ptr, x.ptr, 4, 96, Q.Q8_0)
+        assert e.value.code == 3  # unsupported shape
+        with pytest.raises(tla.TlaError) as e:
+            eng.matmul(out.ptr, w.ptr, x.ptr, 4, 64, 5)  # Q5_0: not a format of the reference
+        assert e.value.code == 1
+        with pytest.raises(tla.TlaError) as e:
+            eng.matmul(out.ptr, w.ptr + 2, x.ptr, 1, 64, Q.Q8_0)
+        assert e.value.code == 1

@@ -34,7 +34,9 @@ TLA_ERR_DEVICE = 4
 TLA_ERR_OUT_OF_MEMORY = 5
 TLA_ROTATE = 1
 
-KERNEL_DECODE, KERNEL_PREFILL, KERNEL_APPEND = range(3)
+KERNEL_DECODE, KERNEL_PREFILL, KERNEL_APPEND, KERNEL_GEMV = range(4)
+# weight formats: the reference's ggml_type ids (src/gguf.h:23-32)
+W_F32, W_F16, W_Q4_0, W_Q8_0, W_Q6_K = 0, 1, 2, 8, 14
 OPT_DECODE_SPLIT = 0
 
 
@@ -81,6 +83,12 @@ SIGNATURES = {
     "tla_memcpy_d2d": (C.c_int, [_vp, _vp, _vp, C.c_size_t]),
     "tla_rope": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
     "tla_softmax": (C.c_int, [_vp, _vp, C.c_int]),
+    "tla_matmul": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
+    "tla_rmsnorm": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_float]),
+    "tla_vec_add": (C.c_int, [_vp, _vp, _vp, C.c_int]),
+    "tla_attn_qkv": (C.c_int, [_vp, C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp,
+                               C.c_int]),
+    "tla_attn_out": (C.c_int, [_vp, C.c_int, _vp, _vp, _vp, C.c_int]),
     "tla_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
     "tla_rope_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
     "tla_decode": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int,
@@ -230,6 +238,24 @@ class Engine:
         _check(lib().tla_prefill(self.h, pos0, n_tok, layer0, n_step_layers,
                                  TLA_ROTATE if rotate else 0, out, q, k, v, key_cache,
                                  value_cache), "tla_prefill")
+
+    # ---- projections either side of the attention block -------------------------
+    def matmul(self, out: int, w: int, x: int, rows: int, cols: int, wtype: int):
+        _check(lib().tla_matmul(self.h, out, w, x, rows, cols, wtype), "tla_matmul")
+
+    def rmsnorm(self, out: int, x: int, weight: int, size: int, eps: float):
+        _check(lib().tla_rmsnorm(self.h, out, x, weight, size, eps), "tla_rmsnorm")
+
+    def vec_add(self, out: int, x: int, size: int):
+        _check(lib().tla_vec_add(self.h, out, x, size), "tla_vec_add")
+
+    def attn_qkv(self, n_seq: int, q: int, k: int, v: int, x: int, norm_w: int | None, eps: float,
+                 wq: int, wk: int, wv: int, wtype: int):
+        _check(lib().tla_attn_qkv(self.h, n_seq, q, k, v, x, norm_w, eps, wq, wk, wv, wtype),
+               "tla_attn_qkv")
+
+    def attn_out(self, n_seq: int, x: int, wo: int, xb2: int, wtype: int):
+        _check(lib().tla_attn_out(self.h, n_seq, x, wo, xb2, wtype), "tla_attn_out")
 
     # ---- measurement --------------------------------------------------------------
     def set_option(self, option: int, value: int):

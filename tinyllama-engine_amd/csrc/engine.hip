@@ -4,6 +4,7 @@
 #include <algorithm>
 #include <cmath>
 #include <cstdarg>
+#include <cstdint>
 #include <cstdio>
 #include <cstring>
 #include <string>
@@ -438,6 +439,148 @@ int tla_softmax(tla_engine* e, float* x_dev, int size)
     if (int rc = set_device(e)) return rc;
     const hipError_t err = launch_softmax(x_dev, size, e->stream);
     if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "softmax launch: %s", hipGetErrorString(err));
+    return ok();
+}
+
+// ---- projections -------------------------------------------------------------
+
+namespace {
+
+// x vectors staged in LDS per launch: at most this many bytes, well inside a
+// workgroup's share of the CU's LDS.
+constexpr int kGemvLdsBytes = 60 * 1024;
+
+int gemv_chunk(int n_seq, int cols)
+{
+    return std::max(1, std::min({n_seq, kGemvMaxVec, kGemvLdsBytes / (cols * 4)}));
+}
+
+// Shape and pointer checks shared by the matrix-vector entry points.
+int check_gemv(int type, int cols, int n_vec, const void* w)
+{
+    if (weight_row_bytes(type, cols) == 0 || (type != kQ6_K && cols % 32 != 0) ||
+        (type == kQ6_K && cols % 256 != 0))
+        return fail(TLA_ERR_INVALID_ARGUMENT, "weight type %d with %d columns", type, cols);
+    if (cols < 64 || cols % 64 != 0 || cols * 4 > kGemvLdsBytes)
+        return fail(TLA_ERR_UNSUPPORTED, "cols %d: multiples of 64 up to %d are supported", cols,
+                    kGemvLdsBytes / 4);
+    if (static_cast<long long>(n_vec) * cols * 4 > kGemvLdsBytes)
+        return fail(TLA_ERR_UNSUPPORTED, "%d vectors of %d floats exceed %d bytes of LDS", n_vec,
+                    cols, kGemvLdsBytes);
+    if (reinterpret_cast<std::uintptr_t>(w) % 16 != 0)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "weights must be 16-byte aligned");
+    return TLA_OK;
+}
+
+int run_gemv(tla_engine* e, int type, const GemvParams& p)
+{
+    return launch(e, TLA_KERNEL_GEMV, "gemv", [&] { return launch_gemv(type, p, e->stream); });
+}
+
+}  // namespace
+
+int tla_matmul(tla_engine* e, float* out_dev, const void* w_dev, const float* x_dev, int rows,
+               int cols, int type)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!out_dev || !w_dev || !x_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (rows < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "rows %d < 1", rows);
+    if (int rc = check_gemv(type, cols, 1, w_dev)) return rc;
+    if (int rc = set_device(e)) return rc;
+    GemvParams p{};
+    p.seg[0] = {static_cast<const unsigned char*>(w_dev), out_dev, rows, 0};
+    p.n_seg = 1;
+    p.total_rows = rows;
+    p.cols = cols;
+    p.row_bytes = static_cast<int>(weight_row_bytes(type, cols));
+    p.n_vec = 1;
+    p.x = x_dev;
+    p.x_stride = cols;
+    if (int rc = run_gemv(e, type, p)) return rc;
+    return ok();
+}
+
+int tla_rmsnorm(tla_engine* e, float* out_dev, const float* x_dev, const float* weight_dev,
+                int size, float eps)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!out_dev || !x_dev || !weight_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (size < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "size %d < 1", size);
+    if (int rc = set_device(e)) return rc;
+    const hipError_t err = launch_rmsnorm(out_dev, x_dev, weight_dev, size, eps, e->stream);
+    if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "rmsnorm launch: %s", hipGetErrorString(err));
+    return ok();
+}
+
+int tla_vec_add(tla_engine* e, float* out_dev, const float* x_dev, int size)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!out_dev || !x_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (size < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "size %d < 1", size);
+    if (int rc = set_device(e)) return rc;
+    const hipError_t err = launch_vec_add(out_dev, x_dev, size, e->stream);
+    if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "vec_add launch: %s", hipGetErrorString(err));
+    return ok();
+}
+
+int tla_attn_qkv(tla_engine* e, int n_seq, float* q_dev, float* k_dev, float* v_dev,
+                 const float* x_dev, const float* norm_w_dev, float eps, const void* wq_dev,
+                 const void* wk_dev, const void* wv_dev, int type)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!q_dev || !k_dev || !v_dev || !x_dev || !wq_dev || !wk_dev || !wv_dev)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (n_seq < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_seq %d < 1", n_seq);
+    const int embd = e->cfg.n_embd, kv = e->kv_dim;
+    const int chunk = gemv_chunk(n_seq, embd);
+    if (int rc = check_gemv(type, embd, chunk, wq_dev)) return rc;
+    if (reinterpret_cast<std::uintptr_t>(wk_dev) % 16 || reinterpret_cast<std::uintptr_t>(wv_dev) % 16)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "weights must be 16-byte aligned");
+    if (int rc = set_device(e)) return rc;
+    for (int s0 = 0; s0 < n_seq; s0 += chunk) {
+        const int nv = std::min(chunk, n_seq - s0);
+        GemvParams p{};
+        p.seg[0] = {static_cast<const unsigned char*>(wq_dev), q_dev + static_cast<long long>(s0) * embd, embd, embd};
+        p.seg[1] = {static_cast<const unsigned char*>(wk_dev), k_dev + static_cast<long long>(s0) * kv, kv, kv};
+        p.seg[2] = {static_cast<const unsigned char*>(wv_dev), v_dev + static_cast<long long>(s0) * kv, kv, kv};
+        p.n_seg = 3;
+        p.total_rows = embd + 2 * kv;
+        p.cols = embd;
+        p.row_bytes = static_cast<int>(weight_row_bytes(type, embd));
+        p.n_vec = nv;
+        p.x = x_dev + static_cast<long long>(s0) * embd;
+        p.x_stride = embd;
+        p.norm_w = norm_w_dev;
+        p.eps = eps;
+        if (int rc = run_gemv(e, type, p)) return rc;
+    }
+    return ok();
+}
+
+int tla_attn_out(tla_engine* e, int n_seq, float* x_dev, const void* wo_dev, const float* xb2_dev,
+                 int type)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!x_dev || !wo_dev || !xb2_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (n_seq < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_seq %d < 1", n_seq);
+    const int embd = e->cfg.n_embd;
+    const int chunk = gemv_chunk(n_seq, embd);
+    if (int rc = check_gemv(type, embd, chunk, wo_dev)) return rc;
+    if (int rc = set_device(e)) return rc;
+    for (int s0 = 0; s0 < n_seq; s0 += chunk) {
+        const int nv = std::min(chunk, n_seq - s0);
+        GemvParams p{};
+        p.seg[0] = {static_cast<const unsigned char*>(wo_dev), x_dev + static_cast<long long>(s0) * embd, embd, embd};
+        p.n_seg = 1;
+        p.total_rows = embd;
+        p.cols = embd;
+        p.row_bytes = static_cast<int>(weight_row_bytes(type, embd));
+        p.n_vec = nv;
+        p.x = xb2_dev + static_cast<long long>(s0) * embd;
+        p.x_stride = embd;
+        p.add = 1;
+        if (int rc = run_gemv(e, type, p)) return rc;
+    }
     return ok();
 }
 

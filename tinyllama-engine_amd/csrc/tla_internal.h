@@ -84,6 +84,39 @@ struct PrefillParams {
 hipError_t launch_prefill_append(const PrefillParams& p, hipStream_t s);
 hipError_t launch_prefill_attention(const PrefillParams& p, hipStream_t s);
 
+// ---- projections (matrix-vector products) ---------------------------------
+// Weight type ids: the reference's ggml_type values (src/gguf.h:23-32).
+enum WeightType { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ6_K = 14 };
+constexpr int kGemvMaxVec = 8;    // vectors per launch (x staged in LDS)
+constexpr int kGemvMaxSeg = 3;    // matrices per launch (Wq, Wk, Wv)
+
+struct GemvSegment {
+    const unsigned char* w;  // [rows][row_bytes]
+    float* out;              // out[v * out_stride + row]
+    int rows;
+    long long out_stride;
+};
+
+struct GemvParams {
+    GemvSegment seg[kGemvMaxSeg];
+    int n_seg;
+    int total_rows;          // sum of seg[].rows
+    int cols;                // multiple of 64 (of 256 for Q6_K)
+    int row_bytes;
+    int n_vec;               // 1..kGemvMaxVec
+    const float* x;          // x[v * x_stride + col]
+    long long x_stride;
+    const float* norm_w;     // non-null: x is replaced by rmsnorm(x, norm_w, eps)
+    float eps;
+    int add;                 // 1: out += W.x (residual), 0: out = W.x
+};
+
+long long weight_row_bytes(int type, int cols);  // 0 if the type is unknown
+hipError_t launch_gemv(int type, const GemvParams& p, hipStream_t s);
+hipError_t launch_rmsnorm(float* out, const float* x, const float* w, int size, float eps,
+                          hipStream_t s);
+hipError_t launch_vec_add(float* out, const float* x, int size, hipStream_t s);
+
 // ---- small ops -------------------------------------------------------------
 struct RopeParams {
     float* q;

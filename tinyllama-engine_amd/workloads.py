@@ -26,7 +26,7 @@ Q_DIM, KV_DIM = N_HEAD * HEAD_DIM, N_HEAD_KV * HEAD_DIM
 FREQ_BASE = 10000.0
 
 WORKLOAD_IDS = {"decode_single": 1, "decode_model": 2, "decode_ragged": 3, "prefill": 4,
-                "decode_long": 5}
+                "decode_long": 5, "weights": 6, "block": 7}
 
 
 def rng(workload: str | int, salt: int = 0) -> np.random.Generator:
@@ -156,3 +156,49 @@ def make_prefill(n_layers: int = 22, n_tok: int = 512, pos0: int = 0, salt: int 
     k = normal(g, (n_layers, n_tok, n_head_kv * HEAD_DIM))
     v = normal(g, (n_layers, n_tok, n_head_kv * HEAD_DIM))
     return PrefillCase(n_layers, n_tok, pos0, q, k, v, n_head, n_head_kv)
+
+
+# ---- weights in the reference's GGUF formats ---------------------------------
+# Type ids: ggml_type (src/gguf.h:23-32); block layouts src/gguf.h:56-135.
+W_F32, W_F16, W_Q4_0, W_Q8_0, W_Q6_K = 0, 1, 2, 8, 14
+W_NAMES = {W_F32: "f32", W_F16: "f16", W_Q4_0: "q4_0", W_Q8_0: "q8_0", W_Q6_K: "q6_k"}
+
+
+def weight_row_bytes(wtype: int, cols: int) -> int:
+    return {W_F32: 4 * cols, W_F16: 2 * cols, W_Q8_0: 34 * (cols // 32),
+            W_Q4_0: 18 * (cols // 32), W_Q6_K: 210 * (cols // 256)}[wtype]
+
+
+def _f16_bits(a: np.ndarray) -> np.ndarray:
+    return np.asarray(a, np.float16).view(np.uint8).reshape(*np.shape(a), 2)
+
+
+def make_weights(wtype: int, rows: int, cols: int, salt: int = 0) -> np.ndarray:
+    """Seeded random weights as the raw bytes (uint8, [rows * row_bytes]) of a
+    row-major [rows][cols] matrix.  Scales are chosen so W.x with x ~ N(0,1)
+    stays O(1) per row at cols = 2048."""
+    g = rng("weights", salt * 64 + wtype)
+    if wtype == W_F32:
+        return normal(g, (rows, cols), 0.02).view(np.uint8).reshape(-1)
+    if wtype == W_F16:
+        return _f16_bits(normal(g, (rows, cols), 0.02)).reshape(-1)
+    if wtype == W_Q8_0:
+        nb = cols // 32
+        blk = np.empty((rows, nb, 34), np.uint8)
+        blk[..., 0:2] = _f16_bits(g.uniform(0.0002, 0.0003, (rows, nb)))
+        blk[..., 2:34] = g.integers(-128, 128, (rows, nb, 32)).astype(np.int8).view(np.uint8)
+        return blk.reshape(-1)
+    if wtype == W_Q4_0:
+        nb = cols // 32
+        blk = np.empty((rows, nb, 18), np.uint8)
+        blk[..., 0:2] = _f16_bits(g.uniform(0.003, 0.006, (rows, nb)))
+        blk[..., 2:18] = g.integers(0, 256, (rows, nb, 16)).astype(np.uint8)
+        return blk.reshape(-1)
+    if wtype == W_Q6_K:
+        nb = cols // 256
+        blk = np.empty((rows, nb, 210), np.uint8)
+        blk[..., 0:192] = g.integers(0, 256, (rows, nb, 192)).astype(np.uint8)
+        blk[..., 192:208] = g.integers(-32, 32, (rows, nb, 16)).astype(np.int8).view(np.uint8)
+        blk[..., 208:210] = _f16_bits(g.uniform(0.0001, 0.0002, (rows, nb)))
+        return blk.reshape(-1)
+    raise ValueError(wtype)
