@@ -22,7 +22,9 @@ the 256 MB Infinity Cache, steps rotate over 5 copies of the whole cache
 
 Other workloads (--workload): decode_long (16384 context, batch 8, 22 layers),
 decode_ragged (64 sequences, L in [256, 2048], 22 layers), prefill,
-decode_single (one layer, position 127: reported as latency), copy (the
+decode_single (one layer, position 127: reported as latency), proj (the
+attention block's projections for a 22-layer decode step, and the GEMV kernel
+on a 32000 x 2048 matrix in every weight format), copy (the
 device copy kernel, used to calibrate rocprofv3 byte counters) and read (a
 plain library reduction over 6 GiB: what HBM delivers to a read stream, the
 practical ceiling the decode figures sit under).
@@ -315,6 +317,96 @@ def run_copy(steps, warmup, nbytes=1 << 30):
             "value": 2 * nbytes / (ms * 1e-3) / 1e9}
 
 
+def run_proj(steps, warmup, n_layers=22, wtype=W.W_F16):
+    """The attention block's projections for one decode step of every layer,
+    issued as a forward pass issues them: per layer, one fused
+    rmsnorm + Wq/Wk/Wv launch (tla_attn_qkv) and one Wo + residual launch
+    (tla_attn_out), batch 1.  Weights are distinct per layer (F16: 415 MB,
+    beyond the 256 MB Infinity Cache).  Also the GEMV kernel alone on a
+    vocabulary-sized matrix (32000 x 2048, the output projection's shape) in
+    every weight format."""
+    embd, kv = 2048, 256
+    eng = tla.Engine(tla.Config.tinyllama(n_layers=n_layers, n_ctx=16))
+    arrays = []
+
+    def dev(a):
+        d = eng.array(a)
+        arrays.append(d)
+        return d
+
+    layers = []
+    for layer in range(n_layers):
+        layers.append({"wq": dev(W.make_weights(wtype, embd, embd, salt=4 * layer)),
+                       "wk": dev(W.make_weights(wtype, kv, embd, salt=4 * layer + 1)),
+                       "wv": dev(W.make_weights(wtype, kv, embd, salt=4 * layer + 2)),
+                       "wo": dev(W.make_weights(wtype, embd, embd, salt=4 * layer + 3)),
+                       "nw": dev(np.ones(embd, np.float32))})
+    rg = np.random.default_rng(0)
+    x = dev(rg.standard_normal(embd).astype(np.float32))
+    xb2 = dev(rg.standard_normal(embd).astype(np.float32))
+    q, k, v = dev(np.zeros(embd, np.float32)), dev(np.zeros(kv, np.float32)), dev(np.zeros(kv, np.float32))
+    step_bytes = n_layers * (2 * W.weight_row_bytes(wtype, embd) * embd
+                             + 2 * W.weight_row_bytes(wtype, embd) * kv)
+
+    def step(i):
+        for L in layers:
+            eng.attn_qkv(1, q.ptr, k.ptr, v.ptr, x.ptr, L["nw"].ptr, 1e-5, L["wq"].ptr, L["wk"].ptr,
+                         L["wv"].ptr, wtype)
+            eng.attn_out(1, x.ptr, L["wo"].ptr, xb2.ptr, wtype)
+
+    ms = time_steps(eng, step, steps, warmup)
+    k_ms, k_n = kernel_avg_ms(eng, step, max(2, steps // 5), tla.KERNEL_GEMV)
+    dev_ms = k_ms * 2 * n_layers  # the step's kernels back to back
+    log(f"[bench] proj {W.W_NAMES[wtype]} x {n_layers} layers, batch 1: {ms * 1e3:.1f} us/step "
+        f"end to end, {step_bytes / 1e6:.0f} MB of weights -> {step_bytes / ms / 1e6:.0f} GB/s; "
+        f"{2 * n_layers} launches of {k_ms * 1e3:.2f} us -> {step_bytes / dev_ms / 1e6:.0f} GB/s "
+        f"in-kernel")
+    for a in arrays:
+        a.free()
+    # the GEMV kernel alone on one large matrix, each format
+    big = {}
+    rows = 32000
+    for t in (W.W_F32, W.W_F16, W.W_Q8_0, W.W_Q4_0, W.W_Q6_K):
+        wd = eng.array(W.make_weights(t, rows, embd, salt=99))
+        xd = eng.array(rg.standard_normal(embd).astype(np.float32))
+        od = eng.array((rows,))
+        nbytes = W.weight_row_bytes(t, embd) * rows
+        copies = 1
+        extra = []
+        if nbytes < 300e6:  # rotate copies so the working set exceeds the Infinity Cache
+            copies = int(np.ceil(300e6 / nbytes))
+            extra = [eng.array(W.make_weights(t, rows, embd, salt=100 + c)) for c in range(copies - 1)]
+        ws = [wd] + extra
+
+        def one(i):
+            eng.matmul(od.ptr, ws[i % copies].ptr, xd.ptr, rows, embd, t)
+
+        # One launch per Python call is host-bound here (the call costs more
+        # than the kernel), so the kernel's own duration comes from the HIP
+        # event pair around each launch.
+        for i in range(warmup):
+            one(i)
+        t_ms, _ = kernel_avg_ms(eng, one, steps, tla.KERNEL_GEMV)
+        big[W.W_NAMES[t]] = {"us": round(t_ms * 1e3, 2), "bytes": nbytes,
+                             "GB_s": round(nbytes / t_ms / 1e6, 1),
+                             "frac": round(nbytes / t_ms / 1e6 / HBM_PEAK_GBS, 4)}
+        log(f"[bench] matmul {W.W_NAMES[t]} {rows}x{embd}: {t_ms * 1e3:.1f} us, "
+            f"{nbytes / t_ms / 1e6:.0f} GB/s ({nbytes / t_ms / 1e6 / HBM_PEAK_GBS:.1%}), "
+            f"{copies} rotated copies")
+        for a in [wd, xd, od] + extra:
+            a.free()
+    eng.close()
+    value = step_bytes / (dev_ms * 1e-3) / 1e9
+    return {"workload": "proj", "metric": "attention-block projection weight GB/s (% HBM peak)",
+            "value": value, "unit": "GB/s", "ms_per_step": dev_ms, "end_to_end_ms": ms,
+            "weight_bytes": step_bytes, "launch_us": round(k_ms * 1e3, 2), "launches": k_n,
+            "roofline": {"bound": "hbm", "achieved": big["q8_0"]["GB_s"], "peak": HBM_PEAK_GBS,
+                         "unit": "GB/s", "frac": big["q8_0"]["frac"],
+                         "traffic": profiled_traffic("gemv_kernel", "matmul_q8_0"),
+                         "kernel": "gemv_kernel", "config": "matmul q8_0 32000x2048"},
+            "matmul_32000x2048": big}
+
+
 def run_read(steps, warmup, nbytes=6 << 30):
     """HBM read ceiling: torch's sum over an nbytes float32 tensor (a library
     streaming reduction, nothing of this build), timed with events on torch's
@@ -345,7 +437,7 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode_model",
                     choices=["decode_model", "decode_long", "decode_ragged", "decode_single",
-                             "prefill", "copy", "read"])
+                             "prefill", "proj", "copy", "read"])
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill half")
     ap.add_argument("--split", type=int, default=0, help="decode split length (0 = auto)")
@@ -364,6 +456,19 @@ def main():
         return
     if args.workload == "read":
         print(json.dumps(run_read(args.steps, args.warmup)))
+        return
+    if args.workload == "proj":
+        p = run_proj(args.steps, args.warmup)
+        line = {"metric": p["metric"], "value": round(p["value"], 1), "unit": "GB/s", "n_gpus": 1,
+                "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(p["ms_per_step"], 4),
+                "higher_is_better": True, "scaling": "weak", "vs_baseline": None, "dtype": "f16",
+                "data": "synthetic",
+                "config": {"workload": "proj", "n_layers": 22, "n_embd": 2048, "kv_dim": 256,
+                           "weights": "f16", "batch": 1, "parallelism": "none"},
+                "roofline": p["roofline"], "launch_us": p["launch_us"],
+                "end_to_end_ms": round(p["end_to_end_ms"], 4),
+                "matmul_32000x2048": p["matmul_32000x2048"]}
+        print(json.dumps(line))
         return
     if args.workload == "prefill":
         p = run_prefill(args.steps, args.warmup, cpu)

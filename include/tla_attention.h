@@ -170,7 +170,7 @@ enum tla_weight_type {
 
 /* matmul() src/ops.h:64-66: out[rows] = W[rows][cols] . x[cols], device
  * pointers.  cols must be a multiple of 64 (of 256 for Q6_K) and at most
- * 15360 (x is staged in 60 KiB of LDS); other shapes return
+ * 13632 (x is staged in 60 KiB of LDS); other shapes return
  * TLA_ERR_UNSUPPORTED.  fp32 accumulation; equal
  * to the reference to fp32 rounding (the sums are grouped differently). */
 int tla_matmul(tla_engine* e, float* out_dev, const void* w_dev, const float* x_dev, int rows,

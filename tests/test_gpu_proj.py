@@ -44,7 +44,10 @@ def check_rows(got, ora, raw, x, t, rows, cols, what):
     assert eor <= ORACLE_TOL, what
 
 
-SHAPES = [(1, 64), (3, 128), (64, 512), (256, 2048), (2048, 2048), (300, 5632), (37, 4096)]
+# The last two have enough rows for the launches that give each lane group
+# several rows (32 lanes per row at 1024 columns, 64 at 2560).
+SHAPES = [(1, 64), (3, 128), (64, 512), (256, 2048), (2048, 2048), (300, 5632), (37, 4096),
+          (20000, 1024), (8200, 2560)]
 
 
 @pytest.mark.parametrize("t,name", TYPES)

@@ -450,9 +450,13 @@ namespace {
 // workgroup's share of the CU's LDS.
 constexpr int kGemvLdsBytes = 60 * 1024;
 
+// LDS bytes for one staged x vector: the floats, 4 floats of padding per 64
+// and one sum per 16.
+int gemv_lds_per_vec(int cols) { return (cols + cols / 8) * 4; }
+
 int gemv_chunk(int n_seq, int cols)
 {
-    return std::max(1, std::min({n_seq, kGemvMaxVec, kGemvLdsBytes / (cols * 4)}));
+    return std::max(1, std::min({n_seq, kGemvMaxVec, kGemvLdsBytes / gemv_lds_per_vec(cols)}));
 }
 
 // Shape and pointer checks shared by the matrix-vector entry points.
@@ -461,10 +465,10 @@ int check_gemv(int type, int cols, int n_vec, const void* w)
     if (weight_row_bytes(type, cols) == 0 || (type != kQ6_K && cols % 32 != 0) ||
         (type == kQ6_K && cols % 256 != 0))
         return fail(TLA_ERR_INVALID_ARGUMENT, "weight type %d with %d columns", type, cols);
-    if (cols < 64 || cols % 64 != 0 || cols * 4 > kGemvLdsBytes)
+    if (cols < 64 || cols % 64 != 0 || gemv_lds_per_vec(cols) > kGemvLdsBytes)
         return fail(TLA_ERR_UNSUPPORTED, "cols %d: multiples of 64 up to %d are supported", cols,
-                    kGemvLdsBytes / 4);
-    if (static_cast<long long>(n_vec) * cols * 4 > kGemvLdsBytes)
+                    kGemvLdsBytes / 288 * 64);
+    if (static_cast<long long>(n_vec) * gemv_lds_per_vec(cols) > kGemvLdsBytes)
         return fail(TLA_ERR_UNSUPPORTED, "%d vectors of %d floats exceed %d bytes of LDS", n_vec,
                     cols, kGemvLdsBytes);
     if (reinterpret_cast<std::uintptr_t>(w) % 16 != 0)

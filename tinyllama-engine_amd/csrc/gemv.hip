@@ -17,10 +17,13 @@
 // 4-byte boundary, so it is read with aligned dword loads; Q6_K super-blocks
 // (210 B) are 2-byte aligned and read with 16-bit loads.  32 lanes serve a
 // row when it has at most 32 units (cols <= 2048), else 64; the lanes' dot
-// products meet in a shuffle reduction.  x sits in LDS, read as float4.
+// products meet in a DPP reduction.  x sits in LDS (padded against bank
+// conflicts), read as float4.
 //
 // Products and sums are fp32 but grouped differently from the reference's
 // sequential loops, so results match it to fp32 rounding, not bit for bit.
+#include <algorithm>
+
 #include "rope_math.h"
 #include "tla_internal.h"
 
@@ -30,17 +33,26 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kUnit = 64;  // weights per lane step
 
+// x sits in LDS with 4 floats of padding after every 64: the lanes of a row
+// read 64-float spans 256 B apart, which without padding all start in the
+// same bank; with it, lane i starts 4i banks further.
+__device__ __forceinline__ int xpad(int c) { return c + 4 * (c >> 6); }
+__host__ __device__ constexpr int xs_floats(int cols) { return cols + cols / 16; }
+
 __device__ __forceinline__ float half_bits_to_float(unsigned h)
 {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
 }
 
-// x[c0 .. c0+15] of vector v from LDS (16 floats).
-__device__ __forceinline__ void lds16(const float* xs, int c0, float (&o)[16])
+// kW floats of x (kW = 4, 8 or 16) from LDS starting at column c0, a multiple
+// of kW, so the span does not cross a padding gap.
+template <int kW>
+__device__ __forceinline__ void lds_x(const float* xs, int c0, float* o)
 {
+    const float* base = xs + xpad(c0);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-        const float4 t = *reinterpret_cast<const float4*>(xs + c0 + 4 * i);
+    for (int i = 0; i < kW / 4; ++i) {
+        const float4 t = *reinterpret_cast<const float4*>(base + 4 * i);
         o[4 * i + 0] = t.x;
         o[4 * i + 1] = t.y;
         o[4 * i + 2] = t.z;
@@ -48,104 +60,148 @@ __device__ __forceinline__ void lds16(const float* xs, int c0, float (&o)[16])
     }
 }
 
-// ---- one 64-weight unit of a row, dotted with each vector ----------------
+// 16 bytes from a 4-byte aligned address: one global_load_dwordx4 (the
+// hardware takes dword alignment for multi-dword loads).
+typedef unsigned u32x4_a4 __attribute__((ext_vector_type(4), aligned(4)));
+
+__device__ __forceinline__ void load16_a4(const unsigned char* p, unsigned* o)
+{
+    const u32x4_a4 t = *reinterpret_cast<const u32x4_a4*>(p);
+    o[0] = t.x;
+    o[1] = t.y;
+    o[2] = t.z;
+    o[3] = t.w;
+}
+
+// ---- one 64-weight unit of a row -------------------------------------------
+//
+// The lanes serving a row step through its units together: in a step, lanes
+// l < n hold units u0 + l (n = the step's active lanes).  Each format loads
+// a unit's raw bytes (load), gives the dot product of its q-th group of 16
+// weights with 16 x values before any scale (part), and combines the four
+// parts with the unit's scales (finish).  The x values of group q sit in
+// 16 / kW runs of kW columns; run j starts at xcol(u0, n, l, q, j).  x is
+// read once per group and used for every row a lane holds.  s16[g] is the
+// sum of x over columns 16g .. 16g+15, for the block formats' zero offsets:
+// sum (q - z) x = sum q x - z sum x.
+//
+// F32 and F16 spread a unit over the step's span so that each load
+// instruction of the n lanes reads one contiguous stretch of HBM; the block
+// formats keep a unit's bytes contiguous (a unit is whole blocks).
+
+__device__ __forceinline__ float ub(unsigned w, int k)  // byte k as float (v_cvt_f32_ubyte*)
+{
+    return static_cast<float>((w >> (8 * k)) & 0xFFu);
+}
 
 template <int kType>
 struct Unit;
 
+// 16 float4 pieces; piece i at column 64 u0 + 4 (l + n i).
 template <>
 struct Unit<kF32> {
+    static constexpr int kRows = 1, kW = 4;
     float w[64];
-    __device__ void load(const unsigned char* row, int u)
+    __device__ static int xcol(int u0, int n, int l, int q, int j) { return 64 * u0 + 4 * (l + n * (4 * q + j)); }
+    __device__ void load(const unsigned char* row, int u0, int n, int l)
     {
-        const float4* p = reinterpret_cast<const float4*>(row + u * 256);
+        const float4* p = reinterpret_cast<const float4*>(row) + 16 * u0 + l;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-            const float4 t = p[i];
+            const float4 t = p[n * i];
             w[4 * i] = t.x;
             w[4 * i + 1] = t.y;
             w[4 * i + 2] = t.z;
             w[4 * i + 3] = t.w;
         }
     }
-    __device__ float dot(const float* xs, int u) const
+    __device__ float part(int q, const float (&x)[16]) const
     {
         float s = 0.f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            float xv[16];
-            lds16(xs, u * 64 + 16 * q, xv);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) s += w[16 * q + i] * xv[i];
-        }
+        for (int i = 0; i < 16; ++i) s += w[16 * q + i] * x[i];
         return s;
+    }
+    __device__ float finish(const float (&pt)[4], const float*) const
+    {
+        return (pt[0] + pt[1]) + (pt[2] + pt[3]);
     }
 };
 
+// 8 pieces of 8 halves (16 B); piece i at column 64 u0 + 8 (l + n i).
 template <>
 struct Unit<kF16> {
-    uint4 raw[8];  // 64 halves
-    __device__ void load(const unsigned char* row, int u)
+    static constexpr int kRows = 1, kW = 8;
+    uint4 raw[8];
+    __device__ static int xcol(int u0, int n, int l, int q, int j) { return 64 * u0 + 8 * (l + n * (2 * q + j)); }
+    __device__ void load(const unsigned char* row, int u0, int n, int l)
     {
-        const uint4* p = reinterpret_cast<const uint4*>(row + u * 128);
+        const uint4* p = reinterpret_cast<const uint4*>(row) + 8 * u0 + l;
 #pragma unroll
-        for (int i = 0; i < 8; ++i) raw[i] = p[i];
+        for (int i = 0; i < 8; ++i) raw[i] = p[n * i];
     }
-    __device__ float dot(const float* xs, int u) const
+    __device__ float part(int q, const float (&x)[16]) const
     {
         float s = 0.f;
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
-            float xv[16];
-            lds16(xs, u * 64 + 16 * q, xv);
+        for (int i = 0; i < 2; ++i) {
+            const uint4 r = raw[2 * q + i];
+            const unsigned wd[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
-            for (int i = 0; i < 2; ++i) {
-                const uint4 r = raw[2 * q + i];
-                const unsigned wd[4] = {r.x, r.y, r.z, r.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    s += half_bits_to_float(wd[j] & 0xFFFFu) * xv[8 * i + 2 * j];
-                    s += half_bits_to_float(wd[j] >> 16) * xv[8 * i + 2 * j + 1];
-                }
+            for (int j = 0; j < 4; ++j) {
+                s += half_bits_to_float(wd[j] & 0xFFFFu) * x[8 * i + 2 * j];
+                s += half_bits_to_float(wd[j] >> 16) * x[8 * i + 2 * j + 1];
             }
         }
         return s;
+    }
+    __device__ float finish(const float (&pt)[4], const float*) const
+    {
+        return (pt[0] + pt[1]) + (pt[2] + pt[3]);
     }
 };
 
-// Two Q8_0 blocks (68 bytes, 17 dwords): d0 | qs0[32] | d1 | qs1[32].
+// Two Q8_0 blocks (68 bytes, 17 dwords): d0 | qs0[32] | d1 | qs1[32].  The
+// int8 weights are read as bytes with the sign bit flipped, q + 128 in
+// 0..255, converted by the byte-to-float instructions; the 128 comes back
+// out through the block's x sum.
 template <>
 struct Unit<kQ8_0> {
+    static constexpr int kRows = 2, kW = 16;
     unsigned dw[17];
-    __device__ void load(const unsigned char* row, int u)
+    int u;
+    __device__ static int xcol(int u0, int, int l, int q, int) { return 64 * (u0 + l) + 16 * q; }
+    __device__ void load(const unsigned char* row, int u0, int, int l)
     {
-        const unsigned* p = reinterpret_cast<const unsigned*>(row + u * 68);
+        u = u0 + l;
+        const unsigned char* p = row + u * 68;
 #pragma unroll
-        for (int i = 0; i < 17; ++i) dw[i] = p[i];
+        for (int i = 0; i < 4; ++i) load16_a4(p + 16 * i, dw + 4 * i);
+        dw[16] = *reinterpret_cast<const unsigned*>(p + 64);
     }
-    // byte b (0..67) of the pair, as a signed value
-    __device__ int sbyte(int b) const
+    // four bytes starting at byte b (b even), as a dword
+    __device__ unsigned bytes4(int b) const
     {
-        return static_cast<int>(static_cast<signed char>((dw[b >> 2] >> (8 * (b & 3))) & 0xFFu));
+        return (b & 3) == 0 ? dw[b >> 2] : __builtin_amdgcn_alignbyte(dw[(b >> 2) + 1], dw[b >> 2], 2);
     }
-    __device__ float dot(const float* xs, int u) const
+    __device__ float part(int q, const float (&x)[16]) const
     {
+        const int base = (q < 2 ? 2 : 36) + 16 * (q & 1);  // first qs byte of the group
         float s = 0.f;
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-            const int base = 34 * blk;  // byte offset of the block
-            const float d = half_bits_to_float(blk == 0 ? (dw[0] & 0xFFFFu) : (dw[8] >> 16));
-            float bs = 0.f;
+        for (int i = 0; i < 4; ++i) {
+            const unsigned w = bytes4(base + 4 * i) ^ 0x80808080u;
 #pragma unroll
-            for (int q = 0; q < 2; ++q) {
-                float xv[16];
-                lds16(xs, u * 64 + 32 * blk + 16 * q, xv);
-#pragma unroll
-                for (int i = 0; i < 16; ++i) bs += static_cast<float>(sbyte(base + 2 + 16 * q + i)) * xv[i];
-            }
-            s += d * bs;
+            for (int k = 0; k < 4; ++k) s += ub(w, k) * x[4 * i + k];
         }
         return s;
+    }
+    __device__ float finish(const float (&pt)[4], const float* s16) const
+    {
+        const float d0 = half_bits_to_float(dw[0] & 0xFFFFu), d1 = half_bits_to_float(dw[8] >> 16);
+        const float* z = s16 + 4 * u;
+        return d0 * ((pt[0] - 128.f * z[0]) + (pt[1] - 128.f * z[1])) +
+               d1 * ((pt[2] - 128.f * z[2]) + (pt[3] - 128.f * z[3]));
     }
 };
 
@@ -153,160 +209,434 @@ struct Unit<kQ8_0> {
 // of qs holds element j (low nibble) and j + 16 (high nibble), value - 8.
 template <>
 struct Unit<kQ4_0> {
+    static constexpr int kRows = 2, kW = 16;
     unsigned dw[9];
-    __device__ void load(const unsigned char* row, int u)
+    int u;
+    __device__ static int xcol(int u0, int, int l, int q, int) { return 64 * (u0 + l) + 16 * q; }
+    __device__ void load(const unsigned char* row, int u0, int, int l)
     {
-        const unsigned* p = reinterpret_cast<const unsigned*>(row + u * 36);
-#pragma unroll
-        for (int i = 0; i < 9; ++i) dw[i] = p[i];
+        u = u0 + l;
+        const unsigned char* p = row + u * 36;
+        load16_a4(p, dw);
+        load16_a4(p + 16, dw + 4);
+        dw[8] = *reinterpret_cast<const unsigned*>(p + 32);
     }
-    __device__ unsigned ubyte(int b) const { return (dw[b >> 2] >> (8 * (b & 3))) & 0xFFu; }
-    __device__ float dot(const float* xs, int u) const
+    __device__ unsigned bytes4(int b) const
     {
+        return (b & 3) == 0 ? dw[b >> 2] : __builtin_amdgcn_alignbyte(dw[(b >> 2) + 1], dw[b >> 2], 2);
+    }
+    __device__ float part(int q, const float (&x)[16]) const
+    {
+        const int base = q < 2 ? 2 : 20;  // qs of block q / 2
+        const int shift = 4 * (q & 1);    // low nibbles, then high
         float s = 0.f;
 #pragma unroll
-        for (int blk = 0; blk < 2; ++blk) {
-            const int base = 18 * blk;
-            const float d = half_bits_to_float(blk == 0 ? (dw[0] & 0xFFFFu) : (dw[4] >> 16));
-            float lo[16], hi[16];
-            lds16(xs, u * 64 + 32 * blk, lo);
-            lds16(xs, u * 64 + 32 * blk + 16, hi);
-            float bs = 0.f;
+        for (int i = 0; i < 4; ++i) {
+            const unsigned w = (bytes4(base + 4 * i) >> shift) & 0x0F0F0F0Fu;
 #pragma unroll
-            for (int j = 0; j < 16; ++j) {
-                const unsigned q = ubyte(base + 2 + j);
-                bs += static_cast<float>(static_cast<int>(q & 0xFu) - 8) * lo[j];
-                bs += static_cast<float>(static_cast<int>(q >> 4) - 8) * hi[j];
-            }
-            s += d * bs;
+            for (int k = 0; k < 4; ++k) s += ub(w, k) * x[4 * i + k];
         }
         return s;
+    }
+    __device__ float finish(const float (&pt)[4], const float* s16) const
+    {
+        const float d0 = half_bits_to_float(dw[0] & 0xFFFFu), d1 = half_bits_to_float(dw[4] >> 16);
+        const float* z = s16 + 4 * u;
+        return d0 * ((pt[0] - 8.f * z[0]) + (pt[1] - 8.f * z[1])) +
+               d1 * ((pt[2] - 8.f * z[2]) + (pt[3] - 8.f * z[3]));
     }
 };
 
 // A quarter of a Q6_K super-block (ql[128] qh[64] scales[16] d; 210 bytes):
-// half h, rows l = 16m .. 16m+15 of that half, i.e. elements
-// 128h + l + {0, 32, 64, 96}, the grouping of the reference's loops.
+// half h, l = 16m .. 16m+15 of that half, i.e. elements 128h + l + 32k for
+// k = 0..3, the grouping of the reference's loops; group k has one scale.
+// Super-blocks start on 2-byte boundaries: each 16-byte run is read as five
+// dwords from the dword boundary below it and shifted into place.
 template <>
 struct Unit<kQ6_K> {
-    unsigned short qla[8], qlb[8], qh[8];  // ql[64h+16m ..], ql[64h+32+16m ..], qh[32h+16m ..]
+    static constexpr int kRows = 2, kW = 16;
+    unsigned qla[4], qlb[4], qh[4];  // ql[64h+16m ..], ql[64h+32+16m ..], qh[32h+16m ..]
     int sc[4];
     float d;
-    __device__ void load(const unsigned char* row, int u)
+    int u;
+    __device__ static int col(int u, int q)
     {
+        return 256 * (u >> 2) + 128 * ((u & 3) >> 1) + 16 * (u & 1) + 32 * q;
+    }
+    __device__ static int xcol(int u0, int, int l, int q, int) { return col(u0 + l, q); }
+    // 16 bytes at p (2-byte aligned); reads stay inside [p - 2, p + 18)
+    __device__ static void load16_a2(const unsigned char* p, unsigned* o)
+    {
+        const unsigned sh = static_cast<unsigned>(reinterpret_cast<uintptr_t>(p)) & 3u;
+        const unsigned char* p4 = p - sh;
+        unsigned t[5];
+        load16_a4(p4, t);
+        t[4] = *reinterpret_cast<const unsigned*>(p4 + 16);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) o[i] = __builtin_amdgcn_alignbyte(t[i + 1], t[i], sh);
+    }
+    __device__ void load(const unsigned char* row, int u0, int, int l)
+    {
+        u = u0 + l;
         const int b = u >> 2, q = u & 3, h = q >> 1, m = q & 1;
         const unsigned char* sb = row + 210 * b;
-        const unsigned short* a = reinterpret_cast<const unsigned short*>(sb + 64 * h + 16 * m);
-        const unsigned short* bb = reinterpret_cast<const unsigned short*>(sb + 64 * h + 32 + 16 * m);
-        const unsigned short* c = reinterpret_cast<const unsigned short*>(sb + 128 + 32 * h + 16 * m);
+        load16_a2(sb + 64 * h + 16 * m, qla);
+        load16_a2(sb + 64 * h + 32 + 16 * m, qlb);
+        load16_a2(sb + 128 + 32 * h + 16 * m, qh);
+        // scales 8h .. 8h+7 (bytes 192+8h ..), then d at 208, as 16-bit loads
+        // (the super-block may end at the end of the buffer, so no dword may
+        // reach past byte 209)
+        const unsigned short* s16 = reinterpret_cast<const unsigned short*>(sb + 192 + 8 * h);
+        unsigned short sw[4];
 #pragma unroll
-        for (int i = 0; i < 8; ++i) {
-            qla[i] = a[i];
-            qlb[i] = bb[i];
-            qh[i] = c[i];
-        }
+        for (int k = 0; k < 4; ++k) sw[k] = s16[k];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) sc[k] = static_cast<signed char>(sb[192 + 8 * h + m + 2 * k]);
+        for (int k = 0; k < 4; ++k) sc[k] = static_cast<signed char>(sw[k] >> (8 * m));
         d = half_bits_to_float(*reinterpret_cast<const unsigned short*>(sb + 208));
     }
-    __device__ float dot(const float* xs, int u) const
+    __device__ float part(int k, const float (&x)[16]) const
     {
-        const int b = u >> 2, q = u & 3, h = q >> 1, m = q & 1;
-        const int c0 = 256 * b + 128 * h + 16 * m;
-        float s4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int k = 0; k < 4; ++k) {
-            float xv[16];
-            lds16(xs, c0 + 32 * k, xv);
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const unsigned la = (qla[i >> 1] >> (8 * (i & 1))) & 0xFFu;
-                const unsigned lb = (qlb[i >> 1] >> (8 * (i & 1))) & 0xFFu;
-                const unsigned hb = (qh[i >> 1] >> (8 * (i & 1))) & 0xFFu;
-                const unsigned lo4 = (k == 0) ? (la & 0xFu) : (k == 1) ? (lb & 0xFu) : (k == 2) ? (la >> 4) : (lb >> 4);
-                const int qv = static_cast<int>(lo4 | (((hb >> (2 * k)) & 3u) << 4)) - 32;
-                s4[k] += static_cast<float>(qv) * xv[i];
-            }
-        }
         float s = 0.f;
 #pragma unroll
-        for (int k = 0; k < 4; ++k) s += d * static_cast<float>(sc[k]) * s4[k];
+        for (int i = 0; i < 4; ++i) {
+            const unsigned la = qla[i], lb = qlb[i], hb = qh[i];
+            // 4 low bits of the four weights of dword i, then their 2 high bits
+            const unsigned lo = (k == 0) ? (la & 0x0F0F0F0Fu) : (k == 1) ? (lb & 0x0F0F0F0Fu)
+                              : (k == 2) ? ((la >> 4) & 0x0F0F0F0Fu) : ((lb >> 4) & 0x0F0F0F0Fu);
+            const unsigned q6 = lo | (((hb >> (2 * k)) & 0x03030303u) << 4);  // 0..63 per byte
+#pragma unroll
+            for (int j = 0; j < 4; ++j) s += ub(q6, j) * x[4 * i + j];
+        }
         return s;
+    }
+    __device__ float finish(const float (&pt)[4], const float* s16) const
+    {
+        float s = 0.f;
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+            s += static_cast<float>(sc[k]) * (pt[k] - 32.f * s16[col(u, k) >> 4]);
+        return d * s;
     }
 };
 
+// ---- cross-lane sums with DPP (no LDS round trips) -----------------------------
+
+template <int kCtrl, int kRowMask>
+__device__ __forceinline__ float dpp_add(float v)
+{
+    // the moved value, or 0 where the source lane is outside the row or the
+    // row is masked off
+    const int moved = __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, kRowMask,
+                                                  0xF, true);
+    return v + __builtin_bit_cast(float, moved);
+}
+
+// Sum over each group of kLanesPerRow (32 or 64) lanes; the total lands in the
+// group's last lane.  Inclusive scans inside 16-lane rows (row_shr 1, 2, 4,
+// 8), then row_bcast15 into rows 1 and 3, and for 64 lanes row_bcast31 into
+// rows 2 and 3.
+template <int kLanesPerRow>
+__device__ __forceinline__ float row_sum(float v)
+{
+    v = dpp_add<0x111, 0xF>(v);  // row_shr:1
+    v = dpp_add<0x112, 0xF>(v);  // row_shr:2
+    v = dpp_add<0x114, 0xF>(v);  // row_shr:4
+    v = dpp_add<0x118, 0xF>(v);  // row_shr:8
+    v = dpp_add<0x142, 0xA>(v);  // row_bcast15 -> rows 1, 3
+    if constexpr (kLanesPerRow == 64) v = dpp_add<0x143, 0xC>(v);  // row_bcast31 -> rows 2, 3
+    return v;
+}
+
 // ---- kernel ------------------------------------------------------------------
 
-template <int kType, int kLanesPerRow>
-__global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
+// The rows one lane group holds in a pass: kRows rows kRowsPerWave apart,
+// located in their segments, with the unit step u0 loaded.  Every lane
+// loads: rows past the end read row 0 of the first segment and lanes without
+// a unit in the step read lane 0's, addresses the wave reads anyway or that
+// sit in cache, so the loads need no branch (a branch around a load makes
+// the compiler wait for every load in flight where the paths join).
+// The segment table in scalar registers (readfirstlane pins each field
+// there).  Segments 1 and 2 are kept as byte offsets from segment 0's
+// pointers, so every address a lane forms derives from a kernel-argument
+// pointer and stays a global-memory access.
+__device__ __forceinline__ int sreg(int v) { return __builtin_amdgcn_readfirstlane(v); }
+__device__ __forceinline__ long long sreg(long long v)
 {
-    extern __shared__ float xs_all[];  // [n_vec][cols]
-    __shared__ float s_red[kThreads / 64][kGemvMaxVec];
+    const unsigned long long u = static_cast<unsigned long long>(v);
+    const unsigned lo = static_cast<unsigned>(sreg(static_cast<int>(static_cast<unsigned>(u))));
+    const unsigned hi = static_cast<unsigned>(sreg(static_cast<int>(static_cast<unsigned>(u >> 32))));
+    return static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo);
+}
+__device__ __forceinline__ long long byte_gap(const void* a, const void* b)
+{
+    return sreg(static_cast<long long>(reinterpret_cast<uintptr_t>(a)) -
+                static_cast<long long>(reinterpret_cast<uintptr_t>(b)));
+}
 
-    // Stage x (rmsnorm'ed when asked) in LDS.
-    for (int v = 0; v < p.n_vec; ++v) {
-        const float* xv = p.x + v * p.x_stride;
-        float* xs = xs_all + v * p.cols;
-        if (p.norm_w) {
-            float ss = 0.f;
-            for (int c = threadIdx.x; c < p.cols; c += kThreads) ss += xv[c] * xv[c];
+struct SegRegs {
+    long long w_off[kGemvMaxSeg], out_off[kGemvMaxSeg];  // bytes from segment 0's
+    long long out_stride[kGemvMaxSeg];
+    int rows[kGemvMaxSeg];
+    int n_seg;
+    long long row_bytes;
+
+    __device__ explicit SegRegs(const GemvParams& p)
+    {
+        static_assert(kGemvMaxSeg == 3, "three segments at most");
 #pragma unroll
-            for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-            if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6][0] = ss;
-            __syncthreads();
-            ss = 0.f;
+        for (int i = 0; i < kGemvMaxSeg; ++i) {
+            w_off[i] = i == 0 ? 0 : byte_gap(p.seg[i].w, p.seg[0].w);
+            out_off[i] = i == 0 ? 0 : byte_gap(p.seg[i].out, p.seg[0].out);
+            out_stride[i] = sreg(p.seg[i].out_stride);
+            rows[i] = sreg(p.seg[i].rows);
+        }
+        n_seg = sreg(p.n_seg);
+        row_bytes = sreg(static_cast<long long>(p.row_bytes));
+    }
+};
+
+template <int kType, int kRows>
+struct RowGroup {
+    Unit<kType> un[kRows];
+    const unsigned char* w[kRows];
+    float* out[kRows];
+    long long out_stride[kRows];
+    bool valid[kRows];
+
+    // Segment lookups select among the segment fields held in scalar
+    // registers (SegRegs) instead of indexing the kernel arguments with a
+    // per-lane segment number, which would turn them into vector loads
+    // waited for behind the weights in flight.
+    __device__ void locate(const GemvParams& p, const SegRegs& sr, int r_first, int spacing)
+    {
 #pragma unroll
-            for (int w = 0; w < kThreads / 64; ++w) ss += s_red[w][0];
-            __syncthreads();
-            const float rms = 1.0f / sqrtf(ss / static_cast<float>(p.cols) + p.eps);
-            for (int c = threadIdx.x; c < p.cols; c += kThreads) xs[c] = xv[c] * rms * p.norm_w[c];
-        } else {
-            for (int c = threadIdx.x; c < p.cols; c += kThreads) xs[c] = xv[c];
+        for (int k = 0; k < kRows; ++k) {
+            const int r = r_first + spacing * k;
+            valid[k] = r < p.total_rows;
+            int rr = valid[k] ? r : 0;
+            const bool in1 = sr.n_seg > 1 && rr >= sr.rows[0];
+            rr = in1 ? rr - sr.rows[0] : rr;
+            const bool in2 = in1 && sr.n_seg > 2 && rr >= sr.rows[1];
+            rr = in2 ? rr - sr.rows[1] : rr;
+            const long long w_off = in2 ? sr.w_off[2] : in1 ? sr.w_off[1] : 0;
+            const long long out_off = in2 ? sr.out_off[2] : in1 ? sr.out_off[1] : 0;
+            w[k] = p.seg[0].w + w_off + static_cast<long long>(rr) * sr.row_bytes;
+            out[k] = reinterpret_cast<float*>(reinterpret_cast<char*>(p.seg[0].out) + out_off) + rr;
+            out_stride[k] = in2 ? sr.out_stride[2] : in1 ? sr.out_stride[1] : sr.out_stride[0];
         }
     }
-    __syncthreads();
+    __device__ void load(int u0, int n, int l)
+    {
+        const int lc = l < n ? l : 0;
+#pragma unroll
+        for (int k = 0; k < kRows; ++k) un[k].load(w[k], u0, n, lc);
+    }
+    // One vector: the pass's first unit step and the outputs' old values
+    // (for the residual add), requested together so that both arrive before
+    // anything requested later.
+    float old[kRows];
+    __device__ void request(const GemvParams& p, const SegRegs& sr, int r_first, int spacing, int n_first,
+                            int l)
+    {
+        locate(p, sr, r_first, spacing);
+        load(0, n_first, l);
+#pragma unroll
+        for (int k = 0; k < kRows; ++k) old[k] = *out[k];
+    }
+};
+
+// y[v][r] (+)= W[r] . x[v].  A pass of a wave covers kRows rows per lane
+// group (kRowsPerWave groups).  kMulti: any number of vectors (one row per
+// group then: the dequantised weights of a row stay in registers across the
+// vectors, and those of several rows would not fit); else exactly one.
+//
+// Pipelining: a wave requests its first pass's weights before x is staged,
+// so the HBM round trip overlaps the staging, and each later pass's weights
+// before it computes the current one (two register buffers, A and B).  The
+// grid holds as many workgroups as fit on the GPU at once, so waves keep
+// loads in flight from start to end.
+template <int kType, int kLanesPerRow, int kRows, bool kMulti>
+__global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
+{
+    static_assert(!kMulti || kRows == 1, "several vectors take one row per lane group");
+    constexpr bool kZeroOffsets = kType == kQ8_0 || kType == kQ4_0 || kType == kQ6_K;
+    extern __shared__ float xs_all[];  // [n_vec][xs_floats(cols)] padded, then [n_vec][cols / 16] run sums
+    __shared__ float s_red[kThreads / 64];
 
     constexpr int kRowsPerWave = 64 / kLanesPerRow;
+    constexpr int kPassRows = kRowsPerWave * kRows;
     const int lane = threadIdx.x & 63;
     const int sub = lane / kLanesPerRow;  // which row of the wave's group
     const int l = lane % kLanesPerRow;
     const int wave = blockIdx.x * (kThreads / 64) + (threadIdx.x >> 6);
     const int n_waves = gridDim.x * (kThreads / 64);
     const int units = p.cols / kUnit;
+    const int n_vec = kMulti ? p.n_vec : 1;
+    const int n_pass = (p.total_rows + kPassRows - 1) / kPassRows;
+    const int n_first = min(kLanesPerRow, units);
 
-    for (int r0 = wave * kRowsPerWave; r0 < p.total_rows; r0 += n_waves * kRowsPerWave) {
-        const int r = r0 + sub;
-        // segment of row r (boundaries are per lane group)
-        int seg = 0, row = r;
-        while (seg + 1 < p.n_seg && row >= p.seg[seg].rows) {
-            row -= p.seg[seg].rows;
-            ++seg;
+    // x for one vector of up to kXRegs x kThreads columns is requested
+    // before the weights (loads complete in order, so anything requested
+    // after the weights could only be used once they have all arrived).
+    constexpr int kXRegs = 8;
+    const bool x_early = !kMulti && p.cols <= kXRegs * kThreads;
+    float xr[kXRegs], nr[kXRegs];
+    if (x_early) {
+        const float* nw = p.norm_w ? p.norm_w : p.x;
+#pragma unroll
+        for (int i = 0; i < kXRegs; ++i) {
+            const int c = threadIdx.x + i * kThreads;
+            const int cc = c < p.cols ? c : 0;
+            xr[i] = p.x[cc];
+            nr[i] = nw[cc];
         }
-        const bool valid = r < p.total_rows;
-        const unsigned char* wrow = p.seg[seg].w + static_cast<long long>(valid ? row : 0) * p.row_bytes;
-        float acc[kGemvMaxVec];
+    }
+
+    const SegRegs sr(p);
+    int ps = wave;
+    RowGroup<kType, kRows> ga;
+    [[maybe_unused]] RowGroup<kType, kRows> gb;
+    if constexpr (kMulti) {
+        ga.locate(p, sr, ps * kPassRows + sub, kRowsPerWave);
+        ga.load(0, n_first, l);
+    } else {
+        ga.request(p, sr, ps * kPassRows + sub, kRowsPerWave, n_first, l);
+    }
+
+    // Stage x in LDS, then rmsnorm's scaling in place (each thread rescales
+    // the elements it wrote).
+    const int xs_len = xs_floats(p.cols);
+    for (int v = 0; v < p.n_vec; ++v) {
+        const float* xv = p.x + v * p.x_stride;
+        float* xs = xs_all + v * xs_len;
+        float ss = 0.f;
+        if (x_early) {
 #pragma unroll
-        for (int v = 0; v < kGemvMaxVec; ++v) acc[v] = 0.f;
-        if (valid) {
-            for (int u = l; u < units; u += kLanesPerRow) {
-                Unit<kType> un;
-                un.load(wrow, u);
-#pragma unroll
-                for (int v = 0; v < kGemvMaxVec; ++v)
-                    if (v < p.n_vec) acc[v] += un.dot(xs_all + v * p.cols, u);
+            for (int i = 0; i < kXRegs; ++i) {
+                const int c = threadIdx.x + i * kThreads;
+                if (c < p.cols) {
+                    xs[xpad(c)] = xr[i];
+                    ss += xr[i] * xr[i];
+                }
+            }
+        } else {
+            for (int c = threadIdx.x; c < p.cols; c += kThreads) {
+                const float t = xv[c];
+                xs[xpad(c)] = t;
+                ss += t * t;
             }
         }
+        if (p.norm_w) {
 #pragma unroll
-        for (int v = 0; v < kGemvMaxVec; ++v) {
-            if (v >= p.n_vec) break;
-            float t = acc[v];
+            for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
+            if (lane == 0) s_red[threadIdx.x >> 6] = ss;
+            __syncthreads();
+            ss = 0.f;
 #pragma unroll
-            for (int o = kLanesPerRow / 2; o >= 1; o >>= 1) t += __shfl_xor(t, o);
-            if (valid && l == 0) {
-                float* dst = p.seg[seg].out + v * p.seg[seg].out_stride + row;
-                *dst = p.add ? *dst + t : t;
+            for (int w = 0; w < kThreads / 64; ++w) ss += s_red[w];
+            __syncthreads();  // s_red is reused by the next vector
+            const float rms = 1.0f / sqrtf(ss / static_cast<float>(p.cols) + p.eps);
+            if (x_early) {
+#pragma unroll
+                for (int i = 0; i < kXRegs; ++i) {
+                    const int c = threadIdx.x + i * kThreads;
+                    if (c < p.cols) xs[xpad(c)] = xr[i] * rms * nr[i];
+                }
+            } else {
+                for (int c = threadIdx.x; c < p.cols; c += kThreads)
+                    xs[xpad(c)] = xs[xpad(c)] * rms * p.norm_w[c];
             }
         }
+    }
+    __syncthreads();
+    float* const s16_all = xs_all + p.n_vec * xs_len;
+    const int nb16 = p.cols / 16;
+    if constexpr (kZeroOffsets) {
+        // sums of x over each run of 16 columns
+        for (int i = threadIdx.x; i < p.n_vec * nb16; i += kThreads) {
+            const int v = i / nb16, b = i - v * nb16;
+            const float* xb = xs_all + v * xs_len + xpad(16 * b);
+            float t = 0.f;
+#pragma unroll
+            for (int j = 0; j < 16; ++j) t += xb[j];
+            s16_all[i] = t;
+        }
+        __syncthreads();
+    }
+
+    // One pass over the rows in g (its first unit step already loaded).
+    auto run_pass = [&](RowGroup<kType, kRows>& g) {
+        float acc[kRows][kGemvMaxVec];
+#pragma unroll
+        for (int k = 0; k < kRows; ++k)
+#pragma unroll
+            for (int v = 0; v < kGemvMaxVec; ++v) acc[k][v] = 0.f;
+        for (int u0 = 0; u0 < units; u0 += kLanesPerRow) {
+            const int n = min(kLanesPerRow, units - u0);
+            if (u0 > 0) g.load(u0, n, l);
+            if (l >= n) continue;
+#pragma unroll 1
+            for (int v = 0; v < n_vec; ++v) {
+                const float* xs = xs_all + v * xs_len;
+                float pt[kRows][4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    constexpr int kW = Unit<kType>::kW;
+                    float xv[16];
+#pragma unroll
+                    for (int j = 0; j < 16 / kW; ++j)
+                        lds_x<kW>(xs, Unit<kType>::xcol(u0, n, l, q, j), xv + kW * j);
+#pragma unroll
+                    for (int k = 0; k < kRows; ++k) pt[k][q] = g.un[k].part(q, xv);
+                }
+                const float* s16 = s16_all + v * nb16;
+#pragma unroll
+                for (int k = 0; k < kRows; ++k) {
+                    const float f = g.un[k].finish(pt[k], s16);
+#pragma unroll
+                    for (int vv = 0; vv < kGemvMaxVec; ++vv)
+                        if (vv == v) acc[k][vv] += f;
+                }
+            }
+        }
+        // The group's last lane stores; the old values were read with the
+        // pass's request (one vector) or here (several).
+#pragma unroll
+        for (int k = 0; k < kRows; ++k) {
+#pragma unroll
+            for (int v = 0; v < kGemvMaxVec; ++v) {
+                if (v >= n_vec) break;
+                const float t = row_sum<kLanesPerRow>(acc[k][v]);
+                float* o = g.out[k] + v * g.out_stride[k];
+                const float old = kMulti ? *o : g.old[k];
+                if (g.valid[k] && l == kLanesPerRow - 1) *o = p.add ? old + t : t;
+            }
+        }
+    };
+
+    if constexpr (kMulti) {
+        // One buffer: with several vectors a pass computes long enough per
+        // byte, and two buffers of weights would not fit in registers.
+        while (ps < n_pass) {
+            run_pass(ga);
+            ps += n_waves;
+            if (ps >= n_pass) break;
+            ga.locate(p, sr, ps * kPassRows + sub, kRowsPerWave);
+            ga.load(0, n_first, l);
+        }
+        return;
+    }
+    // Passes ps, ps + n_waves, ... alternate between the buffers; the next
+    // pass's request goes out before the current pass is computed.  Past the
+    // last pass the request reads row 0 again (locate maps it there).
+    while (ps < n_pass) {
+        gb.request(p, sr, (ps + n_waves) * kPassRows + sub, kRowsPerWave, n_first, l);
+        run_pass(ga);
+        ps += n_waves;
+        if (ps >= n_pass) break;
+        ga.request(p, sr, (ps + n_waves) * kPassRows + sub, kRowsPerWave, n_first, l);
+        run_pass(gb);
+        ps += n_waves;
     }
 }
 
@@ -333,19 +663,61 @@ __global__ __launch_bounds__(kThreads) void vec_add_kernel(float* out, const flo
     if (i < size) out[i] += x[i];
 }
 
+// Workgroups of one kernel that fit on the current device at once (its CU
+// count x the occupancy the kernel's registers and LDS allow), cached per
+// device and LDS size.
+template <typename Kernel>
+int resident_blocks(Kernel kernel, size_t lds)
+{
+    struct Entry {
+        int device = -1;
+        size_t lds = 0;
+        int blocks = 0;
+    };
+    static thread_local Entry cache[4];
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return 256;
+    for (const Entry& e : cache)
+        if (e.device == dev && e.lds == lds) return e.blocks;
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess)
+        return 256;
+    const int blocks = std::max(1, cus * std::max(1, per_cu));
+    static thread_local int next = 0;
+    cache[next] = Entry{dev, lds, blocks};
+    next = (next + 1) % 4;
+    return blocks;
+}
+
+template <int kType, int kLanes, int kRows, bool kMulti>
+hipError_t launch_shaped(const GemvParams& p, hipStream_t s)
+{
+    const size_t lds = static_cast<size_t>(p.n_vec) * (xs_floats(p.cols) + p.cols / 16) * sizeof(float);
+    constexpr int kPassRowsPerBlock = (kThreads / 64) * (64 / kLanes) * kRows;
+    const int needed = (p.total_rows + kPassRowsPerBlock - 1) / kPassRowsPerBlock;
+    const auto kernel = gemv_kernel<kType, kLanes, kRows, kMulti>;
+    const int blocks = std::min(needed, resident_blocks(kernel, lds));
+    hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), lds, s, p);
+    return hipGetLastError();
+}
+
+// Lanes per row: 32 when a row has at most 32 units (cols <= 2048), else
+// 64.  Rows per lane group: the format's kRows with one vector when the rows
+// still give every resident wave a pass, else 1.
 template <int kType>
 hipError_t launch_typed(const GemvParams& p, hipStream_t s)
 {
-    const int units = p.cols / kUnit;
-    const size_t lds = static_cast<size_t>(p.n_vec) * p.cols * sizeof(float);
-    const int rows_per_wg = (kThreads / 64) * (units <= 32 ? 2 : 1);
-    int blocks = (p.total_rows + rows_per_wg - 1) / rows_per_wg;
-    if (blocks > 2048) blocks = 2048;
-    if (units <= 32)
-        hipLaunchKernelGGL((gemv_kernel<kType, 32>), dim3(blocks), dim3(kThreads), lds, s, p);
-    else
-        hipLaunchKernelGGL((gemv_kernel<kType, 64>), dim3(blocks), dim3(kThreads), lds, s, p);
-    return hipGetLastError();
+    const bool narrow = p.cols / kUnit <= 32;
+    if (p.n_vec > 1)
+        return narrow ? launch_shaped<kType, 32, 1, true>(p, s) : launch_shaped<kType, 64, 1, true>(p, s);
+    constexpr int kR = Unit<kType>::kRows;
+    if constexpr (kR > 1) {
+        const int passes = (p.total_rows + kR - 1) / kR / (narrow ? 2 : 1);  // wave passes
+        if (passes >= 4 * 256 * 4)
+            return narrow ? launch_shaped<kType, 32, kR, false>(p, s) : launch_shaped<kType, 64, kR, false>(p, s);
+    }
+    return narrow ? launch_shaped<kType, 32, 1, false>(p, s) : launch_shaped<kType, 64, 1, false>(p, s);
 }
 
 }  // namespace
