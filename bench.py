@@ -24,7 +24,8 @@ Other workloads (--workload): decode_long (16384 context, batch 8, 22 layers),
 decode_ragged (64 sequences, L in [256, 2048], 22 layers), prefill,
 decode_single (one layer, position 127: reported as latency), proj (the
 attention block's projections for a 22-layer decode step, and the GEMV kernel
-on a 32000 x 2048 matrix in every weight format), copy (the
+on a 32000 x 2048 matrix in every weight format), matmul (that GEMV alone in
+one format, --wtype), copy (the
 device copy kernel, used to calibrate rocprofv3 byte counters) and read (a
 plain library reduction over 6 GiB: what HBM delivers to a read stream, the
 practical ceiling the decode figures sit under).
@@ -128,6 +129,30 @@ def kernel_avg_ms(eng, step, steps, kernel_id, start=0):
     total, n = eng.profile_read(kernel_id)
     eng.profile(False)
     return total / max(n, 1), n
+
+
+def back_to_back_ms(eng, launch, steps, blocker_ms=1.0):
+    """Average GPU time of `steps` launches queued back to back: a blocker
+    (large F32 matrix-vector products, about blocker_ms of GPU work) is
+    queued first, so that the host has queued every timed launch before the
+    GPU reaches them and the timed region holds no host gaps.  The events
+    bracket only the timed launches."""
+    rows, cols = 8192, 8192  # 256 MiB of F32 weights, ~45 us per launch
+    wb = eng.array((rows * cols * 4,), np.uint8)
+    xb = eng.array(np.zeros(cols, np.float32))
+    ob = eng.array((rows,))
+    n_block = max(1, int(blocker_ms / 0.045))
+    eng.synchronize()
+    for _ in range(n_block):
+        eng.matmul(ob.ptr, wb.ptr, xb.ptr, rows, cols, W.W_F32)
+    eng.event(0)
+    for i in range(steps):
+        launch(i)
+    eng.event(1)
+    eng.synchronize()
+    for a in (wb, xb, ob):
+        a.free()
+    return eng.elapsed(0, 1) / steps
 
 
 def make_decode_case(workload, n_layers=22):
@@ -355,46 +380,20 @@ def run_proj(steps, warmup, n_layers=22, wtype=W.W_F16):
             eng.attn_out(1, x.ptr, L["wo"].ptr, xb2.ptr, wtype)
 
     ms = time_steps(eng, step, steps, warmup)
+    # the same steps queued behind a blocker: the GPU's own time per step
+    # (a step is 44 Python calls, about 5 us of host time each)
+    dev_ms = back_to_back_ms(eng, step, steps, blocker_ms=steps * 2 * n_layers * 0.008)
     k_ms, k_n = kernel_avg_ms(eng, step, max(2, steps // 5), tla.KERNEL_GEMV)
-    dev_ms = k_ms * 2 * n_layers  # the step's kernels back to back
     log(f"[bench] proj {W.W_NAMES[wtype]} x {n_layers} layers, batch 1: {ms * 1e3:.1f} us/step "
-        f"end to end, {step_bytes / 1e6:.0f} MB of weights -> {step_bytes / ms / 1e6:.0f} GB/s; "
-        f"{2 * n_layers} launches of {k_ms * 1e3:.2f} us -> {step_bytes / dev_ms / 1e6:.0f} GB/s "
-        f"in-kernel")
+        f"as issued from Python, {dev_ms * 1e3:.1f} us/step queued back to back; "
+        f"{step_bytes / 1e6:.0f} MB of weights -> {step_bytes / dev_ms / 1e6:.0f} GB/s; "
+        f"per-launch events {k_ms * 1e3:.2f} us")
     for a in arrays:
         a.free()
     # the GEMV kernel alone on one large matrix, each format
     big = {}
-    rows = 32000
     for t in (W.W_F32, W.W_F16, W.W_Q8_0, W.W_Q4_0, W.W_Q6_K):
-        wd = eng.array(W.make_weights(t, rows, embd, salt=99))
-        xd = eng.array(rg.standard_normal(embd).astype(np.float32))
-        od = eng.array((rows,))
-        nbytes = W.weight_row_bytes(t, embd) * rows
-        copies = 1
-        extra = []
-        if nbytes < 300e6:  # rotate copies so the working set exceeds the Infinity Cache
-            copies = int(np.ceil(300e6 / nbytes))
-            extra = [eng.array(W.make_weights(t, rows, embd, salt=100 + c)) for c in range(copies - 1)]
-        ws = [wd] + extra
-
-        def one(i):
-            eng.matmul(od.ptr, ws[i % copies].ptr, xd.ptr, rows, embd, t)
-
-        # One launch per Python call is host-bound here (the call costs more
-        # than the kernel), so the kernel's own duration comes from the HIP
-        # event pair around each launch.
-        for i in range(warmup):
-            one(i)
-        t_ms, _ = kernel_avg_ms(eng, one, steps, tla.KERNEL_GEMV)
-        big[W.W_NAMES[t]] = {"us": round(t_ms * 1e3, 2), "bytes": nbytes,
-                             "GB_s": round(nbytes / t_ms / 1e6, 1),
-                             "frac": round(nbytes / t_ms / 1e6 / HBM_PEAK_GBS, 4)}
-        log(f"[bench] matmul {W.W_NAMES[t]} {rows}x{embd}: {t_ms * 1e3:.1f} us, "
-            f"{nbytes / t_ms / 1e6:.0f} GB/s ({nbytes / t_ms / 1e6 / HBM_PEAK_GBS:.1%}), "
-            f"{copies} rotated copies")
-        for a in [wd, xd, od] + extra:
-            a.free()
+        big[W.W_NAMES[t]] = matmul_kernel(eng, t, steps, warmup)
     eng.close()
     value = step_bytes / (dev_ms * 1e-3) / 1e9
     return {"workload": "proj", "metric": "attention-block projection weight GB/s (% HBM peak)",
@@ -405,6 +404,52 @@ def run_proj(steps, warmup, n_layers=22, wtype=W.W_F16):
                          "traffic": profiled_traffic("gemv_kernel", "matmul_q8_0"),
                          "kernel": "gemv_kernel", "config": "matmul q8_0 32000x2048"},
             "matmul_32000x2048": big}
+
+
+def matmul_kernel(eng, t, steps, warmup, rows=32000, cols=2048):
+    """The GEMV kernel alone on a vocabulary-sized matrix (rows x cols, the
+    output projection's shape) in weight format t, with enough rotated
+    copies of the weights to exceed the Infinity Cache; timed per launch."""
+    rg = np.random.default_rng(1)
+    wd = eng.array(W.make_weights(t, rows, cols, salt=99))
+    xd = eng.array(rg.standard_normal(cols).astype(np.float32))
+    od = eng.array((rows,))
+    nbytes = W.weight_row_bytes(t, cols) * rows
+    copies = 1
+    extra = []
+    if nbytes < 300e6:
+        copies = int(np.ceil(300e6 / nbytes))
+        extra = [eng.array(W.make_weights(t, rows, cols, salt=100 + c)) for c in range(copies - 1)]
+    ws = [wd] + extra
+
+    def one(i):
+        eng.matmul(od.ptr, ws[i % copies].ptr, xd.ptr, rows, cols, t)
+
+    # A Python call per launch costs about as much as the kernel, so the
+    # launches are queued behind a blocker and timed back to back; the HIP
+    # event pair around each launch (which adds the events' own cost) is
+    # reported beside.
+    for i in range(warmup):
+        one(i)
+    t_ms = back_to_back_ms(eng, one, steps)
+    ev_ms, _ = kernel_avg_ms(eng, one, steps, tla.KERNEL_GEMV)
+    out = {"us": round(t_ms * 1e3, 2), "bytes": nbytes, "GB_s": round(nbytes / t_ms / 1e6, 1),
+           "frac": round(nbytes / t_ms / 1e6 / HBM_PEAK_GBS, 4), "ms": t_ms,
+           "per_launch_event_us": round(ev_ms * 1e3, 2)}
+    log(f"[bench] matmul {W.W_NAMES[t]} {rows}x{cols}: {t_ms * 1e3:.1f} us back to back, "
+        f"{nbytes / t_ms / 1e6:.0f} GB/s ({nbytes / t_ms / 1e6 / HBM_PEAK_GBS:.1%}), "
+        f"{copies} rotated copies; per-launch events {ev_ms * 1e3:.1f} us")
+    for a in [wd, xd, od] + extra:
+        a.free()
+    return out
+
+
+def run_matmul(steps, warmup, name):
+    t = {v: k for k, v in W.W_NAMES.items()}[name]
+    eng = tla.Engine(tla.Config.tinyllama(n_layers=1, n_ctx=16))
+    r = matmul_kernel(eng, t, steps, warmup)
+    eng.close()
+    return r
 
 
 def run_read(steps, warmup, nbytes=6 << 30):
@@ -437,7 +482,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode_model",
                     choices=["decode_model", "decode_long", "decode_ragged", "decode_single",
-                             "prefill", "proj", "copy", "read"])
+                             "prefill", "proj", "matmul", "copy", "read"])
+    ap.add_argument("--wtype", default="q8_0", choices=["f32", "f16", "q8_0", "q4_0", "q6_k"],
+                    help="weight format of the matmul workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill half")
     ap.add_argument("--split", type=int, default=0, help="decode split length (0 = auto)")
@@ -456,6 +503,19 @@ def main():
         return
     if args.workload == "read":
         print(json.dumps(run_read(args.steps, args.warmup)))
+        return
+    if args.workload == "matmul":
+        r = run_matmul(args.steps, args.warmup, args.wtype)
+        line = {"metric": "GEMV weight GB/s", "value": r["GB_s"], "unit": "GB/s", "n_gpus": 1,
+                "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(r["ms"], 5),
+                "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+                "dtype": args.wtype, "data": "synthetic",
+                "config": {"workload": "matmul", "rows": 32000, "cols": 2048, "weights": args.wtype,
+                           "batch": 1, "parallelism": "none"},
+                "roofline": {"bound": "hbm", "achieved": r["GB_s"], "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                             "frac": r["frac"],
+                             "traffic": profiled_traffic("gemv_kernel", f"matmul_{args.wtype}")}}
+        print(json.dumps(line))
         return
     if args.workload == "proj":
         p = run_proj(args.steps, args.warmup)

@@ -232,7 +232,10 @@ struct Unit<kQ4_0> {
         float s = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-            const unsigned w = (bytes4(base + 4 * i) >> shift) & 0x0F0F0F0Fu;
+            unsigned w = (bytes4(base + 4 * i) >> shift) & 0x0F0F0F0Fu;
+            // keep the four nibbles as one masked word: left visible, the
+            // compiler folds the mask into a bit-field extract per weight
+            asm volatile("" : "+v"(w));
 #pragma unroll
             for (int k = 0; k < 4; ++k) s += ub(w, k) * x[4 * i + k];
         }
