@@ -200,13 +200,93 @@ int tla_attn_qkv(tla_engine* e, int n_seq, float* q_dev, float* k_dev, float* v_
 int tla_attn_out(tla_engine* e, int n_seq, float* x_dev, const void* wo_dev,
                  const float* xb2_dev, int type);
 
+/* ---- the rest of a layer, and the whole forward pass ------------------ */
+
+/* silu() src/ops.h:118: x = x * (1 / (1 + exp(-x))) in place. */
+int tla_silu(tla_engine* e, float* x_dev, int size);
+
+/* elementwise_mul() src/ops.h:131: a[i] *= b[i]. */
+int tla_elementwise_mul(tla_engine* e, float* a_dev, const float* b_dev, int size);
+
+/* ffn_swiglu() src/ops.h:232-235: out = W_down . (silu(W_gate . in) *
+ * (W_up . in)).  hb, hb2 [n_ff] are left as the reference leaves them (the
+ * gated projection, the up projection).  W_gate, W_up [n_ff][n_embd],
+ * W_down [n_embd][n_ff], all of one type (the reference passes one type). */
+int tla_ffn_swiglu(tla_engine* e, float* out_dev, const float* in_dev, float* hb_dev,
+                   float* hb2_dev, const void* w_gate_dev, const void* w_up_dev,
+                   const void* w_down_dev, int n_ff, int n_embd, int type);
+
+/* The FFN half of a layer (src/forward.cpp:215-228) for n_seq sequences:
+ * x += ffn_swiglu(rmsnorm(x, norm_w, eps)), in two launches (rmsnorm + gate
+ * and up projections; SiLU, gating, down projection and the residual add).
+ * x [n_seq][n_embd]; hb_dev scratch [n_seq][2][n_ff] receives the raw gate
+ * and up projections. */
+int tla_ffn_block(tla_engine* e, int n_seq, float* x_dev, const float* norm_w_dev, float eps,
+                  const void* w_gate_dev, const void* w_up_dev, const void* w_down_dev, int n_ff,
+                  int type, float* hb_dev);
+
+/* embed_token() src/forward.cpp:17-134: out = row `token` of the embedding
+ * table [n_vocab][n_embd] (any of the five types), dequantised with the
+ * reference's expressions (bit-exact). */
+int tla_embed(tla_engine* e, float* out_dev, const void* table_dev, int token, int n_embd,
+              int type);
+
+/* sample_argmax() src/ops.h:249: the first index of the largest logit. */
+int tla_argmax(tla_engine* e, const float* logits_dev, int n_vocab, int* token_host);
+
+/* The weights forward() reads from the GGUF file (src/forward.cpp:167-266),
+ * as device pointers to the tensors' unchanged bytes (16-byte aligned) and
+ * their ggml_type ids.  `output` is token_embd when the file has no
+ * output.weight (tied embeddings, src/forward.cpp:250-258). */
+typedef struct tla_layer_weights {
+    const float* attn_norm;            /* [n_embd] F32 */
+    const void *wq, *wk, *wv, *wo;
+    int type_q, type_k, type_v, type_o;
+    const float* ffn_norm;             /* [n_embd] F32 */
+    const void *w_gate, *w_up, *w_down;
+    int type_ffn;                      /* one type for the three, as ffn_swiglu takes */
+} tla_layer_weights;
+
+typedef struct tla_model {
+    int n_ff, n_vocab;
+    float rms_norm_eps;
+    const void* token_embd;
+    int type_embd;
+    const float* output_norm;          /* [n_embd] F32 */
+    const void* output;
+    int type_output;
+    const tla_layer_weights* layers;   /* host array [cfg.n_layers] */
+} tla_model;
+
+/* forward() src/forward.cpp:167-266 for one token at position pos: the
+ * embedding, every layer (rmsnorm + Q/K/V, RoPE + append + attention, W_o +
+ * residual, rmsnorm + SwiGLU FFN + residual) and the classifier, on the
+ * device: logits_dev [n_vocab].  Caches as from tla_kv_cache_alloc (one
+ * sequence); the residual stream and scratch are the engine's.  5 launches
+ * per layer + 2. */
+int tla_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* value_cache_dev,
+                int token, int pos, float* logits_dev);
+
+/* The generation loop with greedy sampling (src/generate.cpp:56-100 at
+ * temperature 0, without the tokenizer): forward() over the prompt at
+ * positions 0..n_prompt-1, then n_gen tokens each from the argmax of the
+ * previous logits.  The sampled token stays on the device between steps,
+ * so every launch is queued without waiting; tokens_host [n_gen] is
+ * written at the end.  The caller stops at its EOS token, as the reference
+ * does (tokens after it are computed but not used).  Needs n_prompt >= 1
+ * and n_prompt + n_gen - 1 <= n_ctx. */
+int tla_generate_greedy(tla_engine* e, const tla_model* m, float* key_cache_dev,
+                        float* value_cache_dev, const int* prompt_host, int n_prompt, int n_gen,
+                        int* tokens_host);
+
 /* ---- measurement hooks (no reference counterpart) ------------------- */
 enum tla_kernel_id {
     TLA_KERNEL_DECODE = 0,  /* split-KV decode attention: RoPE + append +
                                attention + split merge, one launch           */
     TLA_KERNEL_PREFILL = 1, /* causal MFMA prefill attention                 */
     TLA_KERNEL_APPEND = 2,  /* prefill RoPE + cache append                   */
-    TLA_KERNEL_GEMV = 3,    /* projections: matmul / attn_qkv / attn_out     */
+    TLA_KERNEL_GEMV = 3,    /* projections: matmul / attn_qkv / attn_out /
+                               ffn / classifier                              */
     TLA_KERNEL_COUNT = 4
 };
 /* When enabled, HIP events bracket every launch of each kernel on the

@@ -9,6 +9,9 @@ Two libraries:
                        attention (tl_oracle.c, see its header for citations)
   _ref/libref_ops.so   the reference's own src/ops.cpp, compiled by
                        oracle/Makefile where /root/reference exists; optional.
+  _ref/libref_forward.so  the reference's forward pass and GGUF loader
+                       (forward.cpp, gguf_model.cpp, tokenizer.cpp, ops.cpp),
+                       same origin; optional.
 """
 from __future__ import annotations
 
@@ -21,6 +24,7 @@ import numpy as np
 HERE = os.path.dirname(os.path.abspath(__file__))
 ORACLE_SO = os.path.join(HERE, "liboracle.so")
 REF_SO = os.path.join(HERE, "_ref", "libref_ops.so")
+REF_FWD_SO = os.path.join(HERE, "_ref", "libref_forward.so")
 REF_SRC = "/root/reference/src"
 
 _fp = C.POINTER(C.c_float)
@@ -85,6 +89,17 @@ def oracle() -> C.CDLL:
         lib.oracle_matmul.restype = C.c_int
         lib.oracle_rmsnorm.argtypes = [_fp, _fp, _fp, C.c_int, C.c_float]
         lib.oracle_vec_add.argtypes = [_fp, _fp, C.c_int]
+        lib.oracle_silu.argtypes = [_fp, C.c_int]
+        lib.oracle_elementwise_mul.argtypes = [_fp, _fp, C.c_int]
+        lib.oracle_ffn_swiglu.argtypes = [_fp, _fp, _fp, _fp, C.c_void_p, C.c_void_p, C.c_void_p,
+                                          C.c_int, C.c_int, C.c_int]
+        lib.oracle_ffn_swiglu.restype = C.c_int
+        lib.oracle_embed.argtypes = [_fp, C.c_void_p, C.c_int, C.c_int, C.c_int]
+        lib.oracle_embed.restype = C.c_int
+        lib.oracle_argmax.argtypes = [_fp, C.c_int]
+        lib.oracle_argmax.restype = C.c_int
+        lib.oracle_forward.argtypes = [C.c_void_p, _fp, _fp, _fp, C.c_int, C.c_int, _fp]
+        lib.oracle_forward.restype = C.c_int
         _oracle = lib
     return _oracle
 
@@ -113,6 +128,12 @@ def ref() -> C.CDLL:
         lib.ref_vec_add.argtypes = [_fp, _fp, C.c_int]
         lib.ref_fp16_to_f32.argtypes = [C.c_uint16]
         lib.ref_fp16_to_f32.restype = C.c_float
+        lib.ref_silu.argtypes = [_fp, C.c_int]
+        lib.ref_elementwise_mul.argtypes = [_fp, _fp, C.c_int]
+        lib.ref_ffn_swiglu.argtypes = [_fp, _fp, _fp, _fp, C.c_void_p, C.c_void_p, C.c_void_p,
+                                       C.c_int, C.c_int, C.c_int]
+        lib.ref_argmax.argtypes = [_fp, C.c_int]
+        lib.ref_argmax.restype = C.c_int
         _ref = lib
     return _ref
 
@@ -249,3 +270,147 @@ def vec_add(out: np.ndarray, x: np.ndarray, lib=None) -> np.ndarray:
     x = np.ascontiguousarray(x, dtype=np.float32)
     (oracle().oracle_vec_add if lib is None else lib.ref_vec_add)(fptr(out), fptr(x), out.size)
     return out
+
+
+# ---- FFN, embedding, whole forward pass ------------------------------------
+
+def silu(x: np.ndarray, lib=None) -> np.ndarray:
+    x = np.ascontiguousarray(x, dtype=np.float32).copy()
+    (oracle().oracle_silu if lib is None else lib.ref_silu)(fptr(x), x.size)
+    return x
+
+
+def ffn_swiglu(x, w_gate, w_up, w_down, n_ff, n_embd, wtype, lib=None):
+    """(out, hb, hb2) of ffn_swiglu(); weights are raw bytes."""
+    x = np.ascontiguousarray(x, dtype=np.float32)
+    out = np.zeros(n_embd, np.float32)
+    hb, hb2 = np.zeros(n_ff, np.float32), np.zeros(n_ff, np.float32)
+    ws = [np.ascontiguousarray(w, np.uint8) for w in (w_gate, w_up, w_down)]
+    f = oracle().oracle_ffn_swiglu if lib is None else lib.ref_ffn_swiglu
+    rc = f(fptr(out), fptr(x), fptr(hb), fptr(hb2), ws[0].ctypes.data, ws[1].ctypes.data,
+           ws[2].ctypes.data, n_ff, n_embd, wtype)
+    assert lib is not None or rc == 0
+    return out, hb, hb2
+
+
+def embed(table, token: int, n_embd: int, wtype: int) -> np.ndarray:
+    out = np.zeros(n_embd, np.float32)
+    table = np.ascontiguousarray(table, np.uint8)
+    assert oracle().oracle_embed(fptr(out), table.ctypes.data, token, n_embd, wtype) == 0
+    return out
+
+
+class _Layer(C.Structure):
+    _fields_ = [("attn_norm", C.c_void_p), ("wq", C.c_void_p), ("wk", C.c_void_p),
+                ("wv", C.c_void_p), ("wo", C.c_void_p), ("type_q", C.c_int), ("type_k", C.c_int),
+                ("type_v", C.c_int), ("type_o", C.c_int), ("ffn_norm", C.c_void_p),
+                ("w_gate", C.c_void_p), ("w_up", C.c_void_p), ("w_down", C.c_void_p),
+                ("type_ffn", C.c_int)]
+
+
+class _Model(C.Structure):
+    _fields_ = [("n_layers", C.c_int), ("n_embd", C.c_int), ("n_head", C.c_int),
+                ("n_head_kv", C.c_int), ("n_ff", C.c_int), ("n_vocab", C.c_int), ("n_ctx", C.c_int),
+                ("rope_freq_base", C.c_float), ("rms_norm_eps", C.c_float),
+                ("token_embd", C.c_void_p), ("type_embd", C.c_int), ("output_norm", C.c_void_p),
+                ("output", C.c_void_p), ("type_output", C.c_int), ("layers", C.POINTER(_Layer))]
+
+
+class Model:
+    """The oracle's forward() over a model given as {name: (dims, type, raw
+    bytes)} (workloads.make_model); keeps its own KV cache, like a RunState."""
+
+    def __init__(self, spec, tensors):
+        self.spec, self.t = spec, {k: (d, ty, np.ascontiguousarray(r, np.uint8))
+                                   for k, (d, ty, r) in tensors.items()}
+        ptr = lambda n: self.t[n][2].ctypes.data  # noqa: E731
+        ty = lambda n: self.t[n][1]  # noqa: E731
+        L = (_Layer * spec.n_layers)()
+        for l in range(spec.n_layers):
+            p = f"blk.{l}."
+            L[l] = _Layer(ptr(p + "attn_norm.weight"), ptr(p + "attn_q.weight"),
+                          ptr(p + "attn_k.weight"), ptr(p + "attn_v.weight"),
+                          ptr(p + "attn_output.weight"), ty(p + "attn_q.weight"),
+                          ty(p + "attn_k.weight"), ty(p + "attn_v.weight"),
+                          ty(p + "attn_output.weight"), ptr(p + "ffn_norm.weight"),
+                          ptr(p + "ffn_gate.weight"), ptr(p + "ffn_up.weight"),
+                          ptr(p + "ffn_down.weight"), ty(p + "ffn_gate.weight"))
+        out_name = "output.weight" if "output.weight" in self.t else "token_embd.weight"
+        self._layers = L
+        self._m = _Model(spec.n_layers, spec.n_embd, spec.n_head, spec.n_head_kv, spec.n_ff,
+                         spec.n_vocab, spec.n_ctx, spec.rope_freq_base, spec.rms_norm_eps,
+                         ptr("token_embd.weight"), ty("token_embd.weight"),
+                         ptr("output_norm.weight"), ptr(out_name), ty(out_name), L)
+        cache = spec.n_layers * spec.n_ctx * spec.kv_dim
+        self.kc, self.vc = np.zeros(cache, np.float32), np.zeros(cache, np.float32)
+        self.scratch = np.zeros(5 * spec.n_embd + 2 * spec.kv_dim + spec.n_ctx + 2 * spec.n_ff,
+                                np.float32)
+
+    def forward(self, token: int, pos: int) -> np.ndarray:
+        logits = np.zeros(self.spec.n_vocab, np.float32)
+        rc = oracle().oracle_forward(C.addressof(self._m), fptr(self.kc), fptr(self.vc),
+                                     fptr(self.scratch), token, pos, fptr(logits))
+        assert rc == 0
+        return logits
+
+    def tokens(self, tokens) -> np.ndarray:
+        """Logits [n][n_vocab] of forward() at positions 0..n-1."""
+        return np.stack([self.forward(int(t), i) for i, t in enumerate(tokens)])
+
+    def greedy(self, prompt, n_gen: int):
+        """The prompt loop, then argmax decoding (src/generate.cpp:56-100)."""
+        pos = 0
+        for t in prompt:
+            logits = self.forward(int(t), pos)
+            pos += 1
+        out = []
+        nxt = int(oracle().oracle_argmax(fptr(logits), logits.size))
+        for i in range(n_gen):
+            out.append(nxt)
+            if i + 1 == n_gen:
+                break
+            logits = self.forward(nxt, pos)
+            pos += 1
+            nxt = int(oracle().oracle_argmax(fptr(logits), logits.size))
+        return out
+
+
+_ref_fwd = None
+
+
+def ref_forward_available() -> bool:
+    return os.path.exists(REF_FWD_SO)
+
+
+def ref_forward():
+    """The reference's own forward pass over a GGUF file (oracle/_ref)."""
+    global _ref_fwd
+    if _ref_fwd is None:
+        lib = C.CDLL(REF_FWD_SO)
+        lib.ref_forward_error.restype = C.c_char_p
+        lib.ref_forward_tokens.argtypes = [C.c_char_p, _ip, C.c_int, _fp, _ip]
+        lib.ref_forward_tokens.restype = C.c_int
+        lib.ref_generate_greedy.argtypes = [C.c_char_p, _ip, C.c_int, C.c_int, _ip]
+        lib.ref_generate_greedy.restype = C.c_int
+        _ref_fwd = lib
+    return _ref_fwd
+
+
+def ref_forward_tokens(path: str, tokens, n_vocab: int) -> np.ndarray:
+    lib = ref_forward()
+    toks = np.ascontiguousarray(tokens, np.int32)
+    logits = np.zeros((toks.size, n_vocab), np.float32)
+    nv = np.zeros(1, np.int32)
+    rc = lib.ref_forward_tokens(path.encode(), iptr(toks), toks.size, fptr(logits), iptr(nv))
+    assert rc == 0, lib.ref_forward_error()
+    assert nv[0] == n_vocab
+    return logits
+
+
+def ref_generate_greedy(path: str, prompt, n_gen: int):
+    lib = ref_forward()
+    p = np.ascontiguousarray(prompt, np.int32)
+    out = np.zeros(n_gen, np.int32)
+    rc = lib.ref_generate_greedy(path.encode(), iptr(p), p.size, n_gen, iptr(out))
+    assert rc == 0, lib.ref_forward_error()
+    return out.tolist()

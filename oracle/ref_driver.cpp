@@ -15,6 +15,10 @@
 //   ref_rmsnorm    -> rmsnorm()    src/ops.h:95
 //   ref_vec_add    -> vec_add()    src/ops.h:143
 //   ref_fp16_to_f32 -> fp16_to_f32() src/ops.h:39
+//   ref_silu       -> silu()       src/ops.h:118
+//   ref_elementwise_mul -> elementwise_mul() src/ops.h:131
+//   ref_ffn_swiglu -> ffn_swiglu() src/ops.h:232-235
+//   ref_argmax     -> sample_argmax() src/ops.h:249
 #include <cstddef>
 #include <cstring>
 #include <thread>
@@ -94,5 +98,18 @@ void ref_rmsnorm(float* out, const float* x, const float* weight, int size, floa
 void ref_vec_add(float* out, const float* x, int size) { vec_add(out, x, size); }
 
 float ref_fp16_to_f32(unsigned short h) { return fp16_to_f32(h); }
+
+
+void ref_silu(float* x, int size) { silu(x, size); }
+
+void ref_elementwise_mul(float* a, const float* b, int size) { elementwise_mul(a, b, size); }
+
+void ref_ffn_swiglu(float* out, const float* in, float* hb, float* hb2, const void* w_gate,
+                    const void* w_up, const void* w_down, int n_ff, int n_embd, int type)
+{
+    ffn_swiglu(out, in, hb, hb2, w_gate, w_up, w_down, n_ff, n_embd, static_cast<ggml_type>(type));
+}
+
+int ref_argmax(const float* logits, int n_vocab) { return sample_argmax(logits, n_vocab); }
 
 }  // extern "C"

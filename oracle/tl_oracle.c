@@ -22,6 +22,12 @@
  *                        block layouts src/gguf.h:56-135
  *   oracle_rmsnorm    <- src/ops.cpp:1003-1055 (naive branch)
  *   oracle_vec_add    <- src/ops.cpp:1165-1184 (naive branch)
+ *   oracle_silu, oracle_elementwise_mul <- src/ops.cpp:1107-1148 (naive)
+ *   oracle_ffn_swiglu <- src/ops.cpp:1535-1564
+ *   oracle_embed      <- embed_token() src/forward.cpp:17-134
+ *   oracle_forward    <- forward() src/forward.cpp:167-266 (with the ops above;
+ *                        weights by pointer instead of by GGUF tensor name)
+ *   oracle_argmax     <- sample_argmax() src/ops.cpp:1587-1597
  *
  * Float semantics: every product and sum is rounded separately, as the
  * reference's x86-64 -O2 build does (no FMA in the baseline ISA).  Build with
@@ -61,6 +67,9 @@ enum {
     FAULT_Q4_NIBBLE_ORDER = 7, /* low nibble -> element 2j, high -> 2j+1      */
     FAULT_Q6K_QH_SHIFT = 8,    /* upper 2 bits taken from the wrong qh pair   */
     FAULT_RMS_NO_MEAN = 9,     /* sum of squares not divided by size          */
+    FAULT_SILU_SIGN = 10,      /* sigmoid(+x) instead of sigmoid(-x) flip     */
+    FAULT_FFN_SWAP = 11,       /* silu applied to the up projection           */
+    FAULT_FWD_NO_RESIDUAL = 12,/* attention output replaces x (no residual)   */
 };
 
 /* ---- rope: src/ops.cpp:1223-1281 ------------------------------------- */
@@ -433,4 +442,171 @@ void oracle_rmsnorm(float* out, const float* x, const float* weight, int size, f
 void oracle_vec_add(float* out, const float* x, int size)
 {
     for (int i = 0; i < size; ++i) out[i] += x[i];
+}
+
+/* ---- FFN: src/ops.cpp:1107-1148 and 1535-1564 ------------------------- */
+
+/* silu(x) = x * (1 / (1 + exp(-x))), in place (src/ops.cpp:1107-1115). */
+void oracle_silu(float* x, int size)
+{
+    for (int i = 0; i < size; ++i) {
+        const float val = x[i];
+        const float e = g_fault == FAULT_SILU_SIGN ? expf(val) : expf(-val);
+        const float sigmoid = 1.0f / (1.0f + e);
+        x[i] = val * sigmoid;
+    }
+}
+
+/* a[i] *= b[i] (src/ops.cpp:1128-1148 naive branch). */
+void oracle_elementwise_mul(float* a, const float* b, int size)
+{
+    for (int i = 0; i < size; ++i) a[i] *= b[i];
+}
+
+/* out = W_down . (silu(W_gate . in) * (W_up . in)); hb and hb2 are left as
+ * the reference leaves them (gated gate projection, up projection). */
+int oracle_ffn_swiglu(float* out, const float* in, float* hb, float* hb2, const void* w_gate,
+                      const void* w_up, const void* w_down, int n_ff, int n_embd, int type)
+{
+    if (oracle_matmul(hb, w_gate, in, n_ff, n_embd, type) ||
+        oracle_matmul(hb2, w_up, in, n_ff, n_embd, type))
+        return -1;
+    if (g_fault == FAULT_FFN_SWAP) {
+        oracle_silu(hb2, n_ff);
+    } else {
+        oracle_silu(hb, n_ff);
+    }
+    oracle_elementwise_mul(hb, hb2, n_ff);
+    return oracle_matmul(out, w_down, hb, n_embd, n_ff, type);
+}
+
+/* ---- embed_token: src/forward.cpp:17-134 ------------------------------ */
+/* Row `token` of the embedding table, dequantised element by element with
+ * the reference's expressions (value * scale; Q6_K d * scale * q). */
+int oracle_embed(float* out, const void* table, int token, int n_embd, int type)
+{
+    const long long rb = oracle_row_bytes(type, n_embd);
+    if (rb == 0) return -1;
+    const uint8_t* row = (const uint8_t*)table + rb * (long long)token;
+    if (type == T_F32) {
+        memcpy(out, row, sizeof(float) * (size_t)n_embd);
+    } else if (type == T_F16) {
+        for (int i = 0; i < n_embd; ++i) out[i] = oracle_fp16_to_f32(rd16(row + 2 * i));
+    } else if (type == T_Q8_0) {
+        for (int b = 0; b < n_embd / 32; ++b) {
+            const uint8_t* blk = row + 34 * b;
+            const float scale = oracle_fp16_to_f32(rd16(blk));
+            for (int j = 0; j < 32; ++j) out[32 * b + j] = (float)(int8_t)blk[2 + j] * scale;
+        }
+    } else if (type == T_Q4_0) {
+        for (int b = 0; b < n_embd / 32; ++b) {
+            const uint8_t* blk = row + 18 * b;
+            const float scale = oracle_fp16_to_f32(rd16(blk));
+            for (int j = 0; j < 16; ++j) {
+                const int v0 = (int)(blk[2 + j] & 0x0F) - 8, v1 = (int)(blk[2 + j] >> 4) - 8;
+                out[32 * b + j] = (float)v0 * scale;
+                out[32 * b + j + 16] = (float)v1 * scale;
+            }
+        }
+    } else { /* T_Q6_K */
+        for (int b = 0; b < n_embd / 256; ++b) {
+            const uint8_t* blk = row + 210 * b;
+            const float d = oracle_fp16_to_f32(rd16(blk + 208));
+            for (int half = 0; half < 2; ++half) {
+                const uint8_t* ql = blk + 64 * half;
+                const uint8_t* qh = blk + 128 + 32 * half;
+                const int8_t* sc = (const int8_t*)(blk + 192) + 8 * half;
+                float* o = out + 256 * b + 128 * half;
+                for (int l = 0; l < 32; ++l) {
+                    const int is = l / 16;
+                    const int q1 = ((ql[l] & 0x0F) | (((qh[l] >> 0) & 3) << 4)) - 32;
+                    const int q2 = ((ql[l + 32] & 0x0F) | (((qh[l] >> 2) & 3) << 4)) - 32;
+                    const int q3 = ((ql[l] >> 4) | (((qh[l] >> 4) & 3) << 4)) - 32;
+                    const int q4 = ((ql[l + 32] >> 4) | (((qh[l] >> 6) & 3) << 4)) - 32;
+                    o[l + 0] = d * (float)sc[is + 0] * (float)q1;
+                    o[l + 32] = d * (float)sc[is + 2] * (float)q2;
+                    o[l + 64] = d * (float)sc[is + 4] * (float)q3;
+                    o[l + 96] = d * (float)sc[is + 6] * (float)q4;
+                }
+            }
+        }
+    }
+    return 0;
+}
+
+/* ---- sample_argmax: src/ops.cpp:1587-1597 ----------------------------- */
+int oracle_argmax(const float* logits, int n_vocab)
+{
+    int best = 0;
+    float best_val = logits[0];
+    for (int i = 1; i < n_vocab; ++i)
+        if (logits[i] > best_val) {
+            best_val = logits[i];
+            best = i;
+        }
+    return best;
+}
+
+/* ---- forward: src/forward.cpp:167-266 --------------------------------- */
+typedef struct oracle_layer {
+    const float* attn_norm;
+    const void *wq, *wk, *wv, *wo;
+    int type_q, type_k, type_v, type_o;
+    const float* ffn_norm;
+    const void *w_gate, *w_up, *w_down;
+    int type_ffn;
+} oracle_layer;
+
+typedef struct oracle_model {
+    int n_layers, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx;
+    float rope_freq_base, rms_norm_eps;
+    const void* token_embd;
+    int type_embd;
+    const float* output_norm;
+    const void* output; /* the classifier; token_embd when the file has none */
+    int type_output;
+    const oracle_layer* layers;
+} oracle_model;
+
+/* One token at position pos: state.x ... state.logits as forward() computes
+ * them.  key_cache/value_cache: [n_layers][n_ctx][kv_dim]; scratch holds at
+ * least 5*n_embd + 2*kv_dim + n_ctx + 2*n_ff floats. */
+int oracle_forward(const oracle_model* m, float* key_cache, float* value_cache, float* scratch,
+                   int token, int pos, float* logits)
+{
+    const int n_embd = m->n_embd, kv_dim = m->n_head_kv * (m->n_embd / m->n_head);
+    const int head_dim = m->n_embd / m->n_head;
+    float* x = scratch;
+    float* xb = x + n_embd;
+    float* xb2 = xb + n_embd;
+    float* q = xb2 + n_embd;
+    float* k = q + n_embd;
+    float* v = k + kv_dim;
+    float* att = v + kv_dim;
+    float* hb = att + m->n_ctx;
+    float* hb2 = hb + m->n_ff;
+    if (oracle_embed(x, m->token_embd, token, n_embd, m->type_embd)) return -1;
+    for (int l = 0; l < m->n_layers; ++l) {
+        const oracle_layer* L = &m->layers[l];
+        oracle_rmsnorm(xb, x, L->attn_norm, n_embd, m->rms_norm_eps);
+        if (oracle_matmul(q, L->wq, xb, n_embd, n_embd, L->type_q) ||
+            oracle_matmul(k, L->wk, xb, kv_dim, n_embd, L->type_k) ||
+            oracle_matmul(v, L->wv, xb, kv_dim, n_embd, L->type_v))
+            return -1;
+        oracle_rope(q, k, pos, head_dim, m->n_head, m->n_head_kv, m->rope_freq_base);
+        oracle_attention(xb2, q, k, v, key_cache, value_cache, att, l, pos, m->n_head,
+                         m->n_head_kv, head_dim, m->n_ctx);
+        if (oracle_matmul(xb, L->wo, xb2, n_embd, n_embd, L->type_o)) return -1;
+        if (g_fault == FAULT_FWD_NO_RESIDUAL)
+            memcpy(x, xb, sizeof(float) * (size_t)n_embd);
+        else
+            oracle_vec_add(x, xb, n_embd);
+        oracle_rmsnorm(xb, x, L->ffn_norm, n_embd, m->rms_norm_eps);
+        if (oracle_ffn_swiglu(xb2, xb, hb, hb2, L->w_gate, L->w_up, L->w_down, m->n_ff, n_embd,
+                              L->type_ffn))
+            return -1;
+        oracle_vec_add(x, xb2, n_embd);
+    }
+    oracle_rmsnorm(x, x, m->output_norm, n_embd, m->rms_norm_eps);
+    return oracle_matmul(logits, m->output, x, m->n_vocab, n_embd, m->type_output);
 }

@@ -1,0 +1,53 @@
+"""Writes a GGUF (version 3) file: the header, metadata key/values, tensor
+infos and aligned tensor data, per the published GGUF format (little endian:
+magic "GGUF", u32 version, u64 tensor count, u64 kv count; strings are u64
+length + bytes; tensor info = name, u32 n_dims, u64 dims (ne0 first), u32
+ggml type, u64 offset from the aligned start of the data section).
+
+Used by the tests to hand a seeded random model to the reference's own GGUF
+loader and forward pass (oracle/_ref/libref_forward.so); the GPU path takes
+the same tensors as device pointers."""
+import struct
+
+import numpy as np
+
+GGUF_UINT32, GGUF_FLOAT32, GGUF_STRING, GGUF_ARRAY = 4, 6, 8, 9
+
+
+def _str(s: str) -> bytes:
+    b = s.encode()
+    return struct.pack("<Q", len(b)) + b
+
+
+def write_gguf(path, spec, tensors, alignment: int = 32):
+    kv = [
+        ("general.architecture", GGUF_STRING, _str("llama")),
+        ("general.alignment", GGUF_UINT32, struct.pack("<I", alignment)),
+        ("llama.block_count", GGUF_UINT32, struct.pack("<I", spec.n_layers)),
+        ("llama.embedding_length", GGUF_UINT32, struct.pack("<I", spec.n_embd)),
+        ("llama.attention.head_count", GGUF_UINT32, struct.pack("<I", spec.n_head)),
+        ("llama.attention.head_count_kv", GGUF_UINT32, struct.pack("<I", spec.n_head_kv)),
+        ("llama.feed_forward_length", GGUF_UINT32, struct.pack("<I", spec.n_ff)),
+        ("llama.rope.dimension_count", GGUF_UINT32, struct.pack("<I", spec.head_dim)),
+        ("llama.rope.freq_base", GGUF_FLOAT32, struct.pack("<f", spec.rope_freq_base)),
+        ("llama.context_length", GGUF_UINT32, struct.pack("<I", spec.n_ctx)),
+        ("llama.attention.layer_norm_rms_epsilon", GGUF_FLOAT32,
+         struct.pack("<f", spec.rms_norm_eps)),
+    ]
+    head = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kv)))
+    for key, ty, val in kv:
+        head += _str(key) + struct.pack("<I", ty) + val
+    offsets, off = {}, 0
+    for name, (dims, ty, raw) in tensors.items():
+        offsets[name] = off
+        off += (len(raw) + alignment - 1) // alignment * alignment
+    for name, (dims, ty, raw) in tensors.items():
+        head += _str(name) + struct.pack("<I", len(dims))
+        head += b"".join(struct.pack("<Q", d) for d in dims)
+        head += struct.pack("<IQ", ty, offsets[name])
+    pad = (-len(head)) % alignment
+    with open(path, "wb") as f:
+        f.write(head + b"\0" * pad)
+        for name, (dims, ty, raw) in tensors.items():
+            raw = np.ascontiguousarray(raw, np.uint8).tobytes()
+            f.write(raw + b"\0" * ((-len(raw)) % alignment))

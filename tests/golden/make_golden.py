@@ -207,9 +207,72 @@ def projections(R):
     save("projections.npz", **arrays)
 
 
+# (name, weight type, embedding type, classifier type (None: tied), overrides)
+FORWARD_CASES = [
+    ("q8_0", W.W_Q8_0, None, W.W_Q6_K, {}),
+    ("f16_tied", W.W_F16, None, None, {}),
+    ("q4_0", W.W_Q4_0, W.W_Q6_K, W.W_Q6_K, {}),
+    ("f32", W.W_F32, None, W.W_F32, {}),
+    ("mixed", W.W_Q8_0, W.W_F16, W.W_Q6_K, {"attn_v.weight": W.W_Q6_K, "attn_output.weight": W.W_F16}),
+]
+FORWARD_SPEC = dict(n_layers=2, n_embd=256, n_head=4, n_head_kv=2, n_ff=512, n_vocab=384, n_ctx=64)
+FORWARD_TOKENS = [1, 17, 300, 5, 42, 99, 250, 3, 383, 0, 128, 7]
+GREEDY_PROMPT, GREEDY_N = [1, 17, 300], 16
+
+
+def forward(R):
+    """The reference's own forward() (src/forward.cpp:167-266) and greedy
+    generation loop (src/generate.cpp:56-100) over small seeded models in
+    every weight format, loaded by its GGUF loader from files written by
+    tests/gguf_writer.py; plus silu() and ffn_swiglu() on their own."""
+    import hashlib
+    import tempfile
+
+    sys.path.insert(0, os.path.join(ROOT, "tests"))
+    from gguf_writer import write_gguf
+
+    spec = W.ModelSpec(**FORWARD_SPEC)
+    arrays = {"spec": np.array([FORWARD_SPEC[k] for k in ("n_layers", "n_embd", "n_head",
+                                                          "n_head_kv", "n_ff", "n_vocab", "n_ctx")],
+                               np.int32),
+              "tokens": np.array(FORWARD_TOKENS, np.int32),
+              "prompt": np.array(GREEDY_PROMPT, np.int32)}
+    O.build(with_ref=True)
+    for i, (name, wt, et, ot, ov) in enumerate(FORWARD_CASES):
+        t = W.make_model(spec, wt, salt=i + 1, embd_type=et, output_type=ot, overrides=ov)
+        with tempfile.TemporaryDirectory() as d:
+            path = os.path.join(d, "model.gguf")
+            write_gguf(path, spec, t)
+            digest = hashlib.sha256(open(path, "rb").read()).hexdigest()
+            arrays[f"{name}_logits"] = O.ref_forward_tokens(path, FORWARD_TOKENS, spec.n_vocab)
+            arrays[f"{name}_greedy"] = np.array(
+                O.ref_generate_greedy(path, GREEDY_PROMPT, GREEDY_N), np.int32)
+        arrays[f"{name}_case"] = np.array([i + 1, wt, -1 if et is None else et,
+                                           -1 if ot is None else ot], np.int32)
+        arrays[f"{name}_gguf_sha256"] = np.array(digest)
+        arrays[f"{name}_overrides"] = np.array(repr(sorted(ov.items())))
+    rg = np.random.default_rng(12)
+    x = (rg.standard_normal(1000) * 4).astype(np.float32)
+    x[:6] = [0.0, -0.0, 88.0, -88.0, 1e-30, -104.0]
+    arrays["silu_x"], arrays["silu_out"] = x, O.silu(x, lib=R)
+    n_ff, n_embd = 512, 256
+    for t in (W.W_Q8_0, W.W_F16):
+        nm = W.W_NAMES[t]
+        wg, wu = W.make_weights(t, n_ff, n_embd, salt=31), W.make_weights(t, n_ff, n_embd, salt=32)
+        wd = W.make_weights(t, n_embd, n_ff, salt=33)
+        xin = rg.standard_normal(n_embd).astype(np.float32)
+        out, hb, hb2 = O.ffn_swiglu(xin, wg, wu, wd, n_ff, n_embd, t, lib=R)
+        # weights by seed (make_weights salts 31-33) and digest
+        arrays.update({f"ffn_{nm}_w_sha256": np.array(W.digest(wg, wu, wd)),
+                       f"ffn_{nm}_x": xin, f"ffn_{nm}_out": out, f"ffn_{nm}_hb": hb,
+                       f"ffn_{nm}_hb2": hb2})
+    save("forward.npz", **arrays)
+
+
 SECTIONS = {"softmax": softmax_cases, "rope": rope_cases, "attention": testops_attention,
             "decode_single": decode_single, "decode_peaked": decode_peaked,
-            "decode_ragged": decode_ragged, "prefill": prefill, "projections": projections}
+            "decode_ragged": decode_ragged, "prefill": prefill, "projections": projections,
+            "forward": forward}
 
 
 def main(names):

@@ -1,0 +1,253 @@
+"""GPU parity of the whole forward pass through the C ABI: embed_token
+(src/forward.cpp:17-134), silu / elementwise_mul / ffn_swiglu
+(src/ops.cpp:1107-1148, 1535-1564), the FFN half of a layer
+(src/forward.cpp:215-228), sample_argmax (src/ops.cpp:1587-1597), forward()
+(src/forward.cpp:167-266) and the greedy generation loop
+(src/generate.cpp:56-100).
+
+Tolerances: embed, elementwise_mul, argmax bit-exact; silu within 2 ulp
+(the device expf against glibc's); GEMV-based results per output row within
+2e-5 * sum_j |w_ij x_j| of the oracle; forward() logits within 1e-4 of
+the largest |logit| of the step against the reference's own logits (golden)
+and the oracle's, and the same argmax wherever the top two logits are
+further apart than twice that bound; greedy generation token for token."""
+import numpy as np
+import pytest
+
+import quant_ref as Q
+from conftest import golden
+from forward_ref import model_from_golden
+from helpers import bits, device_arrays, log
+
+pytestmark = pytest.mark.gpu
+
+CASES = ["q8_0", "f16_tied", "q4_0", "f32", "mixed"]
+TYPES = [(Q.F32, "f32"), (Q.F16, "f16"), (Q.Q4_0, "q4_0"), (Q.Q8_0, "q8_0"), (Q.Q6_K, "q6_k")]
+ORACLE_TOL = 2e-5
+LOGIT_TOL = 1e-4
+
+
+def spec_engine(engines, spec):
+    assert spec.head_dim == 64
+    return engines(spec.n_layers, spec.n_ctx, spec.n_head, spec.n_head_kv)
+
+
+@pytest.mark.parametrize("t,name", TYPES)
+def test_embed_bit_exact(O, W, engines, t, name):
+    eng = engines(1, 64)
+    n_vocab, n_embd = 40, 2048
+    raw = W.make_weights(t, n_vocab, n_embd, salt=9)
+    with device_arrays() as track:
+        tab = track(eng.array(raw))
+        out = track(eng.array((n_embd,)))
+        for tok in (0, 1, 23, 39):
+            eng.embed(out.ptr, tab.ptr, tok, n_embd, t)
+            assert np.array_equal(bits(out.download()), bits(O.embed(raw, tok, n_embd, t))), (name, tok)
+
+
+def test_silu_and_elementwise_mul(O, engines):
+    eng = engines(1, 64)
+    g = golden("forward.npz")
+    x = g["silu_x"]
+    rg = np.random.default_rng(4)
+    b = rg.standard_normal(x.size).astype(np.float32)
+    with device_arrays() as track:
+        d = track(eng.array(x))
+        eng.silu(d.ptr, x.size)
+        got = d.download()
+        want = g["silu_out"]  # the reference's silu()
+        ulp = np.spacing(np.abs(want).astype(np.float32))
+        err = np.abs(got.astype(np.float64) - want)
+        log(f"  silu: max error {float((err / np.maximum(ulp, 1e-45)).max()):.1f} ulp")
+        assert np.all(err <= 2 * ulp + 1e-38)
+        bd = track(eng.array(b))
+        eng.elementwise_mul(d.ptr, bd.ptr, x.size)
+        assert np.array_equal(bits(d.download()), bits(got * b))
+
+
+def row_scale(raw, x, t, rows, cols):
+    return Q.matmul_f64(raw, x, t, rows, cols)[1] + 1e-30
+
+
+@pytest.mark.parametrize("t", [Q.Q8_0, Q.F16, Q.Q4_0, Q.Q6_K])
+def test_ffn_swiglu(O, W, engines, t):
+    eng = engines(1, 64, 4, 2)  # n_embd 256
+    n_ff, n_embd = 512, 256
+    wg, wu = W.make_weights(t, n_ff, n_embd, salt=31), W.make_weights(t, n_ff, n_embd, salt=32)
+    wd = W.make_weights(t, n_embd, n_ff, salt=33)
+    xin = np.random.default_rng(t).standard_normal(n_embd).astype(np.float32)
+    out_o, hb_o, hb2_o = O.ffn_swiglu(xin, wg, wu, wd, n_ff, n_embd, t)
+    with device_arrays() as track:
+        dg, du, dd = (track(eng.array(w)) for w in (wg, wu, wd))
+        dx = track(eng.array(xin))
+        out, hb, hb2 = track(eng.array((n_embd,))), track(eng.array((n_ff,))), track(eng.array((n_ff,)))
+        eng.ffn_swiglu(out.ptr, dx.ptr, hb.ptr, hb2.ptr, dg.ptr, du.ptr, dd.ptr, n_ff, n_embd, t)
+        got_out, got_hb, got_hb2 = out.download(), hb.download(), hb2.download()
+    s_up = row_scale(wu, xin, t, n_ff, n_embd)
+    s_gate = row_scale(wg, xin, t, n_ff, n_embd)
+    assert np.max(np.abs(got_hb2 - hb2_o) / s_up) <= ORACLE_TOL
+    # gated: silu(gate) * up, errors of both factors carried through
+    bound = ORACLE_TOL * (s_gate * np.abs(hb2_o) + s_up * np.abs(hb_o / np.where(hb2_o == 0, 1, hb2_o)))
+    assert np.all(np.abs(got_hb - hb_o) <= bound + 1e-6 * np.abs(hb_o) + 1e-30)
+    s_down = row_scale(wd, hb_o, t, n_embd, n_ff)
+    assert np.max(np.abs(got_out - out_o) / s_down) <= 2 * ORACLE_TOL
+
+
+@pytest.mark.parametrize("n_seq", [1, 3, 9])
+def test_ffn_block(O, W, engines, n_seq):
+    """x += ffn_swiglu(rmsnorm(x)) for n_seq vectors (n_ff 5632 columns for
+    the down projection: 64 lanes per row)."""
+    eng = engines(1, 64, 4, 2)
+    t, n_ff, n_embd = Q.Q8_0, 5632, 256
+    wg, wu = W.make_weights(t, n_ff, n_embd, salt=51), W.make_weights(t, n_ff, n_embd, salt=52)
+    wd = W.make_weights(t, n_embd, n_ff, salt=53)
+    rg = np.random.default_rng(n_seq)
+    x = rg.standard_normal((n_seq, n_embd)).astype(np.float32)
+    nw = rg.uniform(0.5, 1.5, n_embd).astype(np.float32)
+    with device_arrays() as track:
+        dg, du, dd = (track(eng.array(w)) for w in (wg, wu, wd))
+        dx, dn = track(eng.array(x)), track(eng.array(nw))
+        hb = track(eng.array((n_seq, 2, n_ff)))
+        eng.ffn_block(n_seq, dx.ptr, dn.ptr, 1e-5, dg.ptr, du.ptr, dd.ptr, n_ff, t, hb.ptr)
+        got = dx.download()
+    for s in range(n_seq):
+        xn = O.rmsnorm(x[s], nw, 1e-5)
+        out, hbo, _ = O.ffn_swiglu(xn, wg, wu, wd, n_ff, n_embd, t)
+        want = x[s] + out
+        scale = row_scale(wd, hbo, t, n_embd, n_ff) + np.abs(x[s])
+        err = float(np.max(np.abs(got[s] - want) / scale))
+        log(f"  ffn_block seq {s}: {err:.2e}")
+        assert err <= 4 * ORACLE_TOL
+
+
+def test_argmax(O, engines):
+    eng = engines(1, 64)
+    rg = np.random.default_rng(8)
+    cases = []
+    x = rg.standard_normal(32000).astype(np.float32)
+    cases.append(x)
+    y = x.copy()
+    y[[5, 900, 31999]] = y.max() + 1  # ties: the first wins
+    cases.append(y)
+    z = x.copy()
+    z[[3, 77]] = np.nan  # NaN never wins
+    cases.append(z)
+    n0 = x.copy()
+    n0[0] = np.nan  # the reference's scan never leaves index 0
+    cases.append(n0)
+    cases.append(np.full(100, -np.inf, np.float32))
+    cases.append(np.array([2.5], np.float32))
+    cases.append(np.concatenate([np.zeros(1025, np.float32), [1.0]]).astype(np.float32))
+    lib = O.oracle()
+    from oracle import fptr
+    for c in cases:
+        with device_arrays() as track:
+            d = track(eng.array(c))
+            got = eng.argmax(d.ptr, c.size)
+        want = lib.oracle_argmax(fptr(np.ascontiguousarray(c)), c.size)
+        assert got == want, (got, want)
+
+
+def run_forward(tla, eng, spec, t, tokens):
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    try:
+        with device_arrays() as track:
+            kc, vc = eng.kv_cache(1)
+            track(kc), track(vc)
+            lg = track(eng.array((spec.n_vocab,)))
+            out = []
+            for i, tok in enumerate(tokens):
+                eng.forward(dm, kc.ptr, vc.ptr, int(tok), i, lg.ptr)
+                out.append(lg.download())
+        return np.stack(out)
+    finally:
+        dm.free()
+
+
+def check_logits(got, want, what):
+    for i in range(got.shape[0]):
+        scale = float(np.abs(want[i]).max())
+        err = float(np.abs(got[i] - want[i]).max())
+        assert err <= LOGIT_TOL * scale, (what, i, err, scale)
+        top2 = np.sort(want[i])[-2:]
+        if top2[1] - top2[0] > 2 * LOGIT_TOL * scale:
+            assert int(np.argmax(got[i])) == int(np.argmax(want[i])), (what, i)
+    log(f"  {what}: max |gpu - ref| / max|logit| = "
+        f"{float((np.abs(got - want).max(axis=1) / np.abs(want).max(axis=1)).max()):.2e}")
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_forward_matches_reference_logits(tla, O, W, engines, name):
+    g = golden("forward.npz")
+    spec, t = model_from_golden(W, g, name)
+    eng = spec_engine(engines, spec)
+    log(f"  tla_forward {name}: {spec.n_layers} layers, n_embd {spec.n_embd}, "
+        f"{len(g['tokens'])} tokens")
+    got = run_forward(tla, eng, spec, t, g["tokens"])
+    check_logits(got, g[f"{name}_logits"], f"{name} vs reference")
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_generate_greedy_matches_reference(tla, O, W, engines, name):
+    g = golden("forward.npz")
+    spec, t = model_from_golden(W, g, name)
+    eng = spec_engine(engines, spec)
+    # the path must not pass near-ties, or token equality would test noise
+    om = O.Model(spec, t)
+    prompt, n = g["prompt"].tolist(), len(g[f"{name}_greedy"])
+    seq = prompt + g[f"{name}_greedy"].tolist()
+    for i in range(len(prompt) - 1 + n - 1):
+        lg = om.forward(seq[i], i)
+        if i >= len(prompt) - 1:
+            top2 = np.sort(lg)[-2:]
+            assert top2[1] - top2[0] > 2 * LOGIT_TOL * np.abs(lg).max(), "near-tie on the path"
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    try:
+        with device_arrays() as track:
+            kc, vc = eng.kv_cache(1)
+            track(kc), track(vc)
+            got = eng.generate_greedy(dm, kc.ptr, vc.ptr, prompt, n)
+    finally:
+        dm.free()
+    log(f"  greedy {name}: {got}")
+    assert got == g[f"{name}_greedy"].tolist()
+
+
+def test_forward_tinyllama_shape(tla, O, W, engines):
+    """TinyLlama's shapes (22 layers, n_embd 2048, 32/4 heads, n_ff 5632,
+    vocabulary 32000), Q8_0 weights with a Q6_K classifier, against the
+    oracle for 3 tokens."""
+    spec = W.ModelSpec(22, 2048, 32, 4, 5632, 32000, 64)
+    t = W.make_model(spec, W.W_Q8_0, salt=77, output_type=W.W_Q6_K)
+    toks = [1, 15043, 29871]
+    om = O.Model(spec, t)
+    want = np.stack([om.forward(tk, i) for i, tk in enumerate(toks)])
+    eng = spec_engine(engines, spec)
+    got = run_forward(tla, eng, spec, t, toks)
+    check_logits(got, want, "tinyllama-shaped q8_0 vs oracle")
+
+
+def test_forward_errors(tla, W, engines):
+    spec = W.ModelSpec(2, 256, 4, 2, 512, 384, 64)
+    t = W.make_model(spec, W.W_Q8_0, salt=3)
+    eng = spec_engine(engines, spec)
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    try:
+        with device_arrays() as track:
+            kc, vc = eng.kv_cache(1)
+            track(kc), track(vc)
+            lg = track(eng.array((spec.n_vocab,)))
+            for tok, pos, code in ((384, 0, 2), (-1, 0, 2), (0, 64, 2)):
+                with pytest.raises(tla.TlaError) as e:
+                    eng.forward(dm, kc.ptr, vc.ptr, tok, pos, lg.ptr)
+                assert e.value.code == code
+            dm.c.n_ff = 544  # whole Q8_0 blocks, not a multiple of 64: unsupported GEMV columns
+            with pytest.raises(tla.TlaError) as e:
+                eng.forward(dm, kc.ptr, vc.ptr, 0, 0, lg.ptr)
+            assert e.value.code == 3
+            dm.c.n_ff = 512
+            with pytest.raises(tla.TlaError) as e:
+                eng.generate_greedy(dm, kc.ptr, vc.ptr, [1, 2], 64)  # 2 + 64 - 1 > n_ctx
+            assert e.value.code == 2
+    finally:
+        dm.free()

@@ -14,6 +14,15 @@ Interfaces mirrored (reference files):
                        (sequence, layer))
     Engine.prefill     the prompt loop src/generate.cpp:56-59, batched
     Engine.kv_cache    RunState::key_cache / value_cache src/run_state.h:93-101
+    Engine.matmul / rmsnorm / vec_add / silu / elementwise_mul / ffn_swiglu
+                       the ops of src/ops.h:64-66, 95-96, 118, 131, 143, 232-235
+    Engine.attn_qkv / attn_out / ffn_block
+                       the halves of a layer src/forward.cpp:180-228
+    Engine.embed       embed_token() src/forward.cpp:17-134
+    Engine.argmax      sample_argmax() src/ops.h:249
+    Engine.forward     forward() src/forward.cpp:167-266 (DeviceModel weights)
+    Engine.generate_greedy  the generation loop src/generate.cpp:56-100 at
+                       temperature 0
 """
 from __future__ import annotations
 
@@ -68,6 +77,23 @@ class Config(C.Structure):
 _vp = C.c_void_p
 _lib = None
 
+
+class LayerWeights(C.Structure):
+    """tla_layer_weights: one layer's device tensors and ggml types."""
+
+    _fields_ = [("attn_norm", _vp), ("wq", _vp), ("wk", _vp), ("wv", _vp), ("wo", _vp),
+                ("type_q", C.c_int), ("type_k", C.c_int), ("type_v", C.c_int), ("type_o", C.c_int),
+                ("ffn_norm", _vp), ("w_gate", _vp), ("w_up", _vp), ("w_down", _vp),
+                ("type_ffn", C.c_int)]
+
+
+class Model(C.Structure):
+    """tla_model: the weights forward() reads (src/forward.cpp:167-266)."""
+
+    _fields_ = [("n_ff", C.c_int), ("n_vocab", C.c_int), ("rms_norm_eps", C.c_float),
+                ("token_embd", _vp), ("type_embd", C.c_int), ("output_norm", _vp),
+                ("output", _vp), ("type_output", C.c_int), ("layers", C.POINTER(LayerWeights))]
+
 # name -> (restype, argtypes); every symbol declared in include/tla_attention.h
 SIGNATURES = {
     "tla_last_error": (C.c_char_p, []),
@@ -89,6 +115,17 @@ SIGNATURES = {
     "tla_attn_qkv": (C.c_int, [_vp, C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp,
                                C.c_int]),
     "tla_attn_out": (C.c_int, [_vp, C.c_int, _vp, _vp, _vp, C.c_int]),
+    "tla_silu": (C.c_int, [_vp, _vp, C.c_int]),
+    "tla_elementwise_mul": (C.c_int, [_vp, _vp, _vp, C.c_int]),
+    "tla_ffn_swiglu": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int,
+                                 C.c_int]),
+    "tla_ffn_block": (C.c_int, [_vp, C.c_int, _vp, _vp, C.c_float, _vp, _vp, _vp, C.c_int,
+                                C.c_int, _vp]),
+    "tla_embed": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
+    "tla_argmax": (C.c_int, [_vp, _vp, C.c_int, C.POINTER(C.c_int)]),
+    "tla_forward": (C.c_int, [_vp, C.POINTER(Model), _vp, _vp, C.c_int, C.c_int, _vp]),
+    "tla_generate_greedy": (C.c_int, [_vp, C.POINTER(Model), _vp, _vp, C.POINTER(C.c_int), C.c_int,
+                                      C.c_int, C.POINTER(C.c_int)]),
     "tla_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
     "tla_rope_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
     "tla_decode": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int,
@@ -257,6 +294,41 @@ class Engine:
     def attn_out(self, n_seq: int, x: int, wo: int, xb2: int, wtype: int):
         _check(lib().tla_attn_out(self.h, n_seq, x, wo, xb2, wtype), "tla_attn_out")
 
+    def silu(self, x: int, size: int):
+        _check(lib().tla_silu(self.h, x, size), "tla_silu")
+
+    def elementwise_mul(self, a: int, b: int, size: int):
+        _check(lib().tla_elementwise_mul(self.h, a, b, size), "tla_elementwise_mul")
+
+    def ffn_swiglu(self, out: int, inp: int, hb: int, hb2: int, w_gate: int, w_up: int,
+                   w_down: int, n_ff: int, n_embd: int, wtype: int):
+        _check(lib().tla_ffn_swiglu(self.h, out, inp, hb, hb2, w_gate, w_up, w_down, n_ff, n_embd,
+                                    wtype), "tla_ffn_swiglu")
+
+    def ffn_block(self, n_seq: int, x: int, norm_w: int, eps: float, w_gate: int, w_up: int,
+                  w_down: int, n_ff: int, wtype: int, hb: int):
+        _check(lib().tla_ffn_block(self.h, n_seq, x, norm_w, eps, w_gate, w_up, w_down, n_ff, wtype,
+                                   hb), "tla_ffn_block")
+
+    def embed(self, out: int, table: int, token: int, n_embd: int, wtype: int):
+        _check(lib().tla_embed(self.h, out, table, token, n_embd, wtype), "tla_embed")
+
+    def argmax(self, logits: int, n_vocab: int) -> int:
+        t = C.c_int()
+        _check(lib().tla_argmax(self.h, logits, n_vocab, C.byref(t)), "tla_argmax")
+        return t.value
+
+    def forward(self, model: "DeviceModel", kc: int, vc: int, token: int, pos: int, logits: int):
+        _check(lib().tla_forward(self.h, C.byref(model.c), kc, vc, token, pos, logits),
+               "tla_forward")
+
+    def generate_greedy(self, model: "DeviceModel", kc: int, vc: int, prompt, n_gen: int):
+        p = (C.c_int * len(prompt))(*[int(t) for t in prompt])
+        out = (C.c_int * n_gen)()
+        _check(lib().tla_generate_greedy(self.h, C.byref(model.c), kc, vc, p, len(prompt), n_gen,
+                                         out), "tla_generate_greedy")
+        return list(out)
+
     # ---- measurement --------------------------------------------------------------
     def set_option(self, option: int, value: int):
         _check(lib().tla_set_option(self.h, option, value), "tla_set_option")
@@ -277,3 +349,37 @@ class Engine:
         ms = C.c_float()
         _check(lib().tla_event_elapsed(self.h, a, b, C.byref(ms)), "tla_event_elapsed")
         return ms.value
+
+
+class DeviceModel:
+    """A model's tensors copied to the device unchanged and described as a
+    tla_model.  `tensors` maps GGUF tensor names to (dims, ggml type, raw
+    bytes), the names forward() looks up (src/forward.cpp:167-266);
+    output.weight falls back to token_embd.weight (tied embeddings)."""
+
+    def __init__(self, engine: Engine, tensors: dict, n_ff: int, n_vocab: int, eps: float):
+        self.engine = engine
+        self.arrays = {}
+        for name, (dims, ty, raw) in tensors.items():
+            self.arrays[name] = engine.array(np.ascontiguousarray(raw, np.uint8))
+        ptr = lambda n: self.arrays[n].ptr  # noqa: E731
+        ty = lambda n: tensors[n][1]  # noqa: E731
+        n_layers = engine.cfg.n_layers
+        self.layers = (LayerWeights * n_layers)()
+        for l in range(n_layers):
+            p = f"blk.{l}."
+            self.layers[l] = LayerWeights(
+                ptr(p + "attn_norm.weight"), ptr(p + "attn_q.weight"), ptr(p + "attn_k.weight"),
+                ptr(p + "attn_v.weight"), ptr(p + "attn_output.weight"), ty(p + "attn_q.weight"),
+                ty(p + "attn_k.weight"), ty(p + "attn_v.weight"), ty(p + "attn_output.weight"),
+                ptr(p + "ffn_norm.weight"), ptr(p + "ffn_gate.weight"), ptr(p + "ffn_up.weight"),
+                ptr(p + "ffn_down.weight"), ty(p + "ffn_gate.weight"))
+        out = "output.weight" if "output.weight" in tensors else "token_embd.weight"
+        self.c = Model(n_ff, n_vocab, eps, ptr("token_embd.weight"), ty("token_embd.weight"),
+                       ptr("output_norm.weight"), ptr(out), ty(out), self.layers)
+        self.weight_bytes = sum(a.nbytes for a in self.arrays.values())
+
+    def free(self):
+        for a in self.arrays.values():
+            a.free()
+        self.arrays = {}

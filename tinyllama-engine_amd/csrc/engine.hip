@@ -94,6 +94,9 @@ struct tla_engine {
     size_t ws_bytes = 0;
     int* counters = nullptr; // per-unit split arrival counters, zero between launches
     size_t n_counters = 0;
+    void* fwd = nullptr;     // forward(): residual stream, q|k|v, attention out, FFN, tokens
+    size_t fwd_bytes = 0;
+    int* argmax_slot = nullptr;
     long long opt_split = 0;
 
     bool prof = false;
@@ -312,6 +315,8 @@ int tla_engine_destroy(tla_engine* e)
         if (ev) (void)hipEventDestroy(ev);
     if (e->ws) (void)hipFree(e->ws);
     if (e->counters) (void)hipFree(e->counters);
+    if (e->fwd) (void)hipFree(e->fwd);
+    if (e->argmax_slot) (void)hipFree(e->argmax_slot);
     if (e->rope) (void)hipFree(e->rope);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     delete e;
@@ -735,6 +740,369 @@ int tla_prefill(tla_engine* e, int pos0, int n_tok, int layer0, int n_step_layer
     if (int rc = launch(e, TLA_KERNEL_PREFILL, "prefill attention",
                         [&] { return launch_prefill_attention(p, e->stream); }))
         return rc;
+    return ok();
+}
+
+// ---- FFN, embedding, sampling, the whole forward pass ------------------------
+
+namespace {
+
+int elementwise_check(tla_engine* e, const void* a, const void* b, int size)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!a || !b) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (size < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "size %d < 1", size);
+    return set_device(e);
+}
+
+int check_hip(hipError_t err, const char* what)
+{
+    if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "%s launch: %s", what, hipGetErrorString(err));
+    return TLA_OK;
+}
+
+// One GEMV launch over a single matrix: out (+)= W . f(x), f = the SwiGLU
+// and / or rmsnorm prologues.
+int gemv1(tla_engine* e, int type, const void* w, float* out, int rows, int cols, const float* x,
+          const float* x2, const float* norm_w, float eps, int add)
+{
+    GemvParams p{};
+    p.seg[0] = {static_cast<const unsigned char*>(w), out, rows, rows};
+    p.n_seg = 1;
+    p.total_rows = rows;
+    p.cols = cols;
+    p.row_bytes = static_cast<int>(weight_row_bytes(type, cols));
+    p.n_vec = 1;
+    p.x = x;
+    p.x_stride = cols;
+    p.x2 = x2;
+    p.norm_w = norm_w;
+    p.eps = eps;
+    p.add = add;
+    return run_gemv(e, type, p);
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<std::uintptr_t>(p) % 16 == 0; }
+
+// Shapes, types and pointers of a model against the engine's config.
+int check_model(const tla_engine* e, const tla_model* m)
+{
+    if (!m || !m->layers) return fail(TLA_ERR_INVALID_ARGUMENT, "model or its layer array is NULL");
+    const int embd = e->cfg.n_embd, kv = e->kv_dim;
+    if (m->n_ff < 1 || m->n_vocab < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_ff, n_vocab must be >= 1");
+    if (!m->token_embd || !m->output_norm || !m->output)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "NULL embedding, output norm or classifier");
+    if (weight_row_bytes(m->type_embd, embd) == 0)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "token_embd type %d", m->type_embd);
+    if (m->type_embd == kQ6_K ? embd % 256 : embd % 32)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "n_embd %d is not whole blocks of type %d", embd,
+                    m->type_embd);
+    if (int rc = check_gemv(m->type_output, embd, 1, m->output)) return rc;
+    for (int l = 0; l < e->cfg.n_layers; ++l) {
+        const tla_layer_weights& L = m->layers[l];
+        if (!L.attn_norm || !L.ffn_norm)
+            return fail(TLA_ERR_INVALID_ARGUMENT, "layer %d: NULL norm weight", l);
+        if (int rc = check_gemv(L.type_q, embd, 1, L.wq)) return rc;
+        if (int rc = check_gemv(L.type_k, embd, 1, L.wk)) return rc;
+        if (int rc = check_gemv(L.type_v, embd, 1, L.wv)) return rc;
+        if (int rc = check_gemv(L.type_o, embd, 1, L.wo)) return rc;
+        if (int rc = check_gemv(L.type_ffn, embd, 1, L.w_gate)) return rc;
+        if (int rc = check_gemv(L.type_ffn, embd, 1, L.w_up)) return rc;
+        if (int rc = check_gemv(L.type_ffn, m->n_ff, 1, L.w_down)) return rc;
+        (void)kv;
+    }
+    return TLA_OK;
+}
+
+// Engine scratch for forward(): x | xb | q | k | v | att | hb | hb2 | logits
+// floats, then n_tokens + 1 ints.
+struct FwdBufs {
+    float *x, *xb, *q, *k, *v, *att, *hb, *hb2, *logits;
+    int* tokens;
+};
+
+int fwd_bufs(tla_engine* e, const tla_model* m, int n_tokens, FwdBufs* b)
+{
+    const size_t embd = e->cfg.n_embd, kv = e->kv_dim, ff = m->n_ff, nv = m->n_vocab;
+    const size_t floats = 4 * embd + 2 * kv + 2 * ff + nv;
+    const size_t bytes = (floats * sizeof(float) + 255) / 256 * 256 + (n_tokens + 1) * sizeof(int);
+    if (bytes > e->fwd_bytes) {
+        TLA_HIP(hipStreamSynchronize(e->stream));
+        if (e->fwd) TLA_HIP(hipFree(e->fwd));
+        e->fwd = nullptr;
+        e->fwd_bytes = 0;
+        const hipError_t err = hipMalloc(&e->fwd, bytes);
+        if (err != hipSuccess)
+            return fail(TLA_ERR_OUT_OF_MEMORY, "forward scratch: %s", hipGetErrorString(err));
+        e->fwd_bytes = bytes;
+    }
+    float* f = static_cast<float*>(e->fwd);
+    b->x = f;
+    b->xb = b->x + embd;
+    b->q = b->xb + embd;
+    b->k = b->q + embd;
+    b->v = b->k + kv;
+    b->att = b->v + kv;
+    b->hb = b->att + embd;
+    b->hb2 = b->hb + ff;
+    b->logits = b->hb2 + ff;
+    b->tokens = reinterpret_cast<int*>(static_cast<char*>(e->fwd) + (floats * sizeof(float) + 255) / 256 * 256);
+    return TLA_OK;
+}
+
+// One forward() step: the token from `token`, or from token_dev when that is
+// non-null; logits written when `logits` is non-null.
+int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, float* vc,
+                 int token, const int* token_dev, int pos, float* logits)
+{
+    const int embd = e->cfg.n_embd, kv = e->kv_dim, ff = m->n_ff;
+    const float eps = m->rms_norm_eps;
+    if (int rc = check_hip(launch_embed(m->type_embd, b.x, static_cast<const unsigned char*>(m->token_embd),
+                                        token, token_dev, embd, e->stream),
+                           "embed"))
+        return rc;
+    for (int l = 0; l < e->cfg.n_layers; ++l) {
+        const tla_layer_weights& L = m->layers[l];
+        // rmsnorm + Q/K/V (src/forward.cpp:180-190): one launch when the
+        // three share a type
+        if (L.type_q == L.type_k && L.type_q == L.type_v) {
+            GemvParams p{};
+            p.seg[0] = {static_cast<const unsigned char*>(L.wq), b.q, embd, embd};
+            p.seg[1] = {static_cast<const unsigned char*>(L.wk), b.k, kv, kv};
+            p.seg[2] = {static_cast<const unsigned char*>(L.wv), b.v, kv, kv};
+            p.n_seg = 3;
+            p.total_rows = embd + 2 * kv;
+            p.cols = embd;
+            p.row_bytes = static_cast<int>(weight_row_bytes(L.type_q, embd));
+            p.n_vec = 1;
+            p.x = b.x;
+            p.x_stride = embd;
+            p.norm_w = L.attn_norm;
+            p.eps = eps;
+            if (int rc = run_gemv(e, L.type_q, p)) return rc;
+        } else {
+            if (int rc = check_hip(launch_rmsnorm(b.xb, b.x, L.attn_norm, embd, eps, e->stream), "rmsnorm"))
+                return rc;
+            if (int rc = gemv1(e, L.type_q, L.wq, b.q, embd, embd, b.xb, nullptr, nullptr, 0.f, 0)) return rc;
+            if (int rc = gemv1(e, L.type_k, L.wk, b.k, kv, embd, b.xb, nullptr, nullptr, 0.f, 0)) return rc;
+            if (int rc = gemv1(e, L.type_v, L.wv, b.v, kv, embd, b.xb, nullptr, nullptr, 0.f, 0)) return rc;
+        }
+        // RoPE + append + attention (src/forward.cpp:192-208)
+        if (int rc = tla_decode(e, 1, &pos, l, 1, TLA_ROTATE, b.att, b.q, b.k, b.v, kc, vc, 0)) return rc;
+        // x += Wo . att (src/forward.cpp:210-213)
+        if (int rc = gemv1(e, L.type_o, L.wo, b.x, embd, embd, b.att, nullptr, nullptr, 0.f, 1)) return rc;
+        // rmsnorm + gate and up projections, then SiLU x up, W_down and the
+        // residual in the down projection's prologue / epilogue
+        // (src/forward.cpp:215-228, src/ops.cpp:1535-1564)
+        {
+            GemvParams p{};
+            p.seg[0] = {static_cast<const unsigned char*>(L.w_gate), b.hb, ff, ff};
+            p.seg[1] = {static_cast<const unsigned char*>(L.w_up), b.hb2, ff, ff};
+            p.n_seg = 2;
+            p.total_rows = 2 * ff;
+            p.cols = embd;
+            p.row_bytes = static_cast<int>(weight_row_bytes(L.type_ffn, embd));
+            p.n_vec = 1;
+            p.x = b.x;
+            p.x_stride = embd;
+            p.norm_w = L.ffn_norm;
+            p.eps = eps;
+            if (int rc = run_gemv(e, L.type_ffn, p)) return rc;
+        }
+        if (int rc = gemv1(e, L.type_ffn, L.w_down, b.x, embd, ff, b.hb, b.hb2, nullptr, 0.f, 1)) return rc;
+    }
+    // final rmsnorm + classifier (src/forward.cpp:241-265)
+    if (logits)
+        if (int rc = gemv1(e, m->type_output, m->output, logits, m->n_vocab, embd, b.x, nullptr,
+                           m->output_norm, eps, 0))
+            return rc;
+    return TLA_OK;
+}
+
+}  // namespace
+
+int tla_silu(tla_engine* e, float* x_dev, int size)
+{
+    if (int rc = elementwise_check(e, x_dev, x_dev, size)) return rc;
+    if (int rc = check_hip(launch_silu(x_dev, size, e->stream), "silu")) return rc;
+    return ok();
+}
+
+int tla_elementwise_mul(tla_engine* e, float* a_dev, const float* b_dev, int size)
+{
+    if (int rc = elementwise_check(e, a_dev, b_dev, size)) return rc;
+    if (int rc = check_hip(launch_elementwise_mul(a_dev, b_dev, size, e->stream), "elementwise_mul")) return rc;
+    return ok();
+}
+
+int tla_ffn_swiglu(tla_engine* e, float* out_dev, const float* in_dev, float* hb_dev,
+                   float* hb2_dev, const void* w_gate_dev, const void* w_up_dev,
+                   const void* w_down_dev, int n_ff, int n_embd, int type)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!out_dev || !in_dev || !hb_dev || !hb2_dev || !w_gate_dev || !w_up_dev || !w_down_dev)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (n_ff < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_ff %d < 1", n_ff);
+    if (int rc = check_gemv(type, n_embd, 1, w_gate_dev)) return rc;
+    if (int rc = check_gemv(type, n_embd, 1, w_up_dev)) return rc;
+    if (int rc = check_gemv(type, n_ff, 1, w_down_dev)) return rc;
+    if (int rc = set_device(e)) return rc;
+    GemvParams p{};
+    p.seg[0] = {static_cast<const unsigned char*>(w_gate_dev), hb_dev, n_ff, n_ff};
+    p.seg[1] = {static_cast<const unsigned char*>(w_up_dev), hb2_dev, n_ff, n_ff};
+    p.n_seg = 2;
+    p.total_rows = 2 * n_ff;
+    p.cols = n_embd;
+    p.row_bytes = static_cast<int>(weight_row_bytes(type, n_embd));
+    p.n_vec = 1;
+    p.x = in_dev;
+    p.x_stride = n_embd;
+    if (int rc = run_gemv(e, type, p)) return rc;
+    if (int rc = check_hip(launch_silu(hb_dev, n_ff, e->stream), "silu")) return rc;
+    if (int rc = check_hip(launch_elementwise_mul(hb_dev, hb2_dev, n_ff, e->stream), "elementwise_mul"))
+        return rc;
+    if (int rc = gemv1(e, type, w_down_dev, out_dev, n_embd, n_ff, hb_dev, nullptr, nullptr, 0.f, 0))
+        return rc;
+    return ok();
+}
+
+int tla_ffn_block(tla_engine* e, int n_seq, float* x_dev, const float* norm_w_dev, float eps,
+                  const void* w_gate_dev, const void* w_up_dev, const void* w_down_dev, int n_ff,
+                  int type, float* hb_dev)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!x_dev || !norm_w_dev || !w_gate_dev || !w_up_dev || !w_down_dev || !hb_dev)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (n_seq < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_seq %d < 1", n_seq);
+    if (n_ff < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_ff %d < 1", n_ff);
+    const int embd = e->cfg.n_embd;
+    const int chunk_up = gemv_chunk(n_seq, embd), chunk_down = gemv_chunk(n_seq, n_ff);
+    if (int rc = check_gemv(type, embd, chunk_up, w_gate_dev)) return rc;
+    if (int rc = check_gemv(type, embd, chunk_up, w_up_dev)) return rc;
+    if (int rc = check_gemv(type, n_ff, chunk_down, w_down_dev)) return rc;
+    if (int rc = set_device(e)) return rc;
+    // hb_dev: [n_seq][2][n_ff], gate then up
+    for (int s0 = 0; s0 < n_seq; s0 += chunk_up) {
+        const int nv = std::min(chunk_up, n_seq - s0);
+        GemvParams p{};
+        float* h = hb_dev + static_cast<long long>(s0) * 2 * n_ff;
+        p.seg[0] = {static_cast<const unsigned char*>(w_gate_dev), h, n_ff, 2LL * n_ff};
+        p.seg[1] = {static_cast<const unsigned char*>(w_up_dev), h + n_ff, n_ff, 2LL * n_ff};
+        p.n_seg = 2;
+        p.total_rows = 2 * n_ff;
+        p.cols = embd;
+        p.row_bytes = static_cast<int>(weight_row_bytes(type, embd));
+        p.n_vec = nv;
+        p.x = x_dev + static_cast<long long>(s0) * embd;
+        p.x_stride = embd;
+        p.norm_w = norm_w_dev;
+        p.eps = eps;
+        if (int rc = run_gemv(e, type, p)) return rc;
+    }
+    for (int s0 = 0; s0 < n_seq; s0 += chunk_down) {
+        const int nv = std::min(chunk_down, n_seq - s0);
+        GemvParams p{};
+        p.seg[0] = {static_cast<const unsigned char*>(w_down_dev), x_dev + static_cast<long long>(s0) * embd,
+                    embd, embd};
+        p.n_seg = 1;
+        p.total_rows = embd;
+        p.cols = n_ff;
+        p.row_bytes = static_cast<int>(weight_row_bytes(type, n_ff));
+        p.n_vec = nv;
+        p.x = hb_dev + static_cast<long long>(s0) * 2 * n_ff;
+        p.x2 = p.x + n_ff;
+        p.x_stride = 2LL * n_ff;
+        p.add = 1;
+        if (int rc = run_gemv(e, type, p)) return rc;
+    }
+    return ok();
+}
+
+int tla_embed(tla_engine* e, float* out_dev, const void* table_dev, int token, int n_embd, int type)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!out_dev || !table_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (token < 0) return fail(TLA_ERR_OUT_OF_RANGE, "token %d < 0", token);
+    if (n_embd < 1 || weight_row_bytes(type, n_embd) == 0 || (type == kQ6_K ? n_embd % 256 : n_embd % 32))
+        return fail(TLA_ERR_INVALID_ARGUMENT, "type %d with n_embd %d", type, n_embd);
+    if (int rc = set_device(e)) return rc;
+    if (int rc = check_hip(launch_embed(type, out_dev, static_cast<const unsigned char*>(table_dev), token,
+                                        nullptr, n_embd, e->stream),
+                           "embed"))
+        return rc;
+    return ok();
+}
+
+int tla_argmax(tla_engine* e, const float* logits_dev, int n_vocab, int* token_host)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!logits_dev || !token_host) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (n_vocab < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_vocab %d < 1", n_vocab);
+    if (int rc = set_device(e)) return rc;
+    if (!e->argmax_slot) TLA_HIP(hipMalloc(reinterpret_cast<void**>(&e->argmax_slot), sizeof(int)));
+    hipError_t err = launch_argmax(e->argmax_slot, nullptr, logits_dev, n_vocab, e->stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(token_host, e->argmax_slot, sizeof(int), hipMemcpyDeviceToHost, e->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
+    if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "argmax: %s", hipGetErrorString(err));
+    return ok();
+}
+
+int tla_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* value_cache_dev,
+                int token, int pos, float* logits_dev)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!key_cache_dev || !value_cache_dev || !logits_dev)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (int rc = check_model(e, m)) return rc;
+    if (token < 0 || token >= m->n_vocab)
+        return fail(TLA_ERR_OUT_OF_RANGE, "token %d outside [0, n_vocab=%d)", token, m->n_vocab);
+    if (pos < 0 || pos >= e->cfg.n_ctx)
+        return fail(TLA_ERR_OUT_OF_RANGE, "pos %d outside [0, n_ctx=%d)", pos, e->cfg.n_ctx);
+    if (int rc = set_device(e)) return rc;
+    FwdBufs b{};
+    if (int rc = fwd_bufs(e, m, 0, &b)) return rc;
+    if (int rc = forward_step(e, m, b, key_cache_dev, value_cache_dev, token, nullptr, pos, logits_dev))
+        return rc;
+    return ok();
+}
+
+int tla_generate_greedy(tla_engine* e, const tla_model* m, float* key_cache_dev,
+                        float* value_cache_dev, const int* prompt_host, int n_prompt, int n_gen,
+                        int* tokens_host)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!key_cache_dev || !value_cache_dev || !prompt_host || !tokens_host)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (int rc = check_model(e, m)) return rc;
+    if (n_prompt < 1 || n_gen < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_prompt, n_gen must be >= 1");
+    if (static_cast<long long>(n_prompt) + n_gen - 1 > e->cfg.n_ctx)
+        return fail(TLA_ERR_OUT_OF_RANGE, "n_prompt + n_gen - 1 = %lld > n_ctx %d",
+                    static_cast<long long>(n_prompt) + n_gen - 1, e->cfg.n_ctx);
+    for (int i = 0; i < n_prompt; ++i)
+        if (prompt_host[i] < 0 || prompt_host[i] >= m->n_vocab)
+            return fail(TLA_ERR_OUT_OF_RANGE, "prompt[%d] = %d outside [0, n_vocab)", i, prompt_host[i]);
+    if (int rc = set_device(e)) return rc;
+    FwdBufs b{};
+    if (int rc = fwd_bufs(e, m, n_gen, &b)) return rc;
+    int pos = 0;
+    // prompt: only the last token's logits are needed (the reference
+    // computes and overwrites the others)
+    for (int i = 0; i < n_prompt; ++i, ++pos)
+        if (int rc = forward_step(e, m, b, key_cache_dev, value_cache_dev, prompt_host[i], nullptr, pos,
+                                  i + 1 == n_prompt ? b.logits : nullptr))
+            return rc;
+    // b.tokens[0]: the current token; b.tokens[1 + i]: generated token i
+    for (int i = 0; i < n_gen; ++i) {
+        if (int rc = check_hip(launch_argmax(b.tokens, b.tokens + 1 + i, b.logits, m->n_vocab, e->stream),
+                               "argmax"))
+            return rc;
+        if (i + 1 == n_gen) break;
+        if (int rc = forward_step(e, m, b, key_cache_dev, value_cache_dev, 0, b.tokens, pos++, b.logits))
+            return rc;
+    }
+    TLA_HIP(hipMemcpyAsync(tokens_host, b.tokens + 1, sizeof(int) * n_gen, hipMemcpyDeviceToHost, e->stream));
+    TLA_HIP(hipStreamSynchronize(e->stream));
     return ok();
 }
 

@@ -44,6 +44,14 @@ __device__ __forceinline__ float half_bits_to_float(unsigned h)
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
 }
 
+// silu(v) = v * (1 / (1 + exp(-v))), with the reference's operation order
+// (src/ops.cpp:1107-1115); expf is the device library's.
+__device__ __forceinline__ float silu(float v)
+{
+    const float sigmoid = 1.0f / (1.0f + expf(-v));
+    return v * sigmoid;
+}
+
 // kW floats of x (kW = 4, 8 or 16) from LDS starting at column c0, a multiple
 // of kW, so the span does not cross a padding gap.
 template <int kW>
@@ -482,10 +490,10 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
     // before the weights (loads complete in order, so anything requested
     // after the weights could only be used once they have all arrived).
     constexpr int kXRegs = 8;
-    const bool x_early = !kMulti && p.cols <= kXRegs * kThreads;
+    const bool x_early = !kMulti && p.cols <= kXRegs * kThreads && !(p.norm_w && p.x2);
     float xr[kXRegs], nr[kXRegs];
     if (x_early) {
-        const float* nw = p.norm_w ? p.norm_w : p.x;
+        const float* nw = p.norm_w ? p.norm_w : p.x2 ? p.x2 : p.x;
 #pragma unroll
         for (int i = 0; i < kXRegs; ++i) {
             const int c = threadIdx.x + i * kThreads;
@@ -506,8 +514,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
         ga.request(p, sr, ps * kPassRows + sub, kRowsPerWave, n_first, l);
     }
 
-    // Stage x in LDS, then rmsnorm's scaling in place (each thread rescales
-    // the elements it wrote).
+    // Stage x in LDS (SwiGLU'd when asked), then rmsnorm's scaling in place
+    // (each thread rescales the elements it wrote).
     const int xs_len = xs_floats(p.cols);
     for (int v = 0; v < p.n_vec; ++v) {
         const float* xv = p.x + v * p.x_stride;
@@ -518,13 +526,15 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
             for (int i = 0; i < kXRegs; ++i) {
                 const int c = threadIdx.x + i * kThreads;
                 if (c < p.cols) {
-                    xs[xpad(c)] = xr[i];
-                    ss += xr[i] * xr[i];
+                    const float t = p.x2 ? silu(xr[i]) * nr[i] : xr[i];
+                    xs[xpad(c)] = t;
+                    ss += t * t;
                 }
             }
         } else {
+            const float* x2v = p.x2 ? p.x2 + v * p.x_stride : nullptr;
             for (int c = threadIdx.x; c < p.cols; c += kThreads) {
-                const float t = xv[c];
+                const float t = x2v ? silu(xv[c]) * x2v[c] : xv[c];
                 xs[xpad(c)] = t;
                 ss += t * t;
             }
@@ -666,6 +676,110 @@ __global__ __launch_bounds__(kThreads) void vec_add_kernel(float* out, const flo
     if (i < size) out[i] += x[i];
 }
 
+__global__ __launch_bounds__(kThreads) void silu_kernel(float* x, int size)
+{
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i < size) x[i] = silu(x[i]);
+}
+
+__global__ __launch_bounds__(kThreads) void elementwise_mul_kernel(float* a, const float* b, int size)
+{
+    const int i = blockIdx.x * kThreads + threadIdx.x;
+    if (i < size) a[i] *= b[i];
+}
+
+// Element i of one table row, with embed_token()'s expressions
+// (src/forward.cpp:17-134): value * scale, Q6_K d * scale * q.
+__device__ float embed_elem(int type, const unsigned char* row, int i)
+{
+    switch (type) {
+    case kF32: return reinterpret_cast<const float*>(row)[i];
+    case kF16: return half_bits_to_float(reinterpret_cast<const unsigned short*>(row)[i]);
+    case kQ8_0: {
+        const unsigned char* blk = row + 34 * (i >> 5);
+        const float scale = half_bits_to_float(blk[0] | (blk[1] << 8));
+        return static_cast<float>(static_cast<signed char>(blk[2 + (i & 31)])) * scale;
+    }
+    case kQ4_0: {
+        const unsigned char* blk = row + 18 * (i >> 5);
+        const float scale = half_bits_to_float(blk[0] | (blk[1] << 8));
+        const int j = i & 31;
+        const int q = j < 16 ? (blk[2 + j] & 0x0F) : (blk[2 + j - 16] >> 4);
+        return static_cast<float>(q - 8) * scale;
+    }
+    default: {  // kQ6_K
+        const unsigned char* blk = row + 210 * (i >> 8);
+        const int r = i & 255, h = r >> 7, k = (r & 127) >> 5, l = r & 31;
+        const unsigned char* ql = blk + 64 * h;
+        const unsigned char* qh = blk + 128 + 32 * h;
+        const signed char* sc = reinterpret_cast<const signed char*>(blk + 192) + 8 * h;
+        const float d = half_bits_to_float(blk[208] | (blk[209] << 8));
+        const int lo = (k & 1) ? ql[l + 32] : ql[l];
+        const int q = ((k < 2 ? (lo & 0x0F) : (lo >> 4)) | (((qh[l] >> (2 * k)) & 3) << 4)) - 32;
+        return d * static_cast<float>(sc[(l >> 4) + 2 * k]) * static_cast<float>(q);
+    }
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void embed_kernel(int type, float* out,
+                                                         const unsigned char* table, long long row_bytes,
+                                                         int token, const int* token_dev, int n)
+{
+    const int t = token_dev ? *token_dev : token;
+    const unsigned char* row = table + row_bytes * t;
+    for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads)
+        out[i] = embed_elem(type, row, i);
+}
+
+// (value, index) pairs: b beats a when larger, or equal at a smaller index;
+// NaN values never beat anything (the reference's strict '>' scan).
+__device__ __forceinline__ bool beats(float vb, int ib, float va, int ia)
+{
+    return vb > va || (vb == va && ib < ia);
+}
+
+__global__ __launch_bounds__(1024) void argmax_kernel(int* out, int* out2, const float* x, int n)
+{
+    __shared__ float s_v[16];
+    __shared__ int s_i[16];
+    float bv = -__builtin_huge_valf();
+    int bi = 0x7fffffff;
+    for (int i = threadIdx.x; i < n; i += 1024) {
+        const float v = x[i];
+        if (beats(v, i, bv, bi)) {
+            bv = v;
+            bi = i;
+        }
+    }
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const float ov = __shfl_xor(bv, o);
+        const int oi = __shfl_xor(bi, o);
+        if (beats(ov, oi, bv, bi)) {
+            bv = ov;
+            bi = oi;
+        }
+    }
+    if ((threadIdx.x & 63) == 0) {
+        s_v[threadIdx.x >> 6] = bv;
+        s_i[threadIdx.x >> 6] = bi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < 16; ++w)
+            if (beats(s_v[w], s_i[w], bv, bi)) {
+                bv = s_v[w];
+                bi = s_i[w];
+            }
+        // nothing above -inf: index 0 (where the scan starts); a NaN at index
+        // 0 is never beaten in the reference's scan, so 0 as well
+        const float x0 = x[0];
+        const int r = (bi == 0x7fffffff || x0 != x0) ? 0 : bi;
+        *out = r;
+        if (out2) *out2 = r;
+    }
+}
+
 // Workgroups of one kernel that fit on the current device at once (its CU
 // count x the occupancy the kernel's registers and LDS allow), cached per
 // device and LDS size.
@@ -753,6 +867,34 @@ hipError_t launch_rmsnorm(float* out, const float* x, const float* w, int size, 
                           hipStream_t s)
 {
     hipLaunchKernelGGL(rmsnorm_kernel, dim3(1), dim3(kThreads), 0, s, out, x, w, size, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_silu(float* x, int size, hipStream_t s)
+{
+    hipLaunchKernelGGL(silu_kernel, dim3((size + kThreads - 1) / kThreads), dim3(kThreads), 0, s, x, size);
+    return hipGetLastError();
+}
+
+hipError_t launch_elementwise_mul(float* a, const float* b, int size, hipStream_t s)
+{
+    hipLaunchKernelGGL(elementwise_mul_kernel, dim3((size + kThreads - 1) / kThreads), dim3(kThreads), 0,
+                       s, a, b, size);
+    return hipGetLastError();
+}
+
+hipError_t launch_embed(int type, float* out, const unsigned char* table, int token,
+                        const int* token_dev, int n, hipStream_t s)
+{
+    const int blocks = std::min(64, (n + kThreads - 1) / kThreads);
+    hipLaunchKernelGGL(embed_kernel, dim3(blocks), dim3(kThreads), 0, s, type, out, table,
+                       weight_row_bytes(type, n), token, token_dev, n);
+    return hipGetLastError();
+}
+
+hipError_t launch_argmax(int* out, int* out2, const float* x, int n, hipStream_t s)
+{
+    hipLaunchKernelGGL(argmax_kernel, dim3(1), dim3(1024), 0, s, out, out2, x, n);
     return hipGetLastError();
 }
 

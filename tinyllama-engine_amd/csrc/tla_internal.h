@@ -106,7 +106,8 @@ struct GemvParams {
     int n_vec;               // 1..kGemvMaxVec
     const float* x;          // x[v * x_stride + col]
     long long x_stride;
-    const float* norm_w;     // non-null: x is replaced by rmsnorm(x, norm_w, eps)
+    const float* x2;         // non-null: x is replaced by silu(x) * x2 (SwiGLU), same stride
+    const float* norm_w;     // non-null: x is (then) replaced by rmsnorm(x, norm_w, eps)
     float eps;
     int add;                 // 1: out += W.x (residual), 0: out = W.x
 };
@@ -116,6 +117,14 @@ hipError_t launch_gemv(int type, const GemvParams& p, hipStream_t s);
 hipError_t launch_rmsnorm(float* out, const float* x, const float* w, int size, float eps,
                           hipStream_t s);
 hipError_t launch_vec_add(float* out, const float* x, int size, hipStream_t s);
+hipError_t launch_silu(float* x, int size, hipStream_t s);
+hipError_t launch_elementwise_mul(float* a, const float* b, int size, hipStream_t s);
+// out[n] = row `token` of the table (token_dev non-null: read it there).
+hipError_t launch_embed(int type, float* out, const unsigned char* table, int token,
+                        const int* token_dev, int n, hipStream_t s);
+// *out = first index of the largest value (NaN never wins; a NaN at 0 gives 0),
+// also stored at out2 when non-null.
+hipError_t launch_argmax(int* out, int* out2, const float* x, int n, hipStream_t s);
 
 // ---- small ops -------------------------------------------------------------
 struct RopeParams {

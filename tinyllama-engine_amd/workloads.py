@@ -202,3 +202,69 @@ def make_weights(wtype: int, rows: int, cols: int, salt: int = 0) -> np.ndarray:
         blk[..., 208:210] = _f16_bits(g.uniform(0.0001, 0.0002, (rows, nb)))
         return blk.reshape(-1)
     raise ValueError(wtype)
+
+
+# ---- a whole model with seeded random weights ----------------------------------
+# Tensor names and shapes as the reference's forward() reads them from a GGUF
+# file (src/forward.cpp:167-266); dims are GGUF order (ne0 = columns).
+
+class ModelSpec:
+    def __init__(self, n_layers, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx,
+                 rope_freq_base=FREQ_BASE, rms_norm_eps=1e-5):
+        self.n_layers, self.n_embd, self.n_head, self.n_head_kv = n_layers, n_embd, n_head, n_head_kv
+        self.n_ff, self.n_vocab, self.n_ctx = n_ff, n_vocab, n_ctx
+        self.rope_freq_base, self.rms_norm_eps = rope_freq_base, rms_norm_eps
+
+    @property
+    def head_dim(self):
+        return self.n_embd // self.n_head
+
+    @property
+    def kv_dim(self):
+        return self.n_head_kv * self.head_dim
+
+
+def tinyllama_spec(n_ctx: int = 2048) -> ModelSpec:
+    return ModelSpec(22, 2048, 32, 4, 5632, 32000, n_ctx)
+
+
+def make_model(spec: ModelSpec, wtype: int = W_Q8_0, salt: int = 0, embd_type: int | None = None,
+               output_type: int | None = W_Q6_K, norm_scale: float = 1.0,
+               overrides: dict | None = None):
+    """{name: (dims, ggml type, raw bytes)} for every tensor forward() reads.
+    Weights come from make_weights (seeded per tensor), norms are F32 in
+    [0.5, 1.5) * norm_scale.  output_type None ties the classifier to
+    token_embd.weight (no output.weight tensor), as TinyLlama files do.
+    overrides maps a tensor-name suffix ("attn_v.weight") to another type."""
+    e, kv, ff = spec.n_embd, spec.kv_dim, spec.n_ff
+    g = rng("weights", 100000 + salt)
+    t = {}
+    overrides = overrides or {}
+
+    def weight(name, rows, cols, ty, s):
+        for suffix, oty in overrides.items():
+            if name.endswith(suffix):
+                ty = oty
+        t[name] = ((cols, rows), ty, make_weights(ty, rows, cols, salt=salt * 4096 + s))
+
+    def norm(name):
+        v = (g.uniform(0.5, 1.5, e) * norm_scale).astype(np.float32)
+        t[name] = ((e,), W_F32, v.view(np.uint8))
+
+    weight("token_embd.weight", spec.n_vocab, e, wtype if embd_type is None else embd_type, 1)
+    for l in range(spec.n_layers):
+        p = f"blk.{l}."
+        s = 16 * (l + 1)
+        norm(p + "attn_norm.weight")
+        weight(p + "attn_q.weight", e, e, wtype, s + 1)
+        weight(p + "attn_k.weight", kv, e, wtype, s + 2)
+        weight(p + "attn_v.weight", kv, e, wtype, s + 3)
+        weight(p + "attn_output.weight", e, e, wtype, s + 4)
+        norm(p + "ffn_norm.weight")
+        weight(p + "ffn_gate.weight", ff, e, wtype, s + 5)
+        weight(p + "ffn_up.weight", ff, e, wtype, s + 6)
+        weight(p + "ffn_down.weight", e, ff, wtype, s + 7)
+    norm("output_norm.weight")
+    if output_type is not None:
+        weight("output.weight", spec.n_vocab, e, output_type, 2)
+    return t
