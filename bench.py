@@ -452,6 +452,91 @@ def run_matmul(steps, warmup, name):
     return r
 
 
+GEN_FORMATS = {"q4_0": (W.W_Q4_0, W.W_Q6_K), "q8_0": (W.W_Q8_0, W.W_Q8_0), "f16": (W.W_F16, W.W_F16)}
+
+
+def run_generate(steps, warmup, cpu, wname="q4_0", n_prompt=32, n_gen=20):
+    """The reference's own benchmark (run_trial, src/benchmark.cpp:113-165)
+    on TinyLlama's shapes with seeded random weights in the layout of the
+    TinyLlama GGUF files (Q4_0 weights with a Q6_K classifier, or Q8_0 / F16
+    throughout): a 32-token prompt through forward(), then 20 greedy decode
+    steps, as one tla_generate_greedy call on the device.  Prefill time =
+    the call with one generated token; decode ms/token = (the call with 21)
+    minus that, over 20.  HIP events on the engine's stream bracket each
+    call, which returns after its last copy, so host time between launches
+    is inside the figure."""
+    wt, ot = GEN_FORMATS[wname]
+    spec = W.tinyllama_spec(n_ctx=2048)
+    t = W.make_model(spec, wt, salt=5, output_type=ot)
+    eng = tla.Engine(tla.Config.tinyllama(n_ctx=spec.n_ctx))
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    kc, vc = eng.kv_cache(1)
+    prompt = [1] + W.rng("block", 3).integers(2, spec.n_vocab, n_prompt - 1).tolist()
+
+    def call(n):
+        eng.synchronize()
+        eng.event(0)
+        toks = eng.generate_greedy(dm, kc.ptr, vc.ptr, prompt, n)
+        eng.event(1)
+        return eng.elapsed(0, 1), toks
+
+    for _ in range(max(1, warmup)):
+        call(n_gen + 1)
+    trials = max(3, steps // 5)
+    pre = median([call(1)[0] for _ in range(trials)])
+    full = median([call(n_gen + 1)[0] for _ in range(trials)])
+    dec = (full - pre) / n_gen
+    _, toks = call(n_gen + 1)
+    # HBM bytes a decode token must move: every weight once (one embedding
+    # row), the KV cache up to its position (mean position of the 20 steps)
+    weight_bytes = sum(len(r) for name, (d, ty, r) in t.items() if name != "token_embd.weight")
+    weight_bytes += W.weight_row_bytes(t["token_embd.weight"][1], spec.n_embd)
+    mean_pos = n_prompt + (n_gen - 1) / 2
+    kv_bytes = spec.n_layers * 2 * spec.kv_dim * 4 * (mean_pos + 1)
+    tok_bytes = weight_bytes + kv_bytes
+    gbs = tok_bytes / dec / 1e6
+    log(f"[bench] generate {wname}: prefill {n_prompt} tokens {pre:.2f} ms ({pre / n_prompt * 1e3:.0f} "
+        f"us/token), decode {dec * 1e3:.0f} us/token = {1e3 / dec:.0f} tok/s; {tok_bytes / 1e6:.0f} MB "
+        f"per token -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}); tokens {toks[:8]}...")
+    res = {"decode_ms_per_token": dec, "prefill_ms": pre, "tok_per_s": 1e3 / dec,
+           "bytes_per_token": tok_bytes, "GB_s": gbs, "frac": gbs / HBM_PEAK_GBS,
+           "n_prompt": n_prompt, "n_gen": n_gen}
+    dm.free()
+    kc.free()
+    vc.free()
+    eng.close()
+    if cpu:
+        res["cpu_baseline"] = cpu_generate_baseline(spec, t, prompt, wname)
+    return res
+
+
+def cpu_generate_baseline(spec, tensors, prompt, wname, n_prompt=8, n_decode=8):
+    """The reference's own forward pass and benchmark loop (oracle/_ref,
+    built from src/forward.cpp, gguf_model.cpp, tokenizer.cpp, ops.cpp) over
+    a GGUF file of the same model, on the host: a bounded sample (8 prompt
+    tokens, 8 decode tokens) with its thread pool at the host's cores, and 4
+    decode tokens on one thread."""
+    import tempfile
+
+    import oracle as O
+    if not O.ref_forward_available():
+        return None
+    from oracle.gguf_writer import write_gguf
+    threads = cpu_threads()
+    with tempfile.TemporaryDirectory() as d:
+        path = os.path.join(d, "model.gguf")
+        write_gguf(path, spec, tensors)
+        _, dn = O.ref_bench_trial(path, prompt[:n_prompt], n_decode, threads)
+        _, d1 = O.ref_bench_trial(path, prompt[:2], 4, 1)
+    ms_n, ms_1 = dn / n_decode, d1 / 4
+    log(f"[bench] cpu reference forward {wname}: {threads} threads {ms_n:.0f} ms/token, "
+        f"1 thread {ms_1:.0f} ms/token")
+    return {"value": round(1e3 / ms_n, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
+            "sample": f"reference forward(), {n_prompt} prompt + {n_decode} decode tokens, "
+                      f"{threads} threads; 1 thread: 4 decode tokens",
+            "ms_per_token": round(ms_n, 2), "single_thread_ms_per_token": round(ms_1, 2)}
+
+
 def run_read(steps, warmup, nbytes=6 << 30):
     """HBM read ceiling: torch's sum over an nbytes float32 tensor (a library
     streaming reduction, nothing of this build), timed with events on torch's
@@ -482,9 +567,9 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode_model",
                     choices=["decode_model", "decode_long", "decode_ragged", "decode_single",
-                             "prefill", "proj", "matmul", "copy", "read"])
-    ap.add_argument("--wtype", default="q8_0", choices=["f32", "f16", "q8_0", "q4_0", "q6_k"],
-                    help="weight format of the matmul workload")
+                             "prefill", "proj", "matmul", "generate", "copy", "read"])
+    ap.add_argument("--wtype", default=None, choices=["f32", "f16", "q8_0", "q4_0", "q6_k"],
+                    help="weight format of the matmul (default q8_0) or generate (q4_0) workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill half")
     ap.add_argument("--split", type=int, default=0, help="decode split length (0 = auto)")
@@ -504,7 +589,28 @@ def main():
     if args.workload == "read":
         print(json.dumps(run_read(args.steps, args.warmup)))
         return
+    if args.workload == "generate":
+        wname = args.wtype or "q4_0"
+        r = run_generate(args.steps, args.warmup, cpu, wname)
+        line = {"metric": "decode tok/s (greedy, TinyLlama shapes)", "value": round(r["tok_per_s"], 1),
+                "unit": "tok/s", "n_gpus": 1, "steps": r["n_gen"], "warmup": args.warmup,
+                "ms_per_step": round(r["decode_ms_per_token"], 4), "higher_is_better": True,
+                "scaling": "weak", "vs_baseline": None, "dtype": f"{wname} weights, f32 compute",
+                "data": "synthetic (seeded random weights)",
+                "config": {"workload": "generate", "model": "TinyLlama-1.1B shapes", "weights": wname,
+                           "prompt_tokens": r["n_prompt"], "decode_tokens": r["n_gen"], "batch": 1,
+                           "parallelism": "none"},
+                "prefill_ms": round(r["prefill_ms"], 3),
+                "roofline": {"bound": "hbm", "achieved": round(r["GB_s"], 1), "peak": HBM_PEAK_GBS,
+                             "unit": "GB/s", "frac": round(r["frac"], 4), "traffic": None,
+                             "kernel": "whole decode step (113 launches)",
+                             "bytes_per_token": int(r["bytes_per_token"])}}
+        if r.get("cpu_baseline"):
+            line["cpu_baseline"] = r["cpu_baseline"]
+        print(json.dumps(line))
+        return
     if args.workload == "matmul":
+        args.wtype = args.wtype or "q8_0"
         r = run_matmul(args.steps, args.warmup, args.wtype)
         line = {"metric": "GEMV weight GB/s", "value": r["GB_s"], "unit": "GB/s", "n_gpus": 1,
                 "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(r["ms"], 5),

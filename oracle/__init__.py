@@ -392,6 +392,8 @@ def ref_forward():
         lib.ref_forward_tokens.restype = C.c_int
         lib.ref_generate_greedy.argtypes = [C.c_char_p, _ip, C.c_int, C.c_int, _ip]
         lib.ref_generate_greedy.restype = C.c_int
+        lib.ref_bench_trial.argtypes = [C.c_char_p, _ip, C.c_int, C.c_int, C.c_int, _dp, _dp]
+        lib.ref_bench_trial.restype = C.c_int
         _ref_fwd = lib
     return _ref_fwd
 
@@ -414,3 +416,13 @@ def ref_generate_greedy(path: str, prompt, n_gen: int):
     rc = lib.ref_generate_greedy(path.encode(), iptr(p), p.size, n_gen, iptr(out))
     assert rc == 0, lib.ref_forward_error()
     return out.tolist()
+
+
+def ref_bench_trial(path: str, prompt, n_decode: int, threads: int):
+    """(prefill ms, decode ms) of one trial of the reference's benchmark loop."""
+    lib = ref_forward()
+    p = np.ascontiguousarray(prompt, np.int32)
+    a, b = np.zeros(1), np.zeros(1)
+    rc = lib.ref_bench_trial(path.encode(), iptr(p), p.size, n_decode, threads, dptr(a), dptr(b))
+    assert rc == 0, lib.ref_forward_error()
+    return float(a[0]), float(b[0])

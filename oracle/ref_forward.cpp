@@ -13,6 +13,11 @@
 //   ref_generate_greedy -> that loop followed by the argmax decode loop of
 //                          src/generate.cpp:63-100 (temperature 0), without
 //                          the tokenizer and the EOS stop.
+//   ref_bench_trial     -> one trial of the reference's benchmark
+//                          (run_trial, src/benchmark.cpp:113-165): prompt
+//                          forward() calls timed, then n_decode greedy steps
+//                          timed, after set_num_threads() (src/ops.h).
+#include <chrono>
 #include <cstring>
 #include <exception>
 #include <string>
@@ -68,6 +73,41 @@ int ref_generate_greedy(const char* path, const int* prompt, int n_prompt, int n
             state.pos++;
             next = sample_argmax(state.logits, nv);
         }
+        return 0;
+    } catch (const std::exception& ex) {
+        g_error = ex.what();
+        return -1;
+    }
+}
+
+int ref_bench_trial(const char* path, const int* prompt, int n_prompt, int n_decode, int threads,
+                    double* prefill_ms, double* decode_ms)
+{
+    try {
+        using Clock = std::chrono::steady_clock;
+        set_num_threads(threads);
+        GGUFModel model(path);
+        RunState state;
+        state.allocate(model.config());
+        const int nv = static_cast<int>(model.config().n_vocab);
+        state.pos = 0;
+        const auto t0 = Clock::now();
+        for (int i = 0; i < n_prompt; ++i) {
+            forward(model, state, prompt[i], state.pos);
+            state.pos++;
+        }
+        const auto t1 = Clock::now();
+        int next = sample_argmax(state.logits, nv);
+        const auto t2 = Clock::now();
+        for (int i = 0; i < n_decode; ++i) {
+            forward(model, state, next, state.pos);
+            state.pos++;
+            next = sample_argmax(state.logits, nv);
+        }
+        const auto t3 = Clock::now();
+        *prefill_ms = std::chrono::duration<double, std::milli>(t1 - t0).count();
+        *decode_ms = std::chrono::duration<double, std::milli>(t3 - t2).count();
+        set_num_threads(1);
         return 0;
     } catch (const std::exception& ex) {
         g_error = ex.what();

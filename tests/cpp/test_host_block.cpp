@@ -6,18 +6,44 @@
 //   - RunState + attention_block (the forward() block, src/forward.cpp:192-208)
 //     over a 64-token sequence on two layers, checked against the CPU oracle
 //     (oracle/tl_oracle.c) within 1e-4 and the KV cache bit for bit,
-//   - the error convention: an out-of-range position throws std::runtime_error.
+//   - the error convention: an out-of-range position throws std::runtime_error,
+//   - DeviceModel + forward (src/forward.cpp:167-266) on a 2-layer model of
+//     TinyLlama's widths with seeded Q8_0 weights and a Q6_K-free tied
+//     classifier, against the oracle's forward within 1e-4 of the largest
+//     logit, and generate_greedy against the oracle's argmax chain.
 #include <cmath>
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <map>
 #include <random>
+#include <string>
 #include <stdexcept>
 #include <vector>
 
 #include "tla_host.h"
 
 extern "C" {
+struct oracle_layer {
+    const float* attn_norm;
+    const void *wq, *wk, *wv, *wo;
+    int type_q, type_k, type_v, type_o;
+    const float* ffn_norm;
+    const void *w_gate, *w_up, *w_down;
+    int type_ffn;
+};
+struct oracle_model {
+    int n_layers, n_embd, n_head, n_head_kv, n_ff, n_vocab, n_ctx;
+    float rope_freq_base, rms_norm_eps;
+    const void* token_embd;
+    int type_embd;
+    const float* output_norm;
+    const void* output;
+    int type_output;
+    const oracle_layer* layers;
+};
+int oracle_forward(const oracle_model* m, float* key_cache, float* value_cache, float* scratch,
+                   int token, int pos, float* logits);
 void oracle_rope(float* q, float* k, int pos, int head_dim, int n_head, int n_head_kv,
                  float freq_base);
 void oracle_attention(float* out, const float* q, const float* k, const float* v,
@@ -204,6 +230,131 @@ static void test_block(tla_host::Engine& eng, const tla_host::Config& cfg)
     check("layer == n_layers throws std::runtime_error", threw);
 }
 
+// Half-precision bits of a positive normal float (truncated mantissa).
+static std::uint16_t half_bits(float f)
+{
+    std::uint32_t b;
+    std::memcpy(&b, &f, 4);
+    const int e = int((b >> 23) & 0xFF) - 127 + 15;
+    return static_cast<std::uint16_t>((e << 10) | ((b >> 13) & 0x3FF));
+}
+
+// Seeded Q8_0 matrix [rows][cols]: scales in [2e-4, 3e-4), int8 weights.
+static std::vector<std::uint8_t> q8_matrix(std::mt19937& gen, int rows, int cols)
+{
+    std::vector<std::uint8_t> m(size_t(rows) * (cols / 32) * 34);
+    std::uniform_real_distribution<float> sd(2e-4f, 3e-4f);
+    std::uniform_int_distribution<int> qd(0, 255);
+    for (size_t b = 0; b < m.size() / 34; ++b) {
+        const std::uint16_t h = half_bits(sd(gen));
+        m[34 * b] = h & 0xFF;
+        m[34 * b + 1] = h >> 8;
+        for (int j = 0; j < 32; ++j) m[34 * b + 2 + j] = static_cast<std::uint8_t>(qd(gen));
+    }
+    return m;
+}
+
+static void test_forward(tla_host::Engine& eng, const tla_host::Config& cfg)
+{
+    std::printf("\n=== DeviceModel + forward (forward.cpp:167-266) ===\n");
+    const int E = int(cfg.n_embd), KV = 256, FF = int(cfg.n_ff), V = int(cfg.n_vocab), L = int(cfg.n_layers);
+    std::mt19937 gen(11);
+    std::uniform_real_distribution<float> nd(0.5f, 1.5f);
+    std::map<std::string, std::vector<std::uint8_t>> bytes;
+    auto norm = [&](const std::string& name) {
+        std::vector<float> v(E);
+        for (float& x : v) x = nd(gen);
+        bytes[name].resize(E * 4);
+        std::memcpy(bytes[name].data(), v.data(), E * 4);
+    };
+    bytes["token_embd.weight"] = q8_matrix(gen, V, E);  // tied classifier: no output.weight
+    norm("output_norm.weight");
+    for (int l = 0; l < L; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        norm(p + "attn_norm.weight");
+        norm(p + "ffn_norm.weight");
+        bytes[p + "attn_q.weight"] = q8_matrix(gen, E, E);
+        bytes[p + "attn_k.weight"] = q8_matrix(gen, KV, E);
+        bytes[p + "attn_v.weight"] = q8_matrix(gen, KV, E);
+        bytes[p + "attn_output.weight"] = q8_matrix(gen, E, E);
+        bytes[p + "ffn_gate.weight"] = q8_matrix(gen, FF, E);
+        bytes[p + "ffn_up.weight"] = q8_matrix(gen, FF, E);
+        bytes[p + "ffn_down.weight"] = q8_matrix(gen, E, FF);
+    }
+    auto lookup = [&](const std::string& name) {
+        auto it = bytes.find(name);
+        if (it == bytes.end()) throw std::runtime_error("Tensor not found: " + name);
+        const bool norm_w = name.find("norm") != std::string::npos;
+        return tla_host::TensorRef{it->second.data(), it->second.size(), norm_w ? 0 : 8};
+    };
+    const float eps = 1e-5f;
+    tla_host::DeviceModel dm(eng, eps, lookup);
+    tla_host::RunState st;
+    st.allocate(cfg, eng);
+
+    std::vector<oracle_layer> ol(L);
+    for (int l = 0; l < L; ++l) {
+        const std::string p = "blk." + std::to_string(l) + ".";
+        auto d = [&](const char* n) { return static_cast<const void*>(bytes[p + n].data()); };
+        ol[l] = {static_cast<const float*>(d("attn_norm.weight")), d("attn_q.weight"), d("attn_k.weight"),
+                 d("attn_v.weight"), d("attn_output.weight"), 8, 8, 8, 8,
+                 static_cast<const float*>(d("ffn_norm.weight")), d("ffn_gate.weight"),
+                 d("ffn_up.weight"), d("ffn_down.weight"), 8};
+    }
+    const oracle_model om = {L, E, int(cfg.n_head), int(cfg.n_head_kv), FF, V, int(cfg.n_ctx),
+                             cfg.rope_freq_base, eps, bytes["token_embd.weight"].data(), 8,
+                             reinterpret_cast<const float*>(bytes["output_norm.weight"].data()),
+                             bytes["token_embd.weight"].data(), 8, ol.data()};
+    std::vector<float> okc(size_t(L) * cfg.n_ctx * KV, 0.f), ovc(okc.size(), 0.f);
+    std::vector<float> scratch(5 * E + 2 * KV + cfg.n_ctx + 2 * FF), ologits(V);
+    const int tokens[6] = {1, 15043, 29871, 31999, 0, 2};
+    float worst = 0.f;
+    for (int pos = 0; pos < 6; ++pos) {
+        tla_host::forward(dm, st, tokens[pos], pos);
+        oracle_forward(&om, okc.data(), ovc.data(), scratch.data(), tokens[pos], pos, ologits.data());
+        float scale = 0.f, err = 0.f;
+        for (int i = 0; i < V; ++i) {
+            scale = std::fmax(scale, std::fabs(ologits[i]));
+            err = std::fmax(err, std::fabs(st.logits[i] - ologits[i]));
+        }
+        worst = std::fmax(worst, err / scale);
+    }
+    std::printf("    max |gpu - oracle| / max|logit| over 6 tokens: %.3g\n", worst);
+    check("forward matches the oracle within 1e-4 of the largest logit", worst <= 1e-4f);
+
+    // greedy: the oracle's argmax chain from a fresh cache
+    std::fill(okc.begin(), okc.end(), 0.f);
+    std::fill(ovc.begin(), ovc.end(), 0.f);
+    const std::vector<int> prompt = {1, 450, 4996};
+    const int n_gen = 8;
+    std::vector<int> want;
+    int pos = 0;
+    for (int t : prompt) oracle_forward(&om, okc.data(), ovc.data(), scratch.data(), t, pos++, ologits.data());
+    bool clear = true;
+    for (int i = 0; i < n_gen; ++i) {
+        int best = 0, second = -1;
+        for (int j = 1; j < V; ++j)
+            if (ologits[j] > ologits[best]) best = j;
+        for (int j = 0; j < V; ++j)
+            if (j != best && (second < 0 || ologits[j] > ologits[second])) second = j;
+        clear = clear && ologits[best] - ologits[second] > 2e-4f * std::fabs(ologits[best]);
+        want.push_back(best);
+        if (i + 1 < n_gen) oracle_forward(&om, okc.data(), ovc.data(), scratch.data(), best, pos++, ologits.data());
+    }
+    tla_host::RunState st2;
+    st2.allocate(cfg, eng);
+    const std::vector<int> got = tla_host::generate_greedy(dm, st2, prompt, n_gen);
+    check("greedy path has no near-ties", clear);
+    check("generate_greedy equals the oracle's argmax chain", got == want);
+    bool threw = false;
+    try {
+        tla_host::forward(dm, st, V, 0);
+    } catch (const std::runtime_error&) {
+        threw = true;
+    }
+    check("token == n_vocab throws std::runtime_error", threw);
+}
+
 int main()
 {
     try {
@@ -219,6 +370,7 @@ int main()
         test_attention(eng);
         test_rope(eng);
         test_block(eng, cfg);
+        test_forward(eng, cfg);
     } catch (const std::exception& e) {
         std::printf("ERROR: %s\n", e.what());
         return 1;

@@ -385,30 +385,38 @@ __device__ __forceinline__ long long byte_gap(const void* a, const void* b)
 }
 
 struct SegRegs {
-    long long w_off[kGemvMaxSeg], out_off[kGemvMaxSeg];  // bytes from segment 0's
-    long long out_stride[kGemvMaxSeg];
-    int rows[kGemvMaxSeg];
+    // Each field of segments 1 and 2 is kept as a difference from the
+    // previous segment's, so that locating a row adds terms selected against
+    // zero: a select between fields of one struct can compile to an indexed
+    // load from a private copy of the struct (scratch memory).
+    long long w_d1, w_d2, out_d1, out_d2;  // byte offsets: segment 1 - 0, 2 - 1
+    long long stride0, stride_d1, stride_d2;
+    int rows0, rows1;
     int n_seg;
     long long row_bytes;
 
     __device__ explicit SegRegs(const GemvParams& p)
     {
         static_assert(kGemvMaxSeg == 3, "three segments at most");
-#pragma unroll
-        for (int i = 0; i < kGemvMaxSeg; ++i) {
-            w_off[i] = i == 0 ? 0 : byte_gap(p.seg[i].w, p.seg[0].w);
-            out_off[i] = i == 0 ? 0 : byte_gap(p.seg[i].out, p.seg[0].out);
-            out_stride[i] = sreg(p.seg[i].out_stride);
-            rows[i] = sreg(p.seg[i].rows);
-        }
+        w_d1 = byte_gap(p.seg[1].w, p.seg[0].w);
+        w_d2 = byte_gap(p.seg[2].w, p.seg[1].w);
+        out_d1 = byte_gap(p.seg[1].out, p.seg[0].out);
+        out_d2 = byte_gap(p.seg[2].out, p.seg[1].out);
+        stride0 = sreg(p.seg[0].out_stride);
+        stride_d1 = sreg(p.seg[1].out_stride - p.seg[0].out_stride);
+        stride_d2 = sreg(p.seg[2].out_stride - p.seg[1].out_stride);
+        rows0 = sreg(p.seg[0].rows);
+        rows1 = sreg(p.seg[1].rows);
         n_seg = sreg(p.n_seg);
         row_bytes = sreg(static_cast<long long>(p.row_bytes));
     }
 };
 
-template <int kType, int kRows>
+// kSteps: unit steps of a row held at once (a row of up to kSteps x lanes
+// units is requested whole); rows with more units load the rest step by step.
+template <int kType, int kRows, int kSteps>
 struct RowGroup {
-    Unit<kType> un[kRows];
+    Unit<kType> un[kSteps][kRows];
     const unsigned char* w[kRows];
     float* out[kRows];
     long long out_stride[kRows];
@@ -425,32 +433,43 @@ struct RowGroup {
             const int r = r_first + spacing * k;
             valid[k] = r < p.total_rows;
             int rr = valid[k] ? r : 0;
-            const bool in1 = sr.n_seg > 1 && rr >= sr.rows[0];
-            rr = in1 ? rr - sr.rows[0] : rr;
-            const bool in2 = in1 && sr.n_seg > 2 && rr >= sr.rows[1];
-            rr = in2 ? rr - sr.rows[1] : rr;
-            const long long w_off = in2 ? sr.w_off[2] : in1 ? sr.w_off[1] : 0;
-            const long long out_off = in2 ? sr.out_off[2] : in1 ? sr.out_off[1] : 0;
+            const bool in1 = sr.n_seg > 1 && rr >= sr.rows0;
+            rr = in1 ? rr - sr.rows0 : rr;
+            const bool in2 = in1 && sr.n_seg > 2 && rr >= sr.rows1;
+            rr = in2 ? rr - sr.rows1 : rr;
+            const long long w_off = (in1 ? sr.w_d1 : 0) + (in2 ? sr.w_d2 : 0);
+            const long long out_off = (in1 ? sr.out_d1 : 0) + (in2 ? sr.out_d2 : 0);
             w[k] = p.seg[0].w + w_off + static_cast<long long>(rr) * sr.row_bytes;
             out[k] = reinterpret_cast<float*>(reinterpret_cast<char*>(p.seg[0].out) + out_off) + rr;
-            out_stride[k] = in2 ? sr.out_stride[2] : in1 ? sr.out_stride[1] : sr.out_stride[0];
+            out_stride[k] = sr.stride0 + (in1 ? sr.stride_d1 : 0) + (in2 ? sr.stride_d2 : 0);
         }
     }
-    __device__ void load(int u0, int n, int l)
+    // Unit step `s` (units u0 .. u0+n-1) into buffer b.
+    __device__ void load(int b, int u0, int n, int l)
     {
         const int lc = l < n ? l : 0;
 #pragma unroll
-        for (int k = 0; k < kRows; ++k) un[k].load(w[k], u0, n, lc);
+        for (int k = 0; k < kRows; ++k) un[b][k].load(w[k], u0, n, lc);
     }
-    // One vector: the pass's first unit step and the outputs' old values
-    // (for the residual add), requested together so that both arrive before
+    // The first kSteps unit steps of the rows (every lane loads: a step
+    // past the row's end reloads step 0).
+    __device__ void load_head(int units, int lanes, int l)
+    {
+#pragma unroll
+        for (int b = 0; b < kSteps; ++b) {
+            const int u0 = b * lanes < units ? b * lanes : 0;
+            load(b, u0, min(lanes, units - u0), l);
+        }
+    }
+    // One vector: the pass's first steps and the outputs' old values (for
+    // the residual add), requested together so that both arrive before
     // anything requested later.
     float old[kRows];
-    __device__ void request(const GemvParams& p, const SegRegs& sr, int r_first, int spacing, int n_first,
-                            int l)
+    __device__ void request(const GemvParams& p, const SegRegs& sr, int r_first, int spacing, int units,
+                            int lanes, int l)
     {
         locate(p, sr, r_first, spacing);
-        load(0, n_first, l);
+        load_head(units, lanes, l);
 #pragma unroll
         for (int k = 0; k < kRows; ++k) old[k] = *out[k];
     }
@@ -466,7 +485,7 @@ struct RowGroup {
 // before it computes the current one (two register buffers, A and B).  The
 // grid holds as many workgroups as fit on the GPU at once, so waves keep
 // loads in flight from start to end.
-template <int kType, int kLanesPerRow, int kRows, bool kMulti>
+template <int kType, int kLanesPerRow, int kRows, int kSteps, bool kMulti>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
 {
     static_assert(!kMulti || kRows == 1, "several vectors take one row per lane group");
@@ -484,12 +503,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
     const int units = p.cols / kUnit;
     const int n_vec = kMulti ? p.n_vec : 1;
     const int n_pass = (p.total_rows + kPassRows - 1) / kPassRows;
-    const int n_first = min(kLanesPerRow, units);
 
     // x for one vector of up to kXRegs x kThreads columns is requested
     // before the weights (loads complete in order, so anything requested
     // after the weights could only be used once they have all arrived).
-    constexpr int kXRegs = 8;
+    // (x for a row of kLanesPerRow x kSteps units, at most)
+    constexpr int kXRegs = kLanesPerRow * kSteps * kUnit / kThreads;
     const bool x_early = !kMulti && p.cols <= kXRegs * kThreads && !(p.norm_w && p.x2);
     float xr[kXRegs], nr[kXRegs];
     if (x_early) {
@@ -505,13 +524,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
 
     const SegRegs sr(p);
     int ps = wave;
-    RowGroup<kType, kRows> ga;
-    [[maybe_unused]] RowGroup<kType, kRows> gb;
+    RowGroup<kType, kRows, kSteps> ga;
+    [[maybe_unused]] RowGroup<kType, kRows, kSteps> gb;
     if constexpr (kMulti) {
         ga.locate(p, sr, ps * kPassRows + sub, kRowsPerWave);
-        ga.load(0, n_first, l);
+        ga.load_head(units, kLanesPerRow, l);
     } else {
-        ga.request(p, sr, ps * kPassRows + sub, kRowsPerWave, n_first, l);
+        ga.request(p, sr, ps * kPassRows + sub, kRowsPerWave, units, kLanesPerRow, l);
     }
 
     // Stage x in LDS (SwiGLU'd when asked), then rmsnorm's scaling in place
@@ -577,20 +596,20 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
         __syncthreads();
     }
 
-    // One pass over the rows in g (its first unit step already loaded).
-    auto run_pass = [&](RowGroup<kType, kRows>& g) {
+    // One pass over the rows in g (its first kSteps unit steps loaded).
+    auto run_pass = [&](RowGroup<kType, kRows, kSteps>& g) {
+        const float* xs_base = xs_all;
         float acc[kRows][kGemvMaxVec];
 #pragma unroll
         for (int k = 0; k < kRows; ++k)
 #pragma unroll
             for (int v = 0; v < kGemvMaxVec; ++v) acc[k][v] = 0.f;
-        for (int u0 = 0; u0 < units; u0 += kLanesPerRow) {
-            const int n = min(kLanesPerRow, units - u0);
-            if (u0 > 0) g.load(u0, n, l);
-            if (l >= n) continue;
+        // dot products of unit step (u0, n) held in buffer b
+        auto step = [&](int b, int u0, int n) {
+            if (l >= n) return;
 #pragma unroll 1
             for (int v = 0; v < n_vec; ++v) {
-                const float* xs = xs_all + v * xs_len;
+                const float* xs = xs_base + v * xs_len;
                 float pt[kRows][4];
 #pragma unroll
                 for (int q = 0; q < 4; ++q) {
@@ -600,17 +619,30 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
                     for (int j = 0; j < 16 / kW; ++j)
                         lds_x<kW>(xs, Unit<kType>::xcol(u0, n, l, q, j), xv + kW * j);
 #pragma unroll
-                    for (int k = 0; k < kRows; ++k) pt[k][q] = g.un[k].part(q, xv);
+                    for (int k = 0; k < kRows; ++k) pt[k][q] = g.un[b][k].part(q, xv);
                 }
                 const float* s16 = s16_all + v * nb16;
 #pragma unroll
                 for (int k = 0; k < kRows; ++k) {
-                    const float f = g.un[k].finish(pt[k], s16);
+                    const float f = g.un[b][k].finish(pt[k], s16);
 #pragma unroll
                     for (int vv = 0; vv < kGemvMaxVec; ++vv)
                         if (vv == v) acc[k][vv] += f;
                 }
             }
+        };
+        if constexpr (kSteps == 1) {
+            // steps after the first (longer rows, several-vector launches
+            // only) load one after another
+            for (int u0 = 0; u0 < units; u0 += kLanesPerRow) {
+                const int n = min(kLanesPerRow, units - u0);
+                if (u0 > 0) g.load(0, u0, n, l);
+                step(0, u0, n);
+            }
+        } else {
+#pragma unroll
+            for (int b = 0; b < kSteps; ++b)
+                if (b * kLanesPerRow < units) step(b, b * kLanesPerRow, min(kLanesPerRow, units - b * kLanesPerRow));
         }
         // The group's last lane stores; the old values were read with the
         // pass's request (one vector) or here (several).
@@ -635,7 +667,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
             ps += n_waves;
             if (ps >= n_pass) break;
             ga.locate(p, sr, ps * kPassRows + sub, kRowsPerWave);
-            ga.load(0, n_first, l);
+            ga.load_head(units, kLanesPerRow, l);
         }
         return;
     }
@@ -643,11 +675,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
     // pass's request goes out before the current pass is computed.  Past the
     // last pass the request reads row 0 again (locate maps it there).
     while (ps < n_pass) {
-        gb.request(p, sr, (ps + n_waves) * kPassRows + sub, kRowsPerWave, n_first, l);
+        gb.request(p, sr, (ps + n_waves) * kPassRows + sub, kRowsPerWave, units, kLanesPerRow, l);
+        __builtin_amdgcn_sched_barrier(0);  // the request goes out before the compute
         run_pass(ga);
         ps += n_waves;
         if (ps >= n_pass) break;
-        ga.request(p, sr, (ps + n_waves) * kPassRows + sub, kRowsPerWave, n_first, l);
+        ga.request(p, sr, (ps + n_waves) * kPassRows + sub, kRowsPerWave, units, kLanesPerRow, l);
+        __builtin_amdgcn_sched_barrier(0);
         run_pass(gb);
         ps += n_waves;
     }
@@ -744,11 +778,21 @@ __global__ __launch_bounds__(1024) void argmax_kernel(int* out, int* out2, const
     __shared__ int s_i[16];
     float bv = -__builtin_huge_valf();
     int bi = 0x7fffffff;
-    for (int i = threadIdx.x; i < n; i += 1024) {
-        const float v = x[i];
-        if (beats(v, i, bv, bi)) {
-            bv = v;
-            bi = i;
+    // eight independent loads in flight per thread
+    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 1024) {
+        float v[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = i0 + j * 1024;
+            v[j] = x[i < n ? i : i0];
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            const int i = i0 + j * 1024;
+            if (i < n && beats(v[j], i, bv, bi)) {
+                bv = v[j];
+                bi = i;
+            }
         }
     }
 #pragma unroll
@@ -807,34 +851,41 @@ int resident_blocks(Kernel kernel, size_t lds)
     return blocks;
 }
 
-template <int kType, int kLanes, int kRows, bool kMulti>
+template <int kType, int kLanes, int kRows, int kSteps, bool kMulti>
 hipError_t launch_shaped(const GemvParams& p, hipStream_t s)
 {
     const size_t lds = static_cast<size_t>(p.n_vec) * (xs_floats(p.cols) + p.cols / 16) * sizeof(float);
     constexpr int kPassRowsPerBlock = (kThreads / 64) * (64 / kLanes) * kRows;
     const int needed = (p.total_rows + kPassRowsPerBlock - 1) / kPassRowsPerBlock;
-    const auto kernel = gemv_kernel<kType, kLanes, kRows, kMulti>;
+    const auto kernel = gemv_kernel<kType, kLanes, kRows, kSteps, kMulti>;
     const int blocks = std::min(needed, resident_blocks(kernel, lds));
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), lds, s, p);
     return hipGetLastError();
 }
 
 // Lanes per row: 32 when a row has at most 32 units (cols <= 2048), else
-// 64.  Rows per lane group: the format's kRows with one vector when the rows
-// still give every resident wave a pass, else 1.
+// 64; a row of up to 128 units (cols <= 8192) is requested whole (two unit
+// steps per lane).  Rows per lane group: the format's kRows with one vector
+// when the rows still give every resident wave a pass, else 1.
 template <int kType>
 hipError_t launch_typed(const GemvParams& p, hipStream_t s)
 {
-    const bool narrow = p.cols / kUnit <= 32;
-    if (p.n_vec > 1)
-        return narrow ? launch_shaped<kType, 32, 1, true>(p, s) : launch_shaped<kType, 64, 1, true>(p, s);
+    const int units = p.cols / kUnit;
+    // several vectors, or rows longer than two steps of 64 lanes: one row per
+    // lane group, steps beyond the first loaded one after another
+    if (p.n_vec > 1 || units > 128)
+        return units <= 32 ? launch_shaped<kType, 32, 1, 1, true>(p, s)
+                           : launch_shaped<kType, 64, 1, 1, true>(p, s);
+    if (units > 64 && units <= 128) return launch_shaped<kType, 64, 1, 2, false>(p, s);
+    const bool narrow = units <= 32;
     constexpr int kR = Unit<kType>::kRows;
     if constexpr (kR > 1) {
         const int passes = (p.total_rows + kR - 1) / kR / (narrow ? 2 : 1);  // wave passes
         if (passes >= 4 * 256 * 4)
-            return narrow ? launch_shaped<kType, 32, kR, false>(p, s) : launch_shaped<kType, 64, kR, false>(p, s);
+            return narrow ? launch_shaped<kType, 32, kR, 1, false>(p, s)
+                          : launch_shaped<kType, 64, kR, 1, false>(p, s);
     }
-    return narrow ? launch_shaped<kType, 32, 1, false>(p, s) : launch_shaped<kType, 64, 1, false>(p, s);
+    return narrow ? launch_shaped<kType, 32, 1, 1, false>(p, s) : launch_shaped<kType, 64, 1, 1, false>(p, s);
 }
 
 }  // namespace

@@ -63,6 +63,7 @@ void RunState::allocate(const Config& cfg, Engine& eng)
     engine = &eng;
     n_embd_ = cfg.n_embd;
     kv_dim_ = cfg.n_head_kv * cfg.head_dim();
+    n_vocab_ = cfg.n_vocab;
 
     x = new float[cfg.n_embd]();
     xb = new float[cfg.n_embd]();
@@ -82,6 +83,10 @@ void RunState::allocate(const Config& cfg, Engine& eng)
     d_qkv = static_cast<float*>(p);
     check(tla_alloc(eng.get(), sizeof(float) * cfg.n_embd, &p), "output staging");
     d_out = static_cast<float*>(p);
+    if (cfg.n_vocab) {
+        check(tla_alloc(eng.get(), sizeof(float) * cfg.n_vocab, &p), "logits");
+        d_logits = static_cast<float*>(p);
+    }
     pos = 0;
 }
 
@@ -102,8 +107,9 @@ void RunState::free_buffers()
         tla_free(engine->get(), value_cache);
         tla_free(engine->get(), d_qkv);
         tla_free(engine->get(), d_out);
+        if (d_logits) tla_free(engine->get(), d_logits);
     }
-    key_cache = value_cache = d_qkv = d_out = nullptr;
+    key_cache = value_cache = d_qkv = d_out = d_logits = nullptr;
     engine = nullptr;
 }
 
@@ -121,6 +127,121 @@ void attention_block(RunState& state, int layer, int pos)
           "rope+attention");
     check(tla_memcpy_d2h(e, state.xb2, state.d_out, sizeof(float) * state.n_embd_),
           "attention output download");
+}
+
+void matmul(Engine& eng, float* out, const void* w, const float* x, int rows, int cols, int type)
+{
+    check(tla_matmul(eng.get(), out, w, x, rows, cols, type), "matmul");
+}
+
+void rmsnorm(Engine& eng, float* out, const float* x, const float* weight, int size, float eps)
+{
+    check(tla_rmsnorm(eng.get(), out, x, weight, size, eps), "rmsnorm");
+}
+
+void vec_add(Engine& eng, float* out, const float* x, int size)
+{
+    check(tla_vec_add(eng.get(), out, x, size), "vec_add");
+}
+
+void silu(Engine& eng, float* x, int size)
+{
+    check(tla_silu(eng.get(), x, size), "silu");
+}
+
+void elementwise_mul(Engine& eng, float* a, const float* b, int size)
+{
+    check(tla_elementwise_mul(eng.get(), a, b, size), "elementwise_mul");
+}
+
+void ffn_swiglu(Engine& eng, float* out, const float* input, float* hb, float* hb2,
+                const void* w_gate, const void* w_up, const void* w_down, int n_ff, int n_embd,
+                int type)
+{
+    check(tla_ffn_swiglu(eng.get(), out, input, hb, hb2, w_gate, w_up, w_down, n_ff, n_embd, type),
+          "ffn_swiglu");
+}
+
+const void* DeviceModel::upload(const TensorRef& t)
+{
+    void* p = nullptr;
+    check(tla_alloc(engine.get(), t.bytes, &p), "weight allocation");
+    buffers_.push_back(p);
+    check(tla_memcpy_h2d(engine.get(), p, t.data, t.bytes), "weight upload");
+    weight_bytes += t.bytes;
+    return p;
+}
+
+DeviceModel::DeviceModel(Engine& eng, float rms_norm_eps, const Lookup& tensor) : engine(eng)
+{
+    const Config& cfg = eng.config();
+    try {
+        const TensorRef embd = tensor("token_embd.weight");
+        model.token_embd = upload(embd);
+        model.type_embd = embd.type;
+        model.output_norm = static_cast<const float*>(upload(tensor("output_norm.weight")));
+        TensorRef out{};
+        bool tied = false;
+        try {
+            out = tensor("output.weight");
+        } catch (const std::exception&) {
+            tied = true;  // tied embeddings (src/forward.cpp:250-258)
+        }
+        model.output = tied ? model.token_embd : upload(out);
+        model.type_output = tied ? embd.type : out.type;
+        model.n_ff = static_cast<int>(cfg.n_ff);
+        model.n_vocab = static_cast<int>(cfg.n_vocab);
+        model.rms_norm_eps = rms_norm_eps;
+        layers.resize(cfg.n_layers);
+        for (std::uint32_t l = 0; l < cfg.n_layers; ++l) {
+            const std::string p = "blk." + std::to_string(l) + ".";
+            tla_layer_weights& L = layers[l];
+            auto w = [&](const char* name, int* type) {
+                const TensorRef t = tensor(p + name);
+                if (type) *type = t.type;
+                return upload(t);
+            };
+            L.attn_norm = static_cast<const float*>(w("attn_norm.weight", nullptr));
+            L.wq = w("attn_q.weight", &L.type_q);
+            L.wk = w("attn_k.weight", &L.type_k);
+            L.wv = w("attn_v.weight", &L.type_v);
+            L.wo = w("attn_output.weight", &L.type_o);
+            L.ffn_norm = static_cast<const float*>(w("ffn_norm.weight", nullptr));
+            L.w_gate = w("ffn_gate.weight", &L.type_ffn);  // one type for the FFN, as ffn_swiglu takes
+            L.w_up = w("ffn_up.weight", nullptr);
+            L.w_down = w("ffn_down.weight", nullptr);
+        }
+        model.layers = layers.data();
+    } catch (...) {
+        for (void* b : buffers_) tla_free(engine.get(), b);
+        throw;
+    }
+}
+
+DeviceModel::~DeviceModel()
+{
+    for (void* b : buffers_) tla_free(engine.get(), b);
+}
+
+void forward(DeviceModel& model, RunState& state, int token, int pos)
+{
+    if (!state.engine || !state.d_logits) throw std::runtime_error("forward: RunState not allocated with n_vocab");
+    tla_engine* e = state.engine->get();
+    check(tla_forward(e, &model.model, state.key_cache, state.value_cache, token, pos, state.d_logits),
+          "forward");
+    check(tla_memcpy_d2h(e, state.logits, state.d_logits, sizeof(float) * state.n_vocab_), "logits download");
+}
+
+std::vector<int> generate_greedy(DeviceModel& model, RunState& state, const std::vector<int>& prompt,
+                                 int n_gen)
+{
+    if (!state.engine) throw std::runtime_error("generate_greedy: RunState not allocated");
+    std::vector<int> out(n_gen > 0 ? n_gen : 0);
+    check(tla_generate_greedy(state.engine->get(), &model.model, state.key_cache, state.value_cache,
+                              prompt.data(), static_cast<int>(prompt.size()), n_gen, out.data()),
+          "generate_greedy");
+    state.pos = static_cast<int>(prompt.size()) + n_gen - 1;
+    return out;
 }
 
 }  // namespace tla_host

@@ -18,11 +18,25 @@
 //                                 after the reference's members
 //   tla_host::attention_block  -> the block of forward() at
 //                                 src/forward.cpp:192-208 (rope + attention)
+//   tla_host::matmul / rmsnorm / vec_add / silu / elementwise_mul / ffn_swiglu
+//                              -> the ops of src/ops.h:64-66, 95-96, 118,
+//                                 131, 143, 232-235 (device pointers)
+//   tla_host::DeviceModel      -> the weights forward() reads from the GGUF
+//                                 file (src/forward.cpp:167-266), copied to
+//                                 the device unchanged
+//   tla_host::forward          -> forward(GGUFModel&, RunState&, token, pos)
+//                                 (src/forward.h): the whole pass on the
+//                                 device, logits into state.logits
+//   tla_host::generate_greedy  -> the generation loop of src/generate.cpp:56-100
+//                                 at temperature 0 (tokens, not text)
 #pragma once
 
+#include <cstddef>
 #include <cstdint>
+#include <functional>
 #include <stdexcept>
 #include <string>
+#include <vector>
 
 #include "tla_attention.h"
 
@@ -89,6 +103,7 @@ struct RunState {
     Engine* engine = nullptr;
     float* d_qkv = nullptr;  // device copy of q | k | v (one transfer)
     float* d_out = nullptr;  // device attention output [n_embd]
+    float* d_logits = nullptr;  // device logits [n_vocab] (forward())
 
     void allocate(const Config& cfg, Engine& eng);
     void free_buffers();
@@ -100,8 +115,10 @@ struct RunState {
 
 private:
     friend void attention_block(RunState& state, int layer, int pos);
+    friend struct DeviceModel;
+    friend void forward(struct DeviceModel& model, RunState& state, int token, int pos);
     float* qkv_host_ = nullptr;  // q | k | v contiguous, so one H2D copy
-    std::uint32_t n_embd_ = 0, kv_dim_ = 0;
+    std::uint32_t n_embd_ = 0, kv_dim_ = 0, n_vocab_ = 0;
 };
 
 // rope(state.q, state.k, pos) + attention(state.xb2, ..., layer, pos) on the
@@ -109,5 +126,54 @@ private:
 // device->host copy of the output into state.xb2.  state.q and state.k are
 // left unrotated on the host (forward() does not read them afterwards).
 void attention_block(RunState& state, int layer, int pos);
+
+// ---- the projections and the FFN (device pointers) --------------------------
+void matmul(Engine& eng, float* out, const void* w, const float* x, int rows, int cols, int type);
+void rmsnorm(Engine& eng, float* out, const float* x, const float* weight, int size, float eps);
+void vec_add(Engine& eng, float* out, const float* x, int size);
+void silu(Engine& eng, float* x, int size);
+void elementwise_mul(Engine& eng, float* a, const float* b, int size);
+void ffn_swiglu(Engine& eng, float* out, const float* input, float* hb, float* hb2,
+                const void* w_gate, const void* w_up, const void* w_down, int n_ff, int n_embd,
+                int type);
+
+// ---- the whole forward pass --------------------------------------------------
+// One tensor as the GGUF file holds it: host bytes and ggml_type id.
+struct TensorRef {
+    const void* data = nullptr;
+    std::size_t bytes = 0;
+    int type = 0;
+};
+
+// The tensors forward() reads, copied to the device.  `tensor(name)` returns
+// a tensor by its GGUF name and throws when it is missing (the reference's
+// GGUFModel::tensor_info does); "output.weight" may be missing (tied
+// embeddings), then token_embd.weight is the classifier.
+struct DeviceModel {
+    using Lookup = std::function<TensorRef(const std::string&)>;
+
+    DeviceModel(Engine& eng, float rms_norm_eps, const Lookup& tensor);
+    ~DeviceModel();
+    DeviceModel(const DeviceModel&) = delete;
+    DeviceModel& operator=(const DeviceModel&) = delete;
+
+    Engine& engine;
+    tla_model model{};
+    std::vector<tla_layer_weights> layers;
+    std::size_t weight_bytes = 0;
+
+private:
+    std::vector<void*> buffers_;
+    const void* upload(const TensorRef& t);
+};
+
+// forward(model, state, token, pos): state.logits (host) receives the
+// n_vocab logits; the KV cache is state's (device).
+void forward(DeviceModel& model, RunState& state, int token, int pos);
+
+// Greedy generation on the device (prompt at positions 0.., then n_gen
+// tokens); returns the generated tokens.
+std::vector<int> generate_greedy(DeviceModel& model, RunState& state, const std::vector<int>& prompt,
+                                 int n_gen);
 
 }  // namespace tla_host
