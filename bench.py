@@ -473,20 +473,25 @@ def run_generate(steps, warmup, cpu, wname="q4_0", n_prompt=32, n_gen=20):
     kc, vc = eng.kv_cache(1)
     prompt = [1] + W.rng("block", 3).integers(2, spec.n_vocab, n_prompt - 1).tolist()
 
-    def call(n):
+    def call(n, batch=False):
         eng.synchronize()
         eng.event(0)
-        toks = eng.generate_greedy(dm, kc.ptr, vc.ptr, prompt, n)
+        toks = eng.generate_greedy(dm, kc.ptr, vc.ptr, prompt, n, batch_prompt=batch)
         eng.event(1)
         return eng.elapsed(0, 1), toks
 
     for _ in range(max(1, warmup)):
         call(n_gen + 1)
+        call(1, True)
     trials = max(3, steps // 5)
     pre = median([call(1)[0] for _ in range(trials)])
+    pre_batch = median([call(1, True)[0] for _ in range(trials)])
     full = median([call(n_gen + 1)[0] for _ in range(trials)])
     dec = (full - pre) / n_gen
     _, toks = call(n_gen + 1)
+    _, toks_b = call(n_gen + 1, True)
+    log(f"[bench] generate {wname}: prompt as one batch {pre_batch:.2f} ms "
+        f"({pre_batch / n_prompt * 1e3:.0f} us/token); same tokens: {toks_b == toks}")
     # HBM bytes a decode token must move: every weight once (one embedding
     # row), the KV cache up to its position (mean position of the 20 steps)
     weight_bytes = sum(len(r) for name, (d, ty, r) in t.items() if name != "token_embd.weight")
@@ -498,7 +503,8 @@ def run_generate(steps, warmup, cpu, wname="q4_0", n_prompt=32, n_gen=20):
     log(f"[bench] generate {wname}: prefill {n_prompt} tokens {pre:.2f} ms ({pre / n_prompt * 1e3:.0f} "
         f"us/token), decode {dec * 1e3:.0f} us/token = {1e3 / dec:.0f} tok/s; {tok_bytes / 1e6:.0f} MB "
         f"per token -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}); tokens {toks[:8]}...")
-    res = {"decode_ms_per_token": dec, "prefill_ms": pre, "tok_per_s": 1e3 / dec,
+    res = {"decode_ms_per_token": dec, "prefill_ms": pre, "prefill_batched_ms": pre_batch,
+           "tok_per_s": 1e3 / dec,
            "bytes_per_token": tok_bytes, "GB_s": gbs, "frac": gbs / HBM_PEAK_GBS,
            "n_prompt": n_prompt, "n_gen": n_gen}
     dm.free()
@@ -601,6 +607,7 @@ def main():
                            "prompt_tokens": r["n_prompt"], "decode_tokens": r["n_gen"], "batch": 1,
                            "parallelism": "none"},
                 "prefill_ms": round(r["prefill_ms"], 3),
+                "prefill_batched_ms": round(r["prefill_batched_ms"], 3),
                 "roofline": {"bound": "hbm", "achieved": round(r["GB_s"], 1), "peak": HBM_PEAK_GBS,
                              "unit": "GB/s", "frac": round(r["frac"], 4), "traffic": None,
                              "kernel": "whole decode step (113 launches)",

@@ -50,7 +50,10 @@ enum tla_flags {
      * kernel, as forward() does with rope() before attention()
      * (src/forward.cpp:192-206).  Without it q and k are taken as already
      * rotated, which is attention()'s contract (src/ops.h:185-186). */
-    TLA_ROTATE = 1
+    TLA_ROTATE = 1,
+    /* tla_generate_greedy: run the prompt through the model as one batch
+     * (tla_prefill_forward) instead of token by token. */
+    TLA_BATCH_PROMPT = 2
 };
 
 /* Shape fields of llama_config_t (src/gguf.h:139-168) that the path uses.
@@ -267,9 +270,21 @@ typedef struct tla_model {
 int tla_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* value_cache_dev,
                 int token, int pos, float* logits_dev);
 
+/* The prompt loop of src/generate.cpp:56-59 as one batch: forward() for
+ * tokens_host[0..n_tok) at positions pos0..pos0+n_tok-1, each layer over all
+ * tokens at once (multi-vector GEMVs, the causal MFMA prefill attention
+ * with RoPE + append in-kernel); logits_dev [n_vocab] receives the last
+ * token's logits (the ones generate() samples from).  The KV cache ends as
+ * after n_tok forward() calls (to fp32 rounding: the attention sums are
+ * grouped differently). */
+int tla_prefill_forward(tla_engine* e, const tla_model* m, float* key_cache_dev,
+                        float* value_cache_dev, const int* tokens_host, int n_tok, int pos0,
+                        float* logits_dev);
+
 /* The generation loop with greedy sampling (src/generate.cpp:56-100 at
  * temperature 0, without the tokenizer): forward() over the prompt at
- * positions 0..n_prompt-1, then n_gen tokens each from the argmax of the
+ * positions 0..n_prompt-1 (token by token, or as one batch with
+ * TLA_BATCH_PROMPT), then n_gen tokens each from the argmax of the
  * previous logits.  The sampled token stays on the device between steps,
  * so every launch is queued without waiting; tokens_host [n_gen] is
  * written at the end.  The caller stops at its EOS token, as the reference
@@ -277,7 +292,7 @@ int tla_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* 
  * and n_prompt + n_gen - 1 <= n_ctx. */
 int tla_generate_greedy(tla_engine* e, const tla_model* m, float* key_cache_dev,
                         float* value_cache_dev, const int* prompt_host, int n_prompt, int n_gen,
-                        int* tokens_host);
+                        int flags, int* tokens_host);
 
 /* ---- measurement hooks (no reference counterpart) ------------------- */
 enum tla_kernel_id {

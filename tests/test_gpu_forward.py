@@ -251,3 +251,79 @@ def test_forward_errors(tla, W, engines):
             assert e.value.code == 2
     finally:
         dm.free()
+
+
+@pytest.mark.parametrize("name", CASES)
+def test_prefill_forward_matches_token_loop(tla, O, W, engines, name):
+    """tla_prefill_forward: the prompt as one batch (src/generate.cpp:56-59
+    batched).  The last token's logits against the reference's (golden),
+    in one call and in two calls (pos0 > 0); the KV cache against the
+    token-by-token device path: layer 0 bit for bit (its inputs are the
+    embeddings in both), later layers within 1e-4 of the largest entry."""
+    g = golden("forward.npz")
+    spec, t = model_from_golden(W, g, name)
+    eng = spec_engine(engines, spec)
+    toks = g["tokens"].tolist()
+    want = g[f"{name}_logits"][-1]
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    try:
+        with device_arrays() as track:
+            kc, vc = eng.kv_cache(1)
+            track(kc), track(vc)
+            kc2, vc2 = eng.kv_cache(1)
+            track(kc2), track(vc2)
+            lg = track(eng.array((spec.n_vocab,)))
+            eng.prefill_forward(dm, kc.ptr, vc.ptr, toks, 0, lg.ptr)
+            check_logits(lg.download()[None], want[None], f"{name} prefill_forward, one batch")
+            eng.prefill_forward(dm, kc2.ptr, vc2.ptr, toks[:7], 0, lg.ptr)
+            eng.prefill_forward(dm, kc2.ptr, vc2.ptr, toks[7:], 7, lg.ptr)
+            check_logits(lg.download()[None], want[None], f"{name} prefill_forward, two batches")
+            batch_k, batch_v = kc.download(), vc.download()
+            # token-by-token device path into fresh caches
+            kc3, vc3 = eng.kv_cache(1)
+            track(kc3), track(vc3)
+            for i, tk in enumerate(toks):
+                eng.forward(dm, kc3.ptr, vc3.ptr, int(tk), i, lg.ptr)
+            loop_k, loop_v = kc3.download(), vc3.download()
+    finally:
+        dm.free()
+    n = len(toks)
+    assert np.array_equal(bits(batch_k[0, 0, :n]), bits(loop_k[0, 0, :n])), "layer 0 keys"
+    assert np.array_equal(bits(batch_v[0, 0, :n]), bits(loop_v[0, 0, :n])), "layer 0 values"
+    for a, b in ((batch_k, loop_k), (batch_v, loop_v)):
+        assert np.abs(a - b).max() <= 1e-4 * np.abs(b).max()
+
+
+@pytest.mark.parametrize("name", ["q8_0", "mixed"])
+def test_generate_greedy_batched_prompt(tla, O, W, engines, name):
+    g = golden("forward.npz")
+    spec, t = model_from_golden(W, g, name)
+    eng = spec_engine(engines, spec)
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    try:
+        with device_arrays() as track:
+            kc, vc = eng.kv_cache(1)
+            track(kc), track(vc)
+            got = eng.generate_greedy(dm, kc.ptr, vc.ptr, g["prompt"].tolist(),
+                                      len(g[f"{name}_greedy"]), batch_prompt=True)
+    finally:
+        dm.free()
+    assert got == g[f"{name}_greedy"].tolist()
+
+
+def test_prefill_forward_errors(tla, W, engines):
+    spec = W.ModelSpec(2, 256, 4, 2, 512, 384, 64)
+    t = W.make_model(spec, W.W_Q8_0, salt=3)
+    eng = spec_engine(engines, spec)
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    try:
+        with device_arrays() as track:
+            kc, vc = eng.kv_cache(1)
+            track(kc), track(vc)
+            lg = track(eng.array((spec.n_vocab,)))
+            for toks, pos0 in (([1, 2, 384], 0), ([1] * 10, 60), ([1], -1)):
+                with pytest.raises(tla.TlaError) as e:
+                    eng.prefill_forward(dm, kc.ptr, vc.ptr, toks, pos0, lg.ptr)
+                assert e.value.code == 2
+    finally:
+        dm.free()

@@ -42,6 +42,7 @@ TLA_ERR_UNSUPPORTED = 3
 TLA_ERR_DEVICE = 4
 TLA_ERR_OUT_OF_MEMORY = 5
 TLA_ROTATE = 1
+TLA_BATCH_PROMPT = 2
 
 KERNEL_DECODE, KERNEL_PREFILL, KERNEL_APPEND, KERNEL_GEMV = range(4)
 # weight formats: the reference's ggml_type ids (src/gguf.h:23-32)
@@ -124,8 +125,10 @@ SIGNATURES = {
     "tla_embed": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
     "tla_argmax": (C.c_int, [_vp, _vp, C.c_int, C.POINTER(C.c_int)]),
     "tla_forward": (C.c_int, [_vp, C.POINTER(Model), _vp, _vp, C.c_int, C.c_int, _vp]),
+    "tla_prefill_forward": (C.c_int, [_vp, C.POINTER(Model), _vp, _vp, C.POINTER(C.c_int), C.c_int,
+                                      C.c_int, _vp]),
     "tla_generate_greedy": (C.c_int, [_vp, C.POINTER(Model), _vp, _vp, C.POINTER(C.c_int), C.c_int,
-                                      C.c_int, C.POINTER(C.c_int)]),
+                                      C.c_int, C.c_int, C.POINTER(C.c_int)]),
     "tla_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
     "tla_rope_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
     "tla_decode": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int,
@@ -322,11 +325,18 @@ class Engine:
         _check(lib().tla_forward(self.h, C.byref(model.c), kc, vc, token, pos, logits),
                "tla_forward")
 
-    def generate_greedy(self, model: "DeviceModel", kc: int, vc: int, prompt, n_gen: int):
+    def prefill_forward(self, model: "DeviceModel", kc: int, vc: int, tokens, pos0: int, logits: int):
+        p = (C.c_int * len(tokens))(*[int(t) for t in tokens])
+        _check(lib().tla_prefill_forward(self.h, C.byref(model.c), kc, vc, p, len(tokens), pos0,
+                                         logits), "tla_prefill_forward")
+
+    def generate_greedy(self, model: "DeviceModel", kc: int, vc: int, prompt, n_gen: int,
+                        batch_prompt: bool = False):
         p = (C.c_int * len(prompt))(*[int(t) for t in prompt])
         out = (C.c_int * n_gen)()
         _check(lib().tla_generate_greedy(self.h, C.byref(model.c), kc, vc, p, len(prompt), n_gen,
-                                         out), "tla_generate_greedy")
+                                         TLA_BATCH_PROMPT if batch_prompt else 0, out),
+               "tla_generate_greedy")
         return list(out)
 
     # ---- measurement --------------------------------------------------------------

@@ -814,18 +814,20 @@ int check_model(const tla_engine* e, const tla_model* m)
     return TLA_OK;
 }
 
-// Engine scratch for forward(): x | xb | q | k | v | att | hb | hb2 | logits
-// floats, then n_tokens + 1 ints.
+// Engine scratch for forward() over `rows` tokens at once: x | xb | q | att
+// [rows][n_embd], k | v [rows][kv_dim], hb [rows][2][n_ff] (gate, up),
+// logits [n_vocab] floats, then n_ints ints.
 struct FwdBufs {
     float *x, *xb, *q, *k, *v, *att, *hb, *hb2, *logits;
     int* tokens;
 };
 
-int fwd_bufs(tla_engine* e, const tla_model* m, int n_tokens, FwdBufs* b)
+int fwd_bufs(tla_engine* e, const tla_model* m, int rows, int n_ints, FwdBufs* b)
 {
     const size_t embd = e->cfg.n_embd, kv = e->kv_dim, ff = m->n_ff, nv = m->n_vocab;
-    const size_t floats = 4 * embd + 2 * kv + 2 * ff + nv;
-    const size_t bytes = (floats * sizeof(float) + 255) / 256 * 256 + (n_tokens + 1) * sizeof(int);
+    const size_t r = static_cast<size_t>(rows);
+    const size_t floats = r * (4 * embd + 2 * kv + 2 * ff) + nv;
+    const size_t bytes = (floats * sizeof(float) + 255) / 256 * 256 + (n_ints + 1) * sizeof(int);
     if (bytes > e->fwd_bytes) {
         TLA_HIP(hipStreamSynchronize(e->stream));
         if (e->fwd) TLA_HIP(hipFree(e->fwd));
@@ -838,14 +840,14 @@ int fwd_bufs(tla_engine* e, const tla_model* m, int n_tokens, FwdBufs* b)
     }
     float* f = static_cast<float*>(e->fwd);
     b->x = f;
-    b->xb = b->x + embd;
-    b->q = b->xb + embd;
-    b->k = b->q + embd;
-    b->v = b->k + kv;
-    b->att = b->v + kv;
-    b->hb = b->att + embd;
-    b->hb2 = b->hb + ff;
-    b->logits = b->hb2 + ff;
+    b->xb = b->x + r * embd;
+    b->q = b->xb + r * embd;
+    b->att = b->q + r * embd;
+    b->k = b->att + r * embd;
+    b->v = b->k + r * kv;
+    b->hb = b->v + r * kv;
+    b->hb2 = b->hb + ff;  // row 0's up projection; row t's gate at hb + 2*n_ff*t
+    b->logits = b->hb + r * 2 * ff;
     b->tokens = reinterpret_cast<int*>(static_cast<char*>(e->fwd) + (floats * sizeof(float) + 255) / 256 * 256);
     return TLA_OK;
 }
@@ -858,7 +860,7 @@ int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc,
     const int embd = e->cfg.n_embd, kv = e->kv_dim, ff = m->n_ff;
     const float eps = m->rms_norm_eps;
     if (int rc = check_hip(launch_embed(m->type_embd, b.x, static_cast<const unsigned char*>(m->token_embd),
-                                        token, token_dev, embd, e->stream),
+                                        token, token_dev, 1, embd, e->stream),
                            "embed"))
         return rc;
     for (int l = 0; l < e->cfg.n_layers; ++l) {
@@ -916,6 +918,71 @@ int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc,
         if (int rc = gemv1(e, m->type_output, m->output, logits, m->n_vocab, embd, b.x, nullptr,
                            m->output_norm, eps, 0))
             return rc;
+    return TLA_OK;
+}
+
+// out[t][rows] = W . x[t] for n vectors x [n][cols], in launches of up to
+// gemv_chunk vectors.
+int gemv_rows(tla_engine* e, int type, const void* w, float* out, int rows, int cols, const float* x, int n)
+{
+    const int chunk = gemv_chunk(n, cols);
+    for (int t0 = 0; t0 < n; t0 += chunk) {
+        GemvParams p{};
+        p.seg[0] = {static_cast<const unsigned char*>(w), out + static_cast<long long>(t0) * rows, rows, rows};
+        p.n_seg = 1;
+        p.total_rows = rows;
+        p.cols = cols;
+        p.row_bytes = static_cast<int>(weight_row_bytes(type, cols));
+        p.n_vec = std::min(chunk, n - t0);
+        p.x = x + static_cast<long long>(t0) * cols;
+        p.x_stride = cols;
+        if (int rc = run_gemv(e, type, p)) return rc;
+    }
+    return TLA_OK;
+}
+
+// The prompt as one batch (n_tok tokens at positions pos0..): embeddings,
+// then per layer rmsnorm + Q/K/V over all tokens, the causal prefill
+// attention (RoPE + append in-kernel), W_o + residual and the FFN, with the
+// multi-vector GEMVs (weights read once per group of up to 8 tokens);
+// logits of the last token only (when `logits` is non-null).
+int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, float* vc,
+                const int* tokens_dev, int n_tok, int pos0, float* logits)
+{
+    const int embd = e->cfg.n_embd, kv = e->kv_dim, ff = m->n_ff;
+    const float eps = m->rms_norm_eps;
+    if (int rc = check_hip(launch_embed(m->type_embd, b.x, static_cast<const unsigned char*>(m->token_embd),
+                                        0, tokens_dev, n_tok, embd, e->stream),
+                           "embed"))
+        return rc;
+    for (int l = 0; l < e->cfg.n_layers; ++l) {
+        const tla_layer_weights& L = m->layers[l];
+        if (L.type_q == L.type_k && L.type_q == L.type_v) {
+            if (int rc = tla_attn_qkv(e, n_tok, b.q, b.k, b.v, b.x, L.attn_norm, eps, L.wq, L.wk, L.wv,
+                                      L.type_q))
+                return rc;
+        } else {
+            for (int t = 0; t < n_tok; ++t)
+                if (int rc = check_hip(launch_rmsnorm(b.xb + static_cast<long long>(t) * embd,
+                                                      b.x + static_cast<long long>(t) * embd, L.attn_norm,
+                                                      embd, eps, e->stream),
+                                       "rmsnorm"))
+                    return rc;
+            if (int rc = gemv_rows(e, L.type_q, L.wq, b.q, embd, embd, b.xb, n_tok)) return rc;
+            if (int rc = gemv_rows(e, L.type_k, L.wk, b.k, kv, embd, b.xb, n_tok)) return rc;
+            if (int rc = gemv_rows(e, L.type_v, L.wv, b.v, kv, embd, b.xb, n_tok)) return rc;
+        }
+        if (int rc = tla_prefill(e, pos0, n_tok, l, 1, TLA_ROTATE, b.att, b.q, b.k, b.v, kc, vc)) return rc;
+        if (int rc = tla_attn_out(e, n_tok, b.x, L.wo, b.att, L.type_o)) return rc;
+        if (int rc = tla_ffn_block(e, n_tok, b.x, L.ffn_norm, eps, L.w_gate, L.w_up, L.w_down, ff,
+                                   L.type_ffn, b.hb))
+            return rc;
+    }
+    if (logits)
+        if (int rc = gemv1(e, m->type_output, m->output, logits, m->n_vocab, embd,
+                           b.x + static_cast<long long>(n_tok - 1) * embd, nullptr, m->output_norm, eps, 0))
+            return rc;
+    (void)kv;
     return TLA_OK;
 }
 
@@ -1027,7 +1094,7 @@ int tla_embed(tla_engine* e, float* out_dev, const void* table_dev, int token, i
         return fail(TLA_ERR_INVALID_ARGUMENT, "type %d with n_embd %d", type, n_embd);
     if (int rc = set_device(e)) return rc;
     if (int rc = check_hip(launch_embed(type, out_dev, static_cast<const unsigned char*>(table_dev), token,
-                                        nullptr, n_embd, e->stream),
+                                        nullptr, 1, n_embd, e->stream),
                            "embed"))
         return rc;
     return ok();
@@ -1061,16 +1128,40 @@ int tla_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* 
         return fail(TLA_ERR_OUT_OF_RANGE, "pos %d outside [0, n_ctx=%d)", pos, e->cfg.n_ctx);
     if (int rc = set_device(e)) return rc;
     FwdBufs b{};
-    if (int rc = fwd_bufs(e, m, 0, &b)) return rc;
+    if (int rc = fwd_bufs(e, m, 1, 0, &b)) return rc;
     if (int rc = forward_step(e, m, b, key_cache_dev, value_cache_dev, token, nullptr, pos, logits_dev))
+        return rc;
+    return ok();
+}
+
+int tla_prefill_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* value_cache_dev,
+                        const int* tokens_host, int n_tok, int pos0, float* logits_dev)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!key_cache_dev || !value_cache_dev || !tokens_host)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (int rc = check_model(e, m)) return rc;
+    if (n_tok < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_tok %d < 1", n_tok);
+    if (pos0 < 0 || static_cast<long long>(pos0) + n_tok > e->cfg.n_ctx)
+        return fail(TLA_ERR_OUT_OF_RANGE, "positions [%d, %lld) outside [0, n_ctx=%d)", pos0,
+                    static_cast<long long>(pos0) + n_tok, e->cfg.n_ctx);
+    for (int i = 0; i < n_tok; ++i)
+        if (tokens_host[i] < 0 || tokens_host[i] >= m->n_vocab)
+            return fail(TLA_ERR_OUT_OF_RANGE, "tokens[%d] = %d outside [0, n_vocab)", i, tokens_host[i]);
+    if (int rc = set_device(e)) return rc;
+    FwdBufs b{};
+    if (int rc = fwd_bufs(e, m, n_tok, n_tok, &b)) return rc;
+    TLA_HIP(hipMemcpyWithStream(b.tokens, tokens_host, sizeof(int) * n_tok, hipMemcpyHostToDevice, e->stream));
+    if (int rc = prompt_step(e, m, b, key_cache_dev, value_cache_dev, b.tokens, n_tok, pos0, logits_dev))
         return rc;
     return ok();
 }
 
 int tla_generate_greedy(tla_engine* e, const tla_model* m, float* key_cache_dev,
                         float* value_cache_dev, const int* prompt_host, int n_prompt, int n_gen,
-                        int* tokens_host)
+                        int flags, int* tokens_host)
 {
+    if (flags & ~TLA_BATCH_PROMPT) return fail(TLA_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
     if (int rc = check_engine(e)) return rc;
     if (!key_cache_dev || !value_cache_dev || !prompt_host || !tokens_host)
         return fail(TLA_ERR_INVALID_ARGUMENT, "NULL pointer");
@@ -1083,15 +1174,25 @@ int tla_generate_greedy(tla_engine* e, const tla_model* m, float* key_cache_dev,
         if (prompt_host[i] < 0 || prompt_host[i] >= m->n_vocab)
             return fail(TLA_ERR_OUT_OF_RANGE, "prompt[%d] = %d outside [0, n_vocab)", i, prompt_host[i]);
     if (int rc = set_device(e)) return rc;
+    const bool batch = (flags & TLA_BATCH_PROMPT) != 0;
     FwdBufs b{};
-    if (int rc = fwd_bufs(e, m, n_gen, &b)) return rc;
+    if (int rc = fwd_bufs(e, m, batch ? n_prompt : 1, n_gen + n_prompt, &b)) return rc;
     int pos = 0;
-    // prompt: only the last token's logits are needed (the reference
-    // computes and overwrites the others)
-    for (int i = 0; i < n_prompt; ++i, ++pos)
-        if (int rc = forward_step(e, m, b, key_cache_dev, value_cache_dev, prompt_host[i], nullptr, pos,
-                                  i + 1 == n_prompt ? b.logits : nullptr))
+    if (batch) {
+        int* prompt_dev = b.tokens + 1 + n_gen;
+        TLA_HIP(hipMemcpyWithStream(prompt_dev, prompt_host, sizeof(int) * n_prompt, hipMemcpyHostToDevice,
+                                    e->stream));
+        if (int rc = prompt_step(e, m, b, key_cache_dev, value_cache_dev, prompt_dev, n_prompt, 0, b.logits))
             return rc;
+        pos = n_prompt;
+    } else {
+        // token by token; only the last token's logits are needed (the
+        // reference computes and overwrites the others)
+        for (int i = 0; i < n_prompt; ++i, ++pos)
+            if (int rc = forward_step(e, m, b, key_cache_dev, value_cache_dev, prompt_host[i], nullptr, pos,
+                                      i + 1 == n_prompt ? b.logits : nullptr))
+                return rc;
+    }
     // b.tokens[0]: the current token; b.tokens[1 + i]: generated token i
     for (int i = 0; i < n_gen; ++i) {
         if (int rc = check_hip(launch_argmax(b.tokens, b.tokens + 1 + i, b.logits, m->n_vocab, e->stream),

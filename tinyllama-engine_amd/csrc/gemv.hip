@@ -755,14 +755,17 @@ __device__ float embed_elem(int type, const unsigned char* row, int i)
     }
 }
 
+// Row blockIdx.y of out [n_tok][n] = table row tokens_dev[blockIdx.y] (or
+// `token` when tokens_dev is null).
 __global__ __launch_bounds__(kThreads) void embed_kernel(int type, float* out,
                                                          const unsigned char* table, long long row_bytes,
-                                                         int token, const int* token_dev, int n)
+                                                         int token, const int* tokens_dev, int n)
 {
-    const int t = token_dev ? *token_dev : token;
+    const int t = tokens_dev ? tokens_dev[blockIdx.y] : token;
     const unsigned char* row = table + row_bytes * t;
+    float* o = out + static_cast<long long>(blockIdx.y) * n;
     for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads)
-        out[i] = embed_elem(type, row, i);
+        o[i] = embed_elem(type, row, i);
 }
 
 // (value, index) pairs: b beats a when larger, or equal at a smaller index;
@@ -935,11 +938,11 @@ hipError_t launch_elementwise_mul(float* a, const float* b, int size, hipStream_
 }
 
 hipError_t launch_embed(int type, float* out, const unsigned char* table, int token,
-                        const int* token_dev, int n, hipStream_t s)
+                        const int* tokens_dev, int n_tok, int n, hipStream_t s)
 {
     const int blocks = std::min(64, (n + kThreads - 1) / kThreads);
-    hipLaunchKernelGGL(embed_kernel, dim3(blocks), dim3(kThreads), 0, s, type, out, table,
-                       weight_row_bytes(type, n), token, token_dev, n);
+    hipLaunchKernelGGL(embed_kernel, dim3(blocks, n_tok), dim3(kThreads), 0, s, type, out, table,
+                       weight_row_bytes(type, n), token, tokens_dev, n);
     return hipGetLastError();
 }
 

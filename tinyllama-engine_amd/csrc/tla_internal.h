@@ -119,9 +119,10 @@ hipError_t launch_rmsnorm(float* out, const float* x, const float* w, int size, 
 hipError_t launch_vec_add(float* out, const float* x, int size, hipStream_t s);
 hipError_t launch_silu(float* x, int size, hipStream_t s);
 hipError_t launch_elementwise_mul(float* a, const float* b, int size, hipStream_t s);
-// out[n] = row `token` of the table (token_dev non-null: read it there).
+// out[t][n] = table row tokens_dev[t] for t < n_tok (tokens_dev null: one
+// row, `token`).
 hipError_t launch_embed(int type, float* out, const unsigned char* table, int token,
-                        const int* token_dev, int n, hipStream_t s);
+                        const int* tokens_dev, int n_tok, int n, hipStream_t s);
 // *out = first index of the largest value (NaN never wins; a NaN at 0 gives 0),
 // also stored at out2 when non-null.
 hipError_t launch_argmax(int* out, int* out2, const float* x, int n, hipStream_t s);

@@ -233,12 +233,13 @@ void forward(DeviceModel& model, RunState& state, int token, int pos)
 }
 
 std::vector<int> generate_greedy(DeviceModel& model, RunState& state, const std::vector<int>& prompt,
-                                 int n_gen)
+                                 int n_gen, bool batch_prompt)
 {
     if (!state.engine) throw std::runtime_error("generate_greedy: RunState not allocated");
     std::vector<int> out(n_gen > 0 ? n_gen : 0);
     check(tla_generate_greedy(state.engine->get(), &model.model, state.key_cache, state.value_cache,
-                              prompt.data(), static_cast<int>(prompt.size()), n_gen, out.data()),
+                              prompt.data(), static_cast<int>(prompt.size()), n_gen, batch_prompt ? TLA_BATCH_PROMPT : 0,
+                              out.data()),
           "generate_greedy");
     state.pos = static_cast<int>(prompt.size()) + n_gen - 1;
     return out;

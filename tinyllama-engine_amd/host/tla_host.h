@@ -171,9 +171,9 @@ private:
 // n_vocab logits; the KV cache is state's (device).
 void forward(DeviceModel& model, RunState& state, int token, int pos);
 
-// Greedy generation on the device (prompt at positions 0.., then n_gen
-// tokens); returns the generated tokens.
+// Greedy generation on the device (prompt at positions 0.., token by token
+// or as one batch, then n_gen tokens); returns the generated tokens.
 std::vector<int> generate_greedy(DeviceModel& model, RunState& state, const std::vector<int>& prompt,
-                                 int n_gen);
+                                 int n_gen, bool batch_prompt = false);
 
 }  // namespace tla_host
