@@ -22,7 +22,8 @@ the 256 MB Infinity Cache, steps rotate over 5 copies of the whole cache
 
 Other workloads (--workload): decode_long (16384 context, batch 8, 22 layers),
 decode_ragged (64 sequences, L in [256, 2048], 22 layers), prefill,
-decode_single (one layer, position 127: reported as latency), proj (the
+decode_single (one layer, position 127: reported as latency), decode_sweep
+(batch 1, 22 layers, contexts 2K-16K), proj (the
 attention block's projections for a 22-layer decode step, and the GEMV kernel
 on a 32000 x 2048 matrix in every weight format), matmul (that GEMV alone in
 one format, --wtype), copy (the
@@ -212,6 +213,35 @@ def run_decode(workload, steps, warmup, cpu, split=0):
     if cpu:
         res["cpu_baseline"] = cpu_decode_baseline(case, n_ctx, workload)
     return res
+
+
+def run_decode_sweep(steps, warmup, contexts=(2048, 4096, 8192, 16384), n_layers=22):
+    """Batch-1 decode steps (22 layers, one sequence, new token at the last
+    position) over a range of contexts: where the fixed costs of one launch
+    stop mattering.  One layer's K/V (N(0,1), seeded) repeated for every
+    layer, as decode_long does; cache copies rotated past the Infinity
+    Cache."""
+    out = []
+    for ctx in contexts:
+        one = W.make_decode("decode_model", 1, 1, ctx, ctx - 1, salt=ctx)
+        rep = lambda a: np.ascontiguousarray(np.repeat(a, n_layers, axis=1))  # noqa: E731
+        case = W.DecodeCase(1, n_layers, ctx, one.pos, rep(one.q), rep(one.k), rep(one.v),
+                            rep(one.kc), rep(one.vc))
+        one_copy = case.kc.nbytes * 2
+        copies = max(1, -(-3 * MALL_BYTES // 2 // one_copy))
+        copies = max(copies, 2 if one_copy < MALL_BYTES else 1)
+        eng = tla.Engine(tla.Config.tinyllama(n_layers=n_layers, n_ctx=ctx))
+        b = DecodeBench(eng, case, copies)
+        ms = time_steps(eng, b.step, steps, warmup)
+        algo = case.algorithmic_bytes
+        gbs = algo / (ms * 1e-3) / 1e9
+        log(f"[bench] decode batch 1, ctx {ctx}, {n_layers} layers: {ms * 1e3:.1f} us/step, "
+            f"{algo / 1e6:.0f} MB -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), {copies} copies")
+        out.append({"ctx": ctx, "us": round(ms * 1e3, 2), "bytes": algo, "GB_s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4)})
+        b.free()
+        eng.close()
+    return out
 
 
 def cpu_threads():
@@ -573,7 +603,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode_model",
                     choices=["decode_model", "decode_long", "decode_ragged", "decode_single",
-                             "prefill", "proj", "matmul", "generate", "copy", "read"])
+                             "prefill", "proj", "matmul", "generate", "decode_sweep", "copy",
+                             "read"])
     ap.add_argument("--wtype", default=None, choices=["f32", "f16", "q8_0", "q4_0", "q6_k"],
                     help="weight format of the matmul (default q8_0) or generate (q4_0) workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -594,6 +625,18 @@ def main():
         return
     if args.workload == "read":
         print(json.dumps(run_read(args.steps, args.warmup)))
+        return
+    if args.workload == "decode_sweep":
+        r = run_decode_sweep(args.steps, args.warmup)
+        last = r[-1]
+        print(json.dumps({"metric": BASELINE_METRIC, "value": last["GB_s"], "unit": "GB/s",
+                          "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": last["us"] / 1e3, "higher_is_better": True,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+                          "data": "synthetic",
+                          "config": {"workload": "decode_sweep", "batch": 1, "n_layers": 22,
+                                     "contexts": [x["ctx"] for x in r], "parallelism": "none"},
+                          "sweep": r}))
         return
     if args.workload == "generate":
         wname = args.wtype or "q4_0"
