@@ -474,10 +474,34 @@ def matmul_kernel(eng, t, steps, warmup, rows=32000, cols=2048):
     return out
 
 
+def gemm_kernel_tflops(eng, t, steps, rows=5632, cols=2048, n_tok=512):
+    """tla_matmul_batch on one matrix (the FFN gate shape by default) for a
+    token batch, back to back: fp32 MFMA TFLOP/s."""
+    rg = np.random.default_rng(2)
+    wd = eng.array(W.make_weights(t, rows, cols, salt=7))
+    xd = eng.array(rg.standard_normal((n_tok, cols)).astype(np.float32))
+    od = eng.array((n_tok, rows))
+
+    def one(i):
+        eng.matmul_batch(od.ptr, wd.ptr, xd.ptr, rows, cols, n_tok, t)
+
+    for i in range(3):
+        one(i)
+    ms = back_to_back_ms(eng, one, steps)
+    flops = 2 * n_tok * rows * cols
+    log(f"[bench] matmul_batch {W.W_NAMES[t]} {rows}x{cols} x {n_tok} tokens: {ms * 1e3:.1f} us, "
+        f"{flops / ms / 1e9:.1f} TFLOP/s ({flops / ms / 1e9 / FP32_MFMA_PEAK_TFLOPS:.1%} of fp32 MFMA)")
+    for a in (wd, xd, od):
+        a.free()
+    return {"us": round(ms * 1e3, 2), "TFLOP_s": round(flops / ms / 1e9, 2)}
+
+
 def run_matmul(steps, warmup, name):
     t = {v: k for k, v in W.W_NAMES.items()}[name]
     eng = tla.Engine(tla.Config.tinyllama(n_layers=1, n_ctx=16))
     r = matmul_kernel(eng, t, steps, warmup)
+    if t != W.W_Q6_K:
+        r["batch512"] = gemm_kernel_tflops(eng, t, steps)
     eng.close()
     return r
 
@@ -522,6 +546,27 @@ def run_generate(steps, warmup, cpu, wname="q4_0", n_prompt=32, n_gen=20):
     _, toks_b = call(n_gen + 1, True)
     log(f"[bench] generate {wname}: prompt as one batch {pre_batch:.2f} ms "
         f"({pre_batch / n_prompt * 1e3:.0f} us/token); same tokens: {toks_b == toks}")
+    # a long prompt as one batch (tla_prefill_forward): the projections on
+    # the MFMA GEMM; GEMM flops = 2 x tokens x (every matrix's rows x cols)
+    # over the layers
+    n_long = 512
+    long_prompt = [1] + W.rng("block", 4).integers(2, spec.n_vocab, n_long - 1).tolist()
+    lg = eng.array((spec.n_vocab,))
+    for _ in range(2):
+        eng.prefill_forward(dm, kc.ptr, vc.ptr, long_prompt, 0, lg.ptr)
+    eng.synchronize()
+    eng.event(0)
+    reps = 3
+    for _ in range(reps):
+        eng.prefill_forward(dm, kc.ptr, vc.ptr, long_prompt, 0, lg.ptr)
+    eng.event(1)
+    long_ms = eng.elapsed(0, 1) / reps
+    lg.free()
+    e_, kvd, ff = spec.n_embd, spec.kv_dim, spec.n_ff
+    gemm_flops = 2 * n_long * spec.n_layers * e_ * (e_ + 2 * kvd + e_ + 2 * ff + ff)
+    log(f"[bench] generate {wname}: {n_long}-token prompt as one batch {long_ms:.2f} ms "
+        f"= {n_long / long_ms * 1e3:.0f} tokens/s; projections {gemm_flops / 1e9:.0f} GFLOP "
+        f"-> {gemm_flops / long_ms / 1e9:.1f} TFLOP/s overall")
     # HBM bytes a decode token must move: every weight once (one embedding
     # row), the KV cache up to its position (mean position of the 20 steps)
     weight_bytes = sum(len(r) for name, (d, ty, r) in t.items() if name != "token_embd.weight")
@@ -534,6 +579,7 @@ def run_generate(steps, warmup, cpu, wname="q4_0", n_prompt=32, n_gen=20):
         f"us/token), decode {dec * 1e3:.0f} us/token = {1e3 / dec:.0f} tok/s; {tok_bytes / 1e6:.0f} MB "
         f"per token -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}); tokens {toks[:8]}...")
     res = {"decode_ms_per_token": dec, "prefill_ms": pre, "prefill_batched_ms": pre_batch,
+           "prompt512_ms": long_ms,
            "tok_per_s": 1e3 / dec,
            "bytes_per_token": tok_bytes, "GB_s": gbs, "frac": gbs / HBM_PEAK_GBS,
            "n_prompt": n_prompt, "n_gen": n_gen}
@@ -651,6 +697,7 @@ def main():
                            "parallelism": "none"},
                 "prefill_ms": round(r["prefill_ms"], 3),
                 "prefill_batched_ms": round(r["prefill_batched_ms"], 3),
+                "prompt512_ms": round(r["prompt512_ms"], 3),
                 "roofline": {"bound": "hbm", "achieved": round(r["GB_s"], 1), "peak": HBM_PEAK_GBS,
                              "unit": "GB/s", "frac": round(r["frac"], 4), "traffic": None,
                              "kernel": "whole decode step (113 launches)",

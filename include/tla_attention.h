@@ -179,6 +179,14 @@ enum tla_weight_type {
 int tla_matmul(tla_engine* e, float* out_dev, const void* w_dev, const float* x_dev, int rows,
                int cols, int type);
 
+/* matmul() over a batch of n_tok vectors: out[t][rows] = W . x[t] (x
+ * [n_tok][cols]), the weights read once per batch tile.  From 16 vectors on,
+ * F32 / F16 / Q8_0 / Q4_0 with rows a multiple of 32 run on the fp32 matrix
+ * cores; other cases as groups of matrix-vector products.  Used for the
+ * prompt's projections. */
+int tla_matmul_batch(tla_engine* e, float* out_dev, const void* w_dev, const float* x_dev, int rows,
+                     int cols, int n_tok, int type);
+
 /* rmsnorm() src/ops.h:95-96: out = x / sqrt(mean(x^2) + eps) * weight. */
 int tla_rmsnorm(tla_engine* e, float* out_dev, const float* x_dev, const float* weight_dev,
                 int size, float eps);

@@ -327,3 +327,31 @@ def test_prefill_forward_errors(tla, W, engines):
                 assert e.value.code == 2
     finally:
         dm.free()
+
+
+@pytest.mark.parametrize("name", ["q8_0", "f16_tied", "q4_0", "mixed"])
+def test_prefill_forward_long_prompt(tla, O, W, engines, name):
+    """A 48-token prompt: the batched projections run on the MFMA GEMM
+    (>= 16 tokens; the mixed model's Q6_K values through GEMVs).  Last
+    token's logits against the oracle's token loop."""
+    g = golden("forward.npz")
+    spec, t = model_from_golden(W, g, name)
+    eng = spec_engine(engines, spec)
+    toks = np.random.default_rng(48).integers(0, spec.n_vocab, 48).tolist()
+    om = O.Model(spec, t)
+    want = om.tokens(toks)[-1]
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    try:
+        with device_arrays() as track:
+            kc, vc = eng.kv_cache(1)
+            track(kc), track(vc)
+            lg = track(eng.array((spec.n_vocab,)))
+            eng.prefill_forward(dm, kc.ptr, vc.ptr, toks, 0, lg.ptr)
+            got = lg.download()
+            k_dev = kc.download()
+    finally:
+        dm.free()
+    check_logits(got[None], want[None], f"{name} 48-token batched prompt vs oracle")
+    kv = spec.kv_dim
+    ok = om.kc.reshape(spec.n_layers, spec.n_ctx, kv)
+    assert np.abs(k_dev[0, :, :48] - ok[:, :48]).max() <= 1e-4 * np.abs(ok[:, :48]).max()

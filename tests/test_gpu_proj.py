@@ -211,3 +211,29 @@ def test_projection_errors(tla, W, engines):
         with pytest.raises(tla.TlaError) as e:
             eng.matmul(out.ptr, w.ptr + 2, x.ptr, 1, 64, Q.Q8_0)
         assert e.value.code == 1
+
+
+BATCH_SHAPES = [(32, 256, 16), (2560, 2048, 33), (64, 5632, 128), (5632, 2048, 130), (96, 512, 300),
+                (48, 256, 7), (40, 512, 20)]  # the last two: GEMV groups (few tokens / rows % 32)
+
+
+@pytest.mark.parametrize("t,name", TYPES)
+@pytest.mark.parametrize("rows,cols,n_tok", BATCH_SHAPES)
+def test_matmul_batch(O, W, engines, t, name, rows, cols, n_tok):
+    """tla_matmul_batch: the MFMA GEMM (>= 16 tokens, rows % 32 == 0, not
+    Q6_K) or groups of GEMVs, per token against the oracle's matmul."""
+    if t == Q.Q6_K and cols % 256:
+        pytest.skip("Q6_K rows are whole 256-weight super-blocks")
+    eng = engines(1, 64)
+    raw = W.make_weights(t, rows, cols, salt=rows + 3 * cols)
+    x = np.random.default_rng(n_tok).standard_normal((n_tok, cols)).astype(np.float32)
+    log(f"  tla_matmul_batch {name} {rows}x{cols}, {n_tok} tokens")
+    with device_arrays() as track:
+        w = track(eng.array(raw))
+        xd = track(eng.array(x))
+        out = track(eng.array((n_tok, rows)))
+        eng.matmul_batch(out.ptr, w.ptr, xd.ptr, rows, cols, n_tok, t)
+        got = out.download()
+    for i in sorted({0, n_tok // 2, n_tok - 1}):
+        check_rows(got[i], O.matmul(raw, x[i], rows, cols, t), raw, x[i], t, rows, cols,
+                   f"{name} {rows}x{cols} token {i}")

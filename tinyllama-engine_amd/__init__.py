@@ -111,6 +111,7 @@ SIGNATURES = {
     "tla_rope": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]),
     "tla_softmax": (C.c_int, [_vp, _vp, C.c_int]),
     "tla_matmul": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
+    "tla_matmul_batch": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tla_rmsnorm": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_float]),
     "tla_vec_add": (C.c_int, [_vp, _vp, _vp, C.c_int]),
     "tla_attn_qkv": (C.c_int, [_vp, C.c_int, _vp, _vp, _vp, _vp, _vp, C.c_float, _vp, _vp, _vp,
@@ -296,6 +297,9 @@ class Engine:
 
     def attn_out(self, n_seq: int, x: int, wo: int, xb2: int, wtype: int):
         _check(lib().tla_attn_out(self.h, n_seq, x, wo, xb2, wtype), "tla_attn_out")
+
+    def matmul_batch(self, out: int, w: int, x: int, rows: int, cols: int, n_tok: int, wtype: int):
+        _check(lib().tla_matmul_batch(self.h, out, w, x, rows, cols, n_tok, wtype), "tla_matmul_batch")
 
     def silu(self, x: int, size: int):
         _check(lib().tla_silu(self.h, x, size), "tla_silu")

@@ -96,6 +96,8 @@ struct tla_engine {
     size_t n_counters = 0;
     void* fwd = nullptr;     // forward(): residual stream, q|k|v, attention out, FFN, tokens
     size_t fwd_bytes = 0;
+    float* gemm_ws = nullptr;  // split-column GEMM partial tiles
+    size_t gemm_ws_bytes = 0;
     int* argmax_slot = nullptr;
     long long opt_split = 0;
 
@@ -316,6 +318,7 @@ int tla_engine_destroy(tla_engine* e)
     if (e->ws) (void)hipFree(e->ws);
     if (e->counters) (void)hipFree(e->counters);
     if (e->fwd) (void)hipFree(e->fwd);
+    if (e->gemm_ws) (void)hipFree(e->gemm_ws);
     if (e->argmax_slot) (void)hipFree(e->argmax_slot);
     if (e->rope) (void)hipFree(e->rope);
     if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -941,6 +944,78 @@ int gemv_rows(tla_engine* e, int type, const void* w, float* out, int rows, int 
     return TLA_OK;
 }
 
+int ensure_gemm_ws(tla_engine* e, size_t bytes)
+{
+    if (bytes <= e->gemm_ws_bytes) return TLA_OK;
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    if (e->gemm_ws) TLA_HIP(hipFree(e->gemm_ws));
+    e->gemm_ws = nullptr;
+    e->gemm_ws_bytes = 0;
+    const hipError_t err = hipMalloc(&e->gemm_ws, bytes);
+    if (err != hipSuccess) return fail(TLA_ERR_OUT_OF_MEMORY, "GEMM workspace: %s", hipGetErrorString(err));
+    e->gemm_ws_bytes = bytes;
+    return TLA_OK;
+}
+
+// Token batches at least this long go through the MFMA GEMM; shorter ones
+// (and weight types it does not take) through the multi-vector GEMV.
+constexpr int kGemmMinTokens = 16;
+
+// out_s[t][row] (+)= W_s[row] . x[t] for the n_seg matrices of `segs`, one
+// type, over n tokens (x rows x_stride floats apart).
+int matrix_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int cols, const float* x,
+                 long long x_stride, int n, int add)
+{
+    int total = 0;
+    bool rows32 = true;
+    for (int i = 0; i < n_seg; ++i) {
+        total += segs[i].rows;
+        rows32 = rows32 && segs[i].rows % 32 == 0;
+    }
+    if (n >= kGemmMinTokens && gemm_supported(type) && rows32 && cols % 32 == 0) {
+        // enough workgroups for the GPU: split the columns when the output
+        // tiles alone are fewer than the CUs (partials summed in order)
+        const long long tiles = static_cast<long long>((total + 63) / 64) * ((n + 127) / 128);
+        const int chunks = cols / 32;
+        int splits = static_cast<int>(std::min<long long>((256 + tiles - 1) / tiles, chunks / 4));
+        splits = std::max(splits, 1);
+        GemmParams p{};
+        if (splits > 1) {
+            if (int rc = ensure_gemm_ws(e, static_cast<size_t>(splits) * n * total * sizeof(float))) return rc;
+            p.part = e->gemm_ws;
+        }
+        p.k_splits = splits;
+        for (int i = 0; i < n_seg; ++i) p.seg[i] = segs[i];
+        p.n_seg = n_seg;
+        p.total_rows = total;
+        p.cols = cols;
+        p.row_bytes = static_cast<int>(weight_row_bytes(type, cols));
+        p.n_tok = n;
+        p.x = x;
+        p.x_stride = x_stride;
+        p.add = add;
+        return launch(e, TLA_KERNEL_GEMV, "gemm", [&] { return launch_gemm(type, p, e->stream); });
+    }
+    const int chunk = std::max(1, std::min({n, kGemvMaxVec, kGemvLdsBytes / gemv_lds_per_vec(cols)}));
+    for (int t0 = 0; t0 < n; t0 += chunk) {
+        GemvParams p{};
+        for (int i = 0; i < n_seg; ++i) {
+            p.seg[i] = segs[i];
+            p.seg[i].out = segs[i].out + static_cast<long long>(t0) * segs[i].out_stride;
+        }
+        p.n_seg = n_seg;
+        p.total_rows = total;
+        p.cols = cols;
+        p.row_bytes = static_cast<int>(weight_row_bytes(type, cols));
+        p.n_vec = std::min(chunk, n - t0);
+        p.x = x + static_cast<long long>(t0) * x_stride;
+        p.x_stride = x_stride;
+        p.add = add;
+        if (int rc = run_gemv(e, type, p)) return rc;
+    }
+    return TLA_OK;
+}
+
 // The prompt as one batch (n_tok tokens at positions pos0..): embeddings,
 // then per layer rmsnorm + Q/K/V over all tokens, the causal prefill
 // attention (RoPE + append in-kernel), W_o + residual and the FFN, with the
@@ -955,28 +1030,43 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
                                         0, tokens_dev, n_tok, embd, e->stream),
                            "embed"))
         return rc;
+    const auto U = [](const void* w) { return static_cast<const unsigned char*>(w); };
     for (int l = 0; l < e->cfg.n_layers; ++l) {
         const tla_layer_weights& L = m->layers[l];
-        if (L.type_q == L.type_k && L.type_q == L.type_v) {
-            if (int rc = tla_attn_qkv(e, n_tok, b.q, b.k, b.v, b.x, L.attn_norm, eps, L.wq, L.wk, L.wv,
-                                      L.type_q))
-                return rc;
-        } else {
-            for (int t = 0; t < n_tok; ++t)
-                if (int rc = check_hip(launch_rmsnorm(b.xb + static_cast<long long>(t) * embd,
-                                                      b.x + static_cast<long long>(t) * embd, L.attn_norm,
-                                                      embd, eps, e->stream),
-                                       "rmsnorm"))
-                    return rc;
-            if (int rc = gemv_rows(e, L.type_q, L.wq, b.q, embd, embd, b.xb, n_tok)) return rc;
-            if (int rc = gemv_rows(e, L.type_k, L.wk, b.k, kv, embd, b.xb, n_tok)) return rc;
-            if (int rc = gemv_rows(e, L.type_v, L.wv, b.v, kv, embd, b.xb, n_tok)) return rc;
-        }
-        if (int rc = tla_prefill(e, pos0, n_tok, l, 1, TLA_ROTATE, b.att, b.q, b.k, b.v, kc, vc)) return rc;
-        if (int rc = tla_attn_out(e, n_tok, b.x, L.wo, b.att, L.type_o)) return rc;
-        if (int rc = tla_ffn_block(e, n_tok, b.x, L.ffn_norm, eps, L.w_gate, L.w_up, L.w_down, ff,
-                                   L.type_ffn, b.hb))
+        // rmsnorm rows, then Q/K/V (src/forward.cpp:180-190)
+        if (int rc = check_hip(launch_rmsnorm_rows(b.xb, b.x, L.attn_norm, n_tok, embd, eps, e->stream),
+                               "rmsnorm rows"))
             return rc;
+        if (L.type_q == L.type_k && L.type_q == L.type_v) {
+            const GemvSegment segs[3] = {{U(L.wq), b.q, embd, embd}, {U(L.wk), b.k, kv, kv}, {U(L.wv), b.v, kv, kv}};
+            if (int rc = matrix_batch(e, L.type_q, segs, 3, embd, b.xb, embd, n_tok, 0)) return rc;
+        } else {
+            const GemvSegment sq{U(L.wq), b.q, embd, embd}, sk{U(L.wk), b.k, kv, kv}, sv{U(L.wv), b.v, kv, kv};
+            if (int rc = matrix_batch(e, L.type_q, &sq, 1, embd, b.xb, embd, n_tok, 0)) return rc;
+            if (int rc = matrix_batch(e, L.type_k, &sk, 1, embd, b.xb, embd, n_tok, 0)) return rc;
+            if (int rc = matrix_batch(e, L.type_v, &sv, 1, embd, b.xb, embd, n_tok, 0)) return rc;
+        }
+        // RoPE + append + causal attention (src/forward.cpp:192-208)
+        if (int rc = tla_prefill(e, pos0, n_tok, l, 1, TLA_ROTATE, b.att, b.q, b.k, b.v, kc, vc)) return rc;
+        // x += Wo . att (src/forward.cpp:210-213)
+        {
+            const GemvSegment so{U(L.wo), b.x, embd, embd};
+            if (int rc = matrix_batch(e, L.type_o, &so, 1, embd, b.att, embd, n_tok, 1)) return rc;
+        }
+        // FFN (src/forward.cpp:215-228): rmsnorm rows, gate and up into
+        // hb [t][gate | up], SiLU x up in place, x += W_down . h
+        if (int rc = check_hip(launch_rmsnorm_rows(b.xb, b.x, L.ffn_norm, n_tok, embd, eps, e->stream),
+                               "rmsnorm rows"))
+            return rc;
+        {
+            const GemvSegment segs[2] = {{U(L.w_gate), b.hb, ff, 2LL * ff}, {U(L.w_up), b.hb + ff, ff, 2LL * ff}};
+            if (int rc = matrix_batch(e, L.type_ffn, segs, 2, embd, b.xb, embd, n_tok, 0)) return rc;
+        }
+        if (int rc = check_hip(launch_swiglu_rows(b.hb, n_tok, ff, e->stream), "swiglu rows")) return rc;
+        {
+            const GemvSegment sd{U(L.w_down), b.x, embd, embd};
+            if (int rc = matrix_batch(e, L.type_ffn, &sd, 1, ff, b.hb, 2LL * ff, n_tok, 1)) return rc;
+        }
     }
     if (logits)
         if (int rc = gemv1(e, m->type_output, m->output, logits, m->n_vocab, embd,
@@ -987,6 +1077,20 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
 }
 
 }  // namespace
+
+int tla_matmul_batch(tla_engine* e, float* out_dev, const void* w_dev, const float* x_dev, int rows,
+                     int cols, int n_tok, int type)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!out_dev || !w_dev || !x_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (rows < 1 || n_tok < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "rows %d, n_tok %d must be >= 1", rows, n_tok);
+    if (int rc = check_gemv(type, cols, 1, w_dev)) return rc;
+    if (reinterpret_cast<std::uintptr_t>(x_dev) % 16) return fail(TLA_ERR_INVALID_ARGUMENT, "x must be 16-byte aligned");
+    if (int rc = set_device(e)) return rc;
+    const GemvSegment seg{static_cast<const unsigned char*>(w_dev), out_dev, rows, rows};
+    if (int rc = matrix_batch(e, type, &seg, 1, cols, x_dev, cols, n_tok, 0)) return rc;
+    return ok();
+}
 
 int tla_silu(tla_engine* e, float* x_dev, int size)
 {

@@ -1,0 +1,325 @@
+// Matrix products for a batch of tokens (the prompt): Y[t][r] (+)= W[r] . X[t]
+// with W in the reference's weight formats (matmul(), src/ops.cpp:959-983,
+// block layouts src/gguf.h:56-135) dequantised in registers and multiplied
+// on the fp32 matrix cores (v_mfma_f32_32x32x2f32).  This is the batched form
+// of the projections forward() makes per token (src/forward.cpp:180-228) when
+// the prompt runs through the model at once.
+//
+// Tiling: a workgroup (4 waves) owns 64 weight rows x 128 tokens; a wave owns
+// 32 rows x 64 tokens (two 32x32 accumulators).  The K dimension advances in
+// chunks of 32 columns (one Q8_0 / Q4_0 block): the chunk's X tile [128
+// tokens][32 columns] is staged once in LDS (row pitch 33 floats: the lanes
+// of an MFMA B operand read 32 tokens at one column, which then fall in 32
+// different banks) and read by the two waves of each token half; each lane
+// loads its own weight row's block and dequantises it into A operands.
+//
+// The contraction order inside a chunk is (s, s + 16) for s = 0..15: MFMA
+// step s takes columns s (A lanes 0-31) and s + 16 (lanes 32-63).  That
+// order follows the Q4_0 byte layout (byte s holds elements s and s + 16)
+// and is applied to X identically, so the sum is unchanged.
+//
+// fp32 products and fp32 accumulation in a different order than the
+// reference's sequential loops: results agree to fp32 rounding.
+#include "tla_internal.h"
+
+namespace tla {
+namespace {
+
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+
+constexpr int kThreads = 256;
+constexpr int kTileRows = 64;   // weight rows per workgroup
+constexpr int kTileToks = 128;  // tokens per workgroup
+constexpr int kChunk = 32;      // columns per K step
+constexpr int kPitch = 33;      // LDS floats per staged token row
+
+__device__ __forceinline__ float half_to_float(unsigned h)
+{
+    return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
+}
+
+// One lane's view of a weight row's 32-column chunk: the 16 values at
+// columns s + 16k (s = 0..15) for the lane's half k.
+template <int kType>
+struct Chunk;
+
+template <>
+struct Chunk<kF32> {
+    float4 w[4];
+    __device__ void load(const unsigned char* row, int c, int k)
+    {
+        const float4* p = reinterpret_cast<const float4*>(row + 4 * (kChunk * c + 16 * k));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) w[i] = p[i];
+    }
+    __device__ float value(int s) const
+    {
+        const float4 v = w[s >> 2];
+        const int e = s & 3;
+        return e == 0 ? v.x : e == 1 ? v.y : e == 2 ? v.z : v.w;
+    }
+};
+
+template <>
+struct Chunk<kF16> {
+    uint4 h[2];
+    __device__ void load(const unsigned char* row, int c, int k)
+    {
+        const uint4* p = reinterpret_cast<const uint4*>(row + 2 * (kChunk * c + 16 * k));
+        h[0] = p[0];
+        h[1] = p[1];
+    }
+    __device__ float value(int s) const
+    {
+        const uint4 v = h[s >> 3];
+        const int d = (s >> 1) & 3;
+        const unsigned w = d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
+        return half_to_float((s & 1) ? (w >> 16) : (w & 0xFFFFu));
+    }
+};
+
+// Q8_0 block: d (fp16) | qs[32] int8; column e is qs[e].
+template <>
+struct Chunk<kQ8_0> {
+    unsigned q[4];
+    float d;
+    __device__ void load(const unsigned char* row, int c, int k)
+    {
+        const unsigned char* b = row + 34 * c;
+        d = half_to_float(b[0] | (b[1] << 8));
+        // 16 bytes at an even address: 16-bit aligned loads, assembled
+        const unsigned short* p = reinterpret_cast<const unsigned short*>(b + 2 + 16 * k);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = p[2 * i] | (static_cast<unsigned>(p[2 * i + 1]) << 16);
+    }
+    __device__ float value(int s) const
+    {
+        const int v = static_cast<signed char>((q[s >> 2] >> (8 * (s & 3))) & 0xFFu);
+        return static_cast<float>(v) * d;
+    }
+};
+
+// Q4_0 block: d (fp16) | qs[16]; byte j holds column j (low nibble) and
+// j + 16 (high nibble), value - 8.  Half k takes the nibble 4k of byte s.
+template <>
+struct Chunk<kQ4_0> {
+    unsigned q[4];
+    float d;
+    int shift;
+    __device__ void load(const unsigned char* row, int c, int k)
+    {
+        const unsigned char* b = row + 18 * c;
+        d = half_to_float(b[0] | (b[1] << 8));
+        const unsigned short* p = reinterpret_cast<const unsigned short*>(b + 2);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) q[i] = p[2 * i] | (static_cast<unsigned>(p[2 * i + 1]) << 16);
+        shift = 4 * k;
+    }
+    __device__ float value(int s) const
+    {
+        const int v = static_cast<int>((q[s >> 2] >> (8 * (s & 3) + shift)) & 0xFu) - 8;
+        return static_cast<float>(v) * d;
+    }
+};
+
+// Y (+)= W . X for the segments of p (each a multiple of 32 rows, so a
+// wave's 32 rows lie in one segment).
+template <int kType>
+__global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p)
+{
+    __shared__ float xs[2][kTileToks * kPitch];
+
+    const int tid = threadIdx.x;
+    const int lane = tid & 63, wave = tid >> 6;
+    const int i = lane & 31, k = lane >> 5;
+    const int row0 = blockIdx.x * kTileRows + (wave & 1) * 32;  // the wave's 32 rows
+    const int wtok = (wave >> 1) * 64;                          // the wave's tokens in the tile
+    const int tok0 = blockIdx.y * kTileToks;
+    // this workgroup's column chunks [c0, c1): all, or its split's share
+    const int n_all = p.cols / kChunk;
+    const int c0 = static_cast<int>(static_cast<long long>(n_all) * blockIdx.z / gridDim.z);
+    const int c1 = static_cast<int>(static_cast<long long>(n_all) * (blockIdx.z + 1) / gridDim.z);
+
+    // the wave's segment (uniform: segment sizes are multiples of 32)
+    int seg = 0, srow = row0;
+    while (seg + 1 < p.n_seg && srow >= p.seg[seg].rows) {
+        srow -= p.seg[seg].rows;
+        ++seg;
+    }
+    const bool rows_valid = row0 < p.total_rows;
+    const GemvSegment S = p.seg[seg];
+    const unsigned char* wrow = S.w + static_cast<long long>(rows_valid ? srow + i : 0) * p.row_bytes;
+
+    // X staging: thread tid moves tokens tid/8 + 32m (m = 0..3), columns
+    // 4(tid%8) .. +3 of a chunk; rows past n_tok stage zeros.
+    const int st = tid >> 3, sc = 4 * (tid & 7);
+    float4 xr[4];
+    auto load_x = [&](int c) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            const int t = tok0 + st + 32 * m;
+            xr[m] = t < p.n_tok
+                        ? *reinterpret_cast<const float4*>(p.x + static_cast<long long>(t) * p.x_stride +
+                                                           kChunk * c + sc)
+                        : make_float4(0.f, 0.f, 0.f, 0.f);
+        }
+    };
+    auto store_x = [&](int b) {
+#pragma unroll
+        for (int m = 0; m < 4; ++m) {
+            float* d = xs[b] + (st + 32 * m) * kPitch + sc;
+            d[0] = xr[m].x;
+            d[1] = xr[m].y;
+            d[2] = xr[m].z;
+            d[3] = xr[m].w;
+        }
+    };
+
+    floatx16 acc0 = {}, acc1 = {};
+    Chunk<kType> wc, wn;
+    wc.load(wrow, c0, k);
+    load_x(c0);
+    store_x(0);
+    __syncthreads();
+    for (int c = c0; c < c1; ++c) {
+        const bool more = c + 1 < c1;
+        if (more) {
+            wn.load(wrow, c + 1, k);
+            load_x(c + 1);
+        }
+        const float* xa = xs[(c - c0) & 1] + (wtok + i) * kPitch + 16 * k;  // token wtok + i
+        const float* xb = xa + 32 * kPitch;                            // token wtok + 32 + i
+#pragma unroll
+        for (int s = 0; s < 16; ++s) {
+            const float a = wc.value(s);
+            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a, xa[s], acc0, 0, 0, 0);
+            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a, xb[s], acc1, 0, 0, 0);
+        }
+        if (more) {
+            store_x((c + 1 - c0) & 1);
+            wc = wn;
+        }
+        __syncthreads();
+    }
+
+    // D[r][t]: lane holds token (lane % 32) of each subtile and rows
+    // (v % 4) + 8 (v / 4) + 4 (lane / 32) of the wave's 32.
+    if (!rows_valid) return;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+        const int t = tok0 + wtok + 32 * h + i;
+        if (t >= p.n_tok) continue;
+        const floatx16& acc = h ? acc1 : acc0;
+        if (gridDim.z > 1) {
+            // partial tile: part[split][t][row], dense over all rows
+            float* o = p.part + (static_cast<long long>(blockIdx.z) * p.n_tok + t) * p.total_rows + row0;
+#pragma unroll
+            for (int v = 0; v < 16; ++v) o[(v & 3) + 8 * (v >> 2) + 4 * k] = acc[v];
+            continue;
+        }
+        float* o = S.out + static_cast<long long>(t) * S.out_stride + srow;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+            const int r = (v & 3) + 8 * (v >> 2) + 4 * k;
+            o[r] = p.add ? o[r] + acc[v] : acc[v];
+        }
+    }
+}
+
+// out[t][row] (+)= sum over splits of part[split][t][row], splits in order.
+__global__ __launch_bounds__(kThreads) void gemm_reduce_kernel(const GemmParams p)
+{
+    const long long n = static_cast<long long>(p.n_tok) * p.total_rows;
+    const long long idx = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
+    if (idx >= n) return;
+    const int t = static_cast<int>(idx / p.total_rows);
+    int r = static_cast<int>(idx - static_cast<long long>(t) * p.total_rows);
+    float sum = 0.f;
+    for (int sp = 0; sp < p.k_splits; ++sp) sum += p.part[sp * n + idx];
+    int seg = 0;
+    while (seg + 1 < p.n_seg && r >= p.seg[seg].rows) {
+        r -= p.seg[seg].rows;
+        ++seg;
+    }
+    float* o = p.seg[seg].out + static_cast<long long>(t) * p.seg[seg].out_stride + r;
+    *o = p.add ? *o + sum : sum;
+}
+
+template <int kType>
+hipError_t launch_typed(const GemmParams& p, hipStream_t s)
+{
+    const int splits = p.k_splits > 1 ? p.k_splits : 1;
+    const dim3 grid((p.total_rows + kTileRows - 1) / kTileRows, (p.n_tok + kTileToks - 1) / kTileToks, splits);
+    hipLaunchKernelGGL(gemm_kernel<kType>, grid, dim3(kThreads), 0, s, p);
+    if (splits > 1) {
+        const long long n = static_cast<long long>(p.n_tok) * p.total_rows;
+        hipLaunchKernelGGL(gemm_reduce_kernel, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)),
+                           dim3(kThreads), 0, s, p);
+    }
+    return hipGetLastError();
+}
+
+// x[t] = x[t] / sqrt(mean(x[t]^2) + eps) * w for each of n_tok rows (one
+// workgroup per row), into out.
+__global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(float* out, const float* x, const float* w,
+                                                                int size, float eps)
+{
+    __shared__ float s_red[kThreads / 64];
+    const float* xr = x + static_cast<long long>(blockIdx.x) * size;
+    float* o = out + static_cast<long long>(blockIdx.x) * size;
+    float ss = 0.f;
+    for (int c = threadIdx.x; c < size; c += kThreads) ss += xr[c] * xr[c];
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
+    __syncthreads();
+    ss = 0.f;
+#pragma unroll
+    for (int i = 0; i < kThreads / 64; ++i) ss += s_red[i];
+    const float rms = 1.0f / sqrtf(ss / static_cast<float>(size) + eps);
+    for (int c = threadIdx.x; c < size; c += kThreads) o[c] = xr[c] * rms * w[c];
+}
+
+// h[t][c] = silu(h[t][c]) * h[t][n_ff + c] in place, rows of 2 n_ff floats
+// (gate then up), with the reference's operation order (src/ops.cpp:1107-1148).
+__global__ __launch_bounds__(kThreads) void swiglu_rows_kernel(float* h, int n_ff)
+{
+    float* g = h + static_cast<long long>(blockIdx.y) * 2 * n_ff;
+    const int c = blockIdx.x * kThreads + threadIdx.x;
+    if (c < n_ff) {
+        const float v = g[c];
+        const float sigmoid = 1.0f / (1.0f + expf(-v));
+        g[c] = (v * sigmoid) * g[n_ff + c];
+    }
+}
+
+}  // namespace
+
+bool gemm_supported(int type) { return type == kF32 || type == kF16 || type == kQ8_0 || type == kQ4_0; }
+
+hipError_t launch_gemm(int type, const GemmParams& p, hipStream_t s)
+{
+    switch (type) {
+    case kF32: return launch_typed<kF32>(p, s);
+    case kF16: return launch_typed<kF16>(p, s);
+    case kQ8_0: return launch_typed<kQ8_0>(p, s);
+    case kQ4_0: return launch_typed<kQ4_0>(p, s);
+    default: return hipErrorInvalidValue;
+    }
+}
+
+hipError_t launch_rmsnorm_rows(float* out, const float* x, const float* w, int n_rows, int size, float eps,
+                               hipStream_t s)
+{
+    hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n_rows), dim3(kThreads), 0, s, out, x, w, size, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_swiglu_rows(float* h, int n_rows, int n_ff, hipStream_t s)
+{
+    hipLaunchKernelGGL(swiglu_rows_kernel, dim3((n_ff + kThreads - 1) / kThreads, n_rows), dim3(kThreads), 0,
+                       s, h, n_ff);
+    return hipGetLastError();
+}
+
+}  // namespace tla

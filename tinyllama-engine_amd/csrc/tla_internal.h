@@ -127,6 +127,32 @@ hipError_t launch_embed(int type, float* out, const unsigned char* table, int to
 // also stored at out2 when non-null.
 hipError_t launch_argmax(int* out, int* out2, const float* x, int n, hipStream_t s);
 
+// ---- token-batch matrix products (gemm.hip) ------------------------------------
+// Y[t][row] (+)= W[row] . X[t] for n_tok tokens on the fp32 matrix cores.
+// Segments as in GemvParams (out[t * out_stride + row]); every segment's rows
+// a multiple of 32, cols a multiple of 32.
+struct GemmParams {
+    GemvSegment seg[kGemvMaxSeg];
+    int n_seg;
+    int total_rows;
+    int cols;
+    int row_bytes;
+    int n_tok;
+    const float* x;          // x[t * x_stride + col]
+    long long x_stride;
+    int add;
+    int k_splits;            // > 1: column ranges on separate workgroups, partial
+    float* part;             //   tiles in part[split][t][total_rows], summed by
+                             //   a second kernel in split order
+};
+
+bool gemm_supported(int type);  // F32, F16, Q8_0, Q4_0
+hipError_t launch_gemm(int type, const GemmParams& p, hipStream_t s);
+hipError_t launch_rmsnorm_rows(float* out, const float* x, const float* w, int n_rows, int size, float eps,
+                               hipStream_t s);
+// h rows of [gate | up] (2 n_ff floats): gate = silu(gate) * up in place.
+hipError_t launch_swiglu_rows(float* h, int n_rows, int n_ff, hipStream_t s);
+
 // ---- small ops -------------------------------------------------------------
 struct RopeParams {
     float* q;
