@@ -973,12 +973,27 @@ int matrix_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, in
         rows32 = rows32 && segs[i].rows % 32 == 0;
     }
     if (n >= kGemmMinTokens && gemm_supported(type) && rows32 && cols % 32 == 0) {
-        // enough workgroups for the GPU: split the columns when the output
-        // tiles alone are fewer than the CUs (partials summed in order)
+        // Column splits (partials summed in order by a second kernel) chosen
+        // by a cost model: the busiest CU runs ceil(tiles * s / 256) tiles of
+        // 1/s of the columns each (co-resident tiles share its matrix cores),
+        // and every split adds a partial tile written and read back.  Tile
+        // time ~ 2*64*128*cols flops at ~0.3 TFLOP/s per CU; partials move
+        // at ~6 TB/s.  (Measured: 5632 x 2048 x 512 tokens is 352 tiles, and
+        // one round of two tiles on 96 CUs set the time.)
         const long long tiles = static_cast<long long>((total + 63) / 64) * ((n + 127) / 128);
         const int chunks = cols / 32;
-        int splits = static_cast<int>(std::min<long long>((256 + tiles - 1) / tiles, chunks / 4));
-        splits = std::max(splits, 1);
+        const double tile_us = 2.0 * 64 * 128 * cols / 0.3e12 * 1e6;
+        const double split_us = static_cast<double>(n) * total * 8 / 6e12 * 1e6;
+        int splits = 1;
+        double best = 1e300;
+        for (int sp = 1; sp <= std::min(16, std::max(1, chunks / 4)); ++sp) {
+            const double per_cu = static_cast<double>((tiles * sp + 255) / 256);
+            const double cost = tile_us * per_cu / sp + (sp > 1 ? split_us * sp : 0.0);
+            if (cost < best * 0.98) {
+                best = cost;
+                splits = sp;
+            }
+        }
         GemmParams p{};
         if (splits > 1) {
             if (int rc = ensure_gemm_ws(e, static_cast<size_t>(splits) * n * total * sizeof(float))) return rc;
