@@ -977,12 +977,11 @@ int matrix_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, in
         // by a cost model: the busiest CU runs ceil(tiles * s / 256) tiles of
         // 1/s of the columns each (co-resident tiles share its matrix cores),
         // and every split adds a partial tile written and read back.  Tile
-        // time ~ 2*64*128*cols flops at ~0.3 TFLOP/s per CU; partials move
-        // at ~6 TB/s.  (Measured: 5632 x 2048 x 512 tokens is 352 tiles, and
-        // one round of two tiles on 96 CUs set the time.)
-        const long long tiles = static_cast<long long>((total + 63) / 64) * ((n + 127) / 128);
+        // time ~ 2*128*128*cols flops at ~0.3 TFLOP/s per CU; partials move
+        // at ~6 TB/s.
+        const long long tiles = static_cast<long long>((total + 127) / 128) * ((n + 127) / 128);
         const int chunks = cols / 32;
-        const double tile_us = 2.0 * 64 * 128 * cols / 0.3e12 * 1e6;
+        const double tile_us = 2.0 * 128 * 128 * cols / 0.3e12 * 1e6;
         const double split_us = static_cast<double>(n) * total * 8 / 6e12 * 1e6;
         int splits = 1;
         double best = 1e300;

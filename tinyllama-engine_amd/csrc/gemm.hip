@@ -5,13 +5,14 @@
 // of the projections forward() makes per token (src/forward.cpp:180-228) when
 // the prompt runs through the model at once.
 //
-// Tiling: a workgroup (4 waves) owns 64 weight rows x 128 tokens; a wave owns
-// 32 rows x 64 tokens (two 32x32 accumulators).  The K dimension advances in
-// chunks of 32 columns (one Q8_0 / Q4_0 block): the chunk's X tile [128
-// tokens][32 columns] is staged once in LDS (row pitch 33 floats: the lanes
-// of an MFMA B operand read 32 tokens at one column, which then fall in 32
-// different banks) and read by the two waves of each token half; each lane
-// loads its own weight row's block and dequantises it into A operands.
+// Tiling: a workgroup (4 waves) owns 128 weight rows x 128 tokens; a wave
+// owns 32 rows x all 128 tokens (four 32x32 accumulators), so each
+// dequantised weight feeds four MFMAs.  The K dimension advances in chunks
+// of 32 columns (one Q8_0 / Q4_0 block): the chunk's X tile [128 tokens][32
+// columns] is staged once in LDS (row pitch 33 floats: the lanes of an MFMA
+// B operand read 32 tokens at one column, which then fall in 32 different
+// banks) and read by all four waves; each lane loads its own weight row's
+// block and dequantises it into A operands.
 //
 // The contraction order inside a chunk is (s, s + 16) for s = 0..15: MFMA
 // step s takes columns s (A lanes 0-31) and s + 16 (lanes 32-63).  That
@@ -28,7 +29,7 @@ namespace {
 typedef float floatx16 __attribute__((ext_vector_type(16)));
 
 constexpr int kThreads = 256;
-constexpr int kTileRows = 64;   // weight rows per workgroup
+constexpr int kTileRows = 128;  // weight rows per workgroup (32 per wave)
 constexpr int kTileToks = 128;  // tokens per workgroup
 constexpr int kChunk = 32;      // columns per K step
 constexpr int kPitch = 33;      // LDS floats per staged token row
@@ -132,8 +133,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p)
     const int tid = threadIdx.x;
     const int lane = tid & 63, wave = tid >> 6;
     const int i = lane & 31, k = lane >> 5;
-    const int row0 = blockIdx.x * kTileRows + (wave & 1) * 32;  // the wave's 32 rows
-    const int wtok = (wave >> 1) * 64;                          // the wave's tokens in the tile
+    const int row0 = blockIdx.x * kTileRows + wave * 32;  // the wave's 32 rows
     const int tok0 = blockIdx.y * kTileToks;
     // this workgroup's column chunks [c0, c1): all, or its split's share
     const int n_all = p.cols / kChunk;
@@ -175,7 +175,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p)
         }
     };
 
-    floatx16 acc0 = {}, acc1 = {};
+    floatx16 acc[4] = {};
     Chunk<kType> wc, wn;
     wc.load(wrow, c0, k);
     load_x(c0);
@@ -187,13 +187,13 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p)
             wn.load(wrow, c + 1, k);
             load_x(c + 1);
         }
-        const float* xa = xs[(c - c0) & 1] + (wtok + i) * kPitch + 16 * k;  // token wtok + i
-        const float* xb = xa + 32 * kPitch;                            // token wtok + 32 + i
+        const float* xt = xs[(c - c0) & 1] + i * kPitch + 16 * k;  // token 32h + i at h * 32 rows
 #pragma unroll
         for (int s = 0; s < 16; ++s) {
             const float a = wc.value(s);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x2f32(a, xa[s], acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x2f32(a, xb[s], acc1, 0, 0, 0);
+#pragma unroll
+            for (int h = 0; h < 4; ++h)
+                acc[h] = __builtin_amdgcn_mfma_f32_32x32x2f32(a, xt[32 * h * kPitch + s], acc[h], 0, 0, 0);
         }
         if (more) {
             store_x((c + 1 - c0) & 1);
@@ -206,22 +206,21 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(const GemmParams p)
     // (v % 4) + 8 (v / 4) + 4 (lane / 32) of the wave's 32.
     if (!rows_valid) return;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
-        const int t = tok0 + wtok + 32 * h + i;
+    for (int h = 0; h < 4; ++h) {
+        const int t = tok0 + 32 * h + i;
         if (t >= p.n_tok) continue;
-        const floatx16& acc = h ? acc1 : acc0;
         if (gridDim.z > 1) {
             // partial tile: part[split][t][row], dense over all rows
             float* o = p.part + (static_cast<long long>(blockIdx.z) * p.n_tok + t) * p.total_rows + row0;
 #pragma unroll
-            for (int v = 0; v < 16; ++v) o[(v & 3) + 8 * (v >> 2) + 4 * k] = acc[v];
+            for (int v = 0; v < 16; ++v) o[(v & 3) + 8 * (v >> 2) + 4 * k] = acc[h][v];
             continue;
         }
         float* o = S.out + static_cast<long long>(t) * S.out_stride + srow;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
             const int r = (v & 3) + 8 * (v >> 2) + 4 * k;
-            o[r] = p.add ? o[r] + acc[v] : acc[v];
+            o[r] = p.add ? o[r] + acc[h][v] : acc[h][v];
         }
     }
 }
