@@ -175,7 +175,7 @@ def make_decode_case(workload, n_layers=22):
     raise ValueError(workload)
 
 
-def run_decode(workload, steps, warmup, cpu, split=0):
+def run_decode(workload, steps, warmup, cpu, split=0, plan=0):
     n_layers = 1 if workload == "decode_single" else 22
     case, n_ctx = make_decode_case(workload, n_layers)
     one_copy = case.kc.nbytes * 2
@@ -186,6 +186,7 @@ def run_decode(workload, steps, warmup, cpu, split=0):
     eng = tla.Engine(tla.Config.tinyllama(n_layers=n_layers, n_ctx=n_ctx))
     if split:
         eng.set_option(tla.OPT_DECODE_SPLIT, split)
+    eng.set_option(tla.OPT_DECODE_PLAN, plan)
     b = DecodeBench(eng, case, copies)
     # A decode step is exactly one launch of the decode kernel, so the HIP
     # events around the K timed steps (engine stream) give its average
@@ -215,7 +216,7 @@ def run_decode(workload, steps, warmup, cpu, split=0):
     return res
 
 
-def run_decode_sweep(steps, warmup, contexts=(2048, 4096, 8192, 16384), n_layers=22):
+def run_decode_sweep(steps, warmup, contexts=(2048, 4096, 8192, 16384), n_layers=22, plan=0):
     """Batch-1 decode steps (22 layers, one sequence, new token at the last
     position) over a range of contexts: where the fixed costs of one launch
     stop mattering.  One layer's K/V (N(0,1), seeded) repeated for every
@@ -231,6 +232,7 @@ def run_decode_sweep(steps, warmup, contexts=(2048, 4096, 8192, 16384), n_layers
         copies = max(1, -(-3 * MALL_BYTES // 2 // one_copy))
         copies = max(copies, 2 if one_copy < MALL_BYTES else 1)
         eng = tla.Engine(tla.Config.tinyllama(n_layers=n_layers, n_ctx=ctx))
+        eng.set_option(tla.OPT_DECODE_PLAN, plan)
         b = DecodeBench(eng, case, copies)
         ms = time_steps(eng, b.step, steps, warmup)
         algo = case.algorithmic_bytes
@@ -642,6 +644,9 @@ def run_read(steps, warmup, nbytes=6 << 30):
 
 # -------------------------------------------------------------------- main --
 
+PLANS = {"auto": tla.PLAN_AUTO, "aligned": tla.PLAN_ALIGNED, "balanced": tla.PLAN_BALANCED}
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -655,7 +660,9 @@ def main():
                     help="weight format of the matmul (default q8_0) or generate (q4_0) workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-prefill", action="store_true", help="skip the prefill half")
-    ap.add_argument("--split", type=int, default=0, help="decode split length (0 = auto)")
+    ap.add_argument("--split", type=int, default=0, help="decode positions per workgroup (0 = auto)")
+    ap.add_argument("--plan", default="auto", choices=["auto", "aligned", "balanced"],
+                    help="decode work plan (default: the engine's choice)")
     ap.add_argument("--extra", action="store_true",
                     help="also measure decode_long and decode_ragged")
     args = ap.parse_args()
@@ -673,7 +680,7 @@ def main():
         print(json.dumps(run_read(args.steps, args.warmup)))
         return
     if args.workload == "decode_sweep":
-        r = run_decode_sweep(args.steps, args.warmup)
+        r = run_decode_sweep(args.steps, args.warmup, plan=PLANS[args.plan])
         last = r[-1]
         print(json.dumps({"metric": BASELINE_METRIC, "value": last["GB_s"], "unit": "GB/s",
                           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
@@ -747,7 +754,7 @@ def main():
         print(json.dumps(line))
         return
 
-    d = run_decode(args.workload, args.steps, args.warmup, cpu, args.split)
+    d = run_decode(args.workload, args.steps, args.warmup, cpu, args.split, PLANS[args.plan])
     cfg = {"decode_model": {"n_seq": 1, "n_layers": 22, "context": 2048},
            "decode_long": {"n_seq": 8, "n_layers": 22, "context": 16384},
            "decode_ragged": {"n_seq": 64, "n_layers": 22, "context": "U[256,2048]"},

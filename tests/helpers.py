@@ -47,13 +47,15 @@ def max_err(a, b):
     return float(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64)).max())
 
 
-def gpu_decode(eng, case, rotate=True, split=0, keep_cache=False):
-    """tla_decode over every (sequence, layer) of `case` in one call.
+def gpu_decode(eng, case, rotate=True, split=0, keep_cache=False, plan=0):
+    """tla_decode over every (sequence, layer) of `case` in one call, with
+    the given positions per workgroup and work plan (0 = the engine's choice).
     Returns (out [n_seq, n_layers, q_dim], key rows at pos, value rows at pos,
     [full caches if keep_cache])."""
     cfg = eng.cfg
     assert cfg.n_layers == case.n_layers and cfg.n_ctx == case.n_ctx
-    eng.set_option(0, split)
+    eng.set_option(tla.OPT_DECODE_SPLIT, split)
+    eng.set_option(tla.OPT_DECODE_PLAN, plan)
     with device_arrays() as track:
         kc, vc = eng.kv_cache(case.n_seq)
         track(kc), track(vc)
@@ -63,7 +65,7 @@ def gpu_decode(eng, case, rotate=True, split=0, keep_cache=False):
         out = track(eng.array(case.q.shape))
         stride = case.n_layers * case.n_ctx * cfg.kv_dim
         log(f"  tla_decode n_seq={case.n_seq} layers={case.n_layers} ctx={case.n_ctx} "
-            f"pos[0]={int(case.pos[0])} rotate={rotate} split={split}")
+            f"pos[0]={int(case.pos[0])} rotate={rotate} split={split} plan={plan}")
         eng.decode(case.pos, 0, case.n_layers, out.ptr, q.ptr, k.ptr, v.ptr, kc.ptr, vc.ptr,
                    stride, rotate)
         res = out.download()
@@ -103,8 +105,8 @@ def oracle_decode(O, case, rotate=True, keep_cache=False):
     return out, krow, vrow
 
 
-def check_decode(O, eng, case, rotate=True, split=0, tol=DECODE_TOL):
-    got, gk, gv = gpu_decode(eng, case, rotate=rotate, split=split)
+def check_decode(O, eng, case, rotate=True, split=0, tol=DECODE_TOL, plan=0):
+    got, gk, gv = gpu_decode(eng, case, rotate=rotate, split=split, plan=plan)
     ref, rk, rv = oracle_decode(O, case, rotate=rotate)
     err = max_err(got, ref)
     log(f"    max-abs error {err:.3e}")

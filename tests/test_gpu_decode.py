@@ -1,6 +1,8 @@
 """GPU parity of decode attention (split-KV, RoPE + append fused) through the
 C ABI, against the golden vectors and the oracle on the same seeded inputs.
 Bar: max-abs 1e-4 on outputs, appended cache rows bit-exact."""
+import itertools
+
 import numpy as np
 import pytest
 
@@ -9,6 +11,8 @@ from helpers import (DECODE_TOL, bits, check_decode, device_arrays, gpu_decode, 
                      oracle_decode)
 
 pytestmark = pytest.mark.gpu
+
+PLANS = (1, 2)  # TLA_PLAN_ALIGNED, TLA_PLAN_BALANCED
 
 
 def test_decode_single_golden(tla, W, engines):
@@ -43,8 +47,8 @@ def test_decode_peaked_golden(tla, W, engines):
     g = golden("decode_peaked.npz")
     case = W.make_decode("decode_long", 1, 1, 1024, 1023, kv_std=0.5, peaked_frac=0.01, salt=7)
     assert W.digest(case.q, case.k, case.v, case.kc, case.vc) == str(g["digest"])
-    for split in (0, 16, 48, 1024):
-        got, krow, vrow = gpu_decode(engines(1, 1024), case, split=split)
+    for split, plan in itertools.product((0, 16, 48, 1024), PLANS):
+        got, krow, vrow = gpu_decode(engines(1, 1024), case, split=split, plan=plan)
         err = max_err(got[0, 0], g["out"])
         log(f"    vs reference: max-abs {err:.3e}")
         assert err <= DECODE_TOL
@@ -107,19 +111,21 @@ def test_reference_testops_cases(tla, engines):
 
 @pytest.mark.parametrize("pos", [0, 1, 15, 16, 17, 63, 64, 100, 511, 512, 1000, 2047])
 @pytest.mark.parametrize("split", [0, 16, 64, 208])
-def test_decode_positions_and_splits(O, W, engines, pos, split):
+@pytest.mark.parametrize("plan", PLANS)
+def test_decode_positions_and_splits(O, W, engines, pos, split, plan):
     case = W.make_decode(11, 1, 2, 2048, pos, salt=pos)
-    check_decode(O, engines(2, 2048), case, split=split)
+    check_decode(O, engines(2, 2048), case, split=split, plan=plan)
 
 
 @pytest.mark.parametrize("n_head,n_head_kv", [(32, 8), (32, 2), (16, 1), (24, 6), (64, 4), (12, 12)])
 @pytest.mark.parametrize("split", [0, 64])
-def test_decode_other_head_shapes(O, W, engines, n_head, n_head_kv, split):
+@pytest.mark.parametrize("plan", PLANS)
+def test_decode_other_head_shapes(O, W, engines, n_head, n_head_kv, split, plan):
     """GQA ratios 1..16, more than one workgroup of kv heads per split (grid
     y > 1) and groups with idle waves; several splits per sequence."""
     case = W.make_decode(13, 2, 2, 1024, [1023, 300], salt=n_head * 100 + n_head_kv,
                          n_head=n_head, n_head_kv=n_head_kv)
-    check_decode(O, engines(2, 1024, n_head, n_head_kv), case, split=split)
+    check_decode(O, engines(2, 1024, n_head, n_head_kv), case, split=split, plan=plan)
 
 
 def test_attention_contract_without_rotation(O, W, engines):
@@ -253,8 +259,9 @@ def test_split_merge_is_stable_under_repetition(O, W, engines, tla):
         q, k, v = track(eng.array(case.q)), track(eng.array(case.k)), track(eng.array(case.v))
         out = track(eng.array(case.q.shape))
         stride = 22 * 2048 * 256
-        for split in (16, 48):
+        for split, plan in itertools.product((16, 48), PLANS):
             eng.set_option(tla.OPT_DECODE_SPLIT, split)
+            eng.set_option(tla.OPT_DECODE_PLAN, plan)
             first = None
             for it in range(200):
                 eng.decode(case.pos, 0, 22, out.ptr, q.ptr, k.ptr, v.ptr, kc.ptr, vc.ptr, stride)
@@ -262,8 +269,21 @@ def test_split_merge_is_stable_under_repetition(O, W, engines, tla):
                 if first is None:
                     first = got
                     err = max_err(got, ref)
-                    log(f"  split {split}: max-abs {err:.3e}")
+                    log(f"  split {split} plan {plan}: max-abs {err:.3e}")
                     assert err <= DECODE_TOL
                 else:
                     assert np.array_equal(bits(got), bits(first)), f"split {split} call {it}"
         eng.set_option(tla.OPT_DECODE_SPLIT, 0)
+        eng.set_option(tla.OPT_DECODE_PLAN, 0)
+
+
+@pytest.mark.parametrize("split", [0, 48, 400, 4096])
+def test_balanced_ranges_across_units(O, W, engines, split):
+    """Balanced plan with workgroup ranges that cross many unit boundaries:
+    short and long sequences mixed, ranges holding many whole units (output
+    written in place) between the two units they share with their
+    neighbours (arrivals deferred to the range's end), and units split
+    across several ranges."""
+    pos = [200, 5, 1023, 30, 16, 511, 100, 63]
+    case = W.make_decode(19, 8, 5, 1024, pos, salt=split)
+    check_decode(O, engines(5, 1024), case, split=split, plan=2)

@@ -6,13 +6,17 @@
 // softmax, and the weighted sum of V.  With `rotate`, RoPE is applied first
 // to q and to the new k, as forward() does (src/forward.cpp:192-196).
 //
-// Work decomposition.  A "unit" is one (sequence, layer).  Its positions
-// 0..pos are cut into splits of split_len positions.  One workgroup = one
-// (unit, split, group of 4 kv heads) and holds 8 waves: two per kv head,
-// which interleave the split's tiles of 16 positions (wave `sub` takes
-// tiles sub, sub + 2, ...).  The workgroup thus streams whole 1 KiB position
-// rows of K and of V.  Each wave keeps the gqa (<= 16) q heads of its kv
-// head in registers and, per tile:
+// Work decomposition.  A "unit" is one (sequence, layer); its positions
+// 0..pos form tiles of 16.  The tiles of all units of a launch, laid end to
+// end, are cut into equal ranges, one per workgroup (about one per CU), so
+// every workgroup streams the same number of tiles however long the units
+// are.  A range holds one or more segments (the part of one unit inside
+// it); the segments of a unit are its splits.  One workgroup covers a group
+// of 4 kv heads and holds 8 waves: two per kv head, which interleave a
+// segment's tiles (wave `sub` takes tiles sub, sub + 2, ...).  The
+// workgroup thus streams whole 1 KiB position rows of K and of V.  Each
+// wave keeps the gqa (<= 16) q heads of its kv head in registers and, per
+// tile:
 //
 //   S^T[16 pos][16 heads] = K[16 pos][64] . Q^T[64][16 heads]
 //                           16 x v_mfma_f32_16x16x4f32, heads gqa..15 zero
@@ -53,6 +57,10 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 constexpr int kKvWaves = kDecodeKvGroup;  // kv heads per workgroup
 constexpr int kSub = 2;                   // position halves per kv head
 constexpr int kWaves = kKvWaves * kSub;   // waves per workgroup
+// Deferred split arrivals per workgroup: only a range's first and last
+// segments can share their unit with another range (every segment between
+// them is a whole unit, merged in place).
+constexpr int kMaxPending = 2;
 
 __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c)
 {
@@ -223,14 +231,18 @@ __device__ __forceinline__ void add_half(const HalfExchange& x, int slot, int la
     for (int i = 0; i < 4; ++i) r.acc[i] = r.acc[i] * a0 + x.acc[slot][i][lane] * a1;
 }
 
-template <int kMaxSeq>
+// kSeg: balanced plan, more than one segment per workgroup possible; the
+// aligned plan's instantiation runs the segment body exactly once.
+template <int kMaxSeq, bool kSeg>
 __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeParams p,
                                                                    const DecodeSeqs<kMaxSeq> b)
 {
     __shared__ int s_last;
     __shared__ float4 s_new[kKvWaves][32];  // appended k row (16 float4) | v row (16 float4)
     __shared__ HalfExchange s_half;
-    __shared__ HalfExchange s_mine;  // this split's partial, for the merge
+    __shared__ HalfExchange s_mine;  // this split's partial, for the merge (!kSeg)
+    __shared__ int2 s_pend[kMaxPending];  // (unit, nsplit) of deferred arrivals (kSeg)
+    __shared__ int s_pend_last[kMaxPending];
     const int lane = threadIdx.x & 63;
     // wave index made explicitly scalar so cache bases stay in SGPRs
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -239,271 +251,325 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     const int kvh = blockIdx.y * kKvWaves + slot;
     const bool active = kvh < p.n_head_kv;  // uniform per wave
 
-    // blockIdx.x -> (sequence rank, split, layer step lb), layers innermost.
-    // Ranks run longest sequence first, so workgroups start roughly longest
-    // first and the last ones to start are short.
-    const int lb = blockIdx.x % p.n_lb;
-    const int rem = blockIdx.x / p.n_lb;
-    int lo = 0, hi = p.n_seq - 1;
-    while (lo < hi) {
-        const int mid = (lo + hi + 1) >> 1;
-        if (b.split_prefix[mid] <= rem) lo = mid; else hi = mid - 1;
-    }
-    const int split = rem - b.split_prefix[lo];
-    const int nsplit = b.split_prefix[lo + 1] - b.split_prefix[lo];
-    const int pos = b.pos[lo];
-    const int seq = b.seq_id[lo];
-    const int unit = seq * p.n_lb + lb;
-    const int layer = p.layer0 + lb;
+    // Workgroup w takes the flat tiles [w * wg_tiles, (w + 1) * wg_tiles).
+    // The range falls into one or more segments, each the part of one unit
+    // inside it; the segments of one unit, in workgroup order, are its
+    // splits.  Balanced (aligned = 0): units end to end, every workgroup
+    // streams the same number of tiles.  Aligned: each unit padded to whole
+    // ranges, so a workgroup has exactly one segment (the unit's last range
+    // may be short).  The loop is uniform per workgroup.
+    const int f_lo = blockIdx.x * p.wg_tiles;
+    const int f_hi = min(f_lo + p.wg_tiles, p.total_tiles);
+    int f = f_lo;
+    int n_pend = 0;  // segments whose arrival is deferred (kSeg)
+    do {
+        int lo = 0, hi = p.n_seq - 1;  // rank: last with tile_prefix <= f
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (b.tile_prefix[mid] <= f) lo = mid; else hi = mid - 1;
+        }
+        const int pos = b.pos[lo];
+        const int seq = b.seq_id[lo];
+        const int unit_tiles = pos / kDecodeTile + 1;
+        // With `aligned`, each unit's space is padded to whole ranges.
+        const int unit_span =
+            p.aligned ? (unit_tiles + p.wg_tiles - 1) / p.wg_tiles * p.wg_tiles : unit_tiles;
+        const int lb = (f - b.tile_prefix[lo]) / unit_span;
+        const int u0 = b.tile_prefix[lo] + lb * unit_span;  // the unit's first flat tile
+        const int u1 = u0 + unit_tiles;
+        const int seg_end = min(f_hi, u1);
+        const int split = blockIdx.x - u0 / p.wg_tiles;
+        const int nsplit = (u1 - 1) / p.wg_tiles - u0 / p.wg_tiles + 1;
+        const int unit = seq * p.n_lb + lb;
+        const int layer = p.layer0 + lb;
 
-    // The split's positions [begin, end) are cut into tiles of 16.  The two
-    // waves of a kv head interleave them, wave `sub` taking tiles sub,
-    // sub + 2, sub + 4, ...: a fixed assignment, so results do not depend
-    // on timing.
-    const int begin = split * p.split_len;
-    const int end = min(pos + 1, begin + p.split_len);  // exclusive
-    const int n_tiles = (end - begin + kDecodeTile - 1) / kDecodeTile;
-    const bool appends = pos < end;  // this split holds `pos`: its last tile does
-    const int special = appends ? n_tiles - 1 : n_tiles;
+        // The segment's positions [begin, end) are cut into tiles of 16.  The
+        // two waves of a kv head interleave them, wave `sub` taking tiles sub,
+        // sub + 2, sub + 4, ...: a fixed assignment, so results do not depend
+        // on timing.
+        const int begin = (f - u0) * kDecodeTile;
+        const int end = min(pos + 1, (seg_end - u0) * kDecodeTile);  // exclusive
+        const int n_tiles = seg_end - f;
+        f = seg_end < u1 ? seg_end : min(f_hi, u0 + unit_span);  // past the padding
+        const bool appends = pos < end;  // this split holds `pos`: its last tile does
+        const int special = appends ? n_tiles - 1 : n_tiles;
 
-    const int hsub = lane & 15;  // q head within the group / K row within the tile
-    const int grp = lane >> 4;   // 0..3
-    const bool head_ok = hsub < p.gqa;
-    const int qh = kvh * p.gqa + hsub;
-    const unsigned kv_dim = (unsigned)p.n_head_kv * kHeadDim;
+        const int hsub = lane & 15;  // q head within the group / K row within the tile
+        const int grp = lane >> 4;   // 0..3
+        const bool head_ok = hsub < p.gqa;
+        const int qh = kvh * p.gqa + hsub;
+        const unsigned kv_dim = (unsigned)p.n_head_kv * kHeadDim;
 
-    // Cache slice of this (sequence, layer, kv head): row r at base + r*kv_dim.
-    const long long cache_off = (long long)seq * p.seq_stride + (long long)layer * p.layer_stride +
-                                (long long)(active ? kvh : 0) * kHeadDim;
-    float* const kc = p.kc + cache_off;
-    float* const vc = p.vc + cache_off;
-    const float* const tab = reinterpret_cast<const float*>(p.rope + (long long)pos * kPairs);
+        // Cache slice of this (sequence, layer, kv head): row r at base + r*kv_dim.
+        const long long cache_off = (long long)seq * p.seq_stride + (long long)layer * p.layer_stride +
+                                    (long long)(active ? kvh : 0) * kHeadDim;
+        float* const kc = p.kc + cache_off;
+        float* const vc = p.vc + cache_off;
+        const float* const tab = reinterpret_cast<const float*>(p.rope + (long long)pos * kPairs);
 
-    // Append (attention() step 1, src/ops.cpp:1370-1371): 16 lanes of the
-    // first wave of the kv head write the (rotated) k row and the v row to
-    // the cache and keep a copy in LDS for the split's last tile.
-    if (active && appends && sub == 0 && lane < 16) {
-        const long long row = ((long long)unit * p.n_head_kv + kvh) * kHeadDim + 4 * lane;
-        const float4 k_in = ldg4(p.k + row);
-        const float4 cs = ldg4(tab + 4 * lane);  // loaded either way: no branch before the loads
-        const float4 vx = ldg4(p.v + row);
-        const float4 kx = p.rotate ? rotate4(k_in, cs) : k_in;
-        stg4(kc + (long long)pos * kv_dim + 4 * lane, kx);
-        stg4(vc + (long long)pos * kv_dim + 4 * lane, vx);
-        s_new[slot][lane] = kx;
-        s_new[slot][16 + lane] = vx;
-    }
-    __syncthreads();
+        // Append (attention() step 1, src/ops.cpp:1370-1371): 16 lanes of the
+        // first wave of the kv head write the (rotated) k row and the v row to
+        // the cache and keep a copy in LDS for the split's last tile.
+        if (active && appends && sub == 0 && lane < 16) {
+            const long long row = ((long long)unit * p.n_head_kv + kvh) * kHeadDim + 4 * lane;
+            const float4 k_in = ldg4(p.k + row);
+            const float4 cs = ldg4(tab + 4 * lane);  // loaded either way: no branch before the loads
+            const float4 vx = ldg4(p.v + row);
+            const float4 kx = p.rotate ? rotate4(k_in, cs) : k_in;
+            stg4(kc + (long long)pos * kv_dim + 4 * lane, kx);
+            stg4(vc + (long long)pos * kv_dim + 4 * lane, vx);
+            s_new[slot][lane] = kx;
+            s_new[slot][16 + lane] = vx;
+        }
+        __syncthreads();
 
-    floatx4 o[4];
+        floatx4 o[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
-    float m_run = -INFINITY;
-    float l_run = 0.f;
+        for (int i = 0; i < 4; ++i) o[i] = floatx4{0.f, 0.f, 0.f, 0.f};
+        float m_run = -INFINITY;
+        float l_run = 0.f;
 
-    if (active) {
-        // B operand of S^T: lane holds q[head hsub][16t + 4grp + c], rotated
-        // with the pairs 8t + 2grp + {0,1} of the table row for `pos`.
-        // The q and table loads, then the first two tiles' loads, are all
-        // issued before q is rotated (below).
-        float4 qv[4], qcs[4];
-        {
-            const float* qrow = p.q + ((long long)unit * p.n_head + (head_ok ? qh : 0)) * kHeadDim;
+        if (active) {
+            // B operand of S^T: lane holds q[head hsub][16t + 4grp + c], rotated
+            // with the pairs 8t + 2grp + {0,1} of the table row for `pos`.
+            // The q and table loads, then the first two tiles' loads, are all
+            // issued before q is rotated (below).
+            float4 qv[4], qcs[4];
+            {
+                const float* qrow = p.q + ((long long)unit * p.n_head + (head_ok ? qh : 0)) * kHeadDim;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                qv[t] = ldg4(qrow + 16 * t + 4 * grp);
-                qcs[t] = ldg4(tab + 2 * (8 * t + 2 * grp));
+                for (int t = 0; t < 4; ++t) {
+                    qv[t] = ldg4(qrow + 16 * t + 4 * grp);
+                    qcs[t] = ldg4(tab + 2 * (8 * t + 2 * grp));
+                }
             }
+
+            // Rows past `end` are masked; they load row `begin` (always valid).
+            // Byte offsets are 32-bit (a unit's cache slice is < 4 GiB) from a
+            // wave-uniform base.
+            auto load_tile = [&](int tile, Tile& tl) {
+                const int p0 = begin + tile * kDecodeTile;
+                int r = p0 + hsub;
+                if (r >= end) r = begin;
+                const unsigned ko = ((unsigned)r * kv_dim + 4u * grp) * 4u;  // bytes
+#pragma unroll
+                for (int t = 0; t < 4; ++t) tl.k[t] = ldg4_at(kc, ko + 64u * t);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    int row = p0 + 4 * grp + i;
+                    if (row >= end) row = begin;
+                    tl.v[i] = ldg4_at(vc, ((unsigned)row * kv_dim + 4u * hsub) * 4u);
+                }
+            };
+
+            // One tile: S^T = K.Q^T, online softmax, O^T += V^T.P^T.
+            auto step = [&](const Tile& tl, int tile) {
+                const int p0 = begin + tile * kDecodeTile;
+                floatx4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    s = mfma16(tl.k[t].x, qv[t].x, s);
+                    s = mfma16(tl.k[t].y, qv[t].y, s);
+                    s = mfma16(tl.k[t].z, qv[t].z, s);
+                    s = mfma16(tl.k[t].w, qv[t].w, s);
+                }
+                // s[r] = S[position p0 + 4grp + r][head hsub]
+                float sc[4];
+                float mx = -INFINITY;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int kp = p0 + 4 * grp + r;
+                    sc[r] = (kp < end) ? s[r] * p.scale_log2 : -INFINITY;
+                    mx = fmaxf(mx, sc[r]);
+                }
+                mx = fmaxf(mx, __shfl_xor(mx, 16));
+                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                const float m_new = fmaxf(m_run, mx);
+                const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
+                m_run = m_new;
+                float ps[4];
+                float lsum = 0.f;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    ps[r] = __builtin_amdgcn_exp2f(sc[r] - m_new);
+                    lsum += ps[r];
+                }
+                l_run = l_run * alpha + lsum;
+#pragma unroll
+                for (int i = 0; i < 4; ++i) o[i] *= alpha;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    o[0] = mfma16(tl.v[r].x, ps[r], o[0]);
+                    o[1] = mfma16(tl.v[r].y, ps[r], o[1]);
+                    o[2] = mfma16(tl.v[r].z, ps[r], o[2]);
+                    o[3] = mfma16(tl.v[r].w, ps[r], o[3]);
+                }
+            };
+
+            // The appending split's last tile holds `pos`; that row comes from
+            // LDS (the copy kept at append), not from the cache, which the
+            // append may not have reached when the tile was loaded.  Rows loaded
+            // for masked lanes (>= end) are `begin`, also replaced when
+            // begin == pos.
+            auto substitute = [&](Tile& tl, int tile) {
+                const int p0 = begin + tile * kDecodeTile;
+                if (p0 + hsub >= pos) {
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) tl.k[t] = s_new[slot][4 * t + grp];
+                }
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const int row = p0 + 4 * grp + i;
+                    if (row == pos || (row >= end && begin == pos)) tl.v[i] = s_new[slot][16 + hsub];
+                }
+            };
+            auto process = [&](Tile& tl, int tile) {
+                if (tile == special) substitute(tl, tile);  // uniform branch
+                step(tl, tile);
+            };
+
+            // Two tiles in flight: while one is computed the other is loading.
+            // Loads are unconditional, so that the count of loads in flight is
+            // the same on every path and waiting for one tile never waits for
+            // the other: a tile index past the end reloads a tile already
+            // loaded (a cache hit) and is not used.
+            constexpr int kStride = 2 * kSub;  // tiles between a wave's ta and its next ta
+            int ca = sub, cb = kSub + sub;
+            Tile ta, tb;
+            load_tile(min(ca, n_tiles - 1), ta);
+            __builtin_amdgcn_sched_barrier(0);  // all of ta's loads before tb's
+            load_tile(min(cb, n_tiles - 1), tb);
+            if (p.rotate) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) qv[t] = rotate4(qv[t], qcs[t]);
+            }
+            if (!head_ok) {
+#pragma unroll
+                for (int t = 0; t < 4; ++t) qv[t] = make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+            do {
+                if (ca < n_tiles) process(ta, ca);  // uniform branches: the loads stay outside
+                const int na = ca + kStride;
+                load_tile(na < n_tiles ? na : min(ca, n_tiles - 1), ta);
+                if (cb < n_tiles) process(tb, cb);
+                const int nb = cb + kStride;
+                load_tile(nb < n_tiles ? nb : min(cb, n_tiles - 1), tb);
+                ca = na;
+                cb = nb;
+            } while (ca < n_tiles);
+
+            // Row sums: each lane group summed different positions of the same head.
+            l_run += __shfl_xor(l_run, 16);
+            l_run += __shfl_xor(l_run, 32);
         }
 
-        // Rows past `end` are masked; they load row `begin` (always valid).
-        // Byte offsets are 32-bit (a unit's cache slice is < 4 GiB) from a
-        // wave-uniform base.
-        auto load_tile = [&](int tile, Tile& tl) {
-            const int p0 = begin + tile * kDecodeTile;
-            int r = p0 + hsub;
-            if (r >= end) r = begin;
-            const unsigned ko = ((unsigned)r * kv_dim + 4u * grp) * 4u;  // bytes
+        // The two halves of each kv head meet in LDS; the first half continues.
+        // o[dt][i] = O[head hsub][16*grp + 4*i + dt]  ->  r.acc[i][dt]
+        Partial r;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) tl.k[t] = ldg4_at(kc, ko + 64u * t);
+        for (int i = 0; i < 4; ++i) r.acc[i] = floatx4{o[0][i], o[1][i], o[2][i], o[3][i]};
+        r.m = m_run;
+        r.l = l_run;
+        if (active && sub == 1) put_half(s_half, slot, lane, r);
+        __syncthreads();
+        if (active && sub == 0) {
+            add_half(s_half, slot, lane, r);
+            // r.acc[i][c] = O[head hsub][d = 16*grp + 4*i + c]
+            if (nsplit == 1) {
+                if (head_ok) {
+                    const float inv = 1.0f / r.l;
+                    float* orow = p.out + ((long long)unit * p.n_head + qh) * kHeadDim + 16 * grp;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                int row = p0 + 4 * grp + i;
-                if (row >= end) row = begin;
-                tl.v[i] = ldg4_at(vc, ((unsigned)row * kv_dim + 4u * hsub) * 4u);
-            }
-        };
-
-        // One tile: S^T = K.Q^T, online softmax, O^T += V^T.P^T.
-        auto step = [&](const Tile& tl, int tile) {
-            const int p0 = begin + tile * kDecodeTile;
-            floatx4 s = {0.f, 0.f, 0.f, 0.f};
+                    for (int i = 0; i < 4; ++i)
+                        stg4(orow + 4 * i, make_float4(r.acc[i][0] * inv, r.acc[i][1] * inv,
+                                                       r.acc[i][2] * inv, r.acc[i][3] * inv));
+                }
+            } else {
+                // The partial goes to the workspace for whichever workgroup merges
+                // (and, with one segment, to LDS in case it is this one).
+                if constexpr (!kSeg) put_half(s_mine, slot, lane, r);
+                if (head_ok) {
+                    const auto rs =
+                        part_rsrc(p.part + part_slot(p, unit, split, kvh), part_floats(p.gqa) * 4);
+                    const int li = grp * p.gqa + hsub;
 #pragma unroll
-            for (int t = 0; t < 4; ++t) {
-                s = mfma16(tl.k[t].x, qv[t].x, s);
-                s = mfma16(tl.k[t].y, qv[t].y, s);
-                s = mfma16(tl.k[t].z, qv[t].z, s);
-                s = mfma16(tl.k[t].w, qv[t].w, s);
-            }
-            // s[r] = S[position p0 + 4grp + r][head hsub]
-            float sc[4];
-            float mx = -INFINITY;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                const int kp = p0 + 4 * grp + r;
-                sc[r] = (kp < end) ? s[r] * p.scale_log2 : -INFINITY;
-                mx = fmaxf(mx, sc[r]);
-            }
-            mx = fmaxf(mx, __shfl_xor(mx, 16));
-            mx = fmaxf(mx, __shfl_xor(mx, 32));
-            const float m_new = fmaxf(m_run, mx);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
-            m_run = m_new;
-            float ps[4];
-            float lsum = 0.f;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                ps[r] = __builtin_amdgcn_exp2f(sc[r] - m_new);
-                lsum += ps[r];
-            }
-            l_run = l_run * alpha + lsum;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) o[i] *= alpha;
-#pragma unroll
-            for (int r = 0; r < 4; ++r) {
-                o[0] = mfma16(tl.v[r].x, ps[r], o[0]);
-                o[1] = mfma16(tl.v[r].y, ps[r], o[1]);
-                o[2] = mfma16(tl.v[r].z, ps[r], o[2]);
-                o[3] = mfma16(tl.v[r].w, ps[r], o[3]);
-            }
-        };
-
-        // The appending split's last tile holds `pos`; that row comes from
-        // LDS (the copy kept at append), not from the cache, which the
-        // append may not have reached when the tile was loaded.  Rows loaded
-        // for masked lanes (>= end) are `begin`, also replaced when
-        // begin == pos.
-        auto substitute = [&](Tile& tl, int tile) {
-            const int p0 = begin + tile * kDecodeTile;
-            if (p0 + hsub >= pos) {
-#pragma unroll
-                for (int t = 0; t < 4; ++t) tl.k[t] = s_new[slot][4 * t + grp];
-            }
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                const int row = p0 + 4 * grp + i;
-                if (row == pos || (row >= end && begin == pos)) tl.v[i] = s_new[slot][16 + hsub];
-            }
-        };
-        auto process = [&](Tile& tl, int tile) {
-            if (tile == special) substitute(tl, tile);  // uniform branch
-            step(tl, tile);
-        };
-
-        // Two tiles in flight: while one is computed the other is loading.
-        // Loads are unconditional, so that the count of loads in flight is
-        // the same on every path and waiting for one tile never waits for
-        // the other: a tile index past the end reloads a tile already
-        // loaded (a cache hit) and is not used.
-        constexpr int kStride = 2 * kSub;  // tiles between a wave's ta and its next ta
-        int ca = sub, cb = kSub + sub;
-        Tile ta, tb;
-        load_tile(min(ca, n_tiles - 1), ta);
-        __builtin_amdgcn_sched_barrier(0);  // all of ta's loads before tb's
-        load_tile(min(cb, n_tiles - 1), tb);
-        if (p.rotate) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) qv[t] = rotate4(qv[t], qcs[t]);
-        }
-        if (!head_ok) {
-#pragma unroll
-            for (int t = 0; t < 4; ++t) qv[t] = make_float4(0.f, 0.f, 0.f, 0.f);
-        }
-        do {
-            if (ca < n_tiles) process(ta, ca);  // uniform branches: the loads stay outside
-            const int na = ca + kStride;
-            load_tile(na < n_tiles ? na : min(ca, n_tiles - 1), ta);
-            if (cb < n_tiles) process(tb, cb);
-            const int nb = cb + kStride;
-            load_tile(nb < n_tiles ? nb : min(cb, n_tiles - 1), tb);
-            ca = na;
-            cb = nb;
-        } while (ca < n_tiles);
-
-        // Row sums: each lane group summed different positions of the same head.
-        l_run += __shfl_xor(l_run, 16);
-        l_run += __shfl_xor(l_run, 32);
-    }
-
-    // The two halves of each kv head meet in LDS; the first half continues.
-    // o[dt][i] = O[head hsub][16*grp + 4*i + dt]  ->  r.acc[i][dt]
-    Partial r;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) r.acc[i] = floatx4{o[0][i], o[1][i], o[2][i], o[3][i]};
-    r.m = m_run;
-    r.l = l_run;
-    if (active && sub == 1) put_half(s_half, slot, lane, r);
-    __syncthreads();
-    if (active && sub == 0) {
-        add_half(s_half, slot, lane, r);
-        // r.acc[i][c] = O[head hsub][d = 16*grp + 4*i + c]
-        if (nsplit == 1) {
-            if (head_ok) {
-                const float inv = 1.0f / r.l;
-                float* orow = p.out + ((long long)unit * p.n_head + qh) * kHeadDim + 16 * grp;
-#pragma unroll
-                for (int i = 0; i < 4; ++i)
-                    stg4(orow + 4 * i, make_float4(r.acc[i][0] * inv, r.acc[i][1] * inv,
-                                                   r.acc[i][2] * inv, r.acc[i][3] * inv));
-            }
-        } else {
-            // The partial goes to the workspace for whichever workgroup merges
-            // and to LDS in case it is this one.
-            put_half(s_mine, slot, lane, r);
-            if (head_ok) {
-                const auto rs =
-                    part_rsrc(p.part + part_slot(p, unit, split, kvh), part_floats(p.gqa) * 4);
-                const int li = grp * p.gqa + hsub;
-#pragma unroll
-                for (int i = 0; i < 4; ++i) st_dev4(r.acc[i], rs, (i * 4 * p.gqa + li) * 16);
-                if (grp == 0) {
-                    st_dev1(r.m, rs, (64 * p.gqa + hsub) * 4);
-                    st_dev1(r.l, rs, (65 * p.gqa + hsub) * 4);
+                    for (int i = 0; i < 4; ++i) st_dev4(r.acc[i], rs, (i * 4 * p.gqa + li) * 16);
+                    if (grp == 0) {
+                        st_dev1(r.m, rs, (64 * p.gqa + hsub) * 4);
+                        st_dev1(r.l, rs, (65 * p.gqa + hsub) * 4);
+                    }
                 }
             }
         }
-    }
 
-    if (nsplit == 1) return;  // uniform per workgroup
-    // Wait until this wave's partial stores are acknowledged at device scope,
-    // then count the split in; the workgroup that completes the count of its
-    // (unit, kv head group) merges.
-    __builtin_amdgcn_s_waitcnt(0);
-    __syncthreads();
-    int* const counter = p.counters + (long long)unit * gridDim.y + blockIdx.y;
-    if (threadIdx.x == 0)
-        s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) ==
-                 nsplit - 1;
-    __syncthreads();
-    if (!s_last) return;
-    if (threadIdx.x == 0)  // every split has arrived: ready for the next launch
-        __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // Both halves of each kv head merge half of the splits, then meet in LDS.
-    const int s_mid = (nsplit + 1) / 2;
-    Partial mr;
-    if (active)
-        mr = merge_range(p, unit, sub == 0 ? 0 : s_mid, sub == 0 ? s_mid : nsplit, split, s_mine,
-                         slot, kvh, lane);
-    if (active && sub == 1) put_half(s_half, slot, lane, mr);
-    __syncthreads();
-    if (!active || sub != 0 || !head_ok) return;
-    add_half(s_half, slot, lane, mr);
-    const float inv = 1.0f / mr.l;
-    float* orow = p.out + ((long long)unit * p.n_head + qh) * kHeadDim + 16 * grp;
+        // Merge of all mn splits of unit mu (split `own` from s_mine, -1: none):
+        // both halves of each kv head merge half of the splits, then meet in LDS.
+        auto merge_unit = [&](int mu, int mn, int own) {
+            const int s_mid = (mn + 1) / 2;
+            Partial mr;
+            if (active)
+                mr = merge_range(p, mu, sub == 0 ? 0 : s_mid, sub == 0 ? s_mid : mn, own, s_mine,
+                                 slot, kvh, lane);
+            if (active && sub == 1) put_half(s_half, slot, lane, mr);
+            __syncthreads();
+            if (active && sub == 0 && head_ok) {
+                add_half(s_half, slot, lane, mr);
+                const float inv = 1.0f / mr.l;
+                float* orow = p.out + ((long long)mu * p.n_head + qh) * kHeadDim + 16 * grp;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-        stg4(orow + 4 * i, make_float4(mr.acc[i][0] * inv, mr.acc[i][1] * inv, mr.acc[i][2] * inv,
-                                       mr.acc[i][3] * inv));
+                for (int i = 0; i < 4; ++i)
+                    stg4(orow + 4 * i, make_float4(mr.acc[i][0] * inv, mr.acc[i][1] * inv,
+                                                   mr.acc[i][2] * inv, mr.acc[i][3] * inv));
+            }
+        };
+
+        if constexpr (kSeg) {
+            // Arrivals are deferred to the end of the range: the partial
+            // stores drain while the next segment streams, instead of
+            // stalling the workgroup in mid-run.
+            if (nsplit > 1) {
+                if (threadIdx.x == 0) s_pend[n_pend] = make_int2(unit, nsplit);
+                ++n_pend;  // uniform
+            }
+            if (n_pend < kMaxPending && f < f_hi) continue;
+            if (n_pend == 0) continue;
+            __builtin_amdgcn_s_waitcnt(0);  // this wave's partial stores acknowledged
+            __syncthreads();
+            if (threadIdx.x < n_pend) {
+                const int2 pu = s_pend[threadIdx.x];
+                int* const counter = p.counters + (long long)pu.x * gridDim.y + blockIdx.y;
+                const bool last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED,
+                                                         __HIP_MEMORY_SCOPE_AGENT) == pu.y - 1;
+                if (last)  // every split has arrived: ready for the next launch
+                    __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+                s_pend_last[threadIdx.x] = last;
+            }
+            __syncthreads();
+            for (int t = 0; t < n_pend; ++t) {
+                if (!s_pend_last[t]) continue;  // uniform
+                const int2 pu = s_pend[t];
+                merge_unit(pu.x, pu.y, -1);
+                __syncthreads();  // s_half is reused by the next merge
+            }
+            n_pend = 0;
+        } else {
+            if (nsplit == 1) continue;  // uniform per workgroup
+            // Wait until this wave's partial stores are acknowledged at device
+            // scope, then count the split in; the workgroup that completes the
+            // count of its (unit, kv head group) merges.
+            __builtin_amdgcn_s_waitcnt(0);
+            __syncthreads();
+            int* const counter = p.counters + (long long)unit * gridDim.y + blockIdx.y;
+            if (threadIdx.x == 0)
+                s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
+            __syncthreads();
+            if (!s_last) continue;
+            if (threadIdx.x == 0)  // every split has arrived: ready for the next launch
+                __hip_atomic_store(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            merge_unit(unit, nsplit, split);
+        }
+    } while (kSeg && f < f_hi);  // segments
 }
 
 }  // namespace
@@ -511,18 +577,23 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
 hipError_t launch_decode(const DecodeParams& p, const DecodeSeqs<kMaxSeqPerLaunch>& seqs,
                          hipStream_t s)
 {
-    dim3 grid(p.total_splits * p.n_lb, (p.n_head_kv + kKvWaves - 1) / kKvWaves);
+    dim3 grid((p.total_tiles + p.wg_tiles - 1) / p.wg_tiles, (p.n_head_kv + kKvWaves - 1) / kKvWaves);
+    const dim3 block(64 * kWaves);
     if (p.n_seq <= 8) {
         DecodeSeqs<8> small{};
         for (int i = 0; i < p.n_seq; ++i) {
             small.pos[i] = seqs.pos[i];
             small.seq_id[i] = seqs.seq_id[i];
         }
-        for (int i = 0; i <= p.n_seq; ++i) small.split_prefix[i] = seqs.split_prefix[i];
-        hipLaunchKernelGGL(decode_split_kernel<8>, grid, dim3(64 * kWaves), 0, s, p, small);
+        for (int i = 0; i <= p.n_seq; ++i) small.tile_prefix[i] = seqs.tile_prefix[i];
+        if (p.aligned)
+            hipLaunchKernelGGL((decode_split_kernel<8, false>), grid, block, 0, s, p, small);
+        else
+            hipLaunchKernelGGL((decode_split_kernel<8, true>), grid, block, 0, s, p, small);
+    } else if (p.aligned) {
+        hipLaunchKernelGGL((decode_split_kernel<kMaxSeqPerLaunch, false>), grid, block, 0, s, p, seqs);
     } else {
-        hipLaunchKernelGGL(decode_split_kernel<kMaxSeqPerLaunch>, grid, dim3(64 * kWaves), 0, s, p,
-                           seqs);
+        hipLaunchKernelGGL((decode_split_kernel<kMaxSeqPerLaunch, true>), grid, block, 0, s, p, seqs);
     }
     return hipGetLastError();
 }

@@ -100,6 +100,8 @@ struct tla_engine {
     size_t gemm_ws_bytes = 0;
     int* argmax_slot = nullptr;
     long long opt_split = 0;
+    int opt_plan = TLA_PLAN_AUTO;
+    int n_cu = 256;          // compute units: decode workgroups per launch
 
     bool prof = false;
     std::vector<std::pair<hipEvent_t, hipEvent_t>> prof_pending[TLA_KERNEL_COUNT];
@@ -212,23 +214,42 @@ float scale_log2(int head_dim)
     return static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
 }
 
-// Positions per split-KV chunk.  Measured on MI355X: splits long enough that
-// about 240 workgroups (one per CU) cover the whole batch, between 64 and
-// 4096 positions -- short splits multiply the partials the merge must read
-// back and each workgroup's fixed start and merge costs, long ones leave CUs
-// idle on small batches.  A batch big enough for several rounds of
-// workgroups takes whole sequences (up to 4096 positions) per workgroup:
-// sequences are dispatched longest first, so the last round is short.
-int plan_split(long long total_positions, int max_len, long long opt)
+// Decode work plans.  One 8-wave workgroup fits a CU.
+//
+// Aligned: every unit (sequence, layer) is cut into splits of one length,
+// each a workgroup of its own.  The length gives about 15/16 of the CUs a
+// split each when that fills one round of workgroups, and is at least 64
+// positions, at most the longest sequence and at most 4096: a bigger batch
+// then takes whole sequences per workgroup, longest first, in several
+// rounds.  No workgroup pays for more than one split's fixed costs.
+//
+// Balanced: the tiles of all units laid end to end are cut into one equal
+// range per CU; a range that meets a unit boundary continues into the next
+// unit.  Every workgroup streams the same number of tiles, but one that
+// crosses a boundary starts its pipeline twice (q and the first tiles
+// loaded with nothing else in flight) and may merge two units at the end.
+//
+// Measured on MI355X (22 layers): one sequence at 2048-16384 positions,
+// aligned (one round of 242 workgroups) 24.2-129.5 us against balanced
+// 30-32 / 133-143 us whatever its workgroup count (217-256): the
+// workgroups that cross a boundary end last.  8 sequences at 16384
+// (aligned: 2.75 rounds of 4096-position splits) 76.2 % of HBM aligned,
+// 77.5 % balanced.  64 ragged sequences (256-2048; ranges span about six
+// units) 70.8 % aligned, 66.6 % balanced.  Hence: aligned when it fits one
+// round; otherwise balanced when a range is no longer than the shortest
+// unit (so it crosses at most one boundary), else aligned.
+long long aligned_wg_tiles(long long total_positions, int max_len, int n_cu)
 {
-    if (opt > 0) {
-        long long s = (opt + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
-        return static_cast<int>(std::min<long long>(std::max<long long>(s, kDecodeTile), 1 << 24));
-    }
-    long long s = (total_positions + 239) / 240;
+    const long long target = std::max(1, n_cu - n_cu / 16);
+    long long s = (total_positions + target - 1) / target;
     s = std::min<long long>(s, max_len);
-    s = (s + kDecodeTile - 1) / kDecodeTile * kDecodeTile;
-    return static_cast<int>(std::min<long long>(std::max<long long>(s, 64), 4096));
+    s = std::min<long long>(std::max<long long>(s, 64), 4096);
+    return (s + kDecodeTile - 1) / kDecodeTile;
+}
+
+long long balanced_wg_tiles(long long total_tiles, int n_cu)
+{
+    return std::max<long long>(4, (total_tiles + n_cu - 1) / n_cu);
 }
 
 }  // namespace
@@ -286,9 +307,11 @@ int tla_engine_create(const tla_config* cfg, int device, tla_engine** out)
     };
     if (int rc = set_device(e)) return bail(rc);
     {
-        const hipError_t err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
+        hipError_t err = hipDeviceGetAttribute(&e->n_cu, hipDeviceAttributeMultiprocessorCount, device);
+        if (err == hipSuccess && e->n_cu < 1) e->n_cu = 1;
+        if (err == hipSuccess) err = hipStreamCreateWithFlags(&e->stream, hipStreamNonBlocking);
         if (err != hipSuccess)
-            return bail(fail(TLA_ERR_DEVICE, "hipStreamCreate: %s", hipGetErrorString(err)));
+            return bail(fail(TLA_ERR_DEVICE, "device query / stream: %s", hipGetErrorString(err)));
     }
     std::vector<float2> tab;
     rope_table_host(tab, cfg->n_ctx, head_dim, cfg->rope_freq_base);
@@ -619,31 +642,50 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
 
     DecodeParams p{};
     DecodeSeqs<kMaxSeqPerLaunch> seqs{};
-    long long total_positions = 0;
-    int max_len = 0;
     for (int s = 0; s < n_seq; ++s) {
         const int pos = pos_host[s];
         if (pos < 0 || pos >= c.n_ctx)
             return fail(TLA_ERR_OUT_OF_RANGE, "pos[%d] = %d outside [0, n_ctx=%d)", s, pos, c.n_ctx);
         seqs.seq_id[s] = s;
-        total_positions += static_cast<long long>(pos + 1) * n_step_layers;
-        max_len = std::max(max_len, pos + 1);
     }
-    // Longest sequences first (ties in caller order): their workgroups start
-    // first, so the last round of workgroups is the shortest.
+    // Ranks by length, longest first (ties in caller order); the flat tile
+    // space lays out each rank's n_step_layers units in turn.
     std::stable_sort(seqs.seq_id, seqs.seq_id + n_seq,
                      [&](int a, int b) { return pos_host[a] > pos_host[b]; });
-    for (int r = 0; r < n_seq; ++r) seqs.pos[r] = pos_host[seqs.seq_id[r]];
-    const int split_len = plan_split(total_positions, max_len, e->opt_split);
-    seqs.split_prefix[0] = 0;
+    long long total_positions = 0, real_tiles = 0;
+    for (int r = 0; r < n_seq; ++r) {
+        seqs.pos[r] = pos_host[seqs.seq_id[r]];
+        total_positions += static_cast<long long>(seqs.pos[r] + 1) * n_step_layers;
+        real_tiles += static_cast<long long>(seqs.pos[r] / kDecodeTile + 1) * n_step_layers;
+    }
+    const long long a_tiles = aligned_wg_tiles(total_positions, seqs.pos[0] + 1, e->n_cu);
+    long long a_groups = 0;  // workgroups of the aligned plan
+    for (int r = 0; r < n_seq; ++r)
+        a_groups += (seqs.pos[r] / kDecodeTile + a_tiles) / a_tiles * n_step_layers;
+    const long long b_tiles = balanced_wg_tiles(real_tiles, e->n_cu);
+    const long long min_unit = seqs.pos[n_seq - 1] / kDecodeTile + 1;  // shortest rank
+    int aligned = e->opt_plan == TLA_PLAN_ALIGNED;
+    if (e->opt_plan == TLA_PLAN_AUTO) aligned = a_groups <= e->n_cu || b_tiles > min_unit;
+    long long wg = aligned ? a_tiles : b_tiles;
+    if (e->opt_split > 0) wg = (e->opt_split + kDecodeTile - 1) / kDecodeTile;
+    wg = std::min(wg, real_tiles);
+    const int wg_tiles = static_cast<int>(wg);
+    // Flat layout; splits of a unit = workgroup ranges it meets.
+    long long total_tiles = 0;
     int max_splits = 1;
     for (int r = 0; r < n_seq; ++r) {
-        const int ns = (seqs.pos[r] + 1 + split_len - 1) / split_len;
-        seqs.split_prefix[r + 1] = seqs.split_prefix[r] + ns;
-        max_splits = std::max(max_splits, ns);
+        const long long unit_tiles = seqs.pos[r] / kDecodeTile + 1;
+        const long long span = aligned ? (unit_tiles + wg - 1) / wg * wg : unit_tiles;
+        seqs.tile_prefix[r] = static_cast<int>(total_tiles);
+        for (int lb = 0; lb < n_step_layers; ++lb) {
+            const long long u0 = total_tiles + lb * span;
+            max_splits = std::max(max_splits,
+                                  static_cast<int>((u0 + unit_tiles - 1) / wg - u0 / wg + 1));
+        }
+        total_tiles += span * n_step_layers;
+        if (total_tiles > 0x3fffffffLL) return fail(TLA_ERR_UNSUPPORTED, "too many positions");
     }
-    if (static_cast<long long>(seqs.split_prefix[n_seq]) * n_step_layers > 0x7fffffffLL)
-        return fail(TLA_ERR_UNSUPPORTED, "too many workgroups");
+    seqs.tile_prefix[n_seq] = static_cast<int>(total_tiles);
     if (int rc = set_device(e)) return rc;
 
     const long long units = static_cast<long long>(n_seq) * n_step_layers;
@@ -672,9 +714,10 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
     p.n_head = c.n_head;
     p.n_head_kv = c.n_head_kv;
     p.gqa = e->gqa;
-    p.split_len = split_len;
+    p.wg_tiles = wg_tiles;
     p.max_splits = max_splits;
-    p.total_splits = seqs.split_prefix[n_seq];
+    p.total_tiles = static_cast<int>(total_tiles);
+    p.aligned = aligned;
     p.rotate = (flags & TLA_ROTATE) ? 1 : 0;
     p.scale_log2 = scale_log2(e->head_dim);
 
@@ -1381,6 +1424,11 @@ int tla_set_option(tla_engine* e, int option, long long value)
     case TLA_OPT_DECODE_SPLIT:
         if (value < 0) return fail(TLA_ERR_INVALID_ARGUMENT, "split %lld < 0", value);
         e->opt_split = value;
+        return ok();
+    case TLA_OPT_DECODE_PLAN:
+        if (value < TLA_PLAN_AUTO || value > TLA_PLAN_BALANCED)
+            return fail(TLA_ERR_INVALID_ARGUMENT, "decode plan %lld not in [0, 2]", value);
+        e->opt_plan = static_cast<int>(value);
         return ok();
     default:
         return fail(TLA_ERR_INVALID_ARGUMENT, "unknown option %d", option);

@@ -38,23 +38,27 @@ struct DecodeParams {
     int n_head;
     int n_head_kv;
     int gqa;
-    int split_len;     // positions per split, multiple of kDecodeTile
-    int max_splits;    // split stride in `part`
-    int total_splits;  // split_prefix[n_seq]
+    int wg_tiles;      // tiles of kDecodeTile positions per workgroup
+    int max_splits;    // split stride in `part`: most workgroups sharing one unit
+    int total_tiles;   // tile_prefix[n_seq]
+    int aligned;       // units padded to a multiple of wg_tiles in the flat space
     int rotate;
     float scale_log2;  // log2(e) / sqrt(head_dim)
 };
 
-// Per-sequence positions and split offsets of one launch, passed by value in
+// Per-sequence positions and tile offsets of one launch, passed by value in
 // the kernel arguments.  Sequences appear by rank, longest first; seq_id maps
-// a rank to the caller's sequence index.  The kernel is instantiated for up
-// to 8 and up to 256 sequences so small batches do not pay for a 3 KiB
-// argument block (about 1 us per launch).
+// a rank to the caller's sequence index.  The units of rank r are its n_lb
+// layers, each of pos[r] / kDecodeTile + 1 tiles (padded to a multiple of
+// wg_tiles when aligned), laid end to end from tile_prefix[r] in one flat
+// tile space that the workgroups cut into equal ranges.  The kernel is instantiated for up to 8 and up to 256 sequences
+// so small batches do not pay for a 3 KiB argument block (about 1 us per
+// launch).
 template <int kMaxSeq>
 struct DecodeSeqs {
-    int pos[kMaxSeq];               // by rank
-    int seq_id[kMaxSeq];            // rank -> sequence index
-    int split_prefix[kMaxSeq + 1];  // cumulative splits, by rank
+    int pos[kMaxSeq];              // by rank
+    int seq_id[kMaxSeq];           // rank -> sequence index
+    int tile_prefix[kMaxSeq + 1];  // first flat tile of each rank's units
 };
 
 hipError_t launch_decode(const DecodeParams& p, const DecodeSeqs<kMaxSeqPerLaunch>& seqs,
