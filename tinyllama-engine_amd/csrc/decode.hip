@@ -429,10 +429,13 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
             };
 
             // Two tiles in flight: while one is computed the other is loading.
-            // Loads are unconditional, so that the count of loads in flight is
-            // the same on every path and waiting for one tile never waits for
-            // the other: a tile index past the end reloads a tile already
-            // loaded (a cache hit) and is not used.
+            // In the steady-state loop both next tiles exist and every load is
+            // unconditional, so the count of loads in flight is the same on
+            // every path and waiting for one tile never waits for the other.
+            // The last round is peeled so that no load is issued for a tile
+            // past the end: an unused load would still hold the wave (and the
+            // split's arrival) for a round trip.  Only the first tb may be a
+            // reload of a loaded tile (n_tiles <= 2 + sub), issued with ta.
             constexpr int kStride = 2 * kSub;  // tiles between a wave's ta and its next ta
             int ca = sub, cb = kSub + sub;
             Tile ta, tb;
@@ -447,16 +450,23 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
 #pragma unroll
                 for (int t = 0; t < 4; ++t) qv[t] = make_float4(0.f, 0.f, 0.f, 0.f);
             }
-            do {
-                if (ca < n_tiles) process(ta, ca);  // uniform branches: the loads stay outside
-                const int na = ca + kStride;
-                load_tile(na < n_tiles ? na : min(ca, n_tiles - 1), ta);
+            while (cb + kStride < n_tiles) {  // uniform; ca < cb
+                process(ta, ca);
+                load_tile(ca + kStride, ta);
+                process(tb, cb);
+                load_tile(cb + kStride, tb);
+                ca += kStride;
+                cb += kStride;
+            }
+            if (ca + kStride < n_tiles) {  // one more ta, no more tb
+                process(ta, ca);
+                load_tile(ca + kStride, ta);
+                process(tb, cb);
+                process(ta, ca + kStride);
+            } else {
+                if (ca < n_tiles) process(ta, ca);
                 if (cb < n_tiles) process(tb, cb);
-                const int nb = cb + kStride;
-                load_tile(nb < n_tiles ? nb : min(cb, n_tiles - 1), tb);
-                ca = na;
-                cb = nb;
-            } while (ca < n_tiles);
+            }
 
             // Row sums: each lane group summed different positions of the same head.
             l_run += __shfl_xor(l_run, 16);
