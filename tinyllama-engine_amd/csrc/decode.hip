@@ -101,6 +101,15 @@ __device__ __forceinline__ floatx4 ld_dev4(__amdgpu_buffer_rsrc_t rs, int byte_o
                               __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, kDeviceScope));
 }
 
+// Bounded cache reads: a raw buffer load whose offset is past the
+// resource's byte count returns zeros without a memory request.
+constexpr unsigned kOutOfRange = 0x80000000u;  // > any slice (engine: < 2^31 - 256 B)
+
+__device__ __forceinline__ float4 ld_rows4(__amdgpu_buffer_rsrc_t rs, unsigned byte_off)
+{
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, 0));
+}
+
 __device__ __forceinline__ float ld_dev1(__amdgpu_buffer_rsrc_t rs, int byte_off)
 {
     return __builtin_bit_cast(float,
@@ -344,21 +353,24 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
                 }
             }
 
-            // Rows past `end` are masked; they load row `begin` (always valid).
-            // Byte offsets are 32-bit (a unit's cache slice is < 4 GiB) from a
-            // wave-uniform base.
+            // Rows at or past `end` are masked; their loads fall outside the
+            // buffer of rows [0, end) and return zeros without a memory
+            // request, so a tile past the end costs no traffic.  Byte offsets
+            // are 32-bit (a slice is < 2 GiB) from a wave-uniform base.
+            const unsigned slice_bytes = (unsigned)end * kv_dim * 4u;
+            const auto krs = __builtin_amdgcn_make_buffer_rsrc(kc, 0, slice_bytes, kRawBufferWord3);
+            const auto vrs = __builtin_amdgcn_make_buffer_rsrc(vc, 0, slice_bytes, kRawBufferWord3);
             auto load_tile = [&](int tile, Tile& tl) {
                 const int p0 = begin + tile * kDecodeTile;
-                int r = p0 + hsub;
-                if (r >= end) r = begin;
-                const unsigned ko = ((unsigned)r * kv_dim + 4u * grp) * 4u;  // bytes
+                const int r = p0 + hsub;
+                const unsigned ko = r < end ? ((unsigned)r * kv_dim + 4u * grp) * 4u : kOutOfRange;
 #pragma unroll
-                for (int t = 0; t < 4; ++t) tl.k[t] = ldg4_at(kc, ko + 64u * t);
+                for (int t = 0; t < 4; ++t) tl.k[t] = ld_rows4(krs, ko + 64u * t);
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
-                    int row = p0 + 4 * grp + i;
-                    if (row >= end) row = begin;
-                    tl.v[i] = ldg4_at(vc, ((unsigned)row * kv_dim + 4u * hsub) * 4u);
+                    const int row = p0 + 4 * grp + i;
+                    tl.v[i] = ld_rows4(
+                        vrs, row < end ? ((unsigned)row * kv_dim + 4u * hsub) * 4u : kOutOfRange);
                 }
             };
 
@@ -408,9 +420,8 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
 
             // The appending split's last tile holds `pos`; that row comes from
             // LDS (the copy kept at append), not from the cache, which the
-            // append may not have reached when the tile was loaded.  Rows loaded
-            // for masked lanes (>= end) are `begin`, also replaced when
-            // begin == pos.
+            // append may not have reached when the tile was loaded.  (K rows
+            // past `pos` take it too; they are masked.)
             auto substitute = [&](Tile& tl, int tile) {
                 const int p0 = begin + tile * kDecodeTile;
                 if (p0 + hsub >= pos) {
@@ -420,7 +431,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
 #pragma unroll
                 for (int i = 0; i < 4; ++i) {
                     const int row = p0 + 4 * grp + i;
-                    if (row == pos || (row >= end && begin == pos)) tl.v[i] = s_new[slot][16 + hsub];
+                    if (row == pos) tl.v[i] = s_new[slot][16 + hsub];
                 }
             };
             auto process = [&](Tile& tl, int tile) {
@@ -434,14 +445,15 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
             // every path and waiting for one tile never waits for the other.
             // The last round is peeled so that no load is issued for a tile
             // past the end: an unused load would still hold the wave (and the
-            // split's arrival) for a round trip.  Only the first tb may be a
-            // reload of a loaded tile (n_tiles <= 2 + sub), issued with ta.
+            // split's arrival) for a round trip.  The first ta and tb may lie
+            // past the end (n_tiles <= 2 + sub): their loads are out of range
+            // and fetch nothing.
             constexpr int kStride = 2 * kSub;  // tiles between a wave's ta and its next ta
             int ca = sub, cb = kSub + sub;
             Tile ta, tb;
-            load_tile(min(ca, n_tiles - 1), ta);
+            load_tile(ca, ta);
             __builtin_amdgcn_sched_barrier(0);  // all of ta's loads before tb's
-            load_tile(min(cb, n_tiles - 1), tb);
+            load_tile(cb, tb);
             if (p.rotate) {
 #pragma unroll
                 for (int t = 0; t < 4; ++t) qv[t] = rotate4(qv[t], qcs[t]);

@@ -288,6 +288,11 @@ int tla_engine_create(const tla_config* cfg, int device, tla_engine** out)
     if (gqa > kMaxGqa)
         return fail(TLA_ERR_UNSUPPORTED, "n_head/n_head_kv = %d > %d", gqa, kMaxGqa);
     if (cfg->n_ctx > (1 << 24)) return fail(TLA_ERR_UNSUPPORTED, "n_ctx %d > 2^24", cfg->n_ctx);
+    // The decode kernel addresses one (sequence, layer) cache slice with
+    // 32-bit byte offsets below 2^31.
+    if (static_cast<long long>(cfg->n_ctx) * cfg->n_head_kv * head_dim * 4 > (1ll << 31) - 256)
+        return fail(TLA_ERR_UNSUPPORTED, "one layer's KV cache (n_ctx x kv_dim x 4 = %lld B) > 2 GiB",
+                    static_cast<long long>(cfg->n_ctx) * cfg->n_head_kv * head_dim * 4);
     if (device < 0) return fail(TLA_ERR_INVALID_ARGUMENT, "device %d < 0", device);
 
     int n_dev = 0;
