@@ -21,6 +21,7 @@
 //
 // fp32 products and fp32 accumulation in a different order than the
 // reference's sequential loops: results agree to fp32 rounding.
+#include "row_math.h"
 #include "tla_internal.h"
 
 namespace tla {
@@ -266,15 +267,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(float* out, cons
     __shared__ float s_red[kThreads / 64];
     const float* xr = x + static_cast<long long>(blockIdx.x) * size;
     float* o = out + static_cast<long long>(blockIdx.x) * size;
-    float ss = 0.f;
-    for (int c = threadIdx.x; c < size; c += kThreads) ss += xr[c] * xr[c];
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < kThreads / 64; ++i) ss += s_red[i];
+    const float ss = row_sum_squares<kThreads>(xr, size, s_red);
     const float rms = 1.0f / sqrtf(ss / static_cast<float>(size) + eps);
     for (int c = threadIdx.x; c < size; c += kThreads) o[c] = xr[c] * rms * w[c];
 }

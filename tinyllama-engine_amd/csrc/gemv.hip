@@ -25,6 +25,7 @@
 #include <algorithm>
 
 #include "rope_math.h"
+#include "row_math.h"
 #include "tla_internal.h"
 
 namespace tla {
@@ -490,7 +491,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
 {
     static_assert(!kMulti || kRows == 1, "several vectors take one row per lane group");
     constexpr bool kZeroOffsets = kType == kQ8_0 || kType == kQ4_0 || kType == kQ6_K;
-    extern __shared__ float xs_all[];  // [n_vec][xs_floats(cols)] padded, then [n_vec][cols / 16] run sums
+    extern __shared__ __align__(16) float xs_all[];  // [n_vec][xs_floats(cols)] padded, then [n_vec][cols / 16] run sums
     __shared__ float s_red[kThreads / 64];
 
     constexpr int kRowsPerWave = 64 / kLanesPerRow;
@@ -506,19 +507,23 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
 
     // x for one vector of up to kXRegs x kThreads columns is requested
     // before the weights (loads complete in order, so anything requested
-    // after the weights could only be used once they have all arrived).
+    // after the weights could only be used once they have all arrived), in
+    // 16-byte pieces: thread t holds columns 4(t + i kThreads) .. +3.
     // (x for a row of kLanesPerRow x kSteps units, at most)
     constexpr int kXRegs = kLanesPerRow * kSteps * kUnit / kThreads;
-    const bool x_early = !kMulti && p.cols <= kXRegs * kThreads && !(p.norm_w && p.x2);
-    float xr[kXRegs], nr[kXRegs];
+    constexpr int kX4 = (kXRegs + 3) / 4;
+    const float* const nw = p.norm_w ? p.norm_w : p.x2 ? p.x2 : p.x;
+    const bool x_early = !kMulti && p.cols <= kXRegs * kThreads && !(p.norm_w && p.x2) &&
+                         aligned16(p.x) && aligned16(nw);
+    const int cols4 = p.cols / 4;
+    float4 xr[kX4], nr[kX4];
     if (x_early) {
-        const float* nw = p.norm_w ? p.norm_w : p.x2 ? p.x2 : p.x;
 #pragma unroll
-        for (int i = 0; i < kXRegs; ++i) {
-            const int c = threadIdx.x + i * kThreads;
-            const int cc = c < p.cols ? c : 0;
-            xr[i] = p.x[cc];
-            nr[i] = nw[cc];
+        for (int i = 0; i < kX4; ++i) {
+            const int c4 = threadIdx.x + i * kThreads;
+            const int cc = c4 < cols4 ? 4 * c4 : 0;
+            xr[i] = ldg4(p.x + cc);
+            nr[i] = ldg4(nw + cc);
         }
     }
 
@@ -536,21 +541,49 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
     // Stage x in LDS (SwiGLU'd when asked), then rmsnorm's scaling in place
     // (each thread rescales the elements it wrote).
     const int xs_len = xs_floats(p.cols);
-    for (int v = 0; v < p.n_vec; ++v) {
+    float* const s16_all = xs_all + p.n_vec * xs_len;
+    const int nb16 = p.cols / 16;
+    if (x_early) {
+        // One vector, from registers.  rmsnorm's sum of squares and the sums
+        // of x over runs of 16 columns (block formats) come from the same
+        // registers, in the orders of row_math.h (the rmsnorm kernels' and
+        // the staging below's): the 4 threads of a run sit in consecutive
+        // lanes.
+        float4 t[kX4];
+        float ss = 0.f;
+#pragma unroll
+        for (int i = 0; i < kX4; ++i) {
+            t[i] = p.x2 ? make_float4(silu(xr[i].x) * nr[i].x, silu(xr[i].y) * nr[i].y,
+                                      silu(xr[i].z) * nr[i].z, silu(xr[i].w) * nr[i].w)
+                        : xr[i];
+            if (threadIdx.x + i * kThreads < cols4) ss += sum_sq4(t[i]);
+        }
+        if (p.norm_w) {
+            ss = block_sum<kThreads>(ss, s_red);
+            const float rms = 1.0f / sqrtf(ss / static_cast<float>(p.cols) + p.eps);
+#pragma unroll
+            for (int i = 0; i < kX4; ++i)
+                t[i] = make_float4(xr[i].x * rms * nr[i].x, xr[i].y * rms * nr[i].y,
+                                   xr[i].z * rms * nr[i].z, xr[i].w * rms * nr[i].w);
+        }
+#pragma unroll
+        for (int i = 0; i < kX4; ++i) {
+            const int c4 = threadIdx.x + i * kThreads;
+            if (c4 < cols4) *reinterpret_cast<float4*>(xs_all + xpad(4 * c4)) = t[i];
+            if constexpr (kZeroOffsets) {
+                // cols4 is a multiple of 16, so the 4 lanes of a run agree on c4 < cols4
+                float r = sum4(t[i]);
+                r += __shfl_xor(r, 1);  // (r0 + r1) + (r2 + r3) in every lane of the run
+                r += __shfl_xor(r, 2);
+                if (c4 < cols4 && (c4 & 3) == 0) s16_all[c4 >> 2] = r;
+            }
+        }
+    }
+    for (int v = 0; v < (x_early ? 0 : p.n_vec); ++v) {
         const float* xv = p.x + v * p.x_stride;
         float* xs = xs_all + v * xs_len;
         float ss = 0.f;
-        if (x_early) {
-#pragma unroll
-            for (int i = 0; i < kXRegs; ++i) {
-                const int c = threadIdx.x + i * kThreads;
-                if (c < p.cols) {
-                    const float t = p.x2 ? silu(xr[i]) * nr[i] : xr[i];
-                    xs[xpad(c)] = t;
-                    ss += t * t;
-                }
-            }
-        } else {
+        {
             const float* x2v = p.x2 ? p.x2 + v * p.x_stride : nullptr;
             for (int c = threadIdx.x; c < p.cols; c += kThreads) {
                 const float t = x2v ? silu(xv[c]) * x2v[c] : xv[c];
@@ -568,30 +601,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
             for (int w = 0; w < kThreads / 64; ++w) ss += s_red[w];
             __syncthreads();  // s_red is reused by the next vector
             const float rms = 1.0f / sqrtf(ss / static_cast<float>(p.cols) + p.eps);
-            if (x_early) {
-#pragma unroll
-                for (int i = 0; i < kXRegs; ++i) {
-                    const int c = threadIdx.x + i * kThreads;
-                    if (c < p.cols) xs[xpad(c)] = xr[i] * rms * nr[i];
-                }
-            } else {
-                for (int c = threadIdx.x; c < p.cols; c += kThreads)
-                    xs[xpad(c)] = xs[xpad(c)] * rms * p.norm_w[c];
-            }
+            for (int c = threadIdx.x; c < p.cols; c += kThreads)
+                xs[xpad(c)] = xs[xpad(c)] * rms * p.norm_w[c];
         }
     }
     __syncthreads();
-    float* const s16_all = xs_all + p.n_vec * xs_len;
-    const int nb16 = p.cols / 16;
-    if constexpr (kZeroOffsets) {
-        // sums of x over each run of 16 columns
+    if (kZeroOffsets && !x_early) {
+        // sums of x over each run of 16 columns, pairwise as above (a run
+        // is contiguous in LDS: 16 divides the 64-column padding period)
         for (int i = threadIdx.x; i < p.n_vec * nb16; i += kThreads) {
             const int v = i / nb16, b = i - v * nb16;
-            const float* xb = xs_all + v * xs_len + xpad(16 * b);
-            float t = 0.f;
-#pragma unroll
-            for (int j = 0; j < 16; ++j) t += xb[j];
-            s16_all[i] = t;
+            const float4* xb = reinterpret_cast<const float4*>(xs_all + v * xs_len + xpad(16 * b));
+            s16_all[i] = (sum4(xb[0]) + sum4(xb[1])) + (sum4(xb[2]) + sum4(xb[3]));
         }
         __syncthreads();
     }
@@ -691,15 +712,7 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(float* out, const flo
                                                            const float* w, int size, float eps)
 {
     __shared__ float s_red[kThreads / 64];
-    float ss = 0.f;
-    for (int c = threadIdx.x; c < size; c += kThreads) ss += x[c] * x[c];
-#pragma unroll
-    for (int o = 32; o >= 1; o >>= 1) ss += __shfl_xor(ss, o);
-    if ((threadIdx.x & 63) == 0) s_red[threadIdx.x >> 6] = ss;
-    __syncthreads();
-    ss = 0.f;
-#pragma unroll
-    for (int i = 0; i < kThreads / 64; ++i) ss += s_red[i];
+    const float ss = row_sum_squares<kThreads>(x, size, s_red);
     const float rms = 1.0f / sqrtf(ss / static_cast<float>(size) + eps);
     for (int c = threadIdx.x; c < size; c += kThreads) out[c] = x[c] * rms * w[c];
 }
