@@ -231,7 +231,9 @@ int tla_ffn_swiglu(tla_engine* e, float* out_dev, const float* in_dev, float* hb
  * x += ffn_swiglu(rmsnorm(x, norm_w, eps)), in two launches (rmsnorm + gate
  * and up projections; SiLU, gating, down projection and the residual add).
  * x [n_seq][n_embd]; hb_dev scratch [n_seq][2][n_ff] receives the raw gate
- * and up projections. */
+ * and up projections, except for one sequence of Q8_0 / Q4_0 / Q6_K weights
+ * (n_embd <= 4096, n_ff even): then the gate half receives SiLU(gate) x up,
+ * formed in the first launch, and the up half is unspecified. */
 int tla_ffn_block(tla_engine* e, int n_seq, float* x_dev, const float* norm_w_dev, float eps,
                   const void* w_gate_dev, const void* w_up_dev, const void* w_down_dev, int n_ff,
                   int type, float* hb_dev);

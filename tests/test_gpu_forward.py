@@ -120,6 +120,34 @@ def test_ffn_block(O, W, engines, n_seq):
         assert err <= 4 * ORACLE_TOL
 
 
+@pytest.mark.parametrize("t", [Q.Q8_0, Q.Q4_0, Q.Q6_K, Q.F16])
+@pytest.mark.parametrize("n_head", [4, 48])
+def test_ffn_block_one_sequence_formats(O, W, engines, t, n_head):
+    """One sequence: block formats form SiLU(gate) x up in the gate/up
+    launch's epilogue (gate and up rows paired in one lane group), with rows
+    of 32 lanes (n_embd 256) and of 64 lanes (n_embd 3072); F16 keeps SwiGLU
+    in the down projection's prologue."""
+    eng = engines(1, 64, n_head, 2 if n_head == 4 else 4)
+    n_ff, n_embd = 1024, 64 * n_head
+    wg, wu = W.make_weights(t, n_ff, n_embd, salt=61), W.make_weights(t, n_ff, n_embd, salt=62)
+    wd = W.make_weights(t, n_embd, n_ff, salt=63)
+    rg = np.random.default_rng(n_head + t)
+    x = rg.standard_normal((1, n_embd)).astype(np.float32)
+    nw = rg.uniform(0.5, 1.5, n_embd).astype(np.float32)
+    with device_arrays() as track:
+        dg, du, dd = (track(eng.array(w)) for w in (wg, wu, wd))
+        dx, dn = track(eng.array(x)), track(eng.array(nw))
+        hb = track(eng.array((1, 2, n_ff)))
+        eng.ffn_block(1, dx.ptr, dn.ptr, 1e-5, dg.ptr, du.ptr, dd.ptr, n_ff, t, hb.ptr)
+        got = dx.download()
+    xn = O.rmsnorm(x[0], nw, 1e-5)
+    out, hbo, _ = O.ffn_swiglu(xn, wg, wu, wd, n_ff, n_embd, t)
+    scale = row_scale(wd, hbo, t, n_embd, n_ff) + np.abs(x[0])
+    err = float(np.max(np.abs(got[0] - (x[0] + out)) / scale))
+    log(f"  ffn_block type {t} n_embd {n_embd}: {err:.2e}")
+    assert err <= 4 * ORACLE_TOL
+
+
 def test_argmax(O, engines):
     eng = engines(1, 64)
     rg = np.random.default_rng(8)

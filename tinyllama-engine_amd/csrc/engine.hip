@@ -945,8 +945,10 @@ int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc,
         // x += Wo . att (src/forward.cpp:210-213)
         if (int rc = gemv1(e, L.type_o, L.wo, b.x, embd, embd, b.att, nullptr, nullptr, 0.f, 1)) return rc;
         // rmsnorm + gate and up projections, then SiLU x up, W_down and the
-        // residual in the down projection's prologue / epilogue
-        // (src/forward.cpp:215-228, src/ops.cpp:1535-1564)
+        // residual (src/forward.cpp:215-228, src/ops.cpp:1535-1564).  SiLU x
+        // up is the gate/up launch's epilogue where the format pairs rows
+        // (computed once), else the down projection's prologue.
+        const bool paired = gemv_can_pair(L.type_ffn, ff, embd);
         {
             GemvParams p{};
             p.seg[0] = {static_cast<const unsigned char*>(L.w_gate), b.hb, ff, ff};
@@ -960,9 +962,12 @@ int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc,
             p.x_stride = embd;
             p.norm_w = L.ffn_norm;
             p.eps = eps;
+            p.pair = paired ? 1 : 0;
             if (int rc = run_gemv(e, L.type_ffn, p)) return rc;
         }
-        if (int rc = gemv1(e, L.type_ffn, L.w_down, b.x, embd, ff, b.hb, b.hb2, nullptr, 0.f, 1)) return rc;
+        if (int rc = gemv1(e, L.type_ffn, L.w_down, b.x, embd, ff, b.hb, paired ? nullptr : b.hb2,
+                           nullptr, 0.f, 1))
+            return rc;
     }
     // final rmsnorm + classifier (src/forward.cpp:241-265)
     if (logits)
@@ -1214,7 +1219,9 @@ int tla_ffn_block(tla_engine* e, int n_seq, float* x_dev, const float* norm_w_de
     if (int rc = check_gemv(type, embd, chunk_up, w_up_dev)) return rc;
     if (int rc = check_gemv(type, n_ff, chunk_down, w_down_dev)) return rc;
     if (int rc = set_device(e)) return rc;
-    // hb_dev: [n_seq][2][n_ff], gate then up
+    // hb_dev: [n_seq][2][n_ff], gate then up; for one sequence in a format
+    // that pairs rows, the gate half receives SiLU(gate) x up directly.
+    const bool paired = n_seq == 1 && gemv_can_pair(type, n_ff, embd);
     for (int s0 = 0; s0 < n_seq; s0 += chunk_up) {
         const int nv = std::min(chunk_up, n_seq - s0);
         GemvParams p{};
@@ -1230,6 +1237,7 @@ int tla_ffn_block(tla_engine* e, int n_seq, float* x_dev, const float* norm_w_de
         p.x_stride = embd;
         p.norm_w = norm_w_dev;
         p.eps = eps;
+        p.pair = paired ? 1 : 0;
         if (int rc = run_gemv(e, type, p)) return rc;
     }
     for (int s0 = 0; s0 < n_seq; s0 += chunk_down) {
@@ -1243,7 +1251,7 @@ int tla_ffn_block(tla_engine* e, int n_seq, float* x_dev, const float* norm_w_de
         p.row_bytes = static_cast<int>(weight_row_bytes(type, n_ff));
         p.n_vec = nv;
         p.x = hb_dev + static_cast<long long>(s0) * 2 * n_ff;
-        p.x2 = p.x + n_ff;
+        p.x2 = paired ? nullptr : p.x + n_ff;
         p.x_stride = 2LL * n_ff;
         p.add = 1;
         if (int rc = run_gemv(e, type, p)) return rc;

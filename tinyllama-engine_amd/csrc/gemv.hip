@@ -503,7 +503,14 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
     const int n_waves = gridDim.x * (kThreads / 64);
     const int units = p.cols / kUnit;
     const int n_vec = kMulti ? p.n_vec : 1;
-    const int n_pass = (p.total_rows + kPassRows - 1) / kPassRows;
+    // Paired (SwiGLU) launches: a pass covers kRowsPerWave rows of the gate
+    // segment, and each lane group holds row r of the gate and row r of the
+    // up matrix (its kRows = 2 rows are seg[0].rows apart).
+    const bool pair = kRows == 2 && !kMulti && p.pair;
+    const int pass_rows = pair ? kRowsPerWave : kPassRows;
+    const int spacing = pair ? __builtin_amdgcn_readfirstlane(p.seg[0].rows) : kRowsPerWave;
+    const int n_pass = pair ? (p.seg[0].rows + kRowsPerWave - 1) / kRowsPerWave
+                            : (p.total_rows + kPassRows - 1) / kPassRows;
 
     // x for one vector of up to kXRegs x kThreads columns is requested
     // before the weights (loads complete in order, so anything requested
@@ -535,7 +542,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
         ga.locate(p, sr, ps * kPassRows + sub, kRowsPerWave);
         ga.load_head(units, kLanesPerRow, l);
     } else {
-        ga.request(p, sr, ps * kPassRows + sub, kRowsPerWave, units, kLanesPerRow, l);
+        ga.request(p, sr, ps * pass_rows + sub, spacing, units, kLanesPerRow, l);
     }
 
     // Stage x in LDS (SwiGLU'd when asked), then rmsnorm's scaling in place
@@ -665,6 +672,16 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
             for (int b = 0; b < kSteps; ++b)
                 if (b * kLanesPerRow < units) step(b, b * kLanesPerRow, min(kLanesPerRow, units - b * kLanesPerRow));
         }
+        if constexpr (kRows == 2 && !kMulti) {
+            if (pair) {
+                // silu(gate) x up with the reference's operation order
+                // (src/ops.cpp:1107-1148), as the batched SwiGLU kernel
+                const float tg = row_sum<kLanesPerRow>(acc[0][0]);
+                const float tu = row_sum<kLanesPerRow>(acc[1][0]);
+                if (g.valid[0] && l == kLanesPerRow - 1) *g.out[0] = silu(tg) * tu;
+                return;
+            }
+        }
         // The group's last lane stores; the old values were read with the
         // pass's request (one vector) or here (several).
 #pragma unroll
@@ -696,12 +713,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
     // pass's request goes out before the current pass is computed.  Past the
     // last pass the request reads row 0 again (locate maps it there).
     while (ps < n_pass) {
-        gb.request(p, sr, (ps + n_waves) * kPassRows + sub, kRowsPerWave, units, kLanesPerRow, l);
+        gb.request(p, sr, (ps + n_waves) * pass_rows + sub, spacing, units, kLanesPerRow, l);
         __builtin_amdgcn_sched_barrier(0);  // the request goes out before the compute
         run_pass(ga);
         ps += n_waves;
         if (ps >= n_pass) break;
-        ga.request(p, sr, (ps + n_waves) * kPassRows + sub, kRowsPerWave, units, kLanesPerRow, l);
+        ga.request(p, sr, (ps + n_waves) * pass_rows + sub, spacing, units, kLanesPerRow, l);
         __builtin_amdgcn_sched_barrier(0);
         run_pass(gb);
         ps += n_waves;
@@ -887,6 +904,12 @@ template <int kType>
 hipError_t launch_typed(const GemvParams& p, hipStream_t s)
 {
     const int units = p.cols / kUnit;
+    if (p.pair) {  // gemv_can_pair: one vector, a two-row format, rows of <= 64 units
+        if constexpr (Unit<kType>::kRows == 2)
+            return units <= 32 ? launch_shaped<kType, 32, 2, 1, false>(p, s)
+                               : launch_shaped<kType, 64, 2, 1, false>(p, s);
+        return hipErrorInvalidValue;
+    }
     // several vectors, or rows longer than two steps of 64 lanes: one row per
     // lane group, steps beyond the first loaded one after another
     if (p.n_vec > 1 || units > 128)
@@ -916,6 +939,13 @@ long long weight_row_bytes(int type, int cols)
     case kQ6_K: return 210LL * (cols / 256);
     default: return 0;
     }
+}
+
+bool gemv_can_pair(int type, int rows, int cols)
+{
+    const int units = cols / kUnit;
+    const bool two_rows = type == kQ8_0 || type == kQ4_0 || type == kQ6_K;
+    return two_rows && units <= 64 && rows % (units <= 32 ? 2 : 1) == 0;
 }
 
 hipError_t launch_gemv(int type, const GemvParams& p, hipStream_t s)

@@ -114,7 +114,13 @@ struct GemvParams {
     const float* norm_w;     // non-null: x is (then) replaced by rmsnorm(x, norm_w, eps)
     float eps;
     int add;                 // 1: out += W.x (residual), 0: out = W.x
+    int pair;                // 1: segments 0 and 1 are the gate and up matrices (equal rows,
+                             // one vector); seg[0].out[r] = silu(gate_r . x) * (up_r . x),
+                             // the reference's SwiGLU; seg[1].out is read, not written
 };
+
+// Whether launch_gemv can pair gate and up rows (pair = 1) for this shape.
+bool gemv_can_pair(int type, int rows, int cols);
 
 long long weight_row_bytes(int type, int cols);  // 0 if the type is unknown
 hipError_t launch_gemv(int type, const GemvParams& p, hipStream_t s);
