@@ -53,7 +53,12 @@ enum tla_flags {
     TLA_ROTATE = 1,
     /* tla_generate_greedy: run the prompt through the model as one batch
      * (tla_prefill_forward) instead of token by token. */
-    TLA_BATCH_PROMPT = 2
+    TLA_BATCH_PROMPT = 2,
+    /* tla_decode: the k and v rows at each token's position are already in
+     * the cache (as the step's projection wrote them, rotated); only the
+     * attention runs, and k_dev / v_dev are not read (may be NULL).  With
+     * TLA_ROTATE, q is still rotated in the kernel. */
+    TLA_KV_IN_CACHE = 4
 };
 
 /* Shape fields of llama_config_t (src/gguf.h:139-168) that the path uses.

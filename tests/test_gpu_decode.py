@@ -287,3 +287,33 @@ def test_balanced_ranges_across_units(O, W, engines, split):
     pos = [200, 5, 1023, 30, 16, 511, 100, 63]
     case = W.make_decode(19, 8, 5, 1024, pos, salt=split)
     check_decode(O, engines(5, 1024), case, split=split, plan=2)
+
+
+@pytest.mark.parametrize("plan", PLANS)
+def test_decode_kv_in_cache_equals_append_path(O, W, engines, tla, plan):
+    """TLA_KV_IN_CACHE (the step's projection has already written the
+    rotated k and v rows at pos, and rotated q): attention alone, reading row
+    pos from the cache, gives bit for bit what the appending path gives."""
+    case = W.make_decode(23, 3, 4, 1024, [0, 300, 1023], salt=3)
+    eng = engines(4, 1024)
+    want, kc_after, vc_after = gpu_decode(eng, case, rotate=True, keep_cache=True, plan=plan)
+    s = O.Shape(n_ctx=1024)
+    q_rot = np.empty_like(case.q)
+    for i in range(case.n_seq):
+        for layer in range(case.n_layers):
+            q_rot[i, layer], _ = O.rope(case.q[i, layer], case.k[i, layer], int(case.pos[i]), s)
+    eng.set_option(tla.OPT_DECODE_PLAN, plan)
+    with device_arrays() as track:
+        kc, vc = eng.kv_cache(case.n_seq)
+        track(kc), track(vc)
+        kc.upload(kc_after)
+        vc.upload(vc_after)
+        q = track(eng.array(q_rot))
+        out = track(eng.array(case.q.shape))
+        stride = case.n_layers * case.n_ctx * eng.cfg.kv_dim
+        eng.decode(case.pos, 0, case.n_layers, out.ptr, q.ptr, 0, 0, kc.ptr, vc.ptr, stride,
+                   rotate=False, kv_in_cache=True)
+        got = out.download()
+        assert np.array_equal(bits(kc.download()), bits(kc_after)), "cache changed"
+    eng.set_option(tla.OPT_DECODE_PLAN, 0)
+    assert np.array_equal(bits(got), bits(want))

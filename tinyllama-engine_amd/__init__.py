@@ -43,6 +43,7 @@ TLA_ERR_DEVICE = 4
 TLA_ERR_OUT_OF_MEMORY = 5
 TLA_ROTATE = 1
 TLA_BATCH_PROMPT = 2
+TLA_KV_IN_CACHE = 4
 
 KERNEL_DECODE, KERNEL_PREFILL, KERNEL_APPEND, KERNEL_GEMV = range(4)
 # weight formats: the reference's ggml_type ids (src/gguf.h:23-32)
@@ -269,10 +270,12 @@ class Engine:
                "tla_rope_attention")
 
     def decode(self, pos, layer0: int, n_step_layers: int, out: int, q: int, k: int, v: int,
-               key_cache: int, value_cache: int, seq_stride: int = 0, rotate: bool = True):
+               key_cache: int, value_cache: int, seq_stride: int = 0, rotate: bool = True,
+               kv_in_cache: bool = False):
         pos = np.ascontiguousarray(pos, dtype=np.int32).reshape(-1)
+        flags = (TLA_ROTATE if rotate else 0) | (TLA_KV_IN_CACHE if kv_in_cache else 0)
         _check(lib().tla_decode(self.h, int(pos.size), pos.ctypes.data_as(C.POINTER(C.c_int)),
-                                layer0, n_step_layers, TLA_ROTATE if rotate else 0, out, q, k, v,
+                                layer0, n_step_layers, flags, out, q, k, v,
                                 key_cache, value_cache, seq_stride), "tla_decode")
 
     def prefill(self, pos0: int, n_tok: int, layer0: int, n_step_layers: int, out: int, q: int,

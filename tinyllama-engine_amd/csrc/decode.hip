@@ -300,7 +300,7 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
         const int end = min(pos + 1, (seg_end - u0) * kDecodeTile);  // exclusive
         const int n_tiles = seg_end - f;
         f = seg_end < u1 ? seg_end : min(f_hi, u0 + unit_span);  // past the padding
-        const bool appends = pos < end;  // this split holds `pos`: its last tile does
+        const bool appends = !p.in_cache && pos < end;  // this split holds `pos` and appends it
         const int special = appends ? n_tiles - 1 : n_tiles;
 
         const int hsub = lane & 15;  // q head within the group / K row within the tile

@@ -514,7 +514,10 @@ int check_gemv(int type, int cols, int n_vec, const void* w)
 
 int run_gemv(tla_engine* e, int type, const GemvParams& p)
 {
-    return launch(e, TLA_KERNEL_GEMV, "gemv", [&] { return launch_gemv(type, p, e->stream); });
+    if (p.rope) return launch(e, TLA_KERNEL_GEMV, "gemv", [&] { return launch_gemv(type, p, e->stream); });
+    GemvParams q = p;
+    q.rope = e->rope;  // read by every launch; rotates nothing with rope_rows = 0
+    return launch(e, TLA_KERNEL_GEMV, "gemv", [&] { return launch_gemv(type, q, e->stream); });
 }
 
 }  // namespace
@@ -634,9 +637,11 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
     if (n_seq < 1 || n_seq > kMaxSeqPerLaunch)
         return fail(TLA_ERR_INVALID_ARGUMENT, "n_seq %d not in [1, %d]", n_seq, kMaxSeqPerLaunch);
     if (!pos_host) return fail(TLA_ERR_INVALID_ARGUMENT, "pos is NULL");
-    if (!out_dev || !q_dev || !k_dev || !v_dev || !key_cache_dev || !value_cache_dev)
+    const bool in_cache = (flags & TLA_KV_IN_CACHE) != 0;
+    if (!out_dev || !q_dev || (!in_cache && (!k_dev || !v_dev)) || !key_cache_dev || !value_cache_dev)
         return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
-    if (flags & ~TLA_ROTATE) return fail(TLA_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
+    if (flags & ~(TLA_ROTATE | TLA_KV_IN_CACHE))
+        return fail(TLA_ERR_INVALID_ARGUMENT, "unknown flags 0x%x", flags);
     if (n_step_layers < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_step_layers %d < 1", n_step_layers);
     if (layer0 < 0 || layer0 + n_step_layers > c.n_layers)
         return fail(TLA_ERR_OUT_OF_RANGE, "layers [%d, %d) outside [0, %d)", layer0,
@@ -724,6 +729,7 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
     p.total_tiles = static_cast<int>(total_tiles);
     p.aligned = aligned;
     p.rotate = (flags & TLA_ROTATE) ? 1 : 0;
+    p.in_cache = in_cache ? 1 : 0;
     p.scale_log2 = scale_log2(e->head_dim);
 
     if (int rc = launch(e, TLA_KERNEL_DECODE, "decode",
@@ -917,12 +923,22 @@ int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc,
     for (int l = 0; l < e->cfg.n_layers; ++l) {
         const tla_layer_weights& L = m->layers[l];
         // rmsnorm + Q/K/V (src/forward.cpp:180-190): one launch when the
-        // three share a type
-        if (L.type_q == L.type_k && L.type_q == L.type_v) {
+        // three share a type.  Where the rows allow it, the launch's epilogue
+        // also applies RoPE to q and k and writes k and v straight into the
+        // cache row at pos (src/forward.cpp:192-196, src/ops.cpp:1370-1371),
+        // so the attention launch only attends.
+        const bool fused = L.type_q == L.type_k && L.type_q == L.type_v;
+        const bool rope_in_gemv = fused && gemv_can_rope(embd);
+        if (fused) {
+            const long long row = static_cast<long long>(l) * e->cfg.n_ctx * kv + static_cast<long long>(pos) * kv;
             GemvParams p{};
             p.seg[0] = {static_cast<const unsigned char*>(L.wq), b.q, embd, embd};
-            p.seg[1] = {static_cast<const unsigned char*>(L.wk), b.k, kv, kv};
-            p.seg[2] = {static_cast<const unsigned char*>(L.wv), b.v, kv, kv};
+            p.seg[1] = {static_cast<const unsigned char*>(L.wk), rope_in_gemv ? kc + row : b.k, kv, kv};
+            p.seg[2] = {static_cast<const unsigned char*>(L.wv), rope_in_gemv ? vc + row : b.v, kv, kv};
+            if (rope_in_gemv) {
+                p.rope = e->rope + static_cast<long long>(pos) * (e->head_dim / 2);
+                p.rope_rows = embd + kv;
+            }
             p.n_seg = 3;
             p.total_rows = embd + 2 * kv;
             p.cols = embd;
@@ -941,7 +957,9 @@ int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc,
             if (int rc = gemv1(e, L.type_v, L.wv, b.v, kv, embd, b.xb, nullptr, nullptr, 0.f, 0)) return rc;
         }
         // RoPE + append + attention (src/forward.cpp:192-208)
-        if (int rc = tla_decode(e, 1, &pos, l, 1, TLA_ROTATE, b.att, b.q, b.k, b.v, kc, vc, 0)) return rc;
+        if (int rc = tla_decode(e, 1, &pos, l, 1, rope_in_gemv ? TLA_KV_IN_CACHE : TLA_ROTATE, b.att, b.q,
+                                b.k, b.v, kc, vc, 0))
+            return rc;
         // x += Wo . att (src/forward.cpp:210-213)
         if (int rc = gemv1(e, L.type_o, L.wo, b.x, embd, embd, b.att, nullptr, nullptr, 0.f, 1)) return rc;
         // rmsnorm + gate and up projections, then SiLU x up, W_down and the

@@ -422,6 +422,7 @@ struct RowGroup {
     float* out[kRows];
     long long out_stride[kRows];
     bool valid[kRows];
+    int row[kRows];  // row index in the launch (segments in order)
 
     // Segment lookups select among the segment fields held in scalar
     // registers (SegRegs) instead of indexing the kernel arguments with a
@@ -432,6 +433,7 @@ struct RowGroup {
 #pragma unroll
         for (int k = 0; k < kRows; ++k) {
             const int r = r_first + spacing * k;
+            row[k] = r;
             valid[k] = r < p.total_rows;
             int rr = valid[k] ? r : 0;
             const bool in1 = sr.n_seg > 1 && rr >= sr.rows0;
@@ -462,17 +464,21 @@ struct RowGroup {
             load(b, u0, min(lanes, units - u0), l);
         }
     }
-    // One vector: the pass's first steps and the outputs' old values (for
-    // the residual add), requested together so that both arrive before
-    // anything requested later.
+    // One vector: the pass's first steps, the outputs' old values (for the
+    // residual add) and the rows' RoPE pair (cos, sin), requested together
+    // so that all arrive before anything requested later.
     float old[kRows];
+    float2 cs[kRows];
     __device__ void request(const GemvParams& p, const SegRegs& sr, int r_first, int spacing, int units,
                             int lanes, int l)
     {
         locate(p, sr, r_first, spacing);
         load_head(units, lanes, l);
 #pragma unroll
-        for (int k = 0; k < kRows; ++k) old[k] = *out[k];
+        for (int k = 0; k < kRows; ++k) {
+            old[k] = *out[k];
+            cs[k] = p.rope[(row[k] & 63) >> 1];
+        }
     }
 };
 
@@ -671,6 +677,21 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
 #pragma unroll
             for (int b = 0; b < kSteps; ++b)
                 if (b * kLanesPerRow < units) step(b, b * kLanesPerRow, min(kLanesPerRow, units - b * kLanesPerRow));
+        }
+        if constexpr (kRows == 1 && kLanesPerRow == 32 && !kMulti) {
+            if (p.rope_rows > 0) {
+                // RoPE of the q and k projections (src/ops.cpp:1252-1262):
+                // rows 2i and 2i+1 of a head are this wave's two lane groups
+                // (a pass is 2 rows from an even row), so the partner's sum
+                // is one lane swap away.  Rows past rope_rows (v) as computed.
+                const float t = row_sum<kLanesPerRow>(acc[0][0]);
+                const float u = __shfl_xor(t, 32);
+                const float2 c = g.cs[0];
+                float y = t;
+                if (g.row[0] < p.rope_rows) y = sub == 0 ? rot_lo(t, u, c.x, c.y) : rot_hi(u, t, c.x, c.y);
+                if (g.valid[0] && l == kLanesPerRow - 1) *g.out[0] = y;
+                return;
+            }
         }
         if constexpr (kRows == 2 && !kMulti) {
             if (pair) {
@@ -904,6 +925,7 @@ template <int kType>
 hipError_t launch_typed(const GemvParams& p, hipStream_t s)
 {
     const int units = p.cols / kUnit;
+    if (p.rope_rows > 0) return launch_shaped<kType, 32, 1, 1, false>(p, s);  // gemv_can_rope
     if (p.pair) {  // gemv_can_pair: one vector, a two-row format, rows of <= 64 units
         if constexpr (Unit<kType>::kRows == 2)
             return units <= 32 ? launch_shaped<kType, 32, 2, 1, false>(p, s)
@@ -939,6 +961,11 @@ long long weight_row_bytes(int type, int cols)
     case kQ6_K: return 210LL * (cols / 256);
     default: return 0;
     }
+}
+
+bool gemv_can_rope(int cols)
+{
+    return cols / kUnit <= 32;
 }
 
 bool gemv_can_pair(int type, int rows, int cols)

@@ -42,6 +42,7 @@ struct DecodeParams {
     int max_splits;    // split stride in `part`: most workgroups sharing one unit
     int total_tiles;   // tile_prefix[n_seq]
     int aligned;       // units padded to a multiple of wg_tiles in the flat space
+    int in_cache;      // k, v rows at pos already in the cache: no append
     int rotate;
     float scale_log2;  // log2(e) / sqrt(head_dim)
 };
@@ -117,10 +118,17 @@ struct GemvParams {
     int pair;                // 1: segments 0 and 1 are the gate and up matrices (equal rows,
                              // one vector); seg[0].out[r] = silu(gate_r . x) * (up_r . x),
                              // the reference's SwiGLU; seg[1].out is read, not written
+    const float2* rope;      // (cos, sin) of the token's position, head_dim / 2 = 32 pairs;
+                             // non-null in every launch (read whether or not used)
+    int rope_rows;           // rows [0, rope_rows) are rotated in pairs (2i, 2i+1) of each
+                             // 64-row head (RoPE of the q and k projections); 0: none
 };
 
 // Whether launch_gemv can pair gate and up rows (pair = 1) for this shape.
 bool gemv_can_pair(int type, int rows, int cols);
+// Whether launch_gemv can rotate row pairs in its epilogue (rope_rows > 0):
+// one vector, rows of at most 32 units (cols <= 2048).
+bool gemv_can_rope(int cols);
 
 long long weight_row_bytes(int type, int cols);  // 0 if the type is unknown
 hipError_t launch_gemv(int type, const GemvParams& p, hipStream_t s);
