@@ -252,6 +252,12 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     __shared__ HalfExchange s_mine;  // this split's partial, for the merge (!kSeg)
     __shared__ int2 s_pend[kMaxPending];  // (unit, nsplit) of deferred arrivals (kSeg)
     __shared__ int s_pend_last[kMaxPending];
+    // Every pointer argument is needed before the first memory request; the
+    // empty asm takes them in scalar registers here, so their loads go out
+    // with the other kernel arguments in one batch (else the compiler
+    // issues them after the first batch has arrived: one more round trip).
+    asm volatile("" ::"s"(p.q), "s"(p.k), "s"(p.v), "s"(p.out), "s"(p.kc), "s"(p.vc), "s"(p.rope),
+                 "s"(p.part));
     const int lane = threadIdx.x & 63;
     // wave index made explicitly scalar so cache bases stay in SGPRs
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -272,19 +278,39 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
     int f = f_lo;
     int n_pend = 0;  // segments whose arrival is deferred (kSeg)
     do {
-        int lo = 0, hi = p.n_seq - 1;  // rank: last with tile_prefix <= f
-        while (lo < hi) {
-            const int mid = (lo + hi + 1) >> 1;
-            if (b.tile_prefix[mid] <= f) lo = mid; else hi = mid - 1;
+        // The rank holding flat tile f: the last with tile_prefix <= f.  Up
+        // to 8 sequences, an unrolled scan selecting among fields at fixed
+        // offsets, so every kernel-argument load goes out in the first batch
+        // (an index found by a search would cost a dependent round trip per
+        // step, microseconds per launch at small contexts).
+        int pos, seq, prefix;
+        if constexpr (kMaxSeq <= 8) {
+            pos = b.pos[0];
+            seq = b.seq_id[0];
+            prefix = b.tile_prefix[0];
+#pragma unroll
+            for (int r = 1; r < kMaxSeq; ++r) {
+                const bool take = r < p.n_seq && b.tile_prefix[r] <= f;
+                pos = take ? b.pos[r] : pos;
+                seq = take ? b.seq_id[r] : seq;
+                prefix = take ? b.tile_prefix[r] : prefix;
+            }
+        } else {
+            int lo = 0, hi = p.n_seq - 1;
+            while (lo < hi) {
+                const int mid = (lo + hi + 1) >> 1;
+                if (b.tile_prefix[mid] <= f) lo = mid; else hi = mid - 1;
+            }
+            pos = b.pos[lo];
+            seq = b.seq_id[lo];
+            prefix = b.tile_prefix[lo];
         }
-        const int pos = b.pos[lo];
-        const int seq = b.seq_id[lo];
         const int unit_tiles = pos / kDecodeTile + 1;
         // With `aligned`, each unit's space is padded to whole ranges.
         const int unit_span =
             p.aligned ? (unit_tiles + p.wg_tiles - 1) / p.wg_tiles * p.wg_tiles : unit_tiles;
-        const int lb = (f - b.tile_prefix[lo]) / unit_span;
-        const int u0 = b.tile_prefix[lo] + lb * unit_span;  // the unit's first flat tile
+        const int lb = (f - prefix) / unit_span;
+        const int u0 = prefix + lb * unit_span;  // the unit's first flat tile
         const int u1 = u0 + unit_tiles;
         const int seg_end = min(f_hi, u1);
         const int split = blockIdx.x - u0 / p.wg_tiles;
