@@ -413,6 +413,12 @@ struct SegRegs {
     }
 };
 
+// Epilogue of a one-vector launch, a template parameter so that plain
+// launches carry none of the others' code: kPlain (y (+)= W.x), kPairEpi
+// (gate and up rows paired, SwiGLU written), kRopeEpi (q and k row pairs
+// rotated).
+constexpr int kPlain = 0, kPairEpi = 1, kRopeEpi = 2;
+
 // kSteps: unit steps of a row held at once (a row of up to kSteps x lanes
 // units is requested whole); rows with more units load the rest step by step.
 template <int kType, int kRows, int kSteps>
@@ -469,6 +475,7 @@ struct RowGroup {
     // so that all arrive before anything requested later.
     float old[kRows];
     float2 cs[kRows];
+    template <int kEpi>
     __device__ void request(const GemvParams& p, const SegRegs& sr, int r_first, int spacing, int units,
                             int lanes, int l)
     {
@@ -477,7 +484,7 @@ struct RowGroup {
 #pragma unroll
         for (int k = 0; k < kRows; ++k) {
             old[k] = *out[k];
-            cs[k] = p.rope[(row[k] & 63) >> 1];
+            if constexpr (kEpi == kRopeEpi) cs[k] = p.rope[(row[k] & 63) >> 1];
         }
     }
 };
@@ -492,10 +499,13 @@ struct RowGroup {
 // before it computes the current one (two register buffers, A and B).  The
 // grid holds as many workgroups as fit on the GPU at once, so waves keep
 // loads in flight from start to end.
-template <int kType, int kLanesPerRow, int kRows, int kSteps, bool kMulti>
+template <int kType, int kLanesPerRow, int kRows, int kSteps, bool kMulti, int kEpi>
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
 {
     static_assert(!kMulti || kRows == 1, "several vectors take one row per lane group");
+    static_assert(kEpi == kPlain || (!kMulti && kSteps == 1), "special epilogues: one vector");
+    static_assert(kEpi != kPairEpi || kRows == 2, "paired rows: two per lane group");
+    static_assert(kEpi != kRopeEpi || (kRows == 1 && kLanesPerRow == 32), "RoPE: pairs in one wave");
     constexpr bool kZeroOffsets = kType == kQ8_0 || kType == kQ4_0 || kType == kQ6_K;
     extern __shared__ __align__(16) float xs_all[];  // [n_vec][xs_floats(cols)] padded, then [n_vec][cols / 16] run sums
     __shared__ float s_red[kThreads / 64];
@@ -512,8 +522,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
     // Paired (SwiGLU) launches: a pass covers kRowsPerWave rows of the gate
     // segment, and each lane group holds row r of the gate and row r of the
     // up matrix (its kRows = 2 rows are seg[0].rows apart).
-    const bool pair = kRows == 2 && !kMulti && p.pair;
-    const int pass_rows = pair ? kRowsPerWave : kPassRows;
+    constexpr bool pair = kEpi == kPairEpi;
+    constexpr int pass_rows = pair ? kRowsPerWave : kPassRows;
     const int spacing = pair ? __builtin_amdgcn_readfirstlane(p.seg[0].rows) : kRowsPerWave;
     const int n_pass = pair ? (p.seg[0].rows + kRowsPerWave - 1) / kRowsPerWave
                             : (p.total_rows + kPassRows - 1) / kPassRows;
@@ -548,7 +558,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
         ga.locate(p, sr, ps * kPassRows + sub, kRowsPerWave);
         ga.load_head(units, kLanesPerRow, l);
     } else {
-        ga.request(p, sr, ps * pass_rows + sub, spacing, units, kLanesPerRow, l);
+        ga.template request<kEpi>(p, sr, ps * pass_rows + sub, spacing, units, kLanesPerRow, l);
     }
 
     // Stage x in LDS (SwiGLU'd when asked), then rmsnorm's scaling in place
@@ -678,8 +688,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
             for (int b = 0; b < kSteps; ++b)
                 if (b * kLanesPerRow < units) step(b, b * kLanesPerRow, min(kLanesPerRow, units - b * kLanesPerRow));
         }
-        if constexpr (kRows == 1 && kLanesPerRow == 32 && !kMulti) {
-            if (p.rope_rows > 0) {
+        if constexpr (kEpi == kRopeEpi) {
+            {
                 // RoPE of the q and k projections (src/ops.cpp:1252-1262):
                 // rows 2i and 2i+1 of a head are this wave's two lane groups
                 // (a pass is 2 rows from an even row), so the partner's sum
@@ -693,8 +703,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
                 return;
             }
         }
-        if constexpr (kRows == 2 && !kMulti) {
-            if (pair) {
+        if constexpr (kEpi == kPairEpi) {
+            {
                 // silu(gate) x up with the reference's operation order
                 // (src/ops.cpp:1107-1148), as the batched SwiGLU kernel
                 const float tg = row_sum<kLanesPerRow>(acc[0][0]);
@@ -734,12 +744,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
     // pass's request goes out before the current pass is computed.  Past the
     // last pass the request reads row 0 again (locate maps it there).
     while (ps < n_pass) {
-        gb.request(p, sr, (ps + n_waves) * pass_rows + sub, spacing, units, kLanesPerRow, l);
+        gb.template request<kEpi>(p, sr, (ps + n_waves) * pass_rows + sub, spacing, units, kLanesPerRow, l);
         __builtin_amdgcn_sched_barrier(0);  // the request goes out before the compute
         run_pass(ga);
         ps += n_waves;
         if (ps >= n_pass) break;
-        ga.request(p, sr, (ps + n_waves) * pass_rows + sub, spacing, units, kLanesPerRow, l);
+        ga.template request<kEpi>(p, sr, (ps + n_waves) * pass_rows + sub, spacing, units, kLanesPerRow, l);
         __builtin_amdgcn_sched_barrier(0);
         run_pass(gb);
         ps += n_waves;
@@ -905,13 +915,13 @@ int resident_blocks(Kernel kernel, size_t lds)
     return blocks;
 }
 
-template <int kType, int kLanes, int kRows, int kSteps, bool kMulti>
+template <int kType, int kLanes, int kRows, int kSteps, bool kMulti, int kEpi = kPlain>
 hipError_t launch_shaped(const GemvParams& p, hipStream_t s)
 {
     const size_t lds = static_cast<size_t>(p.n_vec) * (xs_floats(p.cols) + p.cols / 16) * sizeof(float);
     constexpr int kPassRowsPerBlock = (kThreads / 64) * (64 / kLanes) * kRows;
     const int needed = (p.total_rows + kPassRowsPerBlock - 1) / kPassRowsPerBlock;
-    const auto kernel = gemv_kernel<kType, kLanes, kRows, kSteps, kMulti>;
+    const auto kernel = gemv_kernel<kType, kLanes, kRows, kSteps, kMulti, kEpi>;
     const int blocks = std::min(needed, resident_blocks(kernel, lds));
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), lds, s, p);
     return hipGetLastError();
@@ -925,11 +935,11 @@ template <int kType>
 hipError_t launch_typed(const GemvParams& p, hipStream_t s)
 {
     const int units = p.cols / kUnit;
-    if (p.rope_rows > 0) return launch_shaped<kType, 32, 1, 1, false>(p, s);  // gemv_can_rope
+    if (p.rope_rows > 0) return launch_shaped<kType, 32, 1, 1, false, kRopeEpi>(p, s);  // gemv_can_rope
     if (p.pair) {  // gemv_can_pair: one vector, a two-row format, rows of <= 64 units
         if constexpr (Unit<kType>::kRows == 2)
-            return units <= 32 ? launch_shaped<kType, 32, 2, 1, false>(p, s)
-                               : launch_shaped<kType, 64, 2, 1, false>(p, s);
+            return units <= 32 ? launch_shaped<kType, 32, 2, 1, false, kPairEpi>(p, s)
+                               : launch_shaped<kType, 64, 2, 1, false, kPairEpi>(p, s);
         return hipErrorInvalidValue;
     }
     // several vectors, or rows longer than two steps of 64 lanes: one row per
