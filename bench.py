@@ -774,7 +774,7 @@ def main():
     if cpu:
         line["cpu_baseline"] = d["cpu_baseline"]
     if not args.no_prefill and args.workload == "decode_model":
-        p = run_prefill(max(5, args.steps // 2), max(2, args.warmup // 2), cpu)
+        p = run_prefill(args.steps, args.warmup, cpu)
         line["prefill"] = {k: p[k] for k in ("value", "unit", "ms_per_step", "roofline")}
         line["prefill"]["value"] = round(p["value"], 3)
         line["prefill"]["config"] = {"workload": "prefill", "n_tok": 512, "n_layers": 22}
