@@ -19,6 +19,9 @@ the 256 MB Infinity Cache, steps rotate over 5 copies of the whole cache
   cpu_baseline  the reference's own scalar attention() (oracle/_ref) -- or the
              C restatement when that is not built -- on the host's cores, over
              a bounded sample of the same workload
+  extra      the other decode configurations, measured the same way:
+             decode_long and decode_ragged (GB/s, with roofline) and
+             decode_single (latency, us); --no-extra skips them
 
 Other workloads (--workload): decode_long (16384 context, batch 8, 22 layers),
 decode_ragged (64 sequences, L in [256, 2048], 22 layers), prefill,
@@ -664,7 +667,9 @@ def main():
     ap.add_argument("--plan", default="auto", choices=["auto", "aligned", "balanced"],
                     help="decode work plan (default: the engine's choice)")
     ap.add_argument("--extra", action="store_true",
-                    help="also measure decode_long and decode_ragged")
+                    help="(default) also measure decode_long, decode_ragged and decode_single")
+    ap.add_argument("--no-extra", action="store_true",
+                    help="skip the other decode workloads in the default line")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -780,13 +785,20 @@ def main():
         line["prefill"]["config"] = {"workload": "prefill", "n_tok": 512, "n_layers": 22}
         if cpu:
             line["prefill"]["cpu_baseline"] = p["cpu_baseline"]
-    if args.extra:
+    if not args.no_extra and args.workload == "decode_model":
+        # the other decode configurations, measured the same way (no CPU
+        # baseline): long context x 8 and the ragged batch as HBM
+        # throughput, one layer at position 127 as latency
         line["extra"] = {}
         for wl in ("decode_long", "decode_ragged"):
             e = run_decode(wl, args.steps, args.warmup, False)
             line["extra"][wl] = {"value": round(e["value"], 1), "unit": "GB/s",
                                  "ms_per_step": round(e["ms_per_step"], 4),
                                  "roofline": e["roofline"]}
+        e = run_decode("decode_single", args.steps, args.warmup, False)
+        line["extra"]["decode_single"] = {"value": round(e["ms_per_step"] * 1e3, 2), "unit": "us",
+                                          "higher_is_better": False,
+                                          "note": "1 layer, position 127: latency-bound"}
     print(json.dumps(line))
 
 

@@ -255,6 +255,22 @@ def test_forward_tinyllama_shape(tla, O, W, engines):
     check_logits(got, want, "tinyllama-shaped q8_0 vs oracle")
 
 
+def test_forward_wide_embedding(tla, O, W, engines):
+    """n_embd 3072 (48 q heads on 4 kv heads, rows of 48 units): the Q/K/V
+    launch cannot rotate in its epilogue (rows of more than 32 units), so
+    RoPE and the append run in the attention launch; the gate/up launch
+    pairs rows with 64 lanes each.  Q4_0 weights, 2 layers, 3 tokens
+    against the oracle."""
+    spec = W.ModelSpec(2, 3072, 48, 4, 1024, 512, 64)
+    t = W.make_model(spec, W.W_Q4_0, salt=81)
+    toks = [1, 300, 77]
+    om = O.Model(spec, t)
+    want = np.stack([om.forward(tk, i) for i, tk in enumerate(toks)])
+    eng = spec_engine(engines, spec)
+    got = run_forward(tla, eng, spec, t, toks)
+    check_logits(got, want, "n_embd 3072 q4_0 vs oracle")
+
+
 def test_forward_errors(tla, W, engines):
     spec = W.ModelSpec(2, 256, 4, 2, 512, 384, 64)
     t = W.make_model(spec, W.W_Q8_0, salt=3)
