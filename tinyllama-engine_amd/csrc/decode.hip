@@ -32,20 +32,27 @@
 // loads cover 16 full 256 B head rows of K and of V.  No LDS staging is
 // needed.  Two tiles are in flight per wave: the next tile's loads are
 // issued before the current tile is computed, and q and the first two
-// tiles are requested together at the start.
+// tiles are requested together at the start.  Cache rows are read through
+// buffer resources that end at the segment's last row, so rows past it
+// read as zeros without a memory request.
 //
 // The split that contains `pos` also appends the new token: it writes the
-// (rotated) k row and the v row to the cache, and uses the same register
-// values for position `pos` in its own tile, so it never reads back the
-// row it has just written.
+// (rotated) k row and the v row to the cache and uses the same values,
+// kept in LDS, for position `pos` in its own tile (the value its tile load
+// got from the cache for that row, possibly older than the append, is
+// discarded).  With in_cache (TLA_KV_IN_CACHE) the caller's projection has
+// already written the row, and nothing is appended.
 //
 // Merge.  The two waves of a kv head combine in LDS.  With one split, the
 // result goes to `out` directly.  With several, each split writes its
 // unnormalised O and (running max, sum) to the workspace, waits for the
 // stores, then bumps the arrival counter of its (unit, kv head group); the
 // workgroup that arrives last merges all splits of the unit with
-// log-sum-exp weights, in split order (its own partial from LDS), and
-// resets the counter to zero for the next launch.  One launch per step.
+// log-sum-exp weights, in split order, and resets the counter to zero for
+// the next launch.  The aligned plan's merger takes its own partial from
+// LDS; a balanced-plan workgroup defers its arrivals to the end of its
+// range and reads every partial from the workspace.  Either way the sums
+// do not depend on which workgroup merges.  One launch per step.
 #include "rope_math.h"
 #include "tla_internal.h"
 
