@@ -9,7 +9,14 @@
 //     into LDS, so the input half of the attention block (rmsnorm, Wq, Wk,
 //     Wv; src/forward.cpp:180-190) is one launch with three segments;
 //   - residual epilogue: y += W.x, the output half (Wo then vec_add,
-//     src/forward.cpp:210-213).
+//     src/forward.cpp:210-213);
+//   - SwiGLU, either in the x staging of the down projection (silu(x) * x2)
+//     or, for one vector of a block format, in the epilogue of the gate/up
+//     launch, whose lane groups hold gate row r and up row r together
+//     (src/forward.cpp:215-228);
+//   - RoPE epilogue for the q and k rows (row pairs 2i, 2i+1 of a head are
+//     one wave's two lane groups), whose k and v outputs can be the cache
+//     row itself: RoPE + append (src/forward.cpp:192-196).
 //
 // Work decomposition: the weights of a row are cut into units of 64 (two
 // Q8_0/Q4_0 blocks, 128 B of F16, 256 B of F32, a quarter of a Q6_K
