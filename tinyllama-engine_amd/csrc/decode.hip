@@ -12,9 +12,13 @@
 // every workgroup streams the same number of tiles however long the units
 // are.  A range holds one or more segments (the part of one unit inside
 // it); the segments of a unit are its splits.  One workgroup covers a group
-// of 4 kv heads and holds 8 waves: two per kv head, which interleave a
-// segment's tiles (wave `sub` takes tiles sub, sub + 2, ...).  The
-// workgroup thus streams whole 1 KiB position rows of K and of V.  Each
+// of kv heads (2 in the aligned plan, 4 in the balanced one) with two waves
+// per kv head, which interleave a segment's tiles (wave `sub` takes tiles
+// sub, sub + 2, ...): 512 B or whole 1 KiB runs of each position row of K
+// and of V.  The aligned plan's 4-wave workgroups run two to a CU, which
+// measured faster than one 8-wave workgroup there (23.4 against 24.3 us
+// for 22 layers at 2048 positions); the balanced plan keeps 8 waves, whose
+// 1 KiB runs measured faster at 16384 positions (955 against 972 us).  Each
 // wave keeps the gqa (<= 16) q heads of its kv head in registers and, per
 // tile:
 //
@@ -61,9 +65,7 @@ namespace {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kKvWaves = kDecodeKvGroup;  // kv heads per workgroup
-constexpr int kSub = 2;                   // position halves per kv head
-constexpr int kWaves = kKvWaves * kSub;   // waves per workgroup
+constexpr int kSub = 2;  // position halves per kv head; waves per workgroup = kv heads * kSub
 // Deferred split arrivals per workgroup: only a range's first and last
 // segments can share their unit with another range (every segment between
 // them is a whole unit, merged in place).
@@ -154,10 +156,11 @@ struct Partial {
 // Combine the state of the wave one position-half above (in LDS) into this
 // wave's: the two halves of a kv head meet here.  Either side may be empty
 // (m = -inf, l = 0, acc = 0) but not both.
+template <int kKv>  // kv heads per workgroup
 struct HalfExchange {
-    floatx4 acc[kKvWaves][4][64];
-    float m[kKvWaves][16];
-    float l[kKvWaves][16];
+    floatx4 acc[kKv][4][64];
+    float m[kKv][16];
+    float l[kKv][16];
 };
 
 // Online merge of the partials of splits [s_lo, s_hi) of one unit for one
@@ -167,8 +170,9 @@ struct HalfExchange {
 // other from the workspace, so the order of the sums does not depend on
 // which workgroup merges.  Chunks of 8 splits whose loads are all issued
 // before any is used.
+template <int kKv>
 __device__ Partial merge_range(const DecodeParams& p, int unit, int s_lo, int s_hi, int own,
-                               const HalfExchange& mine, int slot, int kvh, int lane)
+                               const HalfExchange<kKv>& mine, int slot, int kvh, int lane)
 {
     constexpr int kChunk = 8;
     const int hsub = lane & 15, grp = lane >> 4;
@@ -226,7 +230,8 @@ __device__ Partial merge_range(const DecodeParams& p, int unit, int s_lo, int s_
     return r;
 }
 
-__device__ __forceinline__ void put_half(HalfExchange& x, int slot, int lane, const Partial& r)
+template <int kKv>
+__device__ __forceinline__ void put_half(HalfExchange<kKv>& x, int slot, int lane, const Partial& r)
 {
 #pragma unroll
     for (int i = 0; i < 4; ++i) x.acc[slot][i][lane] = r.acc[i];
@@ -236,7 +241,8 @@ __device__ __forceinline__ void put_half(HalfExchange& x, int slot, int lane, co
     }
 }
 
-__device__ __forceinline__ void add_half(const HalfExchange& x, int slot, int lane, Partial& r)
+template <int kKv>
+__device__ __forceinline__ void add_half(const HalfExchange<kKv>& x, int slot, int lane, Partial& r)
 {
     const float m1 = x.m[slot][lane & 15], l1 = x.l[slot][lane & 15];
     const float mm = fmaxf(r.m, m1);
@@ -250,13 +256,14 @@ __device__ __forceinline__ void add_half(const HalfExchange& x, int slot, int la
 // kSeg: balanced plan, more than one segment per workgroup possible; the
 // aligned plan's instantiation runs the segment body exactly once.
 template <int kMaxSeq, bool kSeg>
-__global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeParams p,
-                                                                   const DecodeSeqs<kMaxSeq> b)
+__global__ __launch_bounds__(64 * kSub * decode_kv_group(!kSeg)) void decode_split_kernel(
+    const DecodeParams p, const DecodeSeqs<kMaxSeq> b)
 {
+    constexpr int kKvWaves = decode_kv_group(!kSeg);  // kv heads per workgroup
     __shared__ int s_last;
     __shared__ float4 s_new[kKvWaves][32];  // appended k row (16 float4) | v row (16 float4)
-    __shared__ HalfExchange s_half;
-    __shared__ HalfExchange s_mine;  // this split's partial, for the merge (!kSeg)
+    __shared__ HalfExchange<kKvWaves> s_half;
+    __shared__ HalfExchange<kKvWaves> s_mine;  // this split's partial, for the merge (!kSeg)
     __shared__ int2 s_pend[kMaxPending];  // (unit, nsplit) of deferred arrivals (kSeg)
     __shared__ int s_pend_last[kMaxPending];
     // Every pointer argument is needed before the first memory request; the
@@ -632,8 +639,10 @@ __global__ __launch_bounds__(64 * kWaves) void decode_split_kernel(const DecodeP
 hipError_t launch_decode(const DecodeParams& p, const DecodeSeqs<kMaxSeqPerLaunch>& seqs,
                          hipStream_t s)
 {
-    dim3 grid((p.total_tiles + p.wg_tiles - 1) / p.wg_tiles, (p.n_head_kv + kKvWaves - 1) / kKvWaves);
-    const dim3 block(64 * kWaves);
+    const int kv_group = decode_kv_group(p.aligned);
+    const dim3 grid((p.total_tiles + p.wg_tiles - 1) / p.wg_tiles,
+                    (p.n_head_kv + kv_group - 1) / kv_group);
+    const dim3 block(64 * kSub * kv_group);
     if (p.n_seq <= 8) {
         DecodeSeqs<8> small{};
         for (int i = 0; i < p.n_seq; ++i) {

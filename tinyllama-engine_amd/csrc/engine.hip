@@ -214,7 +214,8 @@ float scale_log2(int head_dim)
     return static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
 }
 
-// Decode work plans.  One 8-wave workgroup fits a CU.
+// Decode work plans.  Either plan has 8 waves per CU: two 4-wave workgroups
+// (aligned, 2 kv heads each) or one 8-wave workgroup (balanced, 4 kv heads).
 //
 // Aligned: every unit (sequence, layer) is cut into splits of one length,
 // each a workgroup of its own.  The length gives about 15/16 of the CUs a
@@ -704,7 +705,8 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
         const size_t bytes = static_cast<size_t>(units) * max_splits * c.n_head_kv * 66 *
                              e->gqa * sizeof(float);
         if (int rc = ensure_ws(e, bytes)) return rc;
-        const long long groups = (c.n_head_kv + kDecodeKvGroup - 1) / kDecodeKvGroup;
+        const int kv_group = decode_kv_group(aligned);
+        const long long groups = (c.n_head_kv + kv_group - 1) / kv_group;
         if (int rc = ensure_counters(e, static_cast<size_t>(units * groups))) return rc;
         p.part = static_cast<float*>(e->ws);
         p.counters = e->counters;

@@ -15,7 +15,13 @@ constexpr int kPairs = kHeadDim / 2;
 constexpr int kMaxGqa = 16;         // q heads per kv head (MFMA N = 16)
 constexpr int kMaxSeqPerLaunch = 256;
 constexpr int kDecodeTile = 16;     // positions per decode MFMA tile
-constexpr int kDecodeKvGroup = 4;   // kv heads per decode workgroup (grid y = groups)
+// kv heads per decode workgroup (grid y = groups), by plan: the aligned
+// plan's single round runs two 4-wave workgroups per CU, the balanced plan
+// one 8-wave workgroup.
+constexpr int decode_kv_group(bool aligned)
+{
+    return aligned ? 2 : 4;
+}
 constexpr int kMaxRopePairs = 128;  // tla_rope: head_dim <= 256
 
 // ---- decode ------------------------------------------------------------
