@@ -110,19 +110,23 @@ def test_reference_testops_cases(tla, engines):
 
 
 @pytest.mark.parametrize("pos", [0, 1, 15, 16, 17, 63, 64, 100, 511, 512, 1000, 2047])
-@pytest.mark.parametrize("split", [0, 16, 64, 208])
+@pytest.mark.parametrize("split", [0, 16, 64, 208, 1024])
 @pytest.mark.parametrize("plan", PLANS)
 def test_decode_positions_and_splits(O, W, engines, pos, split, plan):
+    """Splits of 16..1024 positions: short aligned ranges run two kv heads
+    per workgroup, ranges over 256 positions four."""
     case = W.make_decode(11, 1, 2, 2048, pos, salt=pos)
     check_decode(O, engines(2, 2048), case, split=split, plan=plan)
 
 
 @pytest.mark.parametrize("n_head,n_head_kv", [(32, 8), (32, 2), (16, 1), (24, 6), (64, 4), (12, 12)])
-@pytest.mark.parametrize("split", [0, 64])
+@pytest.mark.parametrize("split", [0, 64, 640])
 @pytest.mark.parametrize("plan", PLANS)
 def test_decode_other_head_shapes(O, W, engines, n_head, n_head_kv, split, plan):
     """GQA ratios 1..16, more than one workgroup of kv heads per split (grid
-    y > 1) and groups with idle waves; several splits per sequence."""
+    y > 1) and groups with idle waves, for groups of 2 kv heads (short
+    aligned ranges) and of 4 (640-position ranges, the balanced plan);
+    several splits per sequence."""
     case = W.make_decode(13, 2, 2, 1024, [1023, 300], salt=n_head * 100 + n_head_kv,
                          n_head=n_head, n_head_kv=n_head_kv)
     check_decode(O, engines(2, 1024, n_head, n_head_kv), case, split=split, plan=plan)

@@ -12,13 +12,14 @@
 // every workgroup streams the same number of tiles however long the units
 // are.  A range holds one or more segments (the part of one unit inside
 // it); the segments of a unit are its splits.  One workgroup covers a group
-// of kv heads (2 in the aligned plan, 4 in the balanced one) with two waves
-// per kv head, which interleave a segment's tiles (wave `sub` takes tiles
-// sub, sub + 2, ...): 512 B or whole 1 KiB runs of each position row of K
-// and of V.  The aligned plan's 4-wave workgroups run two to a CU, which
-// measured faster than one 8-wave workgroup there (23.4 against 24.3 us
-// for 22 layers at 2048 positions); the balanced plan keeps 8 waves, whose
-// 1 KiB runs measured faster at 16384 positions (955 against 972 us).  Each
+// of 2 or 4 kv heads with two waves per kv head, which interleave a
+// segment's tiles (wave `sub` takes tiles sub, sub + 2, ...): 512 B or whole
+// 1 KiB runs of each position row of K and of V.  Two 4-wave workgroups per
+// CU measured faster where fixed costs weigh most (one layer at 128
+// positions: 8.2 against 10.6 us; 22 layers at 2048 positions: 23.4
+// against 24.3 us) and for many rounds of whole sequences;
+// one 8-wave workgroup with 1 KiB runs faster for long ranges (one
+// sequence at 16384: 133 against 138 us; 8 at 16384: 955 against 972).  Each
 // wave keeps the gqa (<= 16) q heads of its kv head in registers and, per
 // tile:
 //
@@ -255,11 +256,11 @@ __device__ __forceinline__ void add_half(const HalfExchange<kKv>& x, int slot, i
 
 // kSeg: balanced plan, more than one segment per workgroup possible; the
 // aligned plan's instantiation runs the segment body exactly once.
-template <int kMaxSeq, bool kSeg>
-__global__ __launch_bounds__(64 * kSub * decode_kv_group(!kSeg)) void decode_split_kernel(
+// kKvWaves: kv heads per workgroup (two waves each).
+template <int kMaxSeq, bool kSeg, int kKvWaves>
+__global__ __launch_bounds__(64 * kSub * kKvWaves) void decode_split_kernel(
     const DecodeParams p, const DecodeSeqs<kMaxSeq> b)
 {
-    constexpr int kKvWaves = decode_kv_group(!kSeg);  // kv heads per workgroup
     __shared__ int s_last;
     __shared__ float4 s_new[kKvWaves][32];  // appended k row (16 float4) | v row (16 float4)
     __shared__ HalfExchange<kKvWaves> s_half;
@@ -634,15 +635,33 @@ __global__ __launch_bounds__(64 * kSub * decode_kv_group(!kSeg)) void decode_spl
     } while (kSeg && f < f_hi);  // segments
 }
 
+// Balanced ranges always use the large group (one 8-wave workgroup).
+template <int kMaxSeq>
+void launch_shape(const DecodeParams& p, const DecodeSeqs<kMaxSeq>& b, dim3 grid, dim3 block,
+                  hipStream_t s)
+{
+    if (!p.aligned)
+        hipLaunchKernelGGL((decode_split_kernel<kMaxSeq, true, kDecodeKvGroupLarge>), grid, block,
+                           0, s, p, b);
+    else if (p.kv_group == kDecodeKvGroupSmall)
+        hipLaunchKernelGGL((decode_split_kernel<kMaxSeq, false, kDecodeKvGroupSmall>), grid, block,
+                           0, s, p, b);
+    else
+        hipLaunchKernelGGL((decode_split_kernel<kMaxSeq, false, kDecodeKvGroupLarge>), grid, block,
+                           0, s, p, b);
+}
+
 }  // namespace
 
 hipError_t launch_decode(const DecodeParams& p, const DecodeSeqs<kMaxSeqPerLaunch>& seqs,
                          hipStream_t s)
 {
-    const int kv_group = decode_kv_group(p.aligned);
+    if ((p.kv_group != kDecodeKvGroupSmall && p.kv_group != kDecodeKvGroupLarge) ||
+        (!p.aligned && p.kv_group != kDecodeKvGroupLarge))
+        return hipErrorInvalidValue;
     const dim3 grid((p.total_tiles + p.wg_tiles - 1) / p.wg_tiles,
-                    (p.n_head_kv + kv_group - 1) / kv_group);
-    const dim3 block(64 * kSub * kv_group);
+                    (p.n_head_kv + p.kv_group - 1) / p.kv_group);
+    const dim3 block(64 * kSub * p.kv_group);
     if (p.n_seq <= 8) {
         DecodeSeqs<8> small{};
         for (int i = 0; i < p.n_seq; ++i) {
@@ -650,14 +669,9 @@ hipError_t launch_decode(const DecodeParams& p, const DecodeSeqs<kMaxSeqPerLaunc
             small.seq_id[i] = seqs.seq_id[i];
         }
         for (int i = 0; i <= p.n_seq; ++i) small.tile_prefix[i] = seqs.tile_prefix[i];
-        if (p.aligned)
-            hipLaunchKernelGGL((decode_split_kernel<8, false>), grid, block, 0, s, p, small);
-        else
-            hipLaunchKernelGGL((decode_split_kernel<8, true>), grid, block, 0, s, p, small);
-    } else if (p.aligned) {
-        hipLaunchKernelGGL((decode_split_kernel<kMaxSeqPerLaunch, false>), grid, block, 0, s, p, seqs);
+        launch_shape(p, small, grid, block, s);
     } else {
-        hipLaunchKernelGGL((decode_split_kernel<kMaxSeqPerLaunch, true>), grid, block, 0, s, p, seqs);
+        launch_shape(p, seqs, grid, block, s);
     }
     return hipGetLastError();
 }

@@ -214,8 +214,8 @@ float scale_log2(int head_dim)
     return static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
 }
 
-// Decode work plans.  Either plan has 8 waves per CU: two 4-wave workgroups
-// (aligned, 2 kv heads each) or one 8-wave workgroup (balanced, 4 kv heads).
+// Decode work plans.  Either has 8 waves per CU: two 4-wave workgroups of
+// 2 kv heads each or one 8-wave workgroup of 4 kv heads (see kv_group).
 //
 // Aligned: every unit (sequence, layer) is cut into splits of one length,
 // each a workgroup of its own.  The length gives about 15/16 of the CUs a
@@ -699,13 +699,24 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
     seqs.tile_prefix[n_seq] = static_cast<int>(total_tiles);
     if (int rc = set_device(e)) return rc;
 
+    // Kv heads per workgroup: two 4-wave workgroups per CU where each
+    // launch's fixed costs weigh most (aligned ranges of at most 256
+    // positions) or the aligned plan runs several rounds; otherwise one
+    // 8-wave workgroup, which streams whole 1 KiB position rows.  Same-box
+    // A/B, 2 against 4 kv heads: 1 layer at 128 positions 8.2 / 10.6 us,
+    // 22 x 2048 23.4 / 24.2 us, 64 ragged sequences (several rounds)
+    // 599 / 607 us; 22 x 4096 (376-position ranges) 40.9 / 40.0 us,
+    // 22 x 16384 135.7 / 131.9 us.
+    const long long ranges = (total_tiles + wg - 1) / wg;
+    const int kv_group = aligned && (ranges > e->n_cu || wg * kDecodeTile <= 256)
+                             ? kDecodeKvGroupSmall
+                             : kDecodeKvGroupLarge;
     const long long units = static_cast<long long>(n_seq) * n_step_layers;
     if (max_splits > 1) {
         // per (unit, split, kv head): 64 output floats + max + sum for each real head
         const size_t bytes = static_cast<size_t>(units) * max_splits * c.n_head_kv * 66 *
                              e->gqa * sizeof(float);
         if (int rc = ensure_ws(e, bytes)) return rc;
-        const int kv_group = decode_kv_group(aligned);
         const long long groups = (c.n_head_kv + kv_group - 1) / kv_group;
         if (int rc = ensure_counters(e, static_cast<size_t>(units * groups))) return rc;
         p.part = static_cast<float*>(e->ws);
@@ -732,6 +743,7 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
     p.aligned = aligned;
     p.rotate = (flags & TLA_ROTATE) ? 1 : 0;
     p.in_cache = in_cache ? 1 : 0;
+    p.kv_group = kv_group;
     p.scale_log2 = scale_log2(e->head_dim);
 
     if (int rc = launch(e, TLA_KERNEL_DECODE, "decode",

@@ -15,13 +15,10 @@ constexpr int kPairs = kHeadDim / 2;
 constexpr int kMaxGqa = 16;         // q heads per kv head (MFMA N = 16)
 constexpr int kMaxSeqPerLaunch = 256;
 constexpr int kDecodeTile = 16;     // positions per decode MFMA tile
-// kv heads per decode workgroup (grid y = groups), by plan: the aligned
-// plan's single round runs two 4-wave workgroups per CU, the balanced plan
-// one 8-wave workgroup.
-constexpr int decode_kv_group(bool aligned)
-{
-    return aligned ? 2 : 4;
-}
+// kv heads per decode workgroup (grid y = groups): 2 (two 4-wave
+// workgroups per CU) or 4 (one 8-wave workgroup), chosen per launch.
+constexpr int kDecodeKvGroupSmall = 2;
+constexpr int kDecodeKvGroupLarge = 4;
 constexpr int kMaxRopePairs = 128;  // tla_rope: head_dim <= 256
 
 // ---- decode ------------------------------------------------------------
@@ -49,6 +46,7 @@ struct DecodeParams {
     int total_tiles;   // tile_prefix[n_seq]
     int aligned;       // units padded to a multiple of wg_tiles in the flat space
     int in_cache;      // k, v rows at pos already in the cache: no append
+    int kv_group;      // kv heads per workgroup: kDecodeKvGroupSmall / Large
     int rotate;
     float scale_log2;  // log2(e) / sqrt(head_dim)
 };
