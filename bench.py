@@ -26,7 +26,8 @@ the 256 MB Infinity Cache, steps rotate over 5 copies of the whole cache
 Other workloads (--workload): decode_long (16384 context, batch 8, 22 layers),
 decode_ragged (64 sequences, L in [256, 2048], 22 layers), prefill,
 decode_single (one layer, position 127: reported as latency), decode_sweep
-(batch 1, 22 layers, contexts 2K-16K), proj (the
+(batch 1, 22 layers, contexts 2K-16K), prefill_sweep (one prompt of 512 to
+4096 tokens, 22 layers), proj (the
 attention block's projections for a 22-layer decode step, and the GEMV kernel
 on a 32000 x 2048 matrix in every weight format), matmul (that GEMV alone in
 one format, --wtype), copy (the
@@ -294,7 +295,7 @@ def cpu_decode_baseline(case, n_ctx, workload, budget_s=10.0):
 
 # ----------------------------------------------------------------- prefill --
 
-def run_prefill(steps, warmup, cpu, n_layers=22, n_tok=512):
+def run_prefill(steps, warmup, cpu, n_layers=22, n_tok=512, label="prefill"):
     case = W.make_prefill(n_layers=n_layers, n_tok=n_tok)
     eng = tla.Engine(tla.Config.tinyllama(n_layers=n_layers, n_ctx=n_tok))
     kc, vc = eng.kv_cache(1)
@@ -318,7 +319,7 @@ def run_prefill(steps, warmup, cpu, n_layers=22, n_tok=512):
                         "traffic": profiled_traffic("prefill_attention_kernel", "prefill"),
                         "algorithmic_flops": flops,
                         "kernel": "prefill_attention_kernel", "launches": k_n}}
-    log(f"[bench] prefill: {ms * 1e3:.1f} us/step ({res['value']:.1f} TFLOP/s), attention kernel "
+    log(f"[bench] {label}: {ms * 1e3:.1f} us/step ({res['value']:.1f} TFLOP/s), attention kernel "
         f"{k_ms * 1e3:.1f} us -> {achieved:.1f} TFLOP/s ({achieved / FP32_MFMA_PEAK_TFLOPS:.1%}), "
         f"append {a_ms * 1e3:.1f} us")
     for a in (kc, vc, q, k, v, out):
@@ -327,6 +328,18 @@ def run_prefill(steps, warmup, cpu, n_layers=22, n_tok=512):
     if cpu:
         res["cpu_baseline"] = cpu_prefill_baseline(case, n_tok)
     return res
+
+
+def run_prefill_sweep(steps, warmup, lengths=(512, 1024, 2048, 4096), n_layers=22):
+    """Causal prefill of one prompt of each length over 22 layers (Q/K/V
+    N(0,1), seeded): the attention kernel's TFLOP/s as the prompt grows."""
+    out = []
+    for n_tok in lengths:
+        r = run_prefill(steps, warmup, False, n_layers, n_tok, label=f"prefill {n_tok} tokens")
+        out.append({"n_tok": n_tok, "us": round(r["prefill_kernel_ms"] * 1e3, 2),
+                    "flops": r["algorithmic_flops"], "TFLOP_s": r["roofline"]["achieved"],
+                    "frac": r["roofline"]["frac"]})
+    return out
 
 
 def cpu_prefill_baseline(case, n_tok, budget_s=8.0):
@@ -657,8 +670,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--workload", default="decode_model",
                     choices=["decode_model", "decode_long", "decode_ragged", "decode_single",
-                             "prefill", "proj", "matmul", "generate", "decode_sweep", "copy",
-                             "read"])
+                             "prefill", "proj", "matmul", "generate", "decode_sweep",
+                             "prefill_sweep", "copy", "read"])
     ap.add_argument("--wtype", default=None, choices=["f32", "f16", "q8_0", "q4_0", "q6_k"],
                     help="weight format of the matmul (default q8_0) or generate (q4_0) workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -694,6 +707,18 @@ def main():
                           "data": "synthetic",
                           "config": {"workload": "decode_sweep", "batch": 1, "n_layers": 22,
                                      "contexts": [x["ctx"] for x in r], "parallelism": "none"},
+                          "sweep": r}))
+        return
+    if args.workload == "prefill_sweep":
+        r = run_prefill_sweep(args.steps, args.warmup)
+        last = r[-1]
+        print(json.dumps({"metric": BASELINE_METRIC, "value": last["TFLOP_s"], "unit": "TFLOP/s",
+                          "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": last["us"] / 1e3, "higher_is_better": True,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+                          "data": "synthetic",
+                          "config": {"workload": "prefill_sweep", "batch": 1, "n_layers": 22,
+                                     "lengths": [x["n_tok"] for x in r], "parallelism": "none"},
                           "sweep": r}))
         return
     if args.workload == "generate":
