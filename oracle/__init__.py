@@ -1,7 +1,7 @@
 """ctypes loaders for the CPU oracle -- TEST INFRASTRUCTURE ONLY.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg import
-this package, as the checker or as the CPU baseline.  The HIP product
+this package: to check the HIP results, or as the CPU baseline.  The HIP product
 (tinyllama-engine_amd/) never imports or links anything here.
 
 Two libraries:

@@ -2,7 +2,7 @@
  * CPU oracle for the grouped-query attention path -- TEST INFRASTRUCTURE ONLY.
  *
  * Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
- * load this library, and only as the checker / the CPU baseline.  The HIP
+ * load this library, and only to check results / as the CPU baseline.  The HIP
  * product never links it and never falls back to it.
  *
  * It restates, in plain C, the reference engine's scalar ("NAIVE" backend)
