@@ -113,7 +113,7 @@ def test_reference_testops_cases(tla, engines):
 @pytest.mark.parametrize("split", [0, 16, 64, 208, 1024])
 @pytest.mark.parametrize("plan", PLANS)
 def test_decode_positions_and_splits(O, W, engines, pos, split, plan):
-    """Splits of 16..1024 positions: short aligned ranges run two kv heads
+    """Splits of 16..1024 positions: short aligned ranges run one kv head
     per workgroup, ranges over 256 positions four."""
     case = W.make_decode(11, 1, 2, 2048, pos, salt=pos)
     check_decode(O, engines(2, 2048), case, split=split, plan=plan)
@@ -124,7 +124,7 @@ def test_decode_positions_and_splits(O, W, engines, pos, split, plan):
 @pytest.mark.parametrize("plan", PLANS)
 def test_decode_other_head_shapes(O, W, engines, n_head, n_head_kv, split, plan):
     """GQA ratios 1..16, more than one workgroup of kv heads per split (grid
-    y > 1) and groups with idle waves, for groups of 2 kv heads (short
+    y > 1) and groups with idle waves, for groups of 1 kv head (short
     aligned ranges) and of 4 (640-position ranges, the balanced plan);
     several splits per sequence."""
     case = W.make_decode(13, 2, 2, 1024, [1023, 300], salt=n_head * 100 + n_head_kv,
@@ -145,7 +145,8 @@ def test_decode_model_full_size(O, W, engines):
 
 
 def test_decode_ragged_full_size(O, W, engines):
-    """64 sequences, context lengths uniform in [256, 2048], 22 layers."""
+    """64 sequences, context lengths uniform in [256, 2048], 22 layers
+    (several rounds of whole sequences: two kv heads per workgroup)."""
     case = W.decode_ragged(n_seq=64, n_layers=22, n_ctx=2048)
     check_decode(O, engines(22, 2048), case)
 

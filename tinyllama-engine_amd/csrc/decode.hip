@@ -12,12 +12,13 @@
 // every workgroup streams the same number of tiles however long the units
 // are.  A range holds one or more segments (the part of one unit inside
 // it); the segments of a unit are its splits.  One workgroup covers a group
-// of 2 or 4 kv heads with two waves per kv head, which interleave a
-// segment's tiles (wave `sub` takes tiles sub, sub + 2, ...): 512 B or whole
-// 1 KiB runs of each position row of K and of V.  Two 4-wave workgroups per
-// CU measured faster where fixed costs weigh most (one layer at 128
-// positions: 8.2 against 10.6 us; 22 layers at 2048 positions: 23.4
-// against 24.3 us) and for many rounds of whole sequences;
+// of 1, 2 or 4 kv heads with two waves per kv head, which interleave a
+// segment's tiles (wave `sub` takes tiles sub, sub + 2, ...): 256 B, 512 B
+// or whole 1 KiB runs of each position row of K and of V.  Smaller
+// workgroups measured faster where fixed costs weigh most (one layer at 128
+// positions: 7.3 / 8.2 / 10.6 us with 1 / 2 / 4 kv heads per workgroup; 22
+// layers at 2048 positions: 23.05 / 23.4 / 24.3 us), 2 kv heads for many
+// rounds of whole sequences (600 against 626 us with 1);
 // one 8-wave workgroup with 1 KiB runs faster for long ranges (one
 // sequence at 16384: 133 against 138 us; 8 at 16384: 955 against 972).  Each
 // wave keeps the gqa (<= 16) q heads of its kv head in registers and, per
@@ -646,6 +647,9 @@ void launch_shape(const DecodeParams& p, const DecodeSeqs<kMaxSeq>& b, dim3 grid
     else if (p.kv_group == kDecodeKvGroupSmall)
         hipLaunchKernelGGL((decode_split_kernel<kMaxSeq, false, kDecodeKvGroupSmall>), grid, block,
                            0, s, p, b);
+    else if (p.kv_group == kDecodeKvGroupMid)
+        hipLaunchKernelGGL((decode_split_kernel<kMaxSeq, false, kDecodeKvGroupMid>), grid, block,
+                           0, s, p, b);
     else
         hipLaunchKernelGGL((decode_split_kernel<kMaxSeq, false, kDecodeKvGroupLarge>), grid, block,
                            0, s, p, b);
@@ -656,7 +660,8 @@ void launch_shape(const DecodeParams& p, const DecodeSeqs<kMaxSeq>& b, dim3 grid
 hipError_t launch_decode(const DecodeParams& p, const DecodeSeqs<kMaxSeqPerLaunch>& seqs,
                          hipStream_t s)
 {
-    if ((p.kv_group != kDecodeKvGroupSmall && p.kv_group != kDecodeKvGroupLarge) ||
+    if ((p.kv_group != kDecodeKvGroupSmall && p.kv_group != kDecodeKvGroupMid &&
+         p.kv_group != kDecodeKvGroupLarge) ||
         (!p.aligned && p.kv_group != kDecodeKvGroupLarge))
         return hipErrorInvalidValue;
     const dim3 grid((p.total_tiles + p.wg_tiles - 1) / p.wg_tiles,

@@ -214,8 +214,9 @@ float scale_log2(int head_dim)
     return static_cast<float>(1.4426950408889634 / std::sqrt(static_cast<double>(head_dim)));
 }
 
-// Decode work plans.  Either has 8 waves per CU: two 4-wave workgroups of
-// 2 kv heads each or one 8-wave workgroup of 4 kv heads (see kv_group).
+// Decode work plans.  Either has 8 waves per CU: four 2-wave workgroups of
+// one kv head, two 4-wave workgroups of 2 or one 8-wave workgroup of 4 (see
+// kv_group).
 //
 // Aligned: every unit (sequence, layer) is cut into splits of one length,
 // each a workgroup of its own.  The length gives about 15/16 of the CUs a
@@ -699,18 +700,18 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
     seqs.tile_prefix[n_seq] = static_cast<int>(total_tiles);
     if (int rc = set_device(e)) return rc;
 
-    // Kv heads per workgroup: two 4-wave workgroups per CU where each
-    // launch's fixed costs weigh most (aligned ranges of at most 256
-    // positions) or the aligned plan runs several rounds; otherwise one
-    // 8-wave workgroup, which streams whole 1 KiB position rows.  Same-box
-    // A/B, 2 against 4 kv heads: 1 layer at 128 positions 8.2 / 10.6 us,
-    // 22 x 2048 23.4 / 24.2 us, 64 ragged sequences (several rounds)
-    // 599 / 607 us; 22 x 4096 (376-position ranges) 40.9 / 40.0 us,
-    // 22 x 16384 135.7 / 131.9 us.
+    // Kv heads per workgroup (two waves each).  Same-box A/B with 1 / 2 / 4:
+    // 1 layer at 128 positions 7.3 / 8.2 / 10.6 us and 22 x 2048 23.05 /
+    // 23.4 / 24.2 us (one round of ranges of at most 256 positions: 1);
+    // 64 ragged sequences, several rounds, 626 / 600 / 607 us (2); 22 x 4096
+    // (376-position ranges) 39.8 / 40.9 / 40.0 us and 22 x 16384 136 /
+    // 135.7 / 131.9 us (4, which streams whole 1 KiB position rows; the
+    // balanced plan always).
     const long long ranges = (total_tiles + wg - 1) / wg;
-    const int kv_group = aligned && (ranges > e->n_cu || wg * kDecodeTile <= 256)
-                             ? kDecodeKvGroupSmall
-                             : kDecodeKvGroupLarge;
+    const int kv_group = !aligned                    ? kDecodeKvGroupLarge
+                         : ranges > e->n_cu           ? kDecodeKvGroupMid
+                         : wg * kDecodeTile <= 256    ? kDecodeKvGroupSmall
+                                                      : kDecodeKvGroupLarge;
     const long long units = static_cast<long long>(n_seq) * n_step_layers;
     if (max_splits > 1) {
         // per (unit, split, kv head): 64 output floats + max + sum for each real head

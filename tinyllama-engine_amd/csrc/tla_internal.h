@@ -15,9 +15,11 @@ constexpr int kPairs = kHeadDim / 2;
 constexpr int kMaxGqa = 16;         // q heads per kv head (MFMA N = 16)
 constexpr int kMaxSeqPerLaunch = 256;
 constexpr int kDecodeTile = 16;     // positions per decode MFMA tile
-// kv heads per decode workgroup (grid y = groups): 2 (two 4-wave
-// workgroups per CU) or 4 (one 8-wave workgroup), chosen per launch.
-constexpr int kDecodeKvGroupSmall = 2;
+// kv heads per decode workgroup (grid y = groups), two waves each, chosen
+// per launch: 1 (2-wave workgroups, four per CU), 2 (two 4-wave workgroups
+// per CU) or 4 (one 8-wave workgroup).
+constexpr int kDecodeKvGroupSmall = 1;
+constexpr int kDecodeKvGroupMid = 2;
 constexpr int kDecodeKvGroupLarge = 4;
 constexpr int kMaxRopePairs = 128;  // tla_rope: head_dim <= 256
 
