@@ -322,3 +322,32 @@ def test_decode_kv_in_cache_equals_append_path(O, W, engines, tla, plan):
         assert np.array_equal(bits(kc.download()), bits(kc_after)), "cache changed"
     eng.set_option(tla.OPT_DECODE_PLAN, 0)
     assert np.array_equal(bits(got), bits(want))
+
+
+@pytest.mark.parametrize("n_seq,n_layers,n_ctx,pos,split", [
+    (1, 22, 2048, [2047], 0),                 # one round of 192-position ranges
+    (5, 2, 1024, [3, 1023, 400, 16, 777], 64),  # ragged, several splits per unit
+    (3, 3, 1024, [1023, 511, 800], 1024),     # whole units, no merge
+])
+def test_decode_group_does_not_change_results(O, W, engines, tla, n_seq, n_layers, n_ctx, pos,
+                                              split):
+    """Aligned launches with 1, 2 and 4 kv heads per workgroup give the same
+    bits: each kv head's partials and their merge order do not depend on
+    which other heads share its workgroup.  An unknown group is an error."""
+    case = W.make_decode(29, n_seq, n_layers, n_ctx, pos, salt=split)
+    eng = engines(n_layers, n_ctx)
+    outs = []
+    try:
+        for group in (1, 2, 4):
+            eng.set_option(tla.OPT_DECODE_GROUP, group)
+            got, gk, gv = gpu_decode(eng, case, split=split, plan=1)
+            outs.append((got, gk, gv))
+        with pytest.raises(tla.TlaError):
+            eng.set_option(tla.OPT_DECODE_GROUP, 3)
+    finally:
+        eng.set_option(tla.OPT_DECODE_GROUP, 0)
+    for got, gk, gv in outs[1:]:
+        assert np.array_equal(bits(got), bits(outs[0][0])), "outputs differ between groups"
+        assert np.array_equal(bits(gk), bits(outs[0][1])) and np.array_equal(bits(gv), bits(outs[0][2]))
+    ref, _, _ = oracle_decode(O, case)
+    assert max_err(outs[0][0], ref) <= DECODE_TOL

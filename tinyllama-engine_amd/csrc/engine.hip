@@ -101,6 +101,7 @@ struct tla_engine {
     int* argmax_slot = nullptr;
     long long opt_split = 0;
     int opt_plan = TLA_PLAN_AUTO;
+    int opt_group = 0;  // kv heads per aligned-plan workgroup, 0 = per launch
     int n_cu = 256;          // compute units: decode workgroups per launch
 
     bool prof = false;
@@ -709,6 +710,7 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
     // balanced plan always).
     const long long ranges = (total_tiles + wg - 1) / wg;
     const int kv_group = !aligned                    ? kDecodeKvGroupLarge
+                         : e->opt_group > 0           ? e->opt_group
                          : ranges > e->n_cu           ? kDecodeKvGroupMid
                          : wg * kDecodeTile <= 256    ? kDecodeKvGroupSmall
                                                       : kDecodeKvGroupLarge;
@@ -1475,6 +1477,12 @@ int tla_set_option(tla_engine* e, int option, long long value)
         if (value < TLA_PLAN_AUTO || value > TLA_PLAN_BALANCED)
             return fail(TLA_ERR_INVALID_ARGUMENT, "decode plan %lld not in [0, 2]", value);
         e->opt_plan = static_cast<int>(value);
+        return ok();
+    case TLA_OPT_DECODE_GROUP:
+        if (value != 0 && value != kDecodeKvGroupSmall && value != kDecodeKvGroupMid &&
+            value != kDecodeKvGroupLarge)
+            return fail(TLA_ERR_INVALID_ARGUMENT, "decode kv group %lld not 0, 1, 2 or 4", value);
+        e->opt_group = static_cast<int>(value);
         return ok();
     default:
         return fail(TLA_ERR_INVALID_ARGUMENT, "unknown option %d", option);
