@@ -82,6 +82,19 @@ def test_prefill_512_tokens_22_layers(O, W, engines):
     assert np.array_equal(bits(vc.reshape(-1)), bits(rvc))
 
 
+def test_prefill_2048_tokens(O, W, engines):
+    """A long prompt (2048 tokens, one of the measured prefill sizes) over 8
+    layers against the oracle loop: every query row sees up to 2048 keys."""
+    case = W.make_prefill(n_layers=8, n_tok=2048, salt=11)
+    out, kc, vc = gpu_prefill(engines(8, 2048), case)
+    ref, rkc, rvc = oracle_prefill(O, case, 8, 2048)
+    err = max_err(out, ref)
+    log(f"    max-abs {err:.3e}")
+    assert err <= PREFILL_TOL
+    assert np.array_equal(bits(kc.reshape(-1)), bits(rkc))
+    assert np.array_equal(bits(vc.reshape(-1)), bits(rvc))
+
+
 @pytest.mark.parametrize("pos0,n_tok", [(0, 1), (0, 31), (0, 33), (7, 100), (64, 64), (100, 5),
                                         (130, 126)])
 def test_prefill_odd_sizes_and_offsets(O, W, engines, pos0, n_tok):
