@@ -255,6 +255,20 @@ def cpu_threads():
     return max(1, min(16, os.cpu_count() or 1))
 
 
+def cpu_host():
+    """The host the CPU baseline ran on: its CPU model and hardware threads."""
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "hardware_threads": os.cpu_count()}
+
+
 def cpu_decode_baseline(case, n_ctx, workload, budget_s=10.0):
     """Time the reference's attention() (oracle/_ref) or the C restatement on
     the host over whole steps of the same workload for about budget_s."""
@@ -291,7 +305,8 @@ def cpu_decode_baseline(case, n_ctx, workload, budget_s=10.0):
             "sample": f"{nn} full steps of {workload} ({case.n_seq} seq x {case.n_layers} layers), "
                       f"median, {threads} threads; 1 thread: {n1} steps",
             "single_thread_value": round(algo / t1 / 1e9, 3),
-            "ms_per_step": round(tn * 1e3, 3), "single_thread_ms_per_step": round(t1 * 1e3, 3)}
+            "ms_per_step": round(tn * 1e3, 3), "single_thread_ms_per_step": round(t1 * 1e3, 3),
+            **cpu_host()}
 
 
 # ----------------------------------------------------------------- prefill --
@@ -380,7 +395,7 @@ def cpu_prefill_baseline(case, n_tok, budget_s=8.0):
     return {"value": round(case.algorithmic_flops / t / 1e12, 5), "unit": "TFLOP/s",
             "cores": threads, "kind": "port",
             "sample": f"{len(times)} full prefill steps (512 tokens x {case.n_layers} layers, one "
-                      f"layer per thread), median"}
+                      f"layer per thread), median", **cpu_host()}
 
 
 # -------------------------------------------------------------------- copy --
@@ -644,7 +659,8 @@ def cpu_generate_baseline(spec, tensors, prompt, wname, n_prompt=8, n_decode=8):
     return {"value": round(1e3 / ms_n, 3), "unit": "tok/s", "cores": threads, "kind": "reference",
             "sample": f"reference forward(), {n_prompt} prompt + {n_decode} decode tokens, "
                       f"{threads} threads; 1 thread: 4 decode tokens",
-            "ms_per_token": round(ms_n, 2), "single_thread_ms_per_token": round(ms_1, 2)}
+            "ms_per_token": round(ms_n, 2), "single_thread_ms_per_token": round(ms_1, 2),
+            **cpu_host()}
 
 
 def run_read(steps, warmup, nbytes=6 << 30):
