@@ -245,9 +245,11 @@ int tla_ffn_block(tla_engine* e, int n_seq, float* x_dev, const float* norm_w_de
 
 /* embed_token() src/forward.cpp:17-134: out = row `token` of the embedding
  * table [n_vocab][n_embd] (any of the five types), dequantised with the
- * reference's expressions (bit-exact). */
+ * reference's expressions (bit-exact).  A token outside [0, n_vocab) is
+ * TLA_ERR_OUT_OF_RANGE and launches nothing (the reference's embed_token()
+ * does not check; its table's row count comes from the GGUF tensor shape). */
 int tla_embed(tla_engine* e, float* out_dev, const void* table_dev, int token, int n_embd,
-              int type);
+              int n_vocab, int type);
 
 /* sample_argmax() src/ops.h:249: the first index of the largest logit. */
 int tla_argmax(tla_engine* e, const float* logits_dev, int n_vocab, int* token_host);

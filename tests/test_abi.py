@@ -35,7 +35,7 @@ def test_library_exports_every_declared_symbol(tla):
     missing = [n for n in sorted(declared_functions()) if not hasattr(lib, n)]
     assert not missing, missing
     assert set(tla.SIGNATURES) == declared_functions()
-    assert lib.tla_abi_version() == 1
+    assert lib.tla_abi_version() == 2
 
 
 def test_host_library_loads(tla):

@@ -33,7 +33,7 @@ def spec_engine(engines, spec):
 
 
 @pytest.mark.parametrize("t,name", TYPES)
-def test_embed_bit_exact(O, W, engines, t, name):
+def test_embed_bit_exact(tla, O, W, engines, t, name):
     eng = engines(1, 64)
     n_vocab, n_embd = 40, 2048
     raw = W.make_weights(t, n_vocab, n_embd, salt=9)
@@ -41,8 +41,12 @@ def test_embed_bit_exact(O, W, engines, t, name):
         tab = track(eng.array(raw))
         out = track(eng.array((n_embd,)))
         for tok in (0, 1, 23, 39):
-            eng.embed(out.ptr, tab.ptr, tok, n_embd, t)
+            eng.embed(out.ptr, tab.ptr, tok, n_embd, n_vocab, t)
             assert np.array_equal(bits(out.download()), bits(O.embed(raw, tok, n_embd, t))), (name, tok)
+        for tok in (-1, n_vocab):  # past either end of the table: an error, nothing launched
+            with pytest.raises(tla.TlaError) as e:
+                eng.embed(out.ptr, tab.ptr, tok, n_embd, n_vocab, t)
+            assert e.value.code == tla.TLA_ERR_OUT_OF_RANGE
 
 
 def test_silu_and_elementwise_mul(O, engines):
@@ -293,6 +297,21 @@ def test_forward_errors(tla, W, engines):
             with pytest.raises(tla.TlaError) as e:
                 eng.generate_greedy(dm, kc.ptr, vc.ptr, [1, 2], 64)  # 2 + 64 - 1 > n_ctx
             assert e.value.code == 2
+            # a NULL projection weight in any layer is rejected before any launch
+            for field in ("wq", "wo", "w_down"):
+                saved = getattr(dm.layers[1], field)
+                setattr(dm.layers[1], field, None)
+                try:
+                    for call in (lambda: eng.forward(dm, kc.ptr, vc.ptr, 0, 0, lg.ptr),
+                                 lambda: eng.prefill_forward(dm, kc.ptr, vc.ptr, [1, 2, 3], 0, lg.ptr),
+                                 lambda: eng.generate_greedy(dm, kc.ptr, vc.ptr, [1, 2], 4)):
+                        with pytest.raises(tla.TlaError) as e:
+                            call()
+                        assert e.value.code == tla.TLA_ERR_INVALID_ARGUMENT, (field, tla.last_error())
+                finally:
+                    setattr(dm.layers[1], field, saved)
+            eng.forward(dm, kc.ptr, vc.ptr, 0, 0, lg.ptr)  # restored: runs
+            eng.synchronize()
     finally:
         dm.free()
 

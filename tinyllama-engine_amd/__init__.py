@@ -125,7 +125,7 @@ SIGNATURES = {
                                  C.c_int]),
     "tla_ffn_block": (C.c_int, [_vp, C.c_int, _vp, _vp, C.c_float, _vp, _vp, _vp, C.c_int,
                                 C.c_int, _vp]),
-    "tla_embed": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int]),
+    "tla_embed": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tla_argmax": (C.c_int, [_vp, _vp, C.c_int, C.POINTER(C.c_int)]),
     "tla_forward": (C.c_int, [_vp, C.POINTER(Model), _vp, _vp, C.c_int, C.c_int, _vp]),
     "tla_prefill_forward": (C.c_int, [_vp, C.POINTER(Model), _vp, _vp, C.POINTER(C.c_int), C.c_int,
@@ -321,8 +321,8 @@ class Engine:
         _check(lib().tla_ffn_block(self.h, n_seq, x, norm_w, eps, w_gate, w_up, w_down, n_ff, wtype,
                                    hb), "tla_ffn_block")
 
-    def embed(self, out: int, table: int, token: int, n_embd: int, wtype: int):
-        _check(lib().tla_embed(self.h, out, table, token, n_embd, wtype), "tla_embed")
+    def embed(self, out: int, table: int, token: int, n_embd: int, n_vocab: int, wtype: int):
+        _check(lib().tla_embed(self.h, out, table, token, n_embd, n_vocab, wtype), "tla_embed")
 
     def argmax(self, logits: int, n_vocab: int) -> int:
         t = C.c_int()

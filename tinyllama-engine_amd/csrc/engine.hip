@@ -173,6 +173,8 @@ int launch(tla_engine* e, int kernel_id, const char* what, Fn&& fn)
     return TLA_OK;
 }
 
+// Split partials for a decode launch (every word is written before it is
+// read within one launch, so no clearing is needed).
 int ensure_ws(tla_engine* e, size_t bytes)
 {
     if (bytes <= e->ws_bytes) return TLA_OK;
@@ -187,7 +189,8 @@ int ensure_ws(tla_engine* e, size_t bytes)
 }
 
 // Arrival counters for `units` (unit, kv head group) pairs.  Zeroed once
-// when (re)allocated; the decode kernel returns every counter it uses to zero.
+// when (re)allocated (by a kernel: no memset node); the decode kernel returns
+// every counter it uses to zero.
 int ensure_counters(tla_engine* e, size_t units)
 {
     if (units <= e->n_counters) return TLA_OK;
@@ -197,11 +200,12 @@ int ensure_counters(tla_engine* e, size_t units)
     e->n_counters = 0;
     const size_t n = std::max<size_t>(units, 1024);
     TLA_HIP(hipMalloc(&e->counters, n * sizeof(int)));
-    TLA_HIP(hipMemsetAsync(e->counters, 0, n * sizeof(int), e->stream));
+    TLA_HIP(launch_zero(e->counters, n * sizeof(int), e->stream));
     TLA_HIP(hipStreamSynchronize(e->stream));
     e->n_counters = n;
     return TLA_OK;
 }
+
 
 int check_engine(const tla_engine* e)
 {
@@ -266,7 +270,7 @@ const char* tla_last_error(void)
 
 int tla_abi_version(void)
 {
-    return 1;
+    return 2;
 }
 
 int tla_engine_create(const tla_config* cfg, int device, tla_engine** out)
@@ -498,9 +502,11 @@ int gemv_chunk(int n_seq, int cols)
     return std::max(1, std::min({n_seq, kGemvMaxVec, kGemvLdsBytes / gemv_lds_per_vec(cols)}));
 }
 
-// Shape and pointer checks shared by the matrix-vector entry points.
+// Shape and pointer checks shared by the matrix-vector entry points (and the
+// model check, so that a NULL weight of any layer is an error, not a launch).
 int check_gemv(int type, int cols, int n_vec, const void* w)
 {
+    if (!w) return fail(TLA_ERR_INVALID_ARGUMENT, "weight pointer is NULL");
     if (weight_row_bytes(type, cols) == 0 || (type != kQ6_K && cols % 32 != 0) ||
         (type == kQ6_K && cols % 256 != 0))
         return fail(TLA_ERR_INVALID_ARGUMENT, "weight type %d with %d columns", type, cols);
@@ -716,9 +722,8 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
                                                       : kDecodeKvGroupLarge;
     const long long units = static_cast<long long>(n_seq) * n_step_layers;
     if (max_splits > 1) {
-        // per (unit, split, kv head): 64 output floats + max + sum for each real head
-        const size_t bytes = static_cast<size_t>(units) * max_splits * c.n_head_kv * 66 *
-                             e->gqa * sizeof(float);
+        // per (unit, split, kv head): 64 output words + max + sum for each real head
+        const size_t bytes = decode_part_bytes(units, max_splits, c.n_head_kv, e->gqa);
         if (int rc = ensure_ws(e, bytes)) return rc;
         const long long groups = (c.n_head_kv + kv_group - 1) / kv_group;
         if (int rc = ensure_counters(e, static_cast<size_t>(units * groups))) return rc;
@@ -1294,11 +1299,14 @@ int tla_ffn_block(tla_engine* e, int n_seq, float* x_dev, const float* norm_w_de
     return ok();
 }
 
-int tla_embed(tla_engine* e, float* out_dev, const void* table_dev, int token, int n_embd, int type)
+int tla_embed(tla_engine* e, float* out_dev, const void* table_dev, int token, int n_embd,
+              int n_vocab, int type)
 {
     if (int rc = check_engine(e)) return rc;
     if (!out_dev || !table_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
-    if (token < 0) return fail(TLA_ERR_OUT_OF_RANGE, "token %d < 0", token);
+    if (n_vocab < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "n_vocab %d < 1", n_vocab);
+    if (token < 0 || token >= n_vocab)
+        return fail(TLA_ERR_OUT_OF_RANGE, "token %d outside [0, n_vocab=%d)", token, n_vocab);
     if (n_embd < 1 || weight_row_bytes(type, n_embd) == 0 || (type == kQ6_K ? n_embd % 256 : n_embd % 32))
         return fail(TLA_ERR_INVALID_ARGUMENT, "type %d with n_embd %d", type, n_embd);
     if (int rc = set_device(e)) return rc;

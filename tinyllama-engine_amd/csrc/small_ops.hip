@@ -85,7 +85,45 @@ __global__ __launch_bounds__(256) void copy1_kernel(unsigned char* __restrict__ 
     for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) dst[i] = src[i];
 }
 
+__global__ __launch_bounds__(256) void zero16_kernel(float4* __restrict__ dst, long long n16)
+{
+    const long long stride = (long long)gridDim.x * 256;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n16; i += stride)
+        dst[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+}
+
+__global__ __launch_bounds__(256) void zero1_kernel(unsigned char* __restrict__ dst, long long n)
+{
+    const long long stride = (long long)gridDim.x * 256;
+    for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) dst[i] = 0;
+}
+
 }  // namespace
+
+hipError_t launch_zero(void* dst, size_t bytes, hipStream_t s)
+{
+    if (bytes == 0) return hipSuccess;
+    const bool aligned = (reinterpret_cast<uintptr_t>(dst) & 15) == 0;
+    const long long n16 = aligned ? (long long)(bytes / 16) : 0;
+    if (n16 > 0) {
+        long long blocks = (n16 + 255) / 256;
+        if (blocks > 256 * 64) blocks = 256 * 64;
+        hipLaunchKernelGGL(zero16_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                           static_cast<float4*>(dst), n16);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    const size_t done = (size_t)n16 * 16;
+    if (done < bytes) {
+        const long long rest = (long long)(bytes - done);
+        long long blocks = (rest + 255) / 256;
+        if (blocks > 4096) blocks = 4096;
+        hipLaunchKernelGGL(zero1_kernel, dim3((unsigned)blocks), dim3(256), 0, s,
+                           static_cast<unsigned char*>(dst) + done, rest);
+        return hipGetLastError();
+    }
+    return hipSuccess;
+}
 
 hipError_t launch_rope(const RopeParams& p, hipStream_t s)
 {

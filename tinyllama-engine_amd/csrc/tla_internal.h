@@ -24,6 +24,10 @@ constexpr int kDecodeKvGroupLarge = 4;
 constexpr int kMaxRopePairs = 128;  // tla_rope: head_dim <= 256
 
 // ---- decode ------------------------------------------------------------
+// Split partials of one decode launch: per (unit, split, kv head), 66 floats
+// per q head of the kv head (64 output floats, running max and sum).
+size_t decode_part_bytes(long long units, int max_splits, int n_head_kv, int gqa);
+
 // One "unit" = one (sequence, layer) decode problem.  unit = seq * n_lb + lb.
 struct DecodeParams {
     const float* q;      // [n_seq][n_lb][n_head][64]
@@ -189,5 +193,7 @@ struct RopeParams {
 hipError_t launch_rope(const RopeParams& p, hipStream_t s);
 hipError_t launch_softmax(float* x, int size, hipStream_t s);
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
+// Zero fill by a kernel (no memset node: safe under stream capture).
+hipError_t launch_zero(void* dst, size_t bytes, hipStream_t s);
 
 }  // namespace tla
