@@ -151,6 +151,25 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
                const float* v_dev, float* key_cache_dev, float* value_cache_dev,
                size_t seq_stride);
 
+/* tla_decode without any allocation: same arguments, same kernels and the
+ * same results bit for bit, but the split partials and arrival counters live
+ * in a fixed per-device static array (32 MiB of partials, 65,536 counters)
+ * instead of the engine's workspace, so the call never allocates device or
+ * host memory (tla_decode grows its workspace with hipMalloc on first use of
+ * a larger shape).  No counterpart in the reference: it is for callers that
+ * cannot allocate -- code under HIP graph capture, tight serving loops,
+ * harnesses that forbid allocation.  A launch whose partials or counters
+ * exceed the array returns TLA_ERR_UNSUPPORTED and launches nothing (e.g. 22
+ * layers x 2048 positions x 1 sequence needs 2 MB; 8 x 22 x 16384 about 5 MB).
+ * The array is shared by every engine on the device and keeps the last
+ * call's contents: calls that overlap on one device (other streams, other
+ * host threads) race.  The counters are zeroed when the first engine is
+ * created on the device, and every launch returns the ones it uses to zero. */
+int tla_decode_noalloc(tla_engine* e, int n_seq, const int* pos_host, int layer0,
+                       int n_step_layers, int flags, float* out_dev, const float* q_dev,
+                       const float* k_dev, const float* v_dev, float* key_cache_dev,
+                       float* value_cache_dev, size_t seq_stride);
+
 /* Causal prefill of n_tok prompt tokens at positions pos0 .. pos0+n_tok-1 of
  * one sequence, for layers layer0 .. layer0+n_step_layers-1.  Equal to the
  * reference's token-by-token prompt loop (src/generate.cpp:56-59) over the

@@ -136,6 +136,8 @@ SIGNATURES = {
     "tla_rope_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
     "tla_decode": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int,
                              _vp, _vp, _vp, _vp, _vp, _vp, C.c_size_t]),
+    "tla_decode_noalloc": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int,
+                                     _vp, _vp, _vp, _vp, _vp, _vp, C.c_size_t]),
     "tla_prefill": (C.c_int, [_vp, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int,
                               _vp, _vp, _vp, _vp, _vp, _vp]),
     "tla_profile_enable": (C.c_int, [_vp, C.c_int]),

@@ -7,6 +7,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
@@ -17,16 +18,16 @@ using namespace tla;
 
 namespace {
 
-thread_local std::string g_last_error;
+// The calling thread's last error message: a fixed buffer, so that no error
+// path allocates (the allocation-free entry point shares these paths).
+thread_local char g_last_error[512];
 
 int fail(int code, const char* fmt, ...)
 {
-    char buf[512];
     va_list ap;
     va_start(ap, fmt);
-    std::vsnprintf(buf, sizeof buf, fmt, ap);
+    std::vsnprintf(g_last_error, sizeof g_last_error, fmt, ap);
     va_end(ap);
-    g_last_error = buf;
     return code;
 }
 
@@ -82,6 +83,28 @@ constexpr int kEventSlots = 64;
 
 }  // namespace
 
+// ---- split scratch of the allocation-free decode entry point ---------------
+// tla_decode_noalloc keeps the split partials and arrival counters of a
+// launch in this fixed array instead of an engine workspace: 32 MiB of
+// partials (66 floats per q head for each (sequence, layer, split, kv head))
+// and 64 Ki counters.  Each device holds its own copy until the process ends.
+// Host code never names it directly: it uses the per-device address from
+// hipGetSymbolAddress, taken once per device when the first engine is created
+// there.
+namespace {
+constexpr size_t kScratchPartBytes = size_t(32) << 20;
+constexpr size_t kScratchCounters = size_t(1) << 16;
+constexpr size_t kScratchBytes = kScratchPartBytes + kScratchCounters * sizeof(int);
+constexpr int kScratchDevices = 64;
+}  // namespace
+
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kScratchDevices] = {};  // device address of `scratch`, per device
+}  // namespace
+
 struct tla_engine {
     tla_config cfg{};
     int device = 0;
@@ -90,6 +113,7 @@ struct tla_engine {
     int gqa = 0;
     hipStream_t stream = nullptr;
     float2* rope = nullptr;  // [n_ctx][head_dim/2]
+    void* scratch = nullptr; // this device's copy of `scratch` (tla_decode_noalloc), or NULL
     void* ws = nullptr;      // split-KV partials
     size_t ws_bytes = 0;
     int* counters = nullptr; // per-unit split arrival counters, zero between launches
@@ -118,6 +142,26 @@ namespace {
 int set_device(tla_engine* e)
 {
     TLA_HIP(hipSetDevice(e->device));
+    return TLA_OK;
+}
+
+// Once per device, with the device current: the device address of the
+// static scratch, and its counters zeroed (every decode launch returns the
+// counters it uses to zero, so they stay zero between launches).  Devices past
+// kScratchDevices get none (tla_decode_noalloc then returns an error).
+int scratch_setup(tla_engine* e)
+{
+    if (e->device >= kScratchDevices) return TLA_OK;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[e->device]) {
+        void* ptr = nullptr;
+        TLA_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+        TLA_HIP(launch_zero(static_cast<char*>(ptr) + kScratchPartBytes, kScratchCounters * sizeof(int),
+                            e->stream));
+        TLA_HIP(hipStreamSynchronize(e->stream));
+        g_scratch_ptr[e->device] = ptr;
+    }
+    e->scratch = g_scratch_ptr[e->device];
     return TLA_OK;
 }
 
@@ -265,7 +309,7 @@ extern "C" {
 
 const char* tla_last_error(void)
 {
-    return g_last_error.c_str();
+    return g_last_error;
 }
 
 int tla_abi_version(void)
@@ -333,6 +377,7 @@ int tla_engine_create(const tla_config* cfg, int device, tla_engine** out)
     if (err != hipSuccess)
         return bail(fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE,
                          "rope table: %s", hipGetErrorString(err)));
+    if (int rc = scratch_setup(e)) return bail(rc);
     *out = e;
     return ok();
 }
@@ -636,10 +681,16 @@ int tla_attn_out(tla_engine* e, int n_seq, float* x_dev, const void* wo_dev, con
     return ok();
 }
 
-int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_step_layers,
-               int flags, float* out_dev, const float* q_dev, const float* k_dev,
-               const float* v_dev, float* key_cache_dev, float* value_cache_dev,
-               size_t seq_stride)
+}  // extern "C"
+
+namespace {
+
+// tla_decode, with the split partials and counters in the engine's workspace
+// (grown on demand) or, with fixed_scratch, in the device's static scratch
+// (no allocation; launches that need more than it holds are rejected).
+int decode_impl(tla_engine* e, bool fixed_scratch, int n_seq, const int* pos_host, int layer0,
+                int n_step_layers, int flags, float* out_dev, const float* q_dev, const float* k_dev,
+                const float* v_dev, float* key_cache_dev, float* value_cache_dev, size_t seq_stride)
 {
     if (int rc = check_engine(e)) return rc;
     const tla_config& c = e->cfg;
@@ -668,9 +719,14 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
         seqs.seq_id[s] = s;
     }
     // Ranks by length, longest first (ties in caller order); the flat tile
-    // space lays out each rank's n_step_layers units in turn.
-    std::stable_sort(seqs.seq_id, seqs.seq_id + n_seq,
-                     [&](int a, int b) { return pos_host[a] > pos_host[b]; });
+    // space lays out each rank's n_step_layers units in turn.  An insertion
+    // sort in place: stable, and no temporary buffer.
+    for (int i = 1; i < n_seq; ++i) {
+        const int id = seqs.seq_id[i];
+        int j = i;
+        for (; j > 0 && pos_host[seqs.seq_id[j - 1]] < pos_host[id]; --j) seqs.seq_id[j] = seqs.seq_id[j - 1];
+        seqs.seq_id[j] = id;
+    }
     long long total_positions = 0, real_tiles = 0;
     for (int r = 0; r < n_seq; ++r) {
         seqs.pos[r] = pos_host[seqs.seq_id[r]];
@@ -722,13 +778,27 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
                                                       : kDecodeKvGroupLarge;
     const long long units = static_cast<long long>(n_seq) * n_step_layers;
     if (max_splits > 1) {
-        // per (unit, split, kv head): 64 output words + max + sum for each real head
+        // per (unit, split, kv head): 64 output floats + max + sum for each real head
         const size_t bytes = decode_part_bytes(units, max_splits, c.n_head_kv, e->gqa);
-        if (int rc = ensure_ws(e, bytes)) return rc;
         const long long groups = (c.n_head_kv + kv_group - 1) / kv_group;
-        if (int rc = ensure_counters(e, static_cast<size_t>(units * groups))) return rc;
-        p.part = static_cast<float*>(e->ws);
-        p.counters = e->counters;
+        const size_t n_counters = static_cast<size_t>(units * groups);
+        if (fixed_scratch) {
+            if (!e->scratch)
+                return fail(TLA_ERR_UNSUPPORTED, "device %d has no static split scratch", e->device);
+            if (bytes > kScratchPartBytes || n_counters > kScratchCounters)
+                return fail(TLA_ERR_UNSUPPORTED,
+                            "this launch needs %zu bytes of split partials and %zu counters; the static "
+                            "scratch holds %zu bytes and %zu counters (use tla_decode, or fewer "
+                            "sequences / layers per call)",
+                            bytes, n_counters, kScratchPartBytes, kScratchCounters);
+            p.part = static_cast<float*>(e->scratch);
+            p.counters = reinterpret_cast<int*>(static_cast<char*>(e->scratch) + kScratchPartBytes);
+        } else {
+            if (int rc = ensure_ws(e, bytes)) return rc;
+            if (int rc = ensure_counters(e, n_counters)) return rc;
+            p.part = static_cast<float*>(e->ws);
+            p.counters = e->counters;
+        }
     }
     p.q = q_dev;
     p.k = k_dev;
@@ -758,6 +828,28 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
                         [&] { return launch_decode(p, seqs, e->stream); }))
         return rc;
     return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_step_layers,
+               int flags, float* out_dev, const float* q_dev, const float* k_dev,
+               const float* v_dev, float* key_cache_dev, float* value_cache_dev,
+               size_t seq_stride)
+{
+    return decode_impl(e, false, n_seq, pos_host, layer0, n_step_layers, flags, out_dev, q_dev, k_dev,
+                       v_dev, key_cache_dev, value_cache_dev, seq_stride);
+}
+
+int tla_decode_noalloc(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_step_layers,
+                       int flags, float* out_dev, const float* q_dev, const float* k_dev,
+                       const float* v_dev, float* key_cache_dev, float* value_cache_dev,
+                       size_t seq_stride)
+{
+    return decode_impl(e, true, n_seq, pos_host, layer0, n_step_layers, flags, out_dev, q_dev, k_dev,
+                       v_dev, key_cache_dev, value_cache_dev, seq_stride);
 }
 
 int tla_attention(tla_engine* e, float* out_dev, const float* q_dev, const float* k_dev,
