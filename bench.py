@@ -170,11 +170,7 @@ def make_decode_case(workload, n_layers=22):
         # one layer's data from the generator (16384 ctx x 8 seqs, peaked
         # keys), repeated for every layer: the byte stream per layer is the
         # same, and host generation stays a few seconds
-        one = W.decode_long(n_seq=8, n_layers=1, n_ctx=16384)
-        rep = lambda a: np.ascontiguousarray(np.repeat(a, n_layers, axis=1))  # noqa: E731
-        case = W.DecodeCase(8, n_layers, 16384, one.pos, rep(one.q), rep(one.k), rep(one.v),
-                            rep(one.kc), rep(one.vc))
-        return case, 16384
+        return W.replicate_layers(W.decode_long_layer(n_seq=8, n_ctx=16384), n_layers), 16384
     if workload == "decode_single":
         return W.decode_single(), 128
     raise ValueError(workload)
@@ -229,10 +225,7 @@ def run_decode_sweep(steps, warmup, contexts=(2048, 4096, 8192, 16384), n_layers
     Cache."""
     out = []
     for ctx in contexts:
-        one = W.make_decode("decode_model", 1, 1, ctx, ctx - 1, salt=ctx)
-        rep = lambda a: np.ascontiguousarray(np.repeat(a, n_layers, axis=1))  # noqa: E731
-        case = W.DecodeCase(1, n_layers, ctx, one.pos, rep(one.q), rep(one.k), rep(one.v),
-                            rep(one.kc), rep(one.vc))
+        case = W.replicate_layers(W.decode_sweep_layer(ctx), n_layers)
         one_copy = case.kc.nbytes * 2
         copies = max(1, -(-3 * MALL_BYTES // 2 // one_copy))
         copies = max(copies, 2 if one_copy < MALL_BYTES else 1)

@@ -351,3 +351,84 @@ def test_decode_group_does_not_change_results(O, W, engines, tla, n_seq, n_layer
         assert np.array_equal(bits(gk), bits(outs[0][1])) and np.array_equal(bits(gv), bits(outs[0][2]))
     ref, _, _ = oracle_decode(O, case)
     assert max_err(outs[0][0], ref) <= DECODE_TOL
+
+
+def replicated_gpu_decode(tla, eng, one, n_layers):
+    """tla_decode with one layer's inputs in every layer, as bench.py times
+    the long-context workloads: the one-layer caches are uploaded into layer
+    0 of each sequence and copied on the device into the other layers' slices
+    (no host copy of the full caches).  Returns out [n_seq, n_layers, q_dim]
+    and the key / value rows appended at pos [n_seq, n_layers, kv_dim]."""
+    cfg = eng.cfg
+    assert cfg.n_layers == n_layers and cfg.n_ctx == one.n_ctx and one.n_layers == 1
+    slice_floats = one.n_ctx * cfg.kv_dim
+    rep = lambda a: np.ascontiguousarray(np.repeat(a, n_layers, axis=1))  # noqa: E731
+    with device_arrays() as track:
+        kc, vc = eng.kv_cache(one.n_seq)
+        track(kc), track(vc)
+        for s in range(one.n_seq):
+            base = s * n_layers * slice_floats * 4
+            for arr, host in ((kc, one.kc), (vc, one.vc)):
+                rc = tla.lib().tla_memcpy_h2d(eng.h, arr.ptr + base, np.ascontiguousarray(host[s, 0]).ctypes.data,
+                                              slice_floats * 4)
+                assert rc == 0, tla.last_error()
+                for layer in range(1, n_layers):
+                    eng.copy(arr.ptr + base + layer * slice_floats * 4, arr.ptr + base, slice_floats * 4)
+        q, k, v = track(eng.array(rep(one.q))), track(eng.array(rep(one.k))), track(eng.array(rep(one.v)))
+        out = track(eng.array((one.n_seq, n_layers, cfg.n_head * 64)))
+        log(f"  tla_decode (auto plan) n_seq={one.n_seq} x {n_layers} layers, ctx {one.n_ctx}")
+        eng.decode(one.pos, 0, n_layers, out.ptr, q.ptr, k.ptr, v.ptr, kc.ptr, vc.ptr, n_layers * slice_floats)
+        got = out.download()
+        rows = np.empty((2, one.n_seq, n_layers, cfg.kv_dim), np.float32)
+        for s in range(one.n_seq):
+            for layer in range(n_layers):
+                off = ((s * n_layers + layer) * one.n_ctx + int(one.pos[s])) * cfg.kv_dim * 4
+                for i, arr in enumerate((kc, vc)):
+                    rc = tla.lib().tla_memcpy_d2h(eng.h, rows[i, s, layer].ctypes.data, arr.ptr + off,
+                                                  cfg.kv_dim * 4)
+                    assert rc == 0, tla.last_error()
+        return got, rows[0], rows[1]
+
+
+def check_replicated_against_fp64(O, one, got, krow, vrow):
+    """Every layer's output of sequence s against the single-layer oracle of
+    s: within 1e-4 of the fp64 value, and no further from the reference's own
+    fp32 result than 1e-4 plus that result's distance from fp64 (at long
+    contexts the reference's sequential sums drift, src/ops.cpp:1500-1508).
+    Appended rows bit-exact for every layer."""
+    ref, rk, rv = oracle_decode(O, one, keep_cache=True)
+    s_ = O.Shape(n_ctx=one.n_ctx)
+    worst = 0.0
+    for si in range(one.n_seq):
+        p = int(one.pos[si])
+        qr, _ = O.rope(one.q[si, 0], one.k[si, 0], p, s_)
+        f64 = O.attention_f64(qr, rk[si, 0].reshape(-1), rv[si, 0].reshape(-1), 0, p, s_)
+        e_ref = np.abs(ref[si, 0].astype(np.float64) - f64)
+        for layer in range(got.shape[1]):
+            g = got[si, layer].astype(np.float64)
+            assert np.all(np.abs(g - f64) <= DECODE_TOL), (si, layer, float(np.abs(g - f64).max()))
+            assert np.all(np.abs(g - ref[si, 0]) <= DECODE_TOL + e_ref), (si, layer)
+            worst = max(worst, float(np.abs(g - f64).max()))
+            assert np.array_equal(bits(krow[si, layer]), bits(rk[si, 0, p])), ("key row", si, layer)
+            assert np.array_equal(bits(vrow[si, layer]), bits(rv[si, 0, p])), ("value row", si, layer)
+    log(f"    worst GPU vs fp64 over all layers: {worst:.2e}")
+
+
+def test_decode_long_full_size(tla, O, W, engines):
+    """The long-context stress workload at the size it is timed: 8 sequences
+    x 22 layers x 16384 positions, peaked keys, one layer's data in every
+    layer (W.decode_long_layer, replicated): the balanced plan's ranges cross
+    unit boundaries, with deferred arrivals and up to three splits per unit."""
+    one = W.decode_long_layer(n_seq=8, n_ctx=16384)
+    got, krow, vrow = replicated_gpu_decode(tla, engines(22, 16384), one, 22)
+    check_replicated_against_fp64(O, one, got, krow, vrow)
+
+
+@pytest.mark.parametrize("ctx", [4096, 8192, 16384])
+def test_decode_sweep_full_size(tla, O, W, engines, ctx):
+    """The batch-1 sweep at the size it is timed: 22 layers at context 4K /
+    8K / 16K (W.decode_sweep_layer, replicated), one round of aligned
+    splits of up to 1504 positions."""
+    one = W.decode_sweep_layer(ctx)
+    got, krow, vrow = replicated_gpu_decode(tla, engines(22, ctx), one, 22)
+    check_replicated_against_fp64(O, one, got, krow, vrow)

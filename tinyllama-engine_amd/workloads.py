@@ -136,6 +136,29 @@ def decode_long(n_seq: int = 8, n_layers: int = 22, n_ctx: int = 16384) -> Decod
                        peaked_frac=0.01)
 
 
+# The long-context workloads are timed with one layer's data in every layer
+# (the byte stream per layer is the same, and host generation stays a few
+# seconds): these are the one-layer cases, replicated by replicate_layers()
+# or, on the device, copied into every layer's slice of the cache.
+
+def decode_long_layer(n_seq: int = 8, n_ctx: int = 16384) -> DecodeCase:
+    """Context 16384, batch 8, peaked keys: one layer."""
+    return decode_long(n_seq=n_seq, n_layers=1, n_ctx=n_ctx)
+
+
+def decode_sweep_layer(n_ctx: int) -> DecodeCase:
+    """Batch 1, new token at the last position of an n_ctx cache: one layer."""
+    return make_decode("decode_model", 1, 1, n_ctx, n_ctx - 1, salt=n_ctx)
+
+
+def replicate_layers(one: DecodeCase, n_layers: int) -> DecodeCase:
+    """A one-layer case with its inputs repeated for n_layers layers (host
+    arrays, n_layers times the one layer's memory)."""
+    rep = lambda a: np.ascontiguousarray(np.repeat(a, n_layers, axis=1))  # noqa: E731
+    return DecodeCase(one.n_seq, n_layers, one.n_ctx, one.pos, rep(one.q), rep(one.k), rep(one.v),
+                      rep(one.kc), rep(one.vc), one.n_head, one.n_head_kv)
+
+
 # ---- prefill inputs -------------------------------------------------------------
 
 class PrefillCase:
