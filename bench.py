@@ -32,9 +32,11 @@ decode_single (one layer, position 127: reported as latency), decode_sweep
 attention block's projections for a 22-layer decode step, and the GEMV kernel
 on a 32000 x 2048 matrix in every weight format), matmul (that GEMV alone in
 one format, --wtype), copy (the
-device copy kernel, used to calibrate rocprofv3 byte counters) and read (a
-plain library reduction over 6 GiB: what HBM delivers to a read stream, the
-practical ceiling the decode figures sit under).
+device copy kernel, used to calibrate rocprofv3 byte counters), read (a
+plain library reduction over 6 GiB) and read_floor (this package's streaming
+read over exactly the bytes of a batch-1 decode step at 2K-16K context: what
+one launch can move in that time, the ceiling the decode step sits under;
+also in the default line's extra).
 """
 from __future__ import annotations
 
@@ -656,6 +658,45 @@ def cpu_generate_baseline(spec, tensors, prompt, wname, n_prompt=8, n_decode=8):
             **cpu_host()}
 
 
+READ_FLOOR_GRIDS = (256, 512, 1024, 2048, 4096, 8192)
+
+
+def run_read_floor(steps, warmup, contexts=(2048, 4096, 8192, 16384), n_layers=22):
+    """The hand-written streaming read (tla_read_floor) over exactly the bytes
+    a batch-1 decode step moves at each context (22 layers, 2048*L + 20480
+    per layer), launches rotating over copies past the Infinity Cache and
+    queued back to back; the best of a few grid sizes.  What one launch can
+    read in the time it takes: the bar for the decode kernel at that size."""
+    eng = tla.Engine(tla.Config.tinyllama(n_layers=1, n_ctx=16))
+    sink = eng.array((max(READ_FLOOR_GRIDS),))
+    out = []
+    for ctx in contexts:
+        nbytes = W.decode_bytes(ctx) * n_layers
+        span = (nbytes + 255) // 256 * 256
+        copies = max(2, -(-3 * MALL_BYTES // 2 // nbytes))
+        buf = tla.DeviceArray(eng, (span * copies,), np.uint8)
+        best = None
+        for grid in READ_FLOOR_GRIDS:
+            def one(i, grid=grid):
+                eng.read_floor(buf.ptr + (i % copies) * span, nbytes, grid, sink.ptr)
+            for i in range(warmup):
+                one(i)
+            ms = back_to_back_ms(eng, one, steps)
+            if best is None or ms < best[0]:
+                best = (ms, grid)
+        ms, grid = best
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        log(f"[bench] read floor {nbytes / 1e6:.1f} MB (decode batch 1 x {n_layers} layers, ctx {ctx}): "
+            f"{ms * 1e3:.2f} us with {grid} workgroups -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), "
+            f"{copies} rotated copies")
+        out.append({"ctx": ctx, "bytes": nbytes, "us": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
+                    "frac": round(gbs / HBM_PEAK_GBS, 4), "workgroups": grid, "copies": copies})
+        buf.free()
+    sink.free()
+    eng.close()
+    return out
+
+
 def run_read(steps, warmup, nbytes=6 << 30):
     """HBM read ceiling: torch's sum over an nbytes float32 tensor (a library
     streaming reduction, none of this package's kernels), timed with events on torch's
@@ -690,7 +731,7 @@ def main():
     ap.add_argument("--workload", default="decode_model",
                     choices=["decode_model", "decode_long", "decode_ragged", "decode_single",
                              "prefill", "proj", "matmul", "generate", "decode_sweep",
-                             "prefill_sweep", "copy", "read"])
+                             "prefill_sweep", "copy", "read", "read_floor"])
     ap.add_argument("--wtype", default=None, choices=["f32", "f16", "q8_0", "q4_0", "q6_k"],
                     help="weight format of the matmul (default q8_0) or generate (q4_0) workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -715,6 +756,16 @@ def main():
         return
     if args.workload == "read":
         print(json.dumps(run_read(args.steps, args.warmup)))
+        return
+    if args.workload == "read_floor":
+        r = run_read_floor(args.steps, args.warmup)
+        print(json.dumps({"metric": "streaming-read floor GB/s (% HBM peak)", "value": r[0]["GB_s"],
+                          "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": r[0]["us"] / 1e3, "higher_is_better": True, "scaling": "weak",
+                          "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+                          "config": {"workload": "read_floor", "bytes": "decode batch 1 x 22 layers",
+                                     "contexts": [x["ctx"] for x in r], "parallelism": "none"},
+                          "sweep": r}))
         return
     if args.workload == "decode_sweep":
         r = run_decode_sweep(args.steps, args.warmup, plan=PLANS[args.plan])
@@ -843,6 +894,12 @@ def main():
         line["extra"]["decode_single"] = {"value": round(e["ms_per_step"] * 1e3, 2), "unit": "us",
                                           "higher_is_better": False,
                                           "note": "1 layer, position 127: latency-bound"}
+        # what one launch can read of the same byte counts (the decode step's
+        # ceiling at batch 1), and the decode kernel's rate over it at 2048
+        floor = run_read_floor(args.steps, args.warmup)
+        line["extra"]["read_floor"] = floor
+        f2k = next(x for x in floor if x["ctx"] == 2048)
+        line["extra"]["decode_model_over_read_floor"] = round(f2k["us"] / (d["ms_per_step"] * 1e3), 4)
     print(json.dumps(line))
 
 

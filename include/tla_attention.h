@@ -351,6 +351,15 @@ int tla_profile_read(tla_engine* e, int kernel_id, double* total_ms, long long* 
 int tla_event_record(tla_engine* e, int slot);
 int tla_event_elapsed(tla_engine* e, int slot_begin, int slot_end, float* ms);
 
+/* Streaming-read floor: read `bytes` at src_dev (16-byte aligned, a multiple
+ * of 16) with n_workgroups workgroups of 256 threads, each summing one
+ * contiguous chunk, on the engine's stream; sink_dev [n_workgroups] floats is
+ * never written in practice (the sums are kept only so the loads stay).  What
+ * one launch can read from HBM in the time it takes -- the bar the decode
+ * kernel's byte rate is set against.  No reference counterpart. */
+int tla_read_floor(tla_engine* e, const void* src_dev, size_t bytes, int n_workgroups,
+                   float* sink_dev);
+
 /* Tuning knobs (0 = automatic). */
 enum tla_option {
     TLA_OPT_DECODE_SPLIT = 0, /* positions per decode workgroup (rounded up to 16) */

@@ -129,3 +129,20 @@ def test_cpp_host_side_program():
     log(r.stdout[-3000:])
     assert r.returncode == 0, r.stdout + r.stderr
     assert " 0 failed" in r.stdout
+
+
+def test_read_floor_reads_and_leaves_the_sink(tla, engines):
+    """The streaming-read hook: runs over an odd byte count and grid, never
+    writes its sink for ordinary data, and validates its arguments before
+    launching."""
+    eng = engines(1, 64)
+    with device_arrays() as track:
+        src = track(eng.array(np.arange(1 << 20, dtype=np.float32)))
+        sink = track(eng.array(np.full(777, 7.0, np.float32)))
+        eng.read_floor(src.ptr, (1 << 22) - 48, 777, sink.ptr)
+        eng.synchronize()
+        assert np.all(sink.download() == 7.0)
+        for nbytes, grid in ((15, 4), (1 << 22, 0), (40, 4)):
+            with pytest.raises(tla.TlaError) as e:
+                eng.read_floor(src.ptr, nbytes, grid, sink.ptr)
+            assert e.value.code == tla.TLA_ERR_INVALID_ARGUMENT

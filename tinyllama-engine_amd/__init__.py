@@ -146,6 +146,7 @@ SIGNATURES = {
     "tla_event_record": (C.c_int, [_vp, C.c_int]),
     "tla_event_elapsed": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "tla_set_option": (C.c_int, [_vp, C.c_int, C.c_longlong]),
+    "tla_read_floor": (C.c_int, [_vp, _vp, C.c_size_t, C.c_int, _vp]),
 }
 
 
@@ -361,6 +362,9 @@ class Engine:
         _check(lib().tla_profile_read(self.h, kernel_id, C.byref(ms), C.byref(n)),
                "tla_profile_read")
         return ms.value, n.value
+
+    def read_floor(self, src: int, nbytes: int, n_workgroups: int, sink: int):
+        _check(lib().tla_read_floor(self.h, src, nbytes, n_workgroups, sink), "tla_read_floor")
 
     def event(self, slot: int):
         _check(lib().tla_event_record(self.h, slot), "tla_event_record")

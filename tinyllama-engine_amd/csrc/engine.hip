@@ -1565,6 +1565,21 @@ int tla_event_elapsed(tla_engine* e, int slot_begin, int slot_end, float* ms)
     return ok();
 }
 
+int tla_read_floor(tla_engine* e, const void* src_dev, size_t bytes, int n_workgroups, float* sink_dev)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!src_dev || !sink_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (bytes < 16 || bytes % 16 != 0 || reinterpret_cast<std::uintptr_t>(src_dev) % 16 != 0)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "bytes %zu: a positive multiple of 16 at a 16-byte aligned address",
+                    bytes);
+    if (n_workgroups < 1 || n_workgroups > (1 << 20))
+        return fail(TLA_ERR_INVALID_ARGUMENT, "n_workgroups %d not in [1, 2^20]", n_workgroups);
+    if (int rc = set_device(e)) return rc;
+    const hipError_t err = launch_read_floor(src_dev, bytes, n_workgroups, sink_dev, e->stream);
+    if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "read floor launch: %s", hipGetErrorString(err));
+    return ok();
+}
+
 int tla_set_option(tla_engine* e, int option, long long value)
 {
     if (int rc = check_engine(e)) return rc;

@@ -98,7 +98,45 @@ __global__ __launch_bounds__(256) void zero1_kernel(unsigned char* __restrict__ 
     for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < n; i += stride) dst[i] = 0;
 }
 
+// Streaming read floor: workgroup w sums the 16-byte words [w * per_wg,
+// (w + 1) * per_wg) of src, each thread eight loads in flight (unrolled), and
+// writes its sum only if it equals a value no sum of these inputs takes, so
+// that the loads stay but nothing is written.  The fastest a single launch
+// can move a given number of bytes from HBM.
+constexpr int kReadUnroll = 8;
+
+__global__ __launch_bounds__(256) void read_floor_kernel(const float4* __restrict__ src, long long n16,
+                                                         long long per_wg, float* __restrict__ sink)
+{
+    const long long lo = (long long)blockIdx.x * per_wg;
+    const long long hi = lo + per_wg < n16 ? lo + per_wg : n16;
+    float acc = 0.f;
+    long long i = lo + threadIdx.x;
+    for (; i + (kReadUnroll - 1) * 256 < hi; i += kReadUnroll * 256) {
+        float4 v[kReadUnroll];
+#pragma unroll
+        for (int u = 0; u < kReadUnroll; ++u) v[u] = src[i + u * 256];
+#pragma unroll
+        for (int u = 0; u < kReadUnroll; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+    }
+    for (; i < hi; i += 256) {
+        const float4 v = src[i];
+        acc += (v.x + v.y) + (v.z + v.w);
+    }
+    if (acc == -1234.5f) sink[blockIdx.x] = acc;
+}
+
 }  // namespace
+
+hipError_t launch_read_floor(const void* src, size_t bytes, int n_wg, float* sink, hipStream_t s)
+{
+    const long long n16 = (long long)(bytes / 16);
+    if (n16 == 0 || n_wg < 1) return hipErrorInvalidValue;
+    const long long per_wg = (n16 + n_wg - 1) / n_wg;
+    hipLaunchKernelGGL(read_floor_kernel, dim3((unsigned)n_wg), dim3(256), 0, s,
+                       static_cast<const float4*>(src), n16, per_wg, sink);
+    return hipGetLastError();
+}
 
 hipError_t launch_zero(void* dst, size_t bytes, hipStream_t s)
 {

@@ -193,6 +193,9 @@ struct RopeParams {
 hipError_t launch_rope(const RopeParams& p, hipStream_t s);
 hipError_t launch_softmax(float* x, int size, hipStream_t s);
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
+// Streaming read of `bytes` (16-byte aligned, whole 16-byte words) by n_wg
+// workgroups, each a contiguous chunk; sink [n_wg] is never written in practice.
+hipError_t launch_read_floor(const void* src, size_t bytes, int n_wg, float* sink, hipStream_t s);
 // Zero fill by a kernel (no memset node: safe under stream capture).
 hipError_t launch_zero(void* dst, size_t bytes, hipStream_t s);
 
