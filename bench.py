@@ -363,11 +363,15 @@ def run_prefill_sweep(steps, warmup, lengths=(512, 1024, 2048, 4096), n_layers=2
 
 
 def cpu_prefill_baseline(case, n_tok, budget_s=8.0):
-    """The C restatement of the reference's token-by-token prompt loop, one
-    layer per host thread (the reference's attention() has no threading)."""
+    """The reference's own token-by-token prompt loop -- its rope() and
+    attention() compiled from src/ops.cpp (oracle/_ref), or the C restatement
+    when that is not built -- one layer per host thread (the reference's
+    attention() has no threading)."""
     from concurrent.futures import ThreadPoolExecutor
 
     import oracle as O
+    kind = "reference" if O.ref_available() else "port"
+    lib = O.ref() if kind == "reference" else None
     s = O.Shape(n_ctx=n_tok, n_layers=1)
     threads = cpu_threads()
     times = []
@@ -379,16 +383,16 @@ def cpu_prefill_baseline(case, n_tok, budget_s=8.0):
             def one(layer):
                 kc = np.zeros(n_tok * 256, np.float32)
                 vc = np.zeros_like(kc)
-                O.prefill(case.q[layer], case.k[layer], case.v[layer], kc, vc, 0, 0, s)
+                O.prefill(case.q[layer], case.k[layer], case.v[layer], kc, vc, 0, 0, s, lib=lib)
 
             list(ex.map(one, range(case.n_layers)))
             times.append(time.perf_counter() - t0)
             if time.perf_counter() > t_end:
                 break
     t = median(times)
-    log(f"[bench] cpu prefill port: {t * 1e3:.0f} ms/step on {threads} threads")
+    log(f"[bench] cpu prefill {kind}: {t * 1e3:.0f} ms/step on {threads} threads")
     return {"value": round(case.algorithmic_flops / t / 1e12, 5), "unit": "TFLOP/s",
-            "cores": threads, "kind": "port",
+            "cores": threads, "kind": kind,
             "sample": f"{len(times)} full prefill steps (512 tokens x {case.n_layers} layers, one "
                       f"layer per thread), median", **cpu_host()}
 

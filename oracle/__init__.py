@@ -123,6 +123,8 @@ def ref() -> C.CDLL:
                                             C.c_size_t, _ip, C.c_int, C.c_int, C.c_int,
                                             C.c_int, C.c_float, C.c_int]
         lib.ref_decode_units_mt.restype = C.c_int
+        lib.ref_prefill.argtypes = [_fp, _fp, _fp, _fp, _fp, _fp, C.c_int, C.c_int, C.c_int,
+                                    C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
         lib.ref_matmul.argtypes = [_fp, C.c_void_p, _fp, C.c_int, C.c_int, C.c_int]
         lib.ref_rmsnorm.argtypes = [_fp, _fp, _fp, C.c_int, C.c_float]
         lib.ref_vec_add.argtypes = [_fp, _fp, C.c_int]
@@ -199,15 +201,17 @@ def attention_f64(q, kc, vc, layer, pos, s: Shape):
     return out
 
 
-def prefill(q, k, v, kc, vc, layer, pos0, s: Shape):
-    """Token-by-token prompt loop; q [T, q_dim], k/v [T, kv_dim] raw."""
+def prefill(q, k, v, kc, vc, layer, pos0, s: Shape, lib=None):
+    """Token-by-token prompt loop; q [T, q_dim], k/v [T, kv_dim] raw.  With
+    lib = ref(), the reference's own rope() + attention() do the loop."""
     q = np.ascontiguousarray(q, dtype=np.float32)
     k = np.ascontiguousarray(k, dtype=np.float32)
     v = np.ascontiguousarray(v, dtype=np.float32)
     t = q.shape[0]
     out = np.zeros((t, s.q_dim), np.float32)
-    oracle().oracle_prefill(fptr(out), fptr(q), fptr(k), fptr(v), fptr(kc), fptr(vc), layer,
-                            pos0, t, s.n_head, s.n_head_kv, s.head_dim, s.n_ctx, s.freq_base)
+    fn = oracle().oracle_prefill if lib is None else lib.ref_prefill
+    fn(fptr(out), fptr(q), fptr(k), fptr(v), fptr(kc), fptr(vc), layer, pos0, t, s.n_head,
+       s.n_head_kv, s.head_dim, s.n_ctx, s.freq_base)
     return out
 
 

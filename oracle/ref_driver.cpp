@@ -85,6 +85,26 @@ int ref_decode_units_mt(int n_threads, int n_units, float* out, const float* q,
     return 0;
 }
 
+// The prompt fed token by token (src/generate.cpp:56-59) through the
+// attention block (src/forward.cpp:192-208): rope() then attention() for
+// token t at position pos0 + t, with the same arguments as oracle_prefill.
+void ref_prefill(float* out, const float* q, const float* k, const float* v, float* key_cache,
+                 float* value_cache, int layer, int pos0, int n_tok, int n_head, int n_head_kv,
+                 int head_dim, int n_ctx, float freq_base)
+{
+    const llama_config_t cfg = make_cfg(layer + 1, n_head, n_head_kv, head_dim, n_ctx);
+    const int qd = n_head * head_dim, kd = n_head_kv * head_dim;
+    std::vector<float> qt(qd), kt(kd), att(n_ctx);
+    for (int t = 0; t < n_tok; ++t) {
+        std::memcpy(qt.data(), q + static_cast<std::size_t>(t) * qd, sizeof(float) * qd);
+        std::memcpy(kt.data(), k + static_cast<std::size_t>(t) * kd, sizeof(float) * kd);
+        rope(qt.data(), kt.data(), pos0 + t, head_dim, n_head, n_head_kv, freq_base);
+        attention(out + static_cast<std::size_t>(t) * qd, qt.data(), kt.data(),
+                  v + static_cast<std::size_t>(t) * kd, key_cache, value_cache, att.data(), layer,
+                  pos0 + t, cfg);
+    }
+}
+
 void ref_matmul(float* out, const void* W, const float* x, int rows, int cols, int type)
 {
     matmul(out, W, x, rows, cols, static_cast<ggml_type>(type));

@@ -181,6 +181,22 @@ def test_live_reference_attention(O):
 
 
 @needs_ref
+def test_live_reference_prefill_loop(O, W):
+    """The prompt loop through the reference's own rope() + attention() (the
+    prefill CPU baseline) equals the restatement bit for bit, outputs and
+    caches, at layer 1 of 2 from a nonzero start position."""
+    case = W.make_prefill(n_layers=1, n_tok=70, salt=13)
+    s = O.Shape(n_ctx=96, n_layers=2)
+    outs = []
+    for lib in (None, O.ref()):
+        kc = np.zeros(2 * 96 * s.kv_dim, np.float32)
+        vc = np.zeros_like(kc)
+        outs.append((O.prefill(case.q[0], case.k[0], case.v[0], kc, vc, 1, 9, s, lib=lib), kc, vc))
+    for a, b in zip(outs[0], outs[1]):
+        assert_bitexact(a, b, "prefill loop")
+
+
+@needs_ref
 def test_live_reference_threaded_units(O, W):
     case = W.make_decode(9, 6, 1, 96, [0, 5, 31, 32, 64, 95])
     s = O.Shape(n_ctx=96)
