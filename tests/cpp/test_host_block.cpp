@@ -21,6 +21,7 @@
 #include <stdexcept>
 #include <vector>
 
+#include "run_state.h"
 #include "tla_host.h"
 
 extern "C" {
@@ -186,7 +187,7 @@ static void test_rope(tla_host::Engine& eng)
 static void test_block(tla_host::Engine& eng, const tla_host::Config& cfg)
 {
     std::printf("\n=== RunState + attention_block (forward.cpp:192-208) ===\n");
-    tla_host::RunState st;
+    RunState st;
     st.allocate(cfg, eng);
     const int kv_dim = 256, n_embd = 2048, n_ctx = int(cfg.n_ctx);
     std::vector<float> hkc(size_t(cfg.n_layers) * n_ctx * kv_dim, 0.f), hvc(hkc.size(), 0.f);
@@ -289,7 +290,7 @@ static void test_forward(tla_host::Engine& eng, const tla_host::Config& cfg)
     };
     const float eps = 1e-5f;
     tla_host::DeviceModel dm(eng, eps, lookup);
-    tla_host::RunState st;
+    RunState st;
     st.allocate(cfg, eng);
 
     std::vector<oracle_layer> ol(L);
@@ -341,7 +342,7 @@ static void test_forward(tla_host::Engine& eng, const tla_host::Config& cfg)
         want.push_back(best);
         if (i + 1 < n_gen) oracle_forward(&om, okc.data(), ovc.data(), scratch.data(), best, pos++, ologits.data());
     }
-    tla_host::RunState st2;
+    RunState st2;
     st2.allocate(cfg, eng);
     const std::vector<int> got = tla_host::generate_greedy(dm, st2, prompt, n_gen);
     check("greedy path has no near-ties", clear);

@@ -2,7 +2,11 @@
 #include "tla_host.h"
 
 #include <cstring>
+#include <memory>
+#include <mutex>
 #include <new>
+
+#include "run_state.h"
 
 namespace tla_host {
 
@@ -57,75 +61,120 @@ void attention(Engine& eng, float* out, const float* q, const float* k, const fl
           "attention");
 }
 
-void RunState::allocate(const Config& cfg, Engine& eng)
+namespace {
+
+std::mutex g_engines_mu;
+Engine* g_engine = nullptr;          // set by use_engine
+std::vector<Engine*> g_own_engines;  // made by engine_for; kept until the process ends
+
+bool same_shape(const Config& a, const Config& b)
 {
-    free_buffers();
-    engine = &eng;
-    n_embd_ = cfg.n_embd;
-    kv_dim_ = cfg.n_head_kv * cfg.head_dim();
-    n_vocab_ = cfg.n_vocab;
-
-    x = new float[cfg.n_embd]();
-    xb = new float[cfg.n_embd]();
-    xb2 = new float[cfg.n_embd]();
-    qkv_host_ = new float[cfg.n_embd + 2 * kv_dim_]();
-    q = qkv_host_;
-    k = q + cfg.n_embd;
-    v = k + kv_dim_;
-    att = new float[cfg.n_ctx]();
-    hb = new float[cfg.n_ff ? cfg.n_ff : 1]();
-    hb2 = new float[cfg.n_ff ? cfg.n_ff : 1]();
-    logits = new float[cfg.n_vocab ? cfg.n_vocab : 1]();
-
-    check(tla_kv_cache_alloc(eng.get(), 1, &key_cache, &value_cache), "KV cache allocation");
-    void* p = nullptr;
-    check(tla_alloc(eng.get(), sizeof(float) * (cfg.n_embd + 2 * kv_dim_), &p), "q|k|v staging");
-    d_qkv = static_cast<float*>(p);
-    check(tla_alloc(eng.get(), sizeof(float) * cfg.n_embd, &p), "output staging");
-    d_out = static_cast<float*>(p);
-    if (cfg.n_vocab) {
-        check(tla_alloc(eng.get(), sizeof(float) * cfg.n_vocab, &p), "logits");
-        d_logits = static_cast<float*>(p);
-    }
-    pos = 0;
+    return a.n_layers == b.n_layers && a.n_embd == b.n_embd && a.n_head == b.n_head &&
+           a.n_head_kv == b.n_head_kv && a.n_ctx == b.n_ctx && a.rope_freq_base == b.rope_freq_base;
 }
 
-void RunState::free_buffers()
+}  // namespace
+
+void use_engine(Engine* eng)
 {
-    delete[] x;
-    delete[] xb;
-    delete[] xb2;
-    delete[] qkv_host_;
-    delete[] att;
-    delete[] hb;
-    delete[] hb2;
-    delete[] logits;
-    x = xb = xb2 = q = k = v = att = hb = hb2 = logits = nullptr;
-    qkv_host_ = nullptr;
-    if (engine) {
-        tla_free(engine->get(), key_cache);
-        tla_free(engine->get(), value_cache);
-        tla_free(engine->get(), d_qkv);
-        tla_free(engine->get(), d_out);
-        if (d_logits) tla_free(engine->get(), d_logits);
-    }
-    key_cache = value_cache = d_qkv = d_out = d_logits = nullptr;
-    engine = nullptr;
+    std::lock_guard<std::mutex> lock(g_engines_mu);
+    g_engine = eng;
 }
 
-void attention_block(RunState& state, int layer, int pos)
+Engine& engine_for(const Config& cfg)
+{
+    std::lock_guard<std::mutex> lock(g_engines_mu);
+    if (g_engine) {
+        if (!same_shape(g_engine->config(), cfg))
+            throw std::runtime_error("RunState::allocate: the engine set with use_engine has another shape");
+        return *g_engine;
+    }
+    for (Engine* e : g_own_engines)
+        if (same_shape(e->config(), cfg)) return *e;
+    // Never destroyed: it serves RunStates for the rest of the process.
+    g_own_engines.push_back(new Engine(cfg));
+    return *g_own_engines.back();
+}
+
+namespace detail {
+
+void allocate_state(::RunState& st, const Config& cfg, Engine& eng)
+{
+    if (!same_shape(eng.config(), cfg))
+        throw std::runtime_error("RunState::allocate: engine and config differ in shape");
+    st.free_buffers();
+    st.engine = &eng;
+    st.n_embd = cfg.n_embd;
+    st.kv_dim = cfg.n_head_kv * cfg.head_dim();
+    st.n_vocab = cfg.n_vocab;
+    try {
+        st.x = new float[cfg.n_embd]();
+        st.xb = new float[cfg.n_embd]();
+        st.xb2 = new float[cfg.n_embd]();
+        st.qkv_host = new float[cfg.n_embd + 2 * st.kv_dim]();
+        st.q = st.qkv_host;
+        st.k = st.q + cfg.n_embd;
+        st.v = st.k + st.kv_dim;
+        st.att = new float[cfg.n_ctx]();
+        st.hb = new float[cfg.n_ff ? cfg.n_ff : 1]();
+        st.hb2 = new float[cfg.n_ff ? cfg.n_ff : 1]();
+        st.logits = new float[cfg.n_vocab ? cfg.n_vocab : 1]();
+        check(tla_kv_cache_alloc(eng.get(), 1, &st.key_cache, &st.value_cache), "KV cache allocation");
+        void* p = nullptr;
+        check(tla_alloc(eng.get(), sizeof(float) * (cfg.n_embd + 2 * st.kv_dim), &p), "q|k|v staging");
+        st.d_qkv = static_cast<float*>(p);
+        check(tla_alloc(eng.get(), sizeof(float) * cfg.n_embd, &p), "output staging");
+        st.d_out = static_cast<float*>(p);
+        if (cfg.n_vocab) {
+            check(tla_alloc(eng.get(), sizeof(float) * cfg.n_vocab, &p), "logits");
+            st.d_logits = static_cast<float*>(p);
+        }
+    } catch (...) {
+        free_state(st);
+        throw;
+    }
+    st.pos = 0;
+}
+
+void free_state(::RunState& st) noexcept
+{
+    delete[] st.x;
+    delete[] st.xb;
+    delete[] st.xb2;
+    delete[] st.qkv_host;
+    delete[] st.att;
+    delete[] st.hb;
+    delete[] st.hb2;
+    delete[] st.logits;
+    st.x = st.xb = st.xb2 = st.q = st.k = st.v = st.att = st.hb = st.hb2 = st.logits = nullptr;
+    st.qkv_host = nullptr;
+    if (st.engine) {
+        tla_engine* e = st.engine->get();
+        if (st.key_cache) tla_free(e, st.key_cache);
+        if (st.value_cache) tla_free(e, st.value_cache);
+        if (st.d_qkv) tla_free(e, st.d_qkv);
+        if (st.d_out) tla_free(e, st.d_out);
+        if (st.d_logits) tla_free(e, st.d_logits);
+    }
+    st.key_cache = st.value_cache = st.d_qkv = st.d_out = st.d_logits = nullptr;
+    st.engine = nullptr;
+}
+
+}  // namespace detail
+
+void attention_block(::RunState& state, int layer, int pos)
 {
     if (!state.engine) throw std::runtime_error("attention_block: RunState not allocated");
     tla_engine* e = state.engine->get();
-    const std::size_t n = state.n_embd_ + 2 * static_cast<std::size_t>(state.kv_dim_);
+    const std::size_t n = state.n_embd + 2 * static_cast<std::size_t>(state.kv_dim);
     check(tla_memcpy_h2d(e, state.d_qkv, state.q, sizeof(float) * n), "q|k|v upload");
     const float* dq = state.d_qkv;
-    const float* dk = dq + state.n_embd_;
-    const float* dv = dk + state.kv_dim_;
+    const float* dk = dq + state.n_embd;
+    const float* dv = dk + state.kv_dim;
     check(tla_rope_attention(e, state.d_out, dq, dk, dv, state.key_cache, state.value_cache, layer,
                              pos),
           "rope+attention");
-    check(tla_memcpy_d2h(e, state.xb2, state.d_out, sizeof(float) * state.n_embd_),
+    check(tla_memcpy_d2h(e, state.xb2, state.d_out, sizeof(float) * state.n_embd),
           "attention output download");
 }
 
@@ -223,16 +272,16 @@ DeviceModel::~DeviceModel()
     for (void* b : buffers_) tla_free(engine.get(), b);
 }
 
-void forward(DeviceModel& model, RunState& state, int token, int pos)
+void forward(DeviceModel& model, ::RunState& state, int token, int pos)
 {
     if (!state.engine || !state.d_logits) throw std::runtime_error("forward: RunState not allocated with n_vocab");
     tla_engine* e = state.engine->get();
     check(tla_forward(e, &model.model, state.key_cache, state.value_cache, token, pos, state.d_logits),
           "forward");
-    check(tla_memcpy_d2h(e, state.logits, state.d_logits, sizeof(float) * state.n_vocab_), "logits download");
+    check(tla_memcpy_d2h(e, state.logits, state.d_logits, sizeof(float) * state.n_vocab), "logits download");
 }
 
-std::vector<int> generate_greedy(DeviceModel& model, RunState& state, const std::vector<int>& prompt,
+std::vector<int> generate_greedy(DeviceModel& model, ::RunState& state, const std::vector<int>& prompt,
                                  int n_gen, bool batch_prompt)
 {
     if (!state.engine) throw std::runtime_error("generate_greedy: RunState not allocated");

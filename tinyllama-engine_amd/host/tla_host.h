@@ -11,9 +11,10 @@
 //                                 src/ops.h:107, attention() src/ops.h:204-206,
 //                                 same argument order, device pointers, plus
 //                                 the engine that replaces `cfg`
-//   tla_host::RunState         -> struct RunState (src/run_state.h:27-182):
-//                                 same members in the same order; key_cache
-//                                 and value_cache hold DEVICE pointers; device
+//   ::RunState (run_state.h)   -> struct RunState (src/run_state.h:27-182),
+//                                 a drop-in for that header: the same global
+//                                 struct, members and lifecycle; key_cache and
+//                                 value_cache hold DEVICE pointers; device
 //                                 staging for the attention block is appended
 //                                 after the reference's members
 //   tla_host::attention_block  -> the block of forward() at
@@ -39,6 +40,10 @@
 #include <vector>
 
 #include "tla_attention.h"
+
+// The reference's own forward declaration (src/forward.h:11,
+// src/generate.h:6); defined in run_state.h.
+struct RunState;
 
 namespace tla_host {
 
@@ -81,51 +86,39 @@ void softmax(Engine& eng, float* x, int size);
 void attention(Engine& eng, float* out, const float* q, const float* k, const float* v,
                float* key_cache, float* value_cache, float* att, int layer, int pos);
 
-// ---- RunState ----------------------------------------------------------------
-struct RunState {
-    // Host scratch, as in the reference (the CPU GEMVs read and write these).
-    float* x = nullptr;
-    float* xb = nullptr;
-    float* xb2 = nullptr;
-    float* q = nullptr;
-    float* k = nullptr;
-    float* v = nullptr;
-    float* att = nullptr;
-    float* hb = nullptr;
-    float* hb2 = nullptr;
-    float* logits = nullptr;
-    // KV cache [n_layers][n_ctx][n_head_kv*head_dim] fp32 -- DEVICE memory.
-    float* key_cache = nullptr;
-    float* value_cache = nullptr;
-    int pos = 0;
+// ---- engines for RunState ------------------------------------------------------
+// The fields of a llama_config_t-like struct that the path reads.
+template <class Cfg>
+Config config_of(const Cfg& c)
+{
+    Config t;
+    t.n_layers = static_cast<std::uint32_t>(c.n_layers);
+    t.n_embd = static_cast<std::uint32_t>(c.n_embd);
+    t.n_head = static_cast<std::uint32_t>(c.n_head);
+    t.n_head_kv = static_cast<std::uint32_t>(c.n_head_kv);
+    t.n_ff = static_cast<std::uint32_t>(c.n_ff);
+    t.n_ctx = static_cast<std::uint32_t>(c.n_ctx);
+    t.n_vocab = static_cast<std::uint32_t>(c.n_vocab);
+    t.rope_freq_base = c.rope_freq_base;
+    return t;
+}
 
-    // ---- appended: device side of the attention block ----
-    Engine* engine = nullptr;
-    float* d_qkv = nullptr;  // device copy of q | k | v (one transfer)
-    float* d_out = nullptr;  // device attention output [n_embd]
-    float* d_logits = nullptr;  // device logits [n_vocab] (forward())
+// The engine RunState::allocate(cfg) uses: the one set here (which must have
+// cfg's attention shape; NULL clears), else one made for cfg on device 0 the
+// first time (one per distinct shape, kept for the rest of the process).
+void use_engine(Engine* eng);
+Engine& engine_for(const Config& cfg);
 
-    void allocate(const Config& cfg, Engine& eng);
-    void free_buffers();
-
-    RunState(const RunState&) = delete;
-    RunState& operator=(const RunState&) = delete;
-    RunState() = default;
-    ~RunState() { free_buffers(); }
-
-private:
-    friend void attention_block(RunState& state, int layer, int pos);
-    friend struct DeviceModel;
-    friend void forward(struct DeviceModel& model, RunState& state, int token, int pos);
-    float* qkv_host_ = nullptr;  // q | k | v contiguous, so one H2D copy
-    std::uint32_t n_embd_ = 0, kv_dim_ = 0, n_vocab_ = 0;
-};
+namespace detail {
+void allocate_state(::RunState& state, const Config& cfg, Engine& eng);
+void free_state(::RunState& state) noexcept;
+}  // namespace detail
 
 // rope(state.q, state.k, pos) + attention(state.xb2, ..., layer, pos) on the
 // device: one host->device copy of q|k|v, one fused launch sequence, one
 // device->host copy of the output into state.xb2.  state.q and state.k are
 // left unrotated on the host (forward() does not read them afterwards).
-void attention_block(RunState& state, int layer, int pos);
+void attention_block(::RunState& state, int layer, int pos);
 
 // ---- the projections and the FFN (device pointers) --------------------------
 void matmul(Engine& eng, float* out, const void* w, const float* x, int rows, int cols, int type);
@@ -169,11 +162,11 @@ private:
 
 // forward(model, state, token, pos): state.logits (host) receives the
 // n_vocab logits; the KV cache is state's (device).
-void forward(DeviceModel& model, RunState& state, int token, int pos);
+void forward(DeviceModel& model, ::RunState& state, int token, int pos);
 
 // Greedy generation on the device (prompt at positions 0.., token by token
 // or as one batch, then n_gen tokens); returns the generated tokens.
-std::vector<int> generate_greedy(DeviceModel& model, RunState& state, const std::vector<int>& prompt,
+std::vector<int> generate_greedy(DeviceModel& model, ::RunState& state, const std::vector<int>& prompt,
                                  int n_gen, bool batch_prompt = false);
 
 }  // namespace tla_host
