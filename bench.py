@@ -64,15 +64,40 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+# The sources each profiled kernel is built from: a profile records their
+# digest, and its byte count is used only while the sources are unchanged.
+KERNEL_SOURCES = {
+    "decode_split_kernel": ("decode.hip", "tla_internal.h", "rope_math.h"),
+    "prefill_attention_kernel": ("prefill.hip", "tla_internal.h", "rope_math.h"),
+    "gemv_kernel": ("gemv.hip", "tla_internal.h", "row_math.h", "rope_math.h"),
+}
+
+
+def kernel_source_digest(kernel):
+    """sha256 (first 16 hex digits) over the kernel's source files."""
+    import hashlib
+    h = hashlib.sha256()
+    for name in KERNEL_SOURCES[kernel]:
+        with open(os.path.join(ROOT, "tinyllama-engine_amd", "csrc", name), "rb") as f:
+            h.update(f.read())
+    return h.hexdigest()[:16]
+
+
 def profiled_traffic(kernel, workload):
     """HBM bytes per launch measured with rocprofv3 (FETCH_SIZE x2.0 +
     WRITE_SIZE x1.0, scaled by the copy-kernel calibration) and recorded in
-    profiles/<kernel>__<workload>.md, or None when not profiled."""
+    profiles/<kernel>__<workload>.md -- or None when not profiled, or when the
+    profile records a digest of the kernel's sources other than the current
+    one (the bytes would belong to another build)."""
     path = os.path.join(ROOT, "profiles", f"{kernel}__{workload}.md")
     if not os.path.exists(path):
         return None
-    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)\s*$", open(path).read(), re.M)
-    return int(m.group(1)) if m else None
+    text = open(path).read()
+    m = re.search(r"^traffic_bytes_per_launch:\s*(\d+)\s*$", text, re.M)
+    d = re.search(r"^source_digest:\s*([0-9a-f]+)\s*$", text, re.M)
+    if not m or not d or d.group(1) != kernel_source_digest(kernel):
+        return None
+    return int(m.group(1))
 
 
 def median(xs):
@@ -747,7 +772,12 @@ def main():
                     help="(default) also measure decode_long, decode_ragged and decode_single")
     ap.add_argument("--no-extra", action="store_true",
                     help="skip the other decode workloads in the default line")
+    ap.add_argument("--source-digest", metavar="KERNEL", choices=sorted(KERNEL_SOURCES),
+                    help="print the digest of a kernel's sources (recorded in its profiles) and exit")
     args = ap.parse_args()
+    if args.source_digest:
+        print(kernel_source_digest(args.source_digest))
+        return
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU only: the library has no multi-GPU path "
