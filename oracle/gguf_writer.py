@@ -20,7 +20,20 @@ def _str(s: str) -> bytes:
     return struct.pack("<Q", len(b)) + b
 
 
-def write_gguf(path, spec, tensors, alignment: int = 32):
+def byte_vocab(n_vocab: int) -> list:
+    """A vocabulary the reference's tokenizer can load and encode any text
+    with: its three special tokens (src/tokenizer.cpp:25-27), the 256 byte
+    tokens "<0xNN>" of its byte fallback (src/tokenizer.cpp:153-160), then
+    filler pieces up to n_vocab."""
+    assert n_vocab >= 259
+    toks = ["<unk>", "<s>", "</s>"] + [f"<0x{b:02X}>" for b in range(256)]
+    return toks + [f"\u2581w{i}" for i in range(n_vocab - len(toks))]
+
+
+def write_gguf(path, spec, tensors, alignment: int = 32, vocab=None):
+    """vocab: None, or token strings written as tokenizer.ggml.tokens (with
+    zero tokenizer.ggml.scores), which the reference's loader reads into its
+    tokenizer (src/gguf_model.cpp:414-460)."""
     kv = [
         ("general.architecture", GGUF_STRING, _str("llama")),
         ("general.alignment", GGUF_UINT32, struct.pack("<I", alignment)),
@@ -35,6 +48,11 @@ def write_gguf(path, spec, tensors, alignment: int = 32):
         ("llama.attention.layer_norm_rms_epsilon", GGUF_FLOAT32,
          struct.pack("<f", spec.rms_norm_eps)),
     ]
+    if vocab is not None:
+        kv.append(("tokenizer.ggml.tokens", GGUF_ARRAY,
+                   struct.pack("<IQ", GGUF_STRING, len(vocab)) + b"".join(_str(t) for t in vocab)))
+        kv.append(("tokenizer.ggml.scores", GGUF_ARRAY,
+                   struct.pack("<IQ", GGUF_FLOAT32, len(vocab)) + b"\0" * (4 * len(vocab))))
     head = bytearray(b"GGUF" + struct.pack("<IQQ", 3, len(tensors), len(kv)))
     for key, ty, val in kv:
         head += _str(key) + struct.pack("<I", ty) + val
