@@ -11,7 +11,7 @@ tla = importlib.import_module("tinyllama-engine_amd")
 
 ORACLE_THREADS = min(16, os.cpu_count() or 4)
 
-# Tolerances.  Decode: the north-star bound, max-abs 1e-4 against the
+# Tolerances.  Decode: the path's stated bound, max-abs 1e-4 against the
 # reference's fp32 attention.  Prefill: fp32 MFMA products with fp32
 # accumulation in a different order than the reference's sequential loops;
 # measured error is ~1e-6 on N(0,1) inputs, bound stated at 1e-4.
