@@ -289,12 +289,23 @@ float scale_log2(int head_dim)
 // units) 70.8 % aligned, 66.6 % balanced.  Hence: aligned when it fits one
 // round; otherwise balanced when a range is no longer than the shortest
 // unit (so it crosses at most one boundary), else aligned.
+//
+// Below 64 positions per split a launch is latency-bound: one tile costs a
+// wave ~1,000 cycles of MFMA (half of it the GQA padding columns), a second
+// batch of tiles a memory round trip, and a split merge ~2 us.  Same-box
+// A/B, back-to-back launches, 1 / 8 / 22 layers (append path; the
+// attention-only path alike): sequences of up to 128 positions as one
+// split each, 6.6-6.9 us at 128 positions against 7.3-7.7 us in splits of
+// 64; of 129-256 positions in splits of 32, 6.5 / 7.6 / 9.9 us at 256
+// against 7.1 / 7.6 / 10.1 us in splits of 64; longer ones in splits of 64
+// (1 layer at 1024: 7.8 us, 8.9 us in splits of 32).
 long long aligned_wg_tiles(long long total_positions, int max_len, int n_cu)
 {
     const long long target = std::max(1, n_cu - n_cu / 16);
     long long s = (total_positions + target - 1) / target;
+    if (s < 64) s = max_len <= 128 ? max_len : max_len <= 256 ? 32 : 64;
     s = std::min<long long>(s, max_len);
-    s = std::min<long long>(std::max<long long>(s, 64), 4096);
+    s = std::min<long long>(std::max<long long>(s, 16), 4096);
     return (s + kDecodeTile - 1) / kDecodeTile;
 }
 
