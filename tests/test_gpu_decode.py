@@ -196,6 +196,19 @@ def test_batch_call_equals_per_sequence_calls(O, W, engines):
         assert max_err(single[0], ref[s]) <= DECODE_TOL
 
 
+@pytest.mark.parametrize("n_seq", [8, 9, 256])
+def test_batch_sizes_at_the_argument_limits(O, W, engines, n_seq):
+    """Batches at the kernel-argument boundaries: 8 sequences (the small
+    argument block and its unrolled rank scan), 9 (the first batch that
+    takes the 256-sequence block and the binary search over ranks) and 256
+    (the most one call takes), with ragged lengths including position 0."""
+    rg = np.random.default_rng(1000 + n_seq)
+    pos = rg.integers(0, 512, n_seq)
+    pos[0], pos[-1] = 0, 511
+    case = W.make_decode(33, n_seq, 1, 512, pos, salt=n_seq)
+    check_decode(O, engines(1, 512), case)
+
+
 def test_decode_is_deterministic(W, engines):
     case = W.make_decode(14, 2, 2, 2048, [2047, 999])
     a, _, _ = gpu_decode(engines(2, 2048), case)
