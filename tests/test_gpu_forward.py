@@ -170,6 +170,14 @@ def test_argmax(O, engines):
     cases.append(np.full(100, -np.inf, np.float32))
     cases.append(np.array([2.5], np.float32))
     cases.append(np.concatenate([np.zeros(1025, np.float32), [1.0]]).astype(np.float32))
+    # past one batch of loads per thread (32768 entries): the maximum in the
+    # last batch, then at the first entry of the second
+    big = rg.standard_normal(70001).astype(np.float32)
+    big[70000] = 9.0
+    cases.append(big)
+    edge = rg.standard_normal(32769).astype(np.float32)
+    edge[32768] = 9.0
+    cases.append(edge)
     lib = O.oracle()
     from oracle import fptr
     for c in cases:

@@ -849,16 +849,20 @@ __global__ __launch_bounds__(1024) void argmax_kernel(int* out, int* out2, const
     __shared__ int s_i[16];
     float bv = -__builtin_huge_valf();
     int bi = 0x7fffffff;
-    // eight independent loads in flight per thread
-    for (int i0 = threadIdx.x; i0 < n; i0 += 8 * 1024) {
-        float v[8];
+    // x[0] (for the NaN rule below) goes out with the first batch
+    const float x0 = x[0];
+    // 32 independent loads in flight per thread: a 32768-entry vocabulary
+    // is one round trip
+    constexpr int kPer = 32;
+    for (int i0 = threadIdx.x; i0 < n; i0 += kPer * 1024) {
+        float v[kPer];
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < kPer; ++j) {
             const int i = i0 + j * 1024;
             v[j] = x[i < n ? i : i0];
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
+        for (int j = 0; j < kPer; ++j) {
             const int i = i0 + j * 1024;
             if (i < n && beats(v[j], i, bv, bi)) {
                 bv = v[j];
@@ -888,7 +892,6 @@ __global__ __launch_bounds__(1024) void argmax_kernel(int* out, int* out2, const
             }
         // nothing above -inf: index 0 (where the scan starts); a NaN at index
         // 0 is never beaten in the reference's scan, so 0 as well
-        const float x0 = x[0];
         const int r = (bi == 0x7fffffff || x0 != x0) ? 0 : bi;
         *out = r;
         if (out2) *out2 = r;
