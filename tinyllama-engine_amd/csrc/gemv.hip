@@ -901,28 +901,32 @@ __global__ __launch_bounds__(1024) void argmax_kernel(int* out, int* out2, const
 // Workgroups of one kernel that fit on the current device at once (its CU
 // count x the occupancy the kernel's registers and LDS allow), cached per
 // device and LDS size.
+// Workgroups of one launch: as many as fit on the GPU at once, or, with
+// `two_per_cu`, at most two per CU.
 template <typename Kernel>
-int resident_blocks(Kernel kernel, size_t lds)
+int resident_blocks(Kernel kernel, size_t lds, bool two_per_cu)
 {
     struct Entry {
         int device = -1;
         size_t lds = 0;
         int blocks = 0;
+        int cus = 0;
     };
     static thread_local Entry cache[4];
     int dev = 0;
     if (hipGetDevice(&dev) != hipSuccess) return 256;
     for (const Entry& e : cache)
-        if (e.device == dev && e.lds == lds) return e.blocks;
+        if (e.device == dev && e.lds == lds) return two_per_cu ? std::min(e.blocks, 2 * e.cus) : e.blocks;
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
         hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, kernel, kThreads, lds) != hipSuccess)
         return 256;
-    const int blocks = std::max(1, cus * std::max(1, per_cu));
+    cus = std::max(1, cus);
+    const int blocks = cus * std::max(1, per_cu);
     static thread_local int next = 0;
-    cache[next] = Entry{dev, lds, blocks};
+    cache[next] = Entry{dev, lds, blocks, cus};
     next = (next + 1) % 4;
-    return blocks;
+    return two_per_cu ? std::min(blocks, 2 * cus) : blocks;
 }
 
 template <int kType, int kLanes, int kRows, int kSteps, bool kMulti, int kEpi = kPlain>
@@ -932,7 +936,15 @@ hipError_t launch_shaped(const GemvParams& p, hipStream_t s)
     constexpr int kPassRowsPerBlock = (kThreads / 64) * (64 / kLanes) * kRows;
     const int needed = (p.total_rows + kPassRowsPerBlock - 1) / kPassRowsPerBlock;
     const auto kernel = gemv_kernel<kType, kLanes, kRows, kSteps, kMulti, kEpi>;
-    const int blocks = std::min(needed, resident_blocks(kernel, lds));
+    // A launch whose x goes through a prologue (rmsnorm, SwiGLU) takes at
+    // most two workgroups per CU: every workgroup stages and normalises x
+    // itself, and fewer, equal shares per CU measured faster.  MI355X, greedy
+    // decode at TinyLlama shapes (the rmsnorm + gate/up launch: 704 -> 512
+    // workgroups; the classifier: its resident grid -> 512): Q4_0 579-588
+    // against 598-601 us per token, Q8_0 645 against 656, F16 790 against
+    // 806.  Launches without a prologue keep the resident grid (the 32000 x
+    // 2048 GEMV alone: F16, F32, Q6_K 0.7-1.2 % slower with the cap).
+    const int blocks = std::min(needed, resident_blocks(kernel, lds, p.norm_w != nullptr || p.x2 != nullptr));
     hipLaunchKernelGGL(kernel, dim3(blocks), dim3(kThreads), lds, s, p);
     return hipGetLastError();
 }
