@@ -44,6 +44,22 @@ __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c)
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
 }
 
+// The two halves of a wave (lanes l and l ^ 32) meet in registers:
+// v_permlane32_swap (gfx950) of x with a copy of x leaves [x_lo, x_lo] in one
+// and [x_hi, x_hi] in the other, so combining the two combines every lane
+// with its partner -- no LDS round trip, as a cross-lane shuffle would take.
+// Written as register-only inline asm: through the compiler's builtin, the
+// two results of the instruction were folded into one (ROCm 7.2), so a sum of
+// both halves read one half twice.  The s_nop pairs cover the instruction's
+// VALU read / write hazards, which the compiler does not track inside asm.
+__device__ __forceinline__ void halves(float x, float& lo, float& hi)
+{
+    unsigned a = __builtin_bit_cast(unsigned, x), b = a;
+    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
+    lo = __builtin_bit_cast(float, a);
+    hi = __builtin_bit_cast(float, b);
+}
+
 __global__ __launch_bounds__(256) void prefill_append_kernel(const PrefillParams p)
 {
     const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
@@ -194,7 +210,11 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
         float mx = s[0];
 #pragma unroll
         for (int gi = 1; gi < 16; ++gi) mx = fmaxf(mx, s[gi]);
-        mx = fmaxf(mx, __shfl_xor(mx, 32));
+        {
+            float lo, hi;
+            halves(mx, lo, hi);
+            mx = fmaxf(lo, hi);
+        }
         // The running max only moves when some row's tile max exceeds it by
         // more than 2^8: probabilities then stay <= 256 and the sums in fp32
         // range, and most tiles skip the rescale of O.  The result is the
@@ -216,14 +236,35 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
         l_run += lsum;
     };
     // O^T += V^T.P^T for the tile in V buffer b (V operand: lane holds
-    // V[8*(gi/4) + 4*half + gi%4][2*col + dt]).
+    // V[8*(gi/4) + 4*half + gi%4][2*col + dt]).  The operands come in four
+    // groups of four gi, two groups in registers: the first two are read at
+    // the top of the step (vread_head, before the next tile's scores and this
+    // tile's softmax), each later one while the group before it is in the
+    // MFMAs, so no MFMA pair waits on an LDS round trip.  The scheduling
+    // barriers keep the compiler from sinking the reads to their uses.
+    float2 vv[2][4];
+    auto vread = [&](int b, int g, float2* dst) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+            dst[i] = *reinterpret_cast<const float2*>(&sv[b][8 * g + 4 * half + i][2 * col]);
+    };
+    auto vread_head = [&](int b) {
+        vread(b, 0, vv[0]);
+        vread(b, 1, vv[1]);
+        __builtin_amdgcn_sched_barrier(0);
+    };
     auto accumulate = [&](const floatx16& s, int b) {
 #pragma unroll
-        for (int gi = 0; gi < 16; ++gi) {
-            const int kin = 8 * (gi >> 2) + 4 * half + (gi & 3);
-            const float2 vv = *reinterpret_cast<const float2*>(&sv[b][kin][2 * col]);
-            o0 = mfma32(vv.x, s[gi], o0);
-            o1 = mfma32(vv.y, s[gi], o1);
+        for (int g = 0; g < 4; ++g) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                o0 = mfma32(vv[g & 1][i].x, s[4 * g + i], o0);
+                o1 = mfma32(vv[g & 1][i].y, s[4 * g + i], o1);
+            }
+            if (g + 2 < 4) {
+                vread(b, g + 2, vv[g & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
     };
 
@@ -249,6 +290,7 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     int j = 0;
     for (; j < n_plain; ++j) {
         if (computes) {
+            vread_head(j & 1);
             const floatx16 s_next = scores((j + 1) & 1);
             softmax(s_cur, j * kKTile, false);
             accumulate(s_cur, j & 1);
@@ -264,6 +306,7 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
         const bool more = j + 1 < n_kt;  // uniform
         if (computes) {
             floatx16 s_next = {};  // unused after the last tile
+            vread_head(j & 1);
             if (more) s_next = scores((j + 1) & 1);
             softmax(s_cur, j * kKTile, true);
             accumulate(s_cur, j & 1);
@@ -279,7 +322,11 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     }
 
     if (!computes) return;
-    l_run += __shfl_xor(l_run, 32);
+    {
+        float lo, hi;
+        halves(l_run, lo, hi);
+        l_run = lo + hi;
+    }
     if (i0 + col >= p.n_tok) return;
     const float inv = 1.0f / l_run;
     // o_dt[4a+b] = O[row][16a + 8*half + 2b + dt]
