@@ -67,8 +67,8 @@ def log(msg):
 # The sources each profiled kernel is built from: a profile records their
 # digest, and its byte count is used only while the sources are unchanged.
 KERNEL_SOURCES = {
-    "decode_split_kernel": ("decode.hip", "tla_internal.h", "rope_math.h"),
-    "prefill_attention_kernel": ("prefill.hip", "tla_internal.h", "rope_math.h"),
+    "decode_split_kernel": ("decode.hip", "tla_internal.h", "rope_math.h", "lane_math.h"),
+    "prefill_attention_kernel": ("prefill.hip", "tla_internal.h", "rope_math.h", "lane_math.h"),
     "gemv_kernel": ("gemv.hip", "tla_internal.h", "row_math.h", "rope_math.h"),
 }
 

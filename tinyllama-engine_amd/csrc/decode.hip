@@ -59,6 +59,7 @@
 // LDS; a balanced-plan workgroup defers its arrivals to the end of its
 // range and reads every partial from the workspace.  Either way the sums
 // do not depend on which workgroup merges.  One launch per step.
+#include "lane_math.h"
 #include "rope_math.h"
 #include "tla_internal.h"
 
@@ -457,8 +458,7 @@ __global__ __launch_bounds__(64 * kSub * kKvWaves) void decode_split_kernel(
                     sc[r] = (kp < end) ? s[r] * p.scale_log2 : -INFINITY;
                     mx = fmaxf(mx, sc[r]);
                 }
-                mx = fmaxf(mx, __shfl_xor(mx, 16));
-                mx = fmaxf(mx, __shfl_xor(mx, 32));
+                mx = max_xor32(max_xor16(mx));  // the tile's 16 positions (lane groups)
                 const float m_new = fmaxf(m_run, mx);
                 const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
                 m_run = m_new;
@@ -544,8 +544,7 @@ __global__ __launch_bounds__(64 * kSub * kKvWaves) void decode_split_kernel(
             }
 
             // Row sums: each lane group summed different positions of the same head.
-            l_run += __shfl_xor(l_run, 16);
-            l_run += __shfl_xor(l_run, 32);
+            l_run = sum_xor32(sum_xor16(l_run));
         }
 
         // The two halves of each kv head meet in LDS; the first half continues.

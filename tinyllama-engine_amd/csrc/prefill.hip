@@ -26,6 +26,7 @@
 //   (workgroup i runs on XCD i % 8) to share that XCD's L2, and each XCD
 //   starts the query tiles with the most key tiles first, across all of its
 //   (layer, kv head) pairs, so the last workgroups to start are short ones.
+#include "lane_math.h"
 #include "rope_math.h"
 #include "tla_internal.h"
 
@@ -42,22 +43,6 @@ constexpr int kXcds = 8;
 __device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c)
 {
     return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
-
-// The two halves of a wave (lanes l and l ^ 32) meet in registers:
-// v_permlane32_swap (gfx950) of x with a copy of x leaves [x_lo, x_lo] in one
-// and [x_hi, x_hi] in the other, so combining the two combines every lane
-// with its partner -- no LDS round trip, as a cross-lane shuffle would take.
-// Written as register-only inline asm: through the compiler's builtin, the
-// two results of the instruction were folded into one (ROCm 7.2), so a sum of
-// both halves read one half twice.  The s_nop pairs cover the instruction's
-// VALU read / write hazards, which the compiler does not track inside asm.
-__device__ __forceinline__ void halves(float x, float& lo, float& hi)
-{
-    unsigned a = __builtin_bit_cast(unsigned, x), b = a;
-    asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1\n\ts_nop 1" : "+v"(a), "+v"(b));
-    lo = __builtin_bit_cast(float, a);
-    hi = __builtin_bit_cast(float, b);
 }
 
 __global__ __launch_bounds__(256) void prefill_append_kernel(const PrefillParams p)
@@ -210,11 +195,7 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
         float mx = s[0];
 #pragma unroll
         for (int gi = 1; gi < 16; ++gi) mx = fmaxf(mx, s[gi]);
-        {
-            float lo, hi;
-            halves(mx, lo, hi);
-            mx = fmaxf(lo, hi);
-        }
+        mx = max_xor32(mx);  // the other half of the keys
         // The running max only moves when some row's tile max exceeds it by
         // more than 2^8: probabilities then stay <= 256 and the sums in fp32
         // range, and most tiles skip the rescale of O.  The result is the
@@ -322,11 +303,7 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     }
 
     if (!computes) return;
-    {
-        float lo, hi;
-        halves(l_run, lo, hi);
-        l_run = lo + hi;
-    }
+    l_run = sum_xor32(l_run);
     if (i0 + col >= p.n_tok) return;
     const float inv = 1.0f / l_run;
     // o_dt[4a+b] = O[row][16a + 8*half + 2b + dt]
