@@ -36,7 +36,9 @@ device copy kernel, used to calibrate rocprofv3 byte counters), read (a
 plain library reduction over 6 GiB) and read_floor (this package's streaming
 read over exactly the bytes of a batch-1 decode step at 2K-16K context: what
 one launch can move in that time, the ceiling the decode step sits under;
-also in the default line's extra).
+also in the default line's extra) and mfma_floor (this package's fp32 MFMA
+loop over the prefill kernel's executed flops: the ceiling the prefill
+kernel sits under; also in the default line's prefill entry).
 """
 from __future__ import annotations
 
@@ -726,6 +728,51 @@ def run_read_floor(steps, warmup, contexts=(2048, 4096, 8192, 16384), n_layers=2
     return out
 
 
+MFMA_FLOOR_GRIDS = (768, 1024, 2048)
+MFMA_FLOOR_WG_FLOPS = 4 * 16 * 2 * 32 * 32 * 2  # per workgroup and round: 4 waves x 16 MFMAs
+
+
+def prefill_executed_flops(n_tok=512, n_layers=22, n_head=32, tile=32, head_dim=64):
+    """fp32 MFMA flops the prefill kernel executes (diagonal tiles whole):
+    per (layer, head), n_qt (n_qt + 1) / 2 tile pairs of 32 queries x 32 keys,
+    two products of 2 x 32 x 32 x head_dim flops each."""
+    n_qt = -(-n_tok // tile)
+    return n_layers * n_head * n_qt * (n_qt + 1) // 2 * 2 * (2 * tile * tile * head_dim)
+
+
+def run_mfma_floor(steps, warmup, flops=None):
+    """The hand-written fp32 MFMA loop (tla_mfma_floor) executing as many
+    v_mfma_f32_32x32x2f32 flops as the 512-token, 22-layer prefill kernel
+    (its diagonal tiles counted whole), launches back to back; the best of a
+    few grid sizes, each after the prefill workload's warmup.  What one
+    launch can execute in the time it takes: the bar for the prefill
+    kernel."""
+    flops = flops or prefill_executed_flops()
+    warmup = max(warmup, PREFILL_MIN_WARMUP)  # the clocks ramp under sustained MFMA work
+    eng = tla.Engine(tla.Config.tinyllama(n_layers=1, n_ctx=16))
+    sink = eng.array((max(MFMA_FLOOR_GRIDS),))
+    best = None
+    for grid in MFMA_FLOOR_GRIDS:
+        iters = max(1, round(flops / (grid * MFMA_FLOOR_WG_FLOPS)))
+
+        def one(i, grid=grid, iters=iters):
+            eng.mfma_floor(grid, iters, sink.ptr)
+        for i in range(warmup):
+            one(i)
+        ms = back_to_back_ms(eng, one, steps)
+        done = grid * iters * MFMA_FLOOR_WG_FLOPS
+        tf = done / (ms * 1e-3) / 1e12
+        if best is None or tf > best["TFLOP_s"]:
+            best = {"flops": done, "us": round(ms * 1e3, 2), "TFLOP_s": round(tf, 2),
+                    "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "workgroups": grid, "iters": iters}
+    log(f"[bench] mfma floor {best['flops'] / 1e9:.2f} GFLOP (the 512-token prefill kernel's executed "
+        f"fp32 MFMA work): {best['us']:.1f} us with {best['workgroups']} workgroups -> "
+        f"{best['TFLOP_s']:.1f} TFLOP/s ({best['frac']:.1%} of {FP32_MFMA_PEAK_TFLOPS})")
+    sink.free()
+    eng.close()
+    return best
+
+
 def run_read(steps, warmup, nbytes=6 << 30):
     """HBM read ceiling: torch's sum over an nbytes float32 tensor (a library
     streaming reduction, none of this package's kernels), timed with events on torch's
@@ -760,7 +807,7 @@ def main():
     ap.add_argument("--workload", default="decode_model",
                     choices=["decode_model", "decode_long", "decode_ragged", "decode_single",
                              "prefill", "proj", "matmul", "generate", "decode_sweep",
-                             "prefill_sweep", "copy", "read", "read_floor"])
+                             "prefill_sweep", "copy", "read", "read_floor", "mfma_floor"])
     ap.add_argument("--wtype", default=None, choices=["f32", "f16", "q8_0", "q4_0", "q6_k"],
                     help="weight format of the matmul (default q8_0) or generate (q4_0) workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -800,6 +847,20 @@ def main():
                           "config": {"workload": "read_floor", "bytes": "decode batch 1 x 22 layers",
                                      "contexts": [x["ctx"] for x in r], "parallelism": "none"},
                           "sweep": r}))
+        return
+    if args.workload == "mfma_floor":
+        r = run_mfma_floor(args.steps, args.warmup)
+        print(json.dumps({"metric": "fp32 MFMA floor TFLOP/s (% MFMA peak)", "value": r["TFLOP_s"],
+                          "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+                          "ms_per_step": r["us"] / 1e3, "higher_is_better": True, "scaling": "weak",
+                          "vs_baseline": None, "dtype": "f32", "data": "synthetic",
+                          "config": {"workload": "mfma_floor",
+                                     "flops": "the 512-token x 22-layer prefill kernel's executed MFMA work",
+                                     "parallelism": "none"},
+                          "roofline": {"bound": "mfma", "achieved": r["TFLOP_s"],
+                                       "peak": FP32_MFMA_PEAK_TFLOPS, "unit": "TFLOP/s",
+                                       "frac": r["frac"], "traffic": None},
+                          "floor": r}))
         return
     if args.workload == "decode_sweep":
         r = run_decode_sweep(args.steps, args.warmup, plan=PLANS[args.plan])
@@ -914,6 +975,12 @@ def main():
         line["prefill"]["config"] = {"workload": "prefill", "n_tok": 512, "n_layers": 22}
         if cpu:
             line["prefill"]["cpu_baseline"] = p["cpu_baseline"]
+        # what one launch can execute of the same fp32 MFMA work, and the
+        # prefill kernel's time over it
+        mf = run_mfma_floor(args.steps, args.warmup)
+        line["prefill"]["mfma_floor"] = mf
+        line["prefill"]["kernel_over_mfma_floor"] = round(
+            mf["us"] * (prefill_executed_flops() / mf["flops"]) / (p["prefill_kernel_ms"] * 1e3), 4)
     if not args.no_extra and args.workload == "decode_model":
         # the other decode configurations, measured the same way (no CPU
         # baseline): long context x 8 and the ragged batch as HBM

@@ -131,6 +131,23 @@ def test_cpp_host_side_program():
     assert " 0 failed" in r.stdout
 
 
+def test_mfma_floor_runs_and_leaves_the_sink(tla, engines):
+    """The fp32 MFMA floor hook: runs a few grids and round counts, never
+    writes its sink for its own operands, and validates its arguments before
+    launching."""
+    eng = engines(1, 64)
+    with device_arrays() as track:
+        sink = track(eng.array(np.full(1024, 7.0, np.float32)))
+        for grid, iters in ((1, 1), (768, 3), (1024, 1)):
+            eng.mfma_floor(grid, iters, sink.ptr)
+        eng.synchronize()
+        assert np.all(sink.download() == 7.0)
+        for grid, iters, ptr in ((0, 1, sink.ptr), (4, 0, sink.ptr), (4, 1, 0)):
+            with pytest.raises(tla.TlaError) as e:
+                eng.mfma_floor(grid, iters, ptr)
+            assert e.value.code == tla.TLA_ERR_INVALID_ARGUMENT
+
+
 def test_read_floor_reads_and_leaves_the_sink(tla, engines):
     """The streaming-read hook: runs over an odd byte count and grid, never
     writes its sink for ordinary data, and validates its arguments before

@@ -147,6 +147,7 @@ SIGNATURES = {
     "tla_event_elapsed": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "tla_set_option": (C.c_int, [_vp, C.c_int, C.c_longlong]),
     "tla_read_floor": (C.c_int, [_vp, _vp, C.c_size_t, C.c_int, _vp]),
+    "tla_mfma_floor": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
 }
 
 
@@ -365,6 +366,9 @@ class Engine:
 
     def read_floor(self, src: int, nbytes: int, n_workgroups: int, sink: int):
         _check(lib().tla_read_floor(self.h, src, nbytes, n_workgroups, sink), "tla_read_floor")
+
+    def mfma_floor(self, n_workgroups: int, iters: int, sink: int):
+        _check(lib().tla_mfma_floor(self.h, n_workgroups, iters, sink), "tla_mfma_floor")
 
     def event(self, slot: int):
         _check(lib().tla_event_record(self.h, slot), "tla_event_record")

@@ -14,6 +14,14 @@
 
 #include "tla_internal.h"
 
+namespace tla {
+// fp32 MFMA floor (small_ops.hip): n_wg workgroups of 4 waves, each wave
+// iters x 16 v_mfma_f32_32x32x2f32; sink [n_wg] is never written in practice.
+// Declared here, not in tla_internal.h: that header is part of the decode,
+// prefill and GEMV kernels' source digests, and this launcher is not.
+hipError_t launch_mfma_floor(int n_wg, int iters, float* sink, hipStream_t s);
+}  // namespace tla
+
 using namespace tla;
 
 namespace {
@@ -1595,6 +1603,20 @@ int tla_read_floor(tla_engine* e, const void* src_dev, size_t bytes, int n_workg
     if (int rc = set_device(e)) return rc;
     const hipError_t err = launch_read_floor(src_dev, bytes, n_workgroups, sink_dev, e->stream);
     if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "read floor launch: %s", hipGetErrorString(err));
+    return ok();
+}
+
+int tla_mfma_floor(tla_engine* e, int n_workgroups, int iters, float* sink_dev)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!sink_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (n_workgroups < 1 || n_workgroups > (1 << 20))
+        return fail(TLA_ERR_INVALID_ARGUMENT, "n_workgroups %d not in [1, 2^20]", n_workgroups);
+    if (iters < 1 || iters > (1 << 20))
+        return fail(TLA_ERR_INVALID_ARGUMENT, "iters %d not in [1, 2^20]", iters);
+    if (int rc = set_device(e)) return rc;
+    const hipError_t err = launch_mfma_floor(n_workgroups, iters, sink_dev, e->stream);
+    if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "mfma floor launch: %s", hipGetErrorString(err));
     return ok();
 }
 

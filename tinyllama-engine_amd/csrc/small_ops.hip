@@ -126,7 +126,49 @@ __global__ __launch_bounds__(256) void read_floor_kernel(const float4* __restric
     if (acc == -1234.5f) sink[blockIdx.x] = acc;
 }
 
+// fp32 MFMA floor: each wave runs `iters` rounds of 16 v_mfma_f32_32x32x2f32
+// on two independent accumulators, operands pseudo-random per lane (so the
+// matrix cores see real bit patterns), and writes its sum only if it equals a
+// value no sum of these operands takes, so that the work stays but nothing is
+// written.  The fastest a single launch can execute a given number of fp32
+// MFMA flops: 2 x 32 x 32 x 2 per instruction.
+typedef float floatx16_t __attribute__((ext_vector_type(16)));
+
+__global__ __launch_bounds__(256) void mfma_floor_kernel(int iters, float* __restrict__ sink)
+{
+    floatx16_t c0, c1;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) { c0[i] = 0.f; c1[i] = 0.f; }
+    float r[16];
+    unsigned h = threadIdx.x * 2654435761u + blockIdx.x * 40503u + 12345u;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        h ^= h << 13;
+        h ^= h >> 17;
+        h ^= h << 5;
+        r[i] = (float)(int)(h & 0xffffff) * (1.0f / 8388608.0f) - 1.0f;
+    }
+    for (int it = 0; it < iters; ++it) {
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(r[(2 * u) & 15], r[(2 * u + 7) & 15], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(r[(2 * u + 1) & 15], r[(2 * u + 8) & 15], c1, 0, 0, 0);
+        }
+    }
+    float acc = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) acc += c0[i] + c1[i];
+    if (acc == -1234.5f) sink[blockIdx.x] = acc;
+}
+
 }  // namespace
+
+hipError_t launch_mfma_floor(int n_wg, int iters, float* sink, hipStream_t s)
+{
+    if (n_wg < 1 || iters < 1) return hipErrorInvalidValue;
+    hipLaunchKernelGGL(mfma_floor_kernel, dim3((unsigned)n_wg), dim3(256), 0, s, iters, sink);
+    return hipGetLastError();
+}
 
 hipError_t launch_read_floor(const void* src, size_t bytes, int n_wg, float* sink, hipStream_t s)
 {
