@@ -72,7 +72,28 @@ struct PrefillGrid {
     int n_hg;     // head groups of 4 waves per kv head
     int n_pairs;  // n_lb * n_head_kv
     int per_xcd;  // workgroup slots per XCD: ceil(n_pairs / 8) * n_hg * n_qt
+    // Quotients by the launch's divisors as multiply-highs: q = mulhi(n, m)
+    // with m = ceil(2^32 / d), exact for n * d < 2^32 (checked at launch); a
+    // divisor of 1 has m = 0 and takes q = n.  The XCDs below n_pairs % 8
+    // (all when it is 0) hold ceil(n_pairs / 8) pairs, the others one fewer.
+    unsigned m_rank_big, m_rank_small;  // pairs per XCD x n_hg
+    unsigned m_hg;                      // n_hg
+    unsigned m_kv;                      // n_head_kv
 };
+
+// The rotation of rotate4 with fused multiply-adds: 8 operations per float4
+// instead of 12, each output within an ulp or so of the separately rounded
+// form.  For operands that are not stored (q).
+__device__ __forceinline__ float4 rotate4_fma(float4 x, float4 cs)
+{
+    return make_float4(__builtin_fmaf(x.x, cs.x, -(x.y * cs.y)), __builtin_fmaf(x.x, cs.y, x.y * cs.x),
+                       __builtin_fmaf(x.z, cs.z, -(x.w * cs.w)), __builtin_fmaf(x.z, cs.w, x.w * cs.z));
+}
+
+__device__ __forceinline__ unsigned div_magic(unsigned n, unsigned m)
+{
+    return m ? __umulhi(n, m) : n;
+}
 
 constexpr float kRescaleSlack = 8.f;  // log2 units
 constexpr int kRowPad = 68;  // LDS row stride (floats): 64 + 4 keeps operand reads conflict-free
@@ -89,16 +110,22 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     // of b / 8.  (layer, kv head) pair i belongs to XCD i % 8, so all query
     // tiles of a pair share one L2; within an XCD, query tiles are handed out
     // longest first (most key tiles) across all its pairs.
+    // The quotients are multiply-highs on scalar registers: a workgroup that
+    // starts beside two MFMA-bound waves gets few vector issue slots, and
+    // the compiler's divisions go through the vector unit.
     const int xcd = blockIdx.x % kXcds;
     const int slot = blockIdx.x / kXcds;
     const int xcd_pairs = (g.n_pairs - xcd + kXcds - 1) / kXcds;
+    const bool big = xcd_pairs * kXcds >= g.n_pairs;  // this XCD holds ceil(n_pairs / 8) pairs
     const int per_rank = xcd_pairs * g.n_hg;
     if (slot >= per_rank * g.n_qt) return;  // whole workgroup
-    const int qt = g.n_qt - 1 - slot / per_rank;
-    const int rem = slot - (slot / per_rank) * per_rank;
-    const int pair = xcd + kXcds * (rem / g.n_hg);  // (lb, kvh)
-    const int hg = rem % g.n_hg;
-    const int lb = pair / p.n_head_kv;
+    const int rank = (int)div_magic((unsigned)slot, big ? g.m_rank_big : g.m_rank_small);
+    const int qt = g.n_qt - 1 - rank;
+    const int rem = slot - rank * per_rank;
+    const int pg = (int)div_magic((unsigned)rem, g.m_hg);
+    const int pair = xcd + kXcds * pg;  // (lb, kvh)
+    const int hg = rem - pg * g.n_hg;
+    const int lb = (int)div_magic((unsigned)pair, g.m_kv);
     const int kvh = pair - lb * p.n_head_kv;
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
@@ -152,11 +179,15 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
             qv[f] = ldg4(qrow + 4 * f);
             cs[f] = ldg4(tab + 2 * (16 * half + 2 * f));
         }
+        // Scaled first, then rotated with fused multiply-adds: q only enters
+        // the scores, so it needs the reference's accuracy, not its bits (the
+        // cache rows, which must match bit for bit, are rotated by the append
+        // kernel), and the new wave does this with few vector issue slots.
 #pragma unroll
         for (int f = 0; f < 8; ++f) {
-            const float4 x = p.rotate ? rotate4(qv[f], cs[f]) : qv[f];
-            qv[f] = make_float4(x.x * p.scale_log2, x.y * p.scale_log2, x.z * p.scale_log2,
-                                x.w * p.scale_log2);
+            const float4 x = make_float4(qv[f].x * p.scale_log2, qv[f].y * p.scale_log2,
+                                         qv[f].z * p.scale_log2, qv[f].w * p.scale_log2);
+            qv[f] = p.rotate ? rotate4_fma(x, cs[f]) : x;
         }
     }
 
@@ -334,6 +365,19 @@ hipError_t launch_prefill_attention(const PrefillParams& p, hipStream_t s)
     g.n_hg = (p.gqa + kWavesP - 1) / kWavesP;
     g.n_pairs = p.n_lb * p.n_head_kv;
     g.per_xcd = (g.n_pairs + kXcds - 1) / kXcds * g.n_hg * g.n_qt;
+    // m = ceil(2^32 / d) (0 for d <= 1); mulhi(n, m) = n / d whenever n * d < 2^32.
+    auto magic = [](long long d) -> unsigned {
+        return d <= 1 ? 0u : (unsigned)(((1ULL << 32) + (unsigned long long)d - 1) / (unsigned long long)d);
+    };
+    const long long rank_big = (long long)((g.n_pairs + kXcds - 1) / kXcds) * g.n_hg;
+    const long long rank_small = (long long)(g.n_pairs / kXcds) * g.n_hg;
+    if ((long long)g.per_xcd * rank_big >= (1LL << 32) || (long long)rank_big * g.n_hg >= (1LL << 32) ||
+        (long long)g.n_pairs * p.n_head_kv >= (1LL << 32))
+        return hipErrorInvalidValue;  // quotients by multiply-high would not be exact
+    g.m_rank_big = magic(rank_big);
+    g.m_rank_small = magic(rank_small);
+    g.m_hg = magic(g.n_hg);
+    g.m_kv = magic(p.n_head_kv);
     hipLaunchKernelGGL(prefill_attention_kernel, dim3(g.per_xcd * kXcds), dim3(64 * kWavesP), 0, s,
                        p, g);
     return hipGetLastError();
