@@ -11,6 +11,8 @@ Tolerances: embed, elementwise_mul, argmax bit-exact; silu within 2 ulp
 the largest |logit| of the step against the reference's own logits (golden)
 and the oracle's, and the same argmax wherever the top two logits are
 further apart than twice that bound; greedy generation token for token."""
+import ast
+
 import numpy as np
 import pytest
 
@@ -426,3 +428,40 @@ def test_prefill_forward_long_prompt(tla, O, W, engines, name):
     kv = spec.kv_dim
     ok = om.kc.reshape(spec.n_layers, spec.n_ctx, kv)
     assert np.abs(k_dev[0, :, :48] - ok[:, :48]).max() <= 1e-4 * np.abs(ok[:, :48]).max()
+
+
+@pytest.mark.parametrize("name", ["q8_0", "f16_tied", "q4_0", "mixed"])
+def test_prefill_forward_library_prompt(tla, O, W, engines, name):
+    """A 300-token prompt: every batched projection takes the library path
+    (weights expanded to fp32, rocBLAS products; >= 256 tokens), Q/K/V as
+    three products and gate | up as one.  The golden case's weights on a
+    320-position context; last token's logits and the whole K cache against
+    the oracle's token loop."""
+    g = golden("forward.npz")
+    base = W.ModelSpec(*[int(v) for v in g["spec"]])
+    spec = W.ModelSpec(base.n_layers, base.n_embd, base.n_head, base.n_head_kv, base.n_ff, base.n_vocab,
+                       320)
+    salt, wt, et, ot = [int(v) for v in g[f"{name}_case"]]
+    ov = dict(ast.literal_eval(str(g[f"{name}_overrides"])))
+    t = W.make_model(spec, wt, salt=salt, embd_type=None if et < 0 else et,
+                     output_type=None if ot < 0 else ot, overrides=ov)
+    eng = spec_engine(engines, spec)
+    n = 300
+    toks = np.random.default_rng(300).integers(0, spec.n_vocab, n).tolist()
+    om = O.Model(spec, t)
+    want = om.tokens(toks)[-1]
+    log(f"  {name}: {n}-token prompt through the library products")
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    try:
+        with device_arrays() as track:
+            kc, vc = eng.kv_cache(1)
+            track(kc), track(vc)
+            lg = track(eng.array((spec.n_vocab,)))
+            eng.prefill_forward(dm, kc.ptr, vc.ptr, toks, 0, lg.ptr)
+            got = lg.download()
+            k_dev = kc.download()
+    finally:
+        dm.free()
+    check_logits(got[None], want[None], f"{name} {n}-token batched prompt vs oracle")
+    ok = om.kc.reshape(spec.n_layers, spec.n_ctx, spec.kv_dim)
+    assert np.abs(k_dev[0, :, :n] - ok[:, :n]).max() <= 1e-4 * np.abs(ok[:, :n]).max()

@@ -12,15 +12,10 @@
 #include <utility>
 #include <vector>
 
-#include "tla_internal.h"
+#include <rocblas/rocblas.h>
 
-namespace tla {
-// fp32 MFMA floor (small_ops.hip): n_wg workgroups of 4 waves, each wave
-// iters x 16 v_mfma_f32_32x32x2f32; sink [n_wg] is never written in practice.
-// Declared here, not in tla_internal.h: that header is part of the decode,
-// prefill and GEMV kernels' source digests, and this launcher is not.
-hipError_t launch_mfma_floor(int n_wg, int iters, float* sink, hipStream_t s);
-}  // namespace tla
+#include "launch_extra.h"
+#include "tla_internal.h"
 
 using namespace tla;
 
@@ -130,6 +125,9 @@ struct tla_engine {
     size_t fwd_bytes = 0;
     float* gemm_ws = nullptr;  // split-column GEMM partial tiles
     size_t gemm_ws_bytes = 0;
+    float* wf = nullptr;       // weights expanded to fp32 for the library product
+    size_t wf_bytes = 0;
+    rocblas_handle blas = nullptr;  // on `stream`, created at the first library product
     int* argmax_slot = nullptr;
     long long opt_split = 0;
     int opt_plan = TLA_PLAN_AUTO;
@@ -418,6 +416,8 @@ int tla_engine_destroy(tla_engine* e)
     if (e->counters) (void)hipFree(e->counters);
     if (e->fwd) (void)hipFree(e->fwd);
     if (e->gemm_ws) (void)hipFree(e->gemm_ws);
+    if (e->wf) (void)hipFree(e->wf);
+    if (e->blas) (void)rocblas_destroy_handle(e->blas);
     if (e->argmax_slot) (void)hipFree(e->argmax_slot);
     if (e->rope) (void)hipFree(e->rope);
     if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -1165,6 +1165,83 @@ int ensure_gemm_ws(tla_engine* e, size_t bytes)
 // (and weight types it does not take) through the multi-vector GEMV.
 constexpr int kGemmMinTokens = 16;
 
+// Batches of at least this many tokens take the library product below.
+// Same-box measurements at TinyLlama's shapes, Q4_0, per layer (Q/K/V,
+// W_o, gate/up, down): 256 tokens 307 us with gemm_kernel against
+// ~290 us, 512 tokens 522 against ~430 us, 1024 tokens 940 against ~690 us;
+// under 256 tokens each library call costs at least ~30 us.
+constexpr int kBlasMinTokens = 256;
+
+int ensure_wf(tla_engine* e, size_t bytes)
+{
+    if (bytes <= e->wf_bytes) return TLA_OK;
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    if (e->wf) TLA_HIP(hipFree(e->wf));
+    e->wf = nullptr;
+    e->wf_bytes = 0;
+    const hipError_t err = hipMalloc(&e->wf, bytes);
+    if (err != hipSuccess)
+        return fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE,
+                    "fp32 weight workspace (%zu bytes): %s", bytes, hipGetErrorString(err));
+    e->wf_bytes = bytes;
+    return TLA_OK;
+}
+
+int ensure_blas(tla_engine* e)
+{
+    if (e->blas) return TLA_OK;
+    rocblas_handle h = nullptr;
+    if (rocblas_create_handle(&h) != rocblas_status_success)
+        return fail(TLA_ERR_DEVICE, "rocblas_create_handle failed");
+    if (rocblas_set_stream(h, e->stream) != rocblas_status_success ||
+        rocblas_set_pointer_mode(h, rocblas_pointer_mode_host) != rocblas_status_success) {
+        (void)rocblas_destroy_handle(h);
+        return fail(TLA_ERR_DEVICE, "rocblas handle set-up failed");
+    }
+    e->blas = h;
+    return TLA_OK;
+}
+
+// out_s[t][row] (+)= W_s[row] . x[t] as rocBLAS fp32 products over the
+// weights expanded to fp32 (launch_dequant_rows): one product per run of
+// segments whose outputs continue each other's columns (gate | up), else
+// one per segment.  In column-major terms C (rows x n, ldc = out_stride) =
+// Wf^T (Wf row-major [rows][cols]) x X (cols x n, ldb = x_stride).
+int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int total, int cols,
+               const float* x, long long x_stride, int n, int add)
+{
+    if (int rc = ensure_blas(e)) return rc;
+    if (int rc = ensure_wf(e, static_cast<size_t>(total) * cols * sizeof(float))) return rc;
+    const long long row_bytes = static_cast<long long>(weight_row_bytes(type, cols));
+    return launch(e, TLA_KERNEL_GEMV, "gemm (library)", [&]() -> hipError_t {
+        long long r0 = 0;
+        for (int i = 0; i < n_seg; ++i) {
+            const hipError_t err = launch_dequant_rows(type, segs[i].w, row_bytes, segs[i].rows, cols,
+                                                       e->wf + r0 * cols, e->stream);
+            if (err != hipSuccess) return err;
+            r0 += segs[i].rows;
+        }
+        const float alpha = 1.0f, beta = add ? 1.0f : 0.0f;
+        r0 = 0;
+        for (int i = 0; i < n_seg;) {
+            int j = i + 1;
+            long long rows = segs[i].rows;
+            while (j < n_seg && segs[j].out_stride == segs[i].out_stride && segs[j].out == segs[i].out + rows) {
+                rows += segs[j].rows;
+                ++j;
+            }
+            const rocblas_status st = rocblas_sgemm(
+                e->blas, rocblas_operation_transpose, rocblas_operation_none, static_cast<rocblas_int>(rows),
+                n, cols, &alpha, e->wf + r0 * cols, cols, x, static_cast<rocblas_int>(x_stride), &beta,
+                segs[i].out, static_cast<rocblas_int>(segs[i].out_stride));
+            if (st != rocblas_status_success) return hipErrorLaunchFailure;
+            r0 += rows;
+            i = j;
+        }
+        return hipGetLastError();
+    });
+}
+
 // out_s[t][row] (+)= W_s[row] . x[t] for the n_seg matrices of `segs`, one
 // type, over n tokens (x rows x_stride floats apart).
 int matrix_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int cols, const float* x,
@@ -1176,6 +1253,9 @@ int matrix_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, in
         total += segs[i].rows;
         rows32 = rows32 && segs[i].rows % 32 == 0;
     }
+    if (n >= kBlasMinTokens && cols % 32 == 0 && (type != kQ6_K || cols % 256 == 0) &&
+        static_cast<long long>(total) * cols < (1LL << 31) && x_stride < (1LL << 31))
+        return blas_batch(e, type, segs, n_seg, total, cols, x, x_stride, n, add);
     if (n >= kGemmMinTokens && gemm_supported(type) && rows32 && cols % 32 == 0) {
         // Column splits (partials summed in order by a second kernel) chosen
         // by a cost model: the busiest CU runs ceil(tiles * s / CUs) tiles of
