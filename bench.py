@@ -543,7 +543,7 @@ def matmul_kernel(eng, t, steps, warmup, rows=32000, cols=2048):
     return out
 
 
-def gemm_kernel_tflops(eng, t, steps, rows=5632, cols=2048, n_tok=512):
+def batch_product_tflops(eng, t, steps, rows=5632, cols=2048, n_tok=512):
     """tla_matmul_batch on one matrix (the FFN gate shape by default) for a
     token batch, back to back: fp32 MFMA TFLOP/s."""
     rg = np.random.default_rng(2)
@@ -570,7 +570,7 @@ def run_matmul(steps, warmup, name):
     eng = tla.Engine(tla.Config.tinyllama(n_layers=1, n_ctx=16))
     r = matmul_kernel(eng, t, steps, warmup)
     if t != W.W_Q6_K:
-        r["batch512"] = gemm_kernel_tflops(eng, t, steps)
+        r["batch512"] = batch_product_tflops(eng, t, steps)
     eng.close()
     return r
 
@@ -615,8 +615,8 @@ def run_generate(steps, warmup, cpu, wname="q4_0", n_prompt=32, n_gen=20):
     _, toks_b = call(n_gen + 1, True)
     log(f"[bench] generate {wname}: prompt as one batch {pre_batch:.2f} ms "
         f"({pre_batch / n_prompt * 1e3:.0f} us/token); same tokens: {toks_b == toks}")
-    # a long prompt as one batch (tla_prefill_forward): the projections on
-    # the MFMA GEMM; GEMM flops = 2 x tokens x (every matrix's rows x cols)
+    # a long prompt as one batch (tla_prefill_forward): the projections as
+    # batched products; flops = 2 x tokens x (every matrix's rows x cols)
     # over the layers
     n_long = 512
     long_prompt = [1] + W.rng("block", 4).integers(2, spec.n_vocab, n_long - 1).tolist()

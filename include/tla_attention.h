@@ -204,13 +204,11 @@ int tla_matmul(tla_engine* e, float* out_dev, const void* w_dev, const float* x_
                int cols, int type);
 
 /* matmul() over a batch of n_tok vectors: out[t][rows] = W . x[t] (x
- * [n_tok][cols]), the weights read once per batch tile.  From 256 vectors
- * on, the weights are expanded to fp32 in an engine workspace (rows x cols
- * floats) and multiplied by rocBLAS's fp32 product (every format); from 16
- * vectors on, F32 / F16 / Q8_0 / Q4_0 with rows a multiple of 32 run on this
- * library's fp32 MFMA kernel; other cases as groups of matrix-vector
- * products.  fp32 accumulation throughout.  Used for the prompt's
- * projections. */
+ * [n_tok][cols]).  From 16 vectors on, the weights are expanded to fp32 in
+ * an engine workspace (rows x cols floats; F32 weights are used as they
+ * are) and multiplied by hipBLASLt's fp32 product; fewer vectors run as
+ * groups of matrix-vector products.  fp32 accumulation throughout.  Used
+ * for the prompt's projections. */
 int tla_matmul_batch(tla_engine* e, float* out_dev, const void* w_dev, const float* x_dev, int rows,
                      int cols, int n_tok, int type);
 

@@ -404,9 +404,9 @@ def test_prefill_forward_errors(tla, W, engines):
 
 @pytest.mark.parametrize("name", ["q8_0", "f16_tied", "q4_0", "mixed"])
 def test_prefill_forward_long_prompt(tla, O, W, engines, name):
-    """A 48-token prompt: the batched projections run on the MFMA GEMM
-    (>= 16 tokens; the mixed model's Q6_K values through GEMVs).  Last
-    token's logits against the oracle's token loop."""
+    """A 48-token prompt: the batched projections as fp32 weights +
+    hipBLASLt products (>= 16 tokens, every format).  Last token's logits
+    against the oracle's token loop."""
     g = golden("forward.npz")
     spec, t = model_from_golden(W, g, name)
     eng = spec_engine(engines, spec)
@@ -432,9 +432,9 @@ def test_prefill_forward_long_prompt(tla, O, W, engines, name):
 
 @pytest.mark.parametrize("name", ["q8_0", "f16_tied", "q4_0", "mixed"])
 def test_prefill_forward_library_prompt(tla, O, W, engines, name):
-    """A 300-token prompt: every batched projection takes the library path
-    (weights expanded to fp32, rocBLAS products; >= 256 tokens), Q/K/V as
-    three products and gate | up as one.  The golden case's weights on a
+    """A 300-token prompt: every batched projection as weights expanded to
+    fp32 and hipBLASLt products, Q/K/V as three products and gate | up as
+    one.  The golden case's weights on a
     320-position context; last token's logits and the whole K cache against
     the oracle's token loop."""
     g = golden("forward.npz")

@@ -214,16 +214,15 @@ def test_projection_errors(tla, W, engines):
 
 
 BATCH_SHAPES = [(32, 256, 16), (2560, 2048, 33), (64, 5632, 128), (5632, 2048, 130), (96, 512, 300),
-                (2048, 2048, 256), (40, 5632, 257),  # the library path (>= 256 tokens)
-                (48, 256, 7), (40, 512, 20)]  # the last two: GEMV groups (few tokens / rows % 32)
+                (2048, 2048, 256), (40, 5632, 257), (48, 256, 7), (40, 512, 20)]  # (48, 256, 7): GEMV groups
 
 
 @pytest.mark.parametrize("t,name", TYPES)
 @pytest.mark.parametrize("rows,cols,n_tok", BATCH_SHAPES)
 def test_matmul_batch(O, W, engines, t, name, rows, cols, n_tok):
-    """tla_matmul_batch: weights expanded to fp32 and rocBLAS products (>=
-    256 tokens), the MFMA GEMM (>= 16 tokens, rows % 32 == 0, not Q6_K) or
-    groups of GEMVs, per token against the oracle's matmul."""
+    """tla_matmul_batch: weights expanded to fp32 and hipBLASLt products
+    (>= 16 tokens) or groups of GEMVs, per token against the oracle's
+    matmul."""
     if t == Q.Q6_K and cols % 256:
         pytest.skip("Q6_K rows are whole 256-weight super-blocks")
     eng = engines(1, 64)

@@ -7,14 +7,14 @@
 #include <cstdint>
 #include <cstdio>
 #include <cstring>
+#include <deque>
 #include <mutex>
 #include <string>
 #include <utility>
 #include <vector>
 
-#include <rocblas/rocblas.h>
+#include <hipblaslt/hipblaslt.h>
 
-#include "launch_extra.h"
 #include "tla_internal.h"
 
 using namespace tla;
@@ -106,6 +106,28 @@ static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 namespace {
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kScratchDevices] = {};  // device address of `scratch`, per device
+
+// One library product shape, C (m x n, ldc) = op(A) (A stored k x m, lda,
+// transposed) x B (k x n, ldb), fp32 in and out, fp32 compute: its
+// descriptors and the first algorithm the library's heuristic returns.
+struct LtPlan {
+    int m = 0, n = 0, k = 0;
+    long long lda = 0, ldb = 0, ldc = 0;
+    hipblasLtMatmulDesc_t desc = nullptr;
+    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
+    hipblasLtMatmulAlgo_t algo{};
+};
+
+void lt_plan_destroy(LtPlan& pl)
+{
+    if (pl.a) (void)hipblasLtMatrixLayoutDestroy(pl.a);
+    if (pl.b) (void)hipblasLtMatrixLayoutDestroy(pl.b);
+    if (pl.c) (void)hipblasLtMatrixLayoutDestroy(pl.c);
+    if (pl.desc) (void)hipblasLtMatmulDescDestroy(pl.desc);
+    pl = LtPlan{};
+}
+
+constexpr size_t kLtWorkspace = 32u << 20;
 }  // namespace
 
 struct tla_engine {
@@ -123,11 +145,11 @@ struct tla_engine {
     size_t n_counters = 0;
     void* fwd = nullptr;     // forward(): residual stream, q|k|v, attention out, FFN, tokens
     size_t fwd_bytes = 0;
-    float* gemm_ws = nullptr;  // split-column GEMM partial tiles
-    size_t gemm_ws_bytes = 0;
     float* wf = nullptr;       // weights expanded to fp32 for the library product
     size_t wf_bytes = 0;
-    rocblas_handle blas = nullptr;  // on `stream`, created at the first library product
+    hipblasLtHandle_t lt = nullptr;  // created at the first library product
+    void* lt_ws = nullptr;           // its workspace (kLtWorkspace bytes)
+    std::deque<LtPlan> lt_plans;     // per product shape (a deque: plans stay put as it grows)
     int* argmax_slot = nullptr;
     long long opt_split = 0;
     int opt_plan = TLA_PLAN_AUTO;
@@ -415,9 +437,10 @@ int tla_engine_destroy(tla_engine* e)
     if (e->ws) (void)hipFree(e->ws);
     if (e->counters) (void)hipFree(e->counters);
     if (e->fwd) (void)hipFree(e->fwd);
-    if (e->gemm_ws) (void)hipFree(e->gemm_ws);
     if (e->wf) (void)hipFree(e->wf);
-    if (e->blas) (void)rocblas_destroy_handle(e->blas);
+    for (LtPlan& pl : e->lt_plans) lt_plan_destroy(pl);
+    if (e->lt_ws) (void)hipFree(e->lt_ws);
+    if (e->lt) (void)hipblasLtDestroy(e->lt);
     if (e->argmax_slot) (void)hipFree(e->argmax_slot);
     if (e->rope) (void)hipFree(e->rope);
     if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -1148,29 +1171,10 @@ int gemv_rows(tla_engine* e, int type, const void* w, float* out, int rows, int 
     return TLA_OK;
 }
 
-int ensure_gemm_ws(tla_engine* e, size_t bytes)
-{
-    if (bytes <= e->gemm_ws_bytes) return TLA_OK;
-    TLA_HIP(hipStreamSynchronize(e->stream));
-    if (e->gemm_ws) TLA_HIP(hipFree(e->gemm_ws));
-    e->gemm_ws = nullptr;
-    e->gemm_ws_bytes = 0;
-    const hipError_t err = hipMalloc(&e->gemm_ws, bytes);
-    if (err != hipSuccess) return fail(TLA_ERR_OUT_OF_MEMORY, "GEMM workspace: %s", hipGetErrorString(err));
-    e->gemm_ws_bytes = bytes;
-    return TLA_OK;
-}
-
-// Token batches at least this long go through the MFMA GEMM; shorter ones
-// (and weight types it does not take) through the multi-vector GEMV.
-constexpr int kGemmMinTokens = 16;
-
-// Batches of at least this many tokens take the library product below.
-// Same-box measurements at TinyLlama's shapes, Q4_0, per layer (Q/K/V,
-// W_o, gate/up, down): 256 tokens 307 us with gemm_kernel against
-// ~290 us, 512 tokens 522 against ~430 us, 1024 tokens 940 against ~690 us;
-// under 256 tokens each library call costs at least ~30 us.
-constexpr int kBlasMinTokens = 256;
+// Token batches at least this long take the library product below; shorter
+// ones the multi-vector GEMV (weights read once per group of up to 8
+// tokens).
+constexpr int kBatchMinTokens = 16;
 
 int ensure_wf(tla_engine* e, size_t bytes)
 {
@@ -1187,56 +1191,116 @@ int ensure_wf(tla_engine* e, size_t bytes)
     return TLA_OK;
 }
 
-int ensure_blas(tla_engine* e)
+int ensure_lt(tla_engine* e)
 {
-    if (e->blas) return TLA_OK;
-    rocblas_handle h = nullptr;
-    if (rocblas_create_handle(&h) != rocblas_status_success)
-        return fail(TLA_ERR_DEVICE, "rocblas_create_handle failed");
-    if (rocblas_set_stream(h, e->stream) != rocblas_status_success ||
-        rocblas_set_pointer_mode(h, rocblas_pointer_mode_host) != rocblas_status_success) {
-        (void)rocblas_destroy_handle(h);
-        return fail(TLA_ERR_DEVICE, "rocblas handle set-up failed");
+    if (e->lt) return TLA_OK;
+    hipblasLtHandle_t h = nullptr;
+    if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return fail(TLA_ERR_DEVICE, "hipblasLtCreate failed");
+    const hipError_t err = hipMalloc(&e->lt_ws, kLtWorkspace);
+    if (err != hipSuccess) {
+        (void)hipblasLtDestroy(h);
+        e->lt_ws = nullptr;
+        return fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE,
+                    "library product workspace: %s", hipGetErrorString(err));
     }
-    e->blas = h;
+    e->lt = h;
     return TLA_OK;
 }
 
-// out_s[t][row] (+)= W_s[row] . x[t] as rocBLAS fp32 products over the
+// The cached plan of a product shape, built (descriptors + the heuristic's
+// first algorithm) at its first use.
+int lt_plan(tla_engine* e, int m, int n, int k, long long lda, long long ldb, long long ldc, const LtPlan** out)
+{
+    for (const LtPlan& pl : e->lt_plans)
+        if (pl.m == m && pl.n == n && pl.k == k && pl.lda == lda && pl.ldb == ldb && pl.ldc == ldc) {
+            *out = &pl;
+            return TLA_OK;
+        }
+    LtPlan pl;
+    pl.m = m, pl.n = n, pl.k = k, pl.lda = lda, pl.ldb = ldb, pl.ldc = ldc;
+    const hipblasOperation_t op_t = HIPBLAS_OP_T, op_n = HIPBLAS_OP_N;
+    hipblasLtMatmulPreference_t pref = nullptr;
+    size_t ws = kLtWorkspace;
+    hipblasLtMatmulHeuristicResult_t res{};
+    int got = 0;
+    const bool ok =
+        hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_t, sizeof(op_t)) ==
+            HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_n, sizeof(op_n)) ==
+            HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatrixLayoutCreate(&pl.a, HIP_R_32F, k, m, lda) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatrixLayoutCreate(&pl.b, HIP_R_32F, k, n, ldb) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatrixLayoutCreate(&pl.c, HIP_R_32F, m, n, ldc) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)) ==
+            HIPBLAS_STATUS_SUCCESS &&
+        hipblasLtMatmulAlgoGetHeuristic(e->lt, pl.desc, pl.a, pl.b, pl.c, pl.c, pref, 1, &res, &got) ==
+            HIPBLAS_STATUS_SUCCESS &&
+        got > 0;
+    if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
+    if (!ok) {
+        lt_plan_destroy(pl);
+        return fail(TLA_ERR_DEVICE, "no library product for %d x %d x %d", m, n, k);
+    }
+    pl.algo = res.algo;
+    e->lt_plans.push_back(pl);
+    *out = &e->lt_plans.back();
+    return TLA_OK;
+}
+
+// out_s[t][row] (+)= W_s[row] . x[t] as hipBLASLt fp32 products over the
 // weights expanded to fp32 (launch_dequant_rows): one product per run of
 // segments whose outputs continue each other's columns (gate | up), else
 // one per segment.  In column-major terms C (rows x n, ldc = out_stride) =
-// Wf^T (Wf row-major [rows][cols]) x X (cols x n, ldb = x_stride).
+// Wf^T (Wf row-major [rows][cols]) x X (cols x n, ldb = x_stride), beta 1
+// for the residual.
 int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int total, int cols,
                const float* x, long long x_stride, int n, int add)
 {
-    if (int rc = ensure_blas(e)) return rc;
-    if (int rc = ensure_wf(e, static_cast<size_t>(total) * cols * sizeof(float))) return rc;
+    // F32 weights are multiplied where they lie (one product per segment);
+    // the other formats are expanded into the workspace first.
+    const bool direct = type == kF32;
+    if (int rc = ensure_lt(e)) return rc;
+    if (!direct)
+        if (int rc = ensure_wf(e, static_cast<size_t>(total) * cols * sizeof(float))) return rc;
+    struct Run {
+        int seg;
+        const float* w;
+        const LtPlan* plan;
+    };
+    Run runs[kGemvMaxSeg];
+    int n_runs = 0;
+    long long r0 = 0;
+    for (int i = 0; i < n_seg;) {
+        int j = i + 1, rows = segs[i].rows;
+        while (!direct && j < n_seg && segs[j].out_stride == segs[i].out_stride &&
+               segs[j].out == segs[i].out + rows)
+            rows += segs[j++].rows;
+        const LtPlan* plan = nullptr;
+        if (int rc = lt_plan(e, rows, n, cols, cols, x_stride, segs[i].out_stride, &plan)) return rc;
+        const float* w = direct ? reinterpret_cast<const float*>(segs[i].w) : e->wf + r0 * cols;
+        runs[n_runs++] = {i, w, plan};
+        r0 += rows;
+        i = j;
+    }
     const long long row_bytes = static_cast<long long>(weight_row_bytes(type, cols));
-    return launch(e, TLA_KERNEL_GEMV, "gemm (library)", [&]() -> hipError_t {
-        long long r0 = 0;
-        for (int i = 0; i < n_seg; ++i) {
+    return launch(e, TLA_KERNEL_GEMV, "batched product", [&]() -> hipError_t {
+        long long w0 = 0;
+        for (int i = 0; i < n_seg && !direct; ++i) {
             const hipError_t err = launch_dequant_rows(type, segs[i].w, row_bytes, segs[i].rows, cols,
-                                                       e->wf + r0 * cols, e->stream);
+                                                       e->wf + w0 * cols, e->stream);
             if (err != hipSuccess) return err;
-            r0 += segs[i].rows;
+            w0 += segs[i].rows;
         }
         const float alpha = 1.0f, beta = add ? 1.0f : 0.0f;
-        r0 = 0;
-        for (int i = 0; i < n_seg;) {
-            int j = i + 1;
-            long long rows = segs[i].rows;
-            while (j < n_seg && segs[j].out_stride == segs[i].out_stride && segs[j].out == segs[i].out + rows) {
-                rows += segs[j].rows;
-                ++j;
-            }
-            const rocblas_status st = rocblas_sgemm(
-                e->blas, rocblas_operation_transpose, rocblas_operation_none, static_cast<rocblas_int>(rows),
-                n, cols, &alpha, e->wf + r0 * cols, cols, x, static_cast<rocblas_int>(x_stride), &beta,
-                segs[i].out, static_cast<rocblas_int>(segs[i].out_stride));
-            if (st != rocblas_status_success) return hipErrorLaunchFailure;
-            r0 += rows;
-            i = j;
+        for (int r = 0; r < n_runs; ++r) {
+            const Run& ru = runs[r];
+            float* out = segs[ru.seg].out;
+            if (hipblasLtMatmul(e->lt, ru.plan->desc, &alpha, ru.w, ru.plan->a, x, ru.plan->b,
+                                &beta, out, ru.plan->c, out, ru.plan->c, &ru.plan->algo, e->lt_ws, kLtWorkspace,
+                                e->stream) != HIPBLAS_STATUS_SUCCESS)
+                return hipErrorLaunchFailure;
         }
         return hipGetLastError();
     });
@@ -1248,59 +1312,10 @@ int matrix_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, in
                  long long x_stride, int n, int add)
 {
     int total = 0;
-    bool rows32 = true;
-    for (int i = 0; i < n_seg; ++i) {
-        total += segs[i].rows;
-        rows32 = rows32 && segs[i].rows % 32 == 0;
-    }
-    if (n >= kBlasMinTokens && cols % 32 == 0 && (type != kQ6_K || cols % 256 == 0) &&
+    for (int i = 0; i < n_seg; ++i) total += segs[i].rows;
+    if (n >= kBatchMinTokens && cols % 32 == 0 && (type != kQ6_K || cols % 256 == 0) &&
         static_cast<long long>(total) * cols < (1LL << 31) && x_stride < (1LL << 31))
         return blas_batch(e, type, segs, n_seg, total, cols, x, x_stride, n, add);
-    if (n >= kGemmMinTokens && gemm_supported(type) && rows32 && cols % 32 == 0) {
-        // Column splits (partials summed in order by a second kernel) chosen
-        // by a cost model: the busiest CU runs ceil(tiles * s / CUs) tiles of
-        // 1/s of the columns each (co-resident tiles share its matrix cores),
-        // and every split adds a partial tile written and read back.  Tile
-        // time ~ 2*128*128*cols flops at ~0.3 TFLOP/s per CU; partials move
-        // at ~6 TB/s.  A CU holding two or more tiles at once gets ~1.2x the
-        // throughput of a lone tile (one wave per SIMD leaves the MFMA pipe
-        // idle while that wave waits on its loads): measured at 512 tokens of
-        // Q4_0 weights, the 2048 x 5632 product takes 153 us in 4 splits (one
-        // tile per CU) and 129 us in 8, the 2048 x 2048 one 65 vs 60 us, the
-        // 2560 x 2048 one 77-85 us in 3 vs 74 us in 6.
-        const long long tiles = static_cast<long long>((total + 127) / 128) * ((n + 127) / 128);
-        const int chunks = cols / 32;
-        const long long cus = std::max(1, e->n_cu);
-        const double tile_us = 2.0 * 128 * 128 * cols / 0.3e12 * 1e6;
-        const double split_us = static_cast<double>(n) * total * 8 / 6e12 * 1e6;
-        int splits = 1;
-        double best = 1e300;
-        for (int sp = 1; sp <= std::min(16, std::max(1, chunks / 4)); ++sp) {
-            const long long per_cu = (tiles * sp + cus - 1) / cus;
-            const double shared = per_cu >= 2 ? 1.0 / 1.2 : 1.0;
-            const double cost = tile_us * per_cu * shared / sp + (sp > 1 ? split_us * sp : 0.0);
-            if (cost < best * 0.98) {
-                best = cost;
-                splits = sp;
-            }
-        }
-        GemmParams p{};
-        if (splits > 1) {
-            if (int rc = ensure_gemm_ws(e, static_cast<size_t>(splits) * n * total * sizeof(float))) return rc;
-            p.part = e->gemm_ws;
-        }
-        p.k_splits = splits;
-        for (int i = 0; i < n_seg; ++i) p.seg[i] = segs[i];
-        p.n_seg = n_seg;
-        p.total_rows = total;
-        p.cols = cols;
-        p.row_bytes = static_cast<int>(weight_row_bytes(type, cols));
-        p.n_tok = n;
-        p.x = x;
-        p.x_stride = x_stride;
-        p.add = add;
-        return launch(e, TLA_KERNEL_GEMV, "gemm", [&] { return launch_gemm(type, p, e->stream); });
-    }
     const int chunk = std::max(1, std::min({n, kGemvMaxVec, kGemvLdsBytes / gemv_lds_per_vec(cols)}));
     for (int t0 = 0; t0 < n; t0 += chunk) {
         GemvParams p{};

@@ -1,7 +1,6 @@
 // Stand-alone device ops: rope (src/ops.cpp:1223-1281), softmax
 // (src/ops.cpp:1072-1091) and a vectorised device copy.
 #include "rope_math.h"
-#include "launch_extra.h"
 #include "tla_internal.h"
 
 namespace tla {

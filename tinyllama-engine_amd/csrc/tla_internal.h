@@ -155,27 +155,13 @@ hipError_t launch_embed(int type, float* out, const unsigned char* table, int to
 // also stored at out2 when non-null.
 hipError_t launch_argmax(int* out, int* out2, const float* x, int n, hipStream_t s);
 
-// ---- token-batch matrix products (gemm.hip) ------------------------------------
-// Y[t][row] (+)= W[row] . X[t] for n_tok tokens on the fp32 matrix cores.
-// Segments as in GemvParams (out[t * out_stride + row]); every segment's rows
-// a multiple of 32, cols a multiple of 32.
-struct GemmParams {
-    GemvSegment seg[kGemvMaxSeg];
-    int n_seg;
-    int total_rows;
-    int cols;
-    int row_bytes;
-    int n_tok;
-    const float* x;          // x[t * x_stride + col]
-    long long x_stride;
-    int add;
-    int k_splits;            // > 1: column ranges on separate workgroups, partial
-    float* part;             //   tiles in part[split][t][total_rows], summed by
-                             //   a second kernel in split order
-};
-
-bool gemm_supported(int type);  // F32, F16, Q8_0, Q4_0
-hipError_t launch_gemm(int type, const GemmParams& p, hipStream_t s);
+// ---- token batches (batch.hip) -------------------------------------------
+// Weights of `rows` rows of `cols` columns in format `type` (row_bytes per
+// row) expanded to fp32 [rows][cols] at out: F32 as is, F16 converted, Q8_0
+// q * d, Q4_0 (q - 8) * d, Q6_K d * scale * q.  cols a multiple of 32 (256
+// for Q6_K).
+hipError_t launch_dequant_rows(int type, const unsigned char* w, long long row_bytes, int rows, int cols,
+                               float* out, hipStream_t s);
 hipError_t launch_rmsnorm_rows(float* out, const float* x, const float* w, int n_rows, int size, float eps,
                                hipStream_t s);
 // h rows of [gate | up] (2 n_ff floats): gate = silu(gate) * up in place.
@@ -196,6 +182,9 @@ hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
 // Streaming read of `bytes` (16-byte aligned, whole 16-byte words) by n_wg
 // workgroups, each a contiguous chunk; sink [n_wg] is never written in practice.
 hipError_t launch_read_floor(const void* src, size_t bytes, int n_wg, float* sink, hipStream_t s);
+// fp32 MFMA floor: n_wg workgroups of 4 waves, each wave iters x 16
+// v_mfma_f32_32x32x2f32; sink [n_wg] is never written in practice.
+hipError_t launch_mfma_floor(int n_wg, int iters, float* sink, hipStream_t s);
 // Zero fill by a kernel (no memset node: safe under stream capture).
 hipError_t launch_zero(void* dst, size_t bytes, hipStream_t s);
 
