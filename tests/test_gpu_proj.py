@@ -238,3 +238,25 @@ def test_matmul_batch(O, W, engines, t, name, rows, cols, n_tok):
     for i in sorted({0, n_tok // 2, n_tok - 1}):
         check_rows(got[i], O.matmul(raw, x[i], rows, cols, t), raw, x[i], t, rows, cols,
                    f"{name} {rows}x{cols} token {i}")
+
+
+def test_matmul_batch_many_shapes(O, W, engines):
+    """260 batch sizes in a row: every size is a new library product shape
+    (descriptors and algorithm cached per shape, the cache starting over
+    past 256 shapes); products before, across and after the reset against
+    the oracle's matmul."""
+    eng = engines(1, 64)
+    rows, cols, t = 32, 64, Q.Q8_0
+    raw = W.make_weights(t, rows, cols, salt=11)
+    x = np.random.default_rng(260).standard_normal((300, cols)).astype(np.float32)
+    with device_arrays() as track:
+        w = track(eng.array(raw))
+        xd = track(eng.array(x))
+        out = track(eng.array((300, rows)))
+        for n_tok in range(16, 276):
+            eng.matmul_batch(out.ptr, w.ptr, xd.ptr, rows, cols, n_tok, t)
+            if n_tok in (16, 200, 271, 275):
+                got = out.download()
+                for i in (0, n_tok - 1):
+                    check_rows(got[i], O.matmul(raw, x[i], rows, cols, t), raw, x[i], t, rows, cols,
+                               f"{n_tok} tokens, token {i}")

@@ -128,6 +128,9 @@ void lt_plan_destroy(LtPlan& pl)
 }
 
 constexpr size_t kLtWorkspace = 32u << 20;
+// Product shapes kept: every prompt length brings up to four (Q/K/V, W_o,
+// gate | up, down); past this many the cache starts over.
+constexpr size_t kLtMaxPlans = 256;
 }  // namespace
 
 struct tla_engine {
@@ -1262,6 +1265,10 @@ int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int 
     // the other formats are expanded into the workspace first.
     const bool direct = type == kF32;
     if (int rc = ensure_lt(e)) return rc;
+    if (e->lt_plans.size() + kGemvMaxSeg > kLtMaxPlans) {  // before any plan of this call is taken
+        for (LtPlan& pl : e->lt_plans) lt_plan_destroy(pl);
+        e->lt_plans.clear();
+    }
     if (!direct)
         if (int rc = ensure_wf(e, static_cast<size_t>(total) * cols * sizeof(float))) return rc;
     struct Run {
