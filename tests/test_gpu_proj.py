@@ -260,3 +260,25 @@ def test_matmul_batch_many_shapes(O, W, engines):
                 for i in (0, n_tok - 1):
                     check_rows(got[i], O.matmul(raw, x[i], rows, cols, t), raw, x[i], t, rows, cols,
                                f"{n_tok} tokens, token {i}")
+
+
+@pytest.mark.parametrize("rows,cols,n_tok", [(2048, 5632, 16), (256, 2048, 300), (11264, 2048, 512)])
+def test_matmul_batch_is_reproducible(W, engines, rows, cols, n_tok):
+    """The library product gives the same bits when repeated (its algorithm
+    is chosen once per shape; a split-K algorithm would have to sum in a
+    fixed order)."""
+    eng = engines(1, 64)
+    raw = W.make_weights(Q.Q4_0, rows, cols, salt=5)
+    x = np.random.default_rng(7).standard_normal((n_tok, cols)).astype(np.float32)
+    with device_arrays() as track:
+        w = track(eng.array(raw))
+        xd = track(eng.array(x))
+        out = track(eng.array((n_tok, rows)))
+        first = None
+        for _ in range(5):
+            eng.matmul_batch(out.ptr, w.ptr, xd.ptr, rows, cols, n_tok, Q.Q4_0)
+            got = out.download()
+            if first is None:
+                first = got
+            else:
+                assert np.array_equal(got.view(np.uint32), first.view(np.uint32))
