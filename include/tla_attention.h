@@ -309,8 +309,9 @@ int tla_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* 
 
 /* The prompt loop of src/generate.cpp:56-59 as one batch: forward() for
  * tokens_host[0..n_tok) at positions pos0..pos0+n_tok-1, each layer over all
- * tokens at once (multi-vector GEMVs, the causal MFMA prefill attention
- * with RoPE + append in-kernel); logits_dev [n_vocab] receives the last
+ * tokens at once (the projections as tla_matmul_batch products, the causal
+ * MFMA prefill attention with RoPE + append in-kernel); logits_dev
+ * [n_vocab] receives the last
  * token's logits (the ones generate() samples from).  The KV cache ends as
  * after n_tok forward() calls (to fp32 rounding: the attention sums are
  * grouped differently). */
