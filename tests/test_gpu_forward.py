@@ -435,7 +435,8 @@ def test_prefill_forward_library_prompt(tla, O, W, engines, name):
     """A 300-token prompt: every batched projection as weights expanded to
     fp32 and hipBLASLt products, Q/K/V as three products and gate | up as
     one.  The golden case's weights on a
-    320-position context; last token's logits and the whole K cache against
+    320-position context, in one call and as two calls of 150 tokens (the
+    second at pos0 = 150); last token's logits and the whole K cache against
     the oracle's token loop."""
     g = golden("forward.npz")
     base = W.ModelSpec(*[int(v) for v in g["spec"]])
@@ -460,8 +461,17 @@ def test_prefill_forward_library_prompt(tla, O, W, engines, name):
             eng.prefill_forward(dm, kc.ptr, vc.ptr, toks, 0, lg.ptr)
             got = lg.download()
             k_dev = kc.download()
+            # the same prompt as two batches of 150 (the second at pos0 = 150)
+            kc2, vc2 = eng.kv_cache(1)
+            track(kc2), track(vc2)
+            eng.prefill_forward(dm, kc2.ptr, vc2.ptr, toks[:150], 0, lg.ptr)
+            eng.prefill_forward(dm, kc2.ptr, vc2.ptr, toks[150:], 150, lg.ptr)
+            got2 = lg.download()
+            k_dev2 = kc2.download()
     finally:
         dm.free()
     check_logits(got[None], want[None], f"{name} {n}-token batched prompt vs oracle")
+    check_logits(got2[None], want[None], f"{name} {n}-token prompt in two batches vs oracle")
     ok = om.kc.reshape(spec.n_layers, spec.n_ctx, spec.kv_dim)
-    assert np.abs(k_dev[0, :, :n] - ok[:, :n]).max() <= 1e-4 * np.abs(ok[:, :n]).max()
+    for kd in (k_dev, k_dev2):
+        assert np.abs(kd[0, :, :n] - ok[:, :n]).max() <= 1e-4 * np.abs(ok[:, :n]).max()
