@@ -430,11 +430,11 @@ def test_prefill_forward_long_prompt(tla, O, W, engines, name):
     assert np.abs(k_dev[0, :, :48] - ok[:, :48]).max() <= 1e-4 * np.abs(ok[:, :48]).max()
 
 
-@pytest.mark.parametrize("name", ["q8_0", "f16_tied", "q4_0", "mixed"])
+@pytest.mark.parametrize("name", ["q8_0", "f16_tied", "q4_0", "f32", "mixed"])
 def test_prefill_forward_library_prompt(tla, O, W, engines, name):
     """A 300-token prompt: every batched projection as weights expanded to
     fp32 and hipBLASLt products, Q/K/V as three products and gate | up as
-    one.  The golden case's weights on a
+    one (F32 weights multiplied where they lie, one product per matrix).  The golden case's weights on a
     320-position context, in one call and as two calls of 150 tokens (the
     second at pos0 = 150); last token's logits and the whole K cache against
     the oracle's token loop."""
