@@ -150,6 +150,15 @@ struct tla_engine {
     size_t fwd_bytes = 0;
     float* wf = nullptr;       // weights expanded to fp32 for the library product
     size_t wf_bytes = 0;
+    // A prompt's layers, expanded to fp32 one layer ahead on a second
+    // stream while the current layer's products run: two layer buffers,
+    // `layer_ready[i]` recorded on `side` once buffer i holds its layer,
+    // `layer_done[i]` on `stream` once the products reading buffer i are
+    // queued behind it.
+    hipStream_t side = nullptr;
+    float* layer_buf[2] = {};
+    size_t layer_buf_bytes = 0;
+    hipEvent_t layer_ready[2] = {}, layer_done[2] = {};
     hipblasLtHandle_t lt = nullptr;  // created at the first library product
     void* lt_ws = nullptr;           // its workspace (kLtWorkspace bytes)
     std::deque<LtPlan> lt_plans;     // per product shape (a deque: plans stay put as it grows)
@@ -441,6 +450,13 @@ int tla_engine_destroy(tla_engine* e)
     if (e->counters) (void)hipFree(e->counters);
     if (e->fwd) (void)hipFree(e->fwd);
     if (e->wf) (void)hipFree(e->wf);
+    if (e->side) (void)hipStreamSynchronize(e->side);
+    for (int i = 0; i < 2; ++i) {
+        if (e->layer_buf[i]) (void)hipFree(e->layer_buf[i]);
+        if (e->layer_ready[i]) (void)hipEventDestroy(e->layer_ready[i]);
+        if (e->layer_done[i]) (void)hipEventDestroy(e->layer_done[i]);
+    }
+    if (e->side) (void)hipStreamDestroy(e->side);
     for (LtPlan& pl : e->lt_plans) lt_plan_destroy(pl);
     if (e->lt_ws) (void)hipFree(e->lt_ws);
     if (e->lt) (void)hipblasLtDestroy(e->lt);
@@ -1258,19 +1274,23 @@ int lt_plan(tla_engine* e, int m, int n, int k, long long lda, long long ldb, lo
 // one per segment.  In column-major terms C (rows x n, ldc = out_stride) =
 // Wf^T (Wf row-major [rows][cols]) x X (cols x n, ldb = x_stride), beta 1
 // for the residual.
+// `expanded`: the segments' weights already expanded to fp32, segment after
+// segment (the prompt's layer buffers); else F32 weights are multiplied
+// where they lie (one product per segment) and the other formats expanded
+// into the workspace first.
 int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int total, int cols,
-               const float* x, long long x_stride, int n, int add)
+               const float* x, long long x_stride, int n, int add, const float* expanded = nullptr)
 {
-    // F32 weights are multiplied where they lie (one product per segment);
-    // the other formats are expanded into the workspace first.
-    const bool direct = type == kF32;
+    const bool direct = !expanded && type == kF32;
+    const bool expand = !expanded && !direct;
     if (int rc = ensure_lt(e)) return rc;
     if (e->lt_plans.size() + kGemvMaxSeg > kLtMaxPlans) {  // before any plan of this call is taken
         for (LtPlan& pl : e->lt_plans) lt_plan_destroy(pl);
         e->lt_plans.clear();
     }
-    if (!direct)
+    if (expand)
         if (int rc = ensure_wf(e, static_cast<size_t>(total) * cols * sizeof(float))) return rc;
+    const float* const wbase = expanded ? expanded : e->wf;
     struct Run {
         int seg;
         const float* w;
@@ -1286,7 +1306,7 @@ int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int 
             rows += segs[j++].rows;
         const LtPlan* plan = nullptr;
         if (int rc = lt_plan(e, rows, n, cols, cols, x_stride, segs[i].out_stride, &plan)) return rc;
-        const float* w = direct ? reinterpret_cast<const float*>(segs[i].w) : e->wf + r0 * cols;
+        const float* w = direct ? reinterpret_cast<const float*>(segs[i].w) : wbase + r0 * cols;
         runs[n_runs++] = {i, w, plan};
         r0 += rows;
         i = j;
@@ -1294,7 +1314,7 @@ int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int 
     const long long row_bytes = static_cast<long long>(weight_row_bytes(type, cols));
     return launch(e, TLA_KERNEL_GEMV, "batched product", [&]() -> hipError_t {
         long long w0 = 0;
-        for (int i = 0; i < n_seg && !direct; ++i) {
+        for (int i = 0; i < n_seg && expand; ++i) {
             const hipError_t err = launch_dequant_rows(type, segs[i].w, row_bytes, segs[i].rows, cols,
                                                        e->wf + w0 * cols, e->stream);
             if (err != hipSuccess) return err;
@@ -1343,11 +1363,107 @@ int matrix_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, in
     return TLA_OK;
 }
 
+// A layer's seven matrices expanded to fp32, one after another: Wq [embd]
+// [embd], Wk, Wv [kv][embd], Wo [embd][embd], W_gate, W_up [ff][embd],
+// W_down [embd][ff].
+struct LayerLayout {
+    long long q, k, v, o, gate, up, down, total;  // offsets in floats
+    LayerLayout(long long embd, long long kv, long long ff)
+    {
+        q = 0;
+        k = q + embd * embd;
+        v = k + kv * embd;
+        o = v + kv * embd;
+        gate = o + embd * embd;
+        up = gate + ff * embd;
+        down = up + ff * embd;
+        total = down + embd * ff;
+    }
+};
+
+// Whether every matrix of every layer takes the library product (the
+// prompt's layers can then be expanded ahead).
+bool layers_expandable(const tla_model* m, int n_layers, int embd, int ff)
+{
+    for (int l = 0; l < n_layers; ++l) {
+        const tla_layer_weights& L = m->layers[l];
+        for (int t : {L.type_q, L.type_k, L.type_v, L.type_o, L.type_ffn})
+            if (t == kQ6_K && (embd % 256 || ff % 256)) return false;
+    }
+    return embd % 32 == 0 && ff % 32 == 0;
+}
+
+int ensure_layer_bufs(tla_engine* e, size_t bytes)
+{
+    if (!e->side) {
+        TLA_HIP(hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking));
+        for (int i = 0; i < 2; ++i) {
+            TLA_HIP(hipEventCreateWithFlags(&e->layer_ready[i], hipEventDisableTiming));
+            TLA_HIP(hipEventCreateWithFlags(&e->layer_done[i], hipEventDisableTiming));
+        }
+    }
+    if (bytes <= e->layer_buf_bytes) return TLA_OK;
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    TLA_HIP(hipStreamSynchronize(e->side));
+    for (int i = 0; i < 2; ++i) {
+        if (e->layer_buf[i]) TLA_HIP(hipFree(e->layer_buf[i]));
+        e->layer_buf[i] = nullptr;
+    }
+    e->layer_buf_bytes = 0;
+    for (int i = 0; i < 2; ++i) {
+        const hipError_t err = hipMalloc(&e->layer_buf[i], bytes);
+        if (err != hipSuccess)
+            return fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE,
+                        "fp32 layer buffers (2 x %zu bytes): %s", bytes, hipGetErrorString(err));
+    }
+    e->layer_buf_bytes = bytes;
+    return TLA_OK;
+}
+
+// Prompts shorter than this expand their layers ahead on the side stream.
+// Same box, TinyLlama Q4_0 prompts: 32 tokens 3.28 against 3.88 ms; at 512
+// tokens the expansions slow the products they share the CUs with (10.62
+// against 10.37 ms), and a grid capped at 64 workgroups is too slow to keep
+// ahead (9.4 ms at 32 tokens).
+constexpr int kAheadMaxTokens = 256;
+
+// Layer l's weights expanded into layer buffer `slot` on the side stream,
+// after the products that last read that buffer; layer_ready[slot] marks
+// the end.  (The expansions are not in tla_profile's sums: they run beside
+// the products.)
+int expand_layer(tla_engine* e, const tla_model* m, int l, int slot, const LayerLayout& lay)
+{
+    const int embd = e->cfg.n_embd, kv = e->kv_dim, ff = m->n_ff;
+    const tla_layer_weights& L = m->layers[l];
+    float* const buf = e->layer_buf[slot];
+    TLA_HIP(hipStreamWaitEvent(e->side, e->layer_done[slot], 0));
+    struct M {
+        const void* w;
+        int type, rows, cols;
+        long long at;
+    } const mats[7] = {{L.wq, L.type_q, embd, embd, lay.q},       {L.wk, L.type_k, kv, embd, lay.k},
+                       {L.wv, L.type_v, kv, embd, lay.v},         {L.wo, L.type_o, embd, embd, lay.o},
+                       {L.w_gate, L.type_ffn, ff, embd, lay.gate}, {L.w_up, L.type_ffn, ff, embd, lay.up},
+                       {L.w_down, L.type_ffn, embd, ff, lay.down}};
+    for (const M& mt : mats)
+        if (int rc = check_hip(launch_dequant_rows(mt.type, static_cast<const unsigned char*>(mt.w),
+                                                   weight_row_bytes(mt.type, mt.cols), mt.rows, mt.cols,
+                                                   buf + mt.at, e->side),
+                               "layer expansion"))
+            return rc;
+    TLA_HIP(hipEventRecord(e->layer_ready[slot], e->side));
+    return TLA_OK;
+}
+
 // The prompt as one batch (n_tok tokens at positions pos0..): embeddings,
 // then per layer rmsnorm + Q/K/V over all tokens, the causal prefill
-// attention (RoPE + append in-kernel), W_o + residual and the FFN, with the
-// multi-vector GEMVs (weights read once per group of up to 8 tokens);
-// logits of the last token only (when `logits` is non-null).
+// attention (RoPE + append in-kernel), W_o + residual and the FFN;
+// logits of the last token only (when `logits` is non-null).  From
+// kBatchMinTokens to kAheadMaxTokens tokens the products are library
+// products whose weights were expanded one layer ahead on the side stream
+// (while the previous layer's products ran); other prompts take
+// matrix_batch (multi-vector GEMVs under kBatchMinTokens, in-stream
+// expansion + library products above).
 int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, float* vc,
                 const int* tokens_dev, int n_tok, int pos0, float* logits)
 {
@@ -1358,15 +1474,38 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
                            "embed"))
         return rc;
     const auto U = [](const void* w) { return static_cast<const unsigned char*>(w); };
-    for (int l = 0; l < e->cfg.n_layers; ++l) {
+    const int n_layers = e->cfg.n_layers;
+    const LayerLayout lay(embd, kv, ff);
+    const bool ahead =
+        n_tok >= kBatchMinTokens && n_tok < kAheadMaxTokens && layers_expandable(m, n_layers, embd, ff);
+    if (ahead) {
+        if (int rc = ensure_lt(e)) return rc;
+        if (int rc = ensure_layer_bufs(e, static_cast<size_t>(lay.total) * sizeof(float))) return rc;
+        if (int rc = expand_layer(e, m, 0, 0, lay)) return rc;
+    }
+    for (int l = 0; l < n_layers; ++l) {
         const tla_layer_weights& L = m->layers[l];
+        const float* const wl = ahead ? e->layer_buf[l & 1] : nullptr;
+        if (ahead) {
+            if (l + 1 < n_layers)
+                if (int rc = expand_layer(e, m, l + 1, (l + 1) & 1, lay)) return rc;
+            TLA_HIP(hipStreamWaitEvent(e->stream, e->layer_ready[l & 1], 0));
+        }
+        // one product run: the expanded layer's weights at `at`, or matrix_batch
+        auto product = [&](int type, const GemvSegment* segs, int n_seg, int cols, const float* x,
+                           long long x_stride, int add, long long at) -> int {
+            if (!ahead) return matrix_batch(e, type, segs, n_seg, cols, x, x_stride, n_tok, add);
+            int total = 0;
+            for (int i = 0; i < n_seg; ++i) total += segs[i].rows;
+            return blas_batch(e, type, segs, n_seg, total, cols, x, x_stride, n_tok, add, wl + at);
+        };
         // rmsnorm rows, then Q/K/V (src/forward.cpp:180-190)
         if (int rc = check_hip(launch_rmsnorm_rows(b.xb, b.x, L.attn_norm, n_tok, embd, eps, e->stream),
                                "rmsnorm rows"))
             return rc;
-        if (L.type_q == L.type_k && L.type_q == L.type_v) {
+        if (ahead || (L.type_q == L.type_k && L.type_q == L.type_v)) {
             const GemvSegment segs[3] = {{U(L.wq), b.q, embd, embd}, {U(L.wk), b.k, kv, kv}, {U(L.wv), b.v, kv, kv}};
-            if (int rc = matrix_batch(e, L.type_q, segs, 3, embd, b.xb, embd, n_tok, 0)) return rc;
+            if (int rc = product(L.type_q, segs, 3, embd, b.xb, embd, 0, lay.q)) return rc;
         } else {
             const GemvSegment sq{U(L.wq), b.q, embd, embd}, sk{U(L.wk), b.k, kv, kv}, sv{U(L.wv), b.v, kv, kv};
             if (int rc = matrix_batch(e, L.type_q, &sq, 1, embd, b.xb, embd, n_tok, 0)) return rc;
@@ -1378,7 +1517,7 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
         // x += Wo . att (src/forward.cpp:210-213)
         {
             const GemvSegment so{U(L.wo), b.x, embd, embd};
-            if (int rc = matrix_batch(e, L.type_o, &so, 1, embd, b.att, embd, n_tok, 1)) return rc;
+            if (int rc = product(L.type_o, &so, 1, embd, b.att, embd, 1, lay.o)) return rc;
         }
         // FFN (src/forward.cpp:215-228): rmsnorm rows, gate and up into
         // hb [t][gate | up], SiLU x up in place, x += W_down . h
@@ -1387,13 +1526,14 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
             return rc;
         {
             const GemvSegment segs[2] = {{U(L.w_gate), b.hb, ff, 2LL * ff}, {U(L.w_up), b.hb + ff, ff, 2LL * ff}};
-            if (int rc = matrix_batch(e, L.type_ffn, segs, 2, embd, b.xb, embd, n_tok, 0)) return rc;
+            if (int rc = product(L.type_ffn, segs, 2, embd, b.xb, embd, 0, lay.gate)) return rc;
         }
         if (int rc = check_hip(launch_swiglu_rows(b.hb, n_tok, ff, e->stream), "swiglu rows")) return rc;
         {
             const GemvSegment sd{U(L.w_down), b.x, embd, embd};
-            if (int rc = matrix_batch(e, L.type_ffn, &sd, 1, ff, b.hb, 2LL * ff, n_tok, 1)) return rc;
+            if (int rc = product(L.type_ffn, &sd, 1, ff, b.hb, 2LL * ff, 1, lay.down)) return rc;
         }
+        if (ahead) TLA_HIP(hipEventRecord(e->layer_done[l & 1], e->stream));  // buffer l & 1 free after this
     }
     if (logits)
         if (int rc = gemv1(e, m->type_output, m->output, logits, m->n_vocab, embd,
