@@ -314,7 +314,9 @@ int tla_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* 
  * [n_vocab] receives the last
  * token's logits (the ones generate() samples from).  The KV cache ends as
  * after n_tok forward() calls (to fp32 rounding: the attention sums are
- * grouped differently). */
+ * grouped differently).  Engine memory it keeps for later calls: prompts of
+ * 16-255 tokens two layers' weights in fp32 (about 350 MB at TinyLlama's
+ * shapes), longer ones the largest matrix in fp32. */
 int tla_prefill_forward(tla_engine* e, const tla_model* m, float* key_cache_dev,
                         float* value_cache_dev, const int* tokens_host, int n_tok, int pos0,
                         float* logits_dev);
