@@ -378,9 +378,12 @@ enum tla_option {
     TLA_OPT_DECODE_SPLIT = 0, /* positions per decode workgroup (rounded up to 16) */
     TLA_OPT_DECODE_PLAN = 1,  /* 1: one split length per sequence; 2: equal ranges across
                                  sequences and layers */
-    TLA_OPT_DECODE_GROUP = 2  /* kv heads per decode workgroup in the plan of one split
+    TLA_OPT_DECODE_GROUP = 2, /* kv heads per decode workgroup in the plan of one split
                                  length: 1, 2 or 4 (the other plan always takes 4);
                                  results do not depend on it */
+    TLA_OPT_STREAM_TILES = 3  /* batched products of 16-32 vectors: vectors per
+                                 workgroup in tiles of 16, 1 or 2; results do not
+                                 depend on it */
 };
 enum tla_decode_plan { TLA_PLAN_AUTO = 0, TLA_PLAN_ALIGNED = 1, TLA_PLAN_BALANCED = 2 };
 int tla_set_option(tla_engine* e, int option, long long value);

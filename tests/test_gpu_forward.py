@@ -431,6 +431,44 @@ def test_prefill_forward_long_prompt(tla, O, W, engines, name):
 
 
 @pytest.mark.parametrize("name", ["q8_0", "f16_tied", "q4_0", "f32", "mixed"])
+def test_prefill_forward_streamed_prompt(tla, O, W, engines, name):
+    """A 32-token prompt, in one call and as two calls of 16 (the second at
+    pos0 = 16): every batched projection as the streamed product (weights
+    dequantised in registers; Q/K/V as one product of three segments where
+    their formats agree).  Last token's logits and the K cache against the
+    oracle's token loop."""
+    g = golden("forward.npz")
+    spec, t = model_from_golden(W, g, name)
+    eng = spec_engine(engines, spec)
+    n = 32
+    toks = np.random.default_rng(32).integers(0, spec.n_vocab, n).tolist()
+    om = O.Model(spec, t)
+    want = om.tokens(toks)[-1]
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    try:
+        with device_arrays() as track:
+            kc, vc = eng.kv_cache(1)
+            track(kc), track(vc)
+            lg = track(eng.array((spec.n_vocab,)))
+            eng.prefill_forward(dm, kc.ptr, vc.ptr, toks, 0, lg.ptr)
+            got = lg.download()
+            k_dev = kc.download()
+            kc2, vc2 = eng.kv_cache(1)
+            track(kc2), track(vc2)
+            eng.prefill_forward(dm, kc2.ptr, vc2.ptr, toks[:16], 0, lg.ptr)
+            eng.prefill_forward(dm, kc2.ptr, vc2.ptr, toks[16:], 16, lg.ptr)
+            got2 = lg.download()
+            k_dev2 = kc2.download()
+    finally:
+        dm.free()
+    check_logits(got[None], want[None], f"{name} {n}-token streamed prompt vs oracle")
+    check_logits(got2[None], want[None], f"{name} {n}-token prompt as 16 + 16 vs oracle")
+    ok = om.kc.reshape(spec.n_layers, spec.n_ctx, spec.kv_dim)
+    for kd in (k_dev, k_dev2):
+        assert np.abs(kd[0, :, :n] - ok[:, :n]).max() <= 1e-4 * np.abs(ok[:, :n]).max()
+
+
+@pytest.mark.parametrize("name", ["q8_0", "f16_tied", "q4_0", "f32", "mixed"])
 def test_prefill_forward_library_prompt(tla, O, W, engines, name):
     """A 300-token prompt: every batched projection as weights expanded to
     fp32 and hipBLASLt products, Q/K/V as three products and gate | up as

@@ -214,15 +214,16 @@ def test_projection_errors(tla, W, engines):
 
 
 BATCH_SHAPES = [(32, 256, 16), (2560, 2048, 33), (64, 5632, 128), (5632, 2048, 130), (96, 512, 300),
-                (2048, 2048, 256), (40, 5632, 257), (48, 256, 7), (40, 512, 20)]  # (48, 256, 7): GEMV groups
+                (2048, 2048, 256), (40, 5632, 257), (48, 256, 7), (40, 512, 20)]
+# (48, 256, 7): GEMV groups; (32, 256, 16), (40, 512, 20): streamed products
 
 
 @pytest.mark.parametrize("t,name", TYPES)
 @pytest.mark.parametrize("rows,cols,n_tok", BATCH_SHAPES)
 def test_matmul_batch(O, W, engines, t, name, rows, cols, n_tok):
-    """tla_matmul_batch: weights expanded to fp32 and hipBLASLt products
-    (>= 16 tokens) or groups of GEMVs, per token against the oracle's
-    matmul."""
+    """tla_matmul_batch: groups of GEMVs (< 16 tokens), the streamed product
+    (16-32 tokens, weights dequantised in registers) or weights expanded to
+    fp32 and hipBLASLt products, per token against the oracle's matmul."""
     if t == Q.Q6_K and cols % 256:
         pytest.skip("Q6_K rows are whole 256-weight super-blocks")
     eng = engines(1, 64)
@@ -238,6 +239,53 @@ def test_matmul_batch(O, W, engines, t, name, rows, cols, n_tok):
     for i in sorted({0, n_tok // 2, n_tok - 1}):
         check_rows(got[i], O.matmul(raw, x[i], rows, cols, t), raw, x[i], t, rows, cols,
                    f"{name} {rows}x{cols} token {i}")
+
+
+STREAM_SHAPES = [(2560, 2048, 16), (2048, 5632, 32), (40, 64, 17), (200, 128, 31)]
+
+
+@pytest.mark.parametrize("t,name", TYPES)
+@pytest.mark.parametrize("rows,cols,n_tok", STREAM_SHAPES)
+def test_matmul_batch_streamed(tla, O, W, engines, t, name, rows, cols, n_tok):
+    """The streamed product (16-32 tokens): rows not a multiple of its 16-row
+    tiles, rows of 2 blocks (two of its four waves idle), token counts not a
+    multiple of 16; every token against the oracle's matmul, and the same
+    bits with one or two token tiles per workgroup (Q6_K takes the library
+    product)."""
+    if t == Q.Q6_K and cols % 256:
+        pytest.skip("Q6_K rows are whole 256-weight super-blocks")
+    eng = engines(1, 64)
+    raw = W.make_weights(t, rows, cols, salt=rows + 5 * cols)
+    x = np.random.default_rng(n_tok + 1).standard_normal((n_tok, cols)).astype(np.float32)
+    log(f"  streamed product {name} {rows}x{cols}, {n_tok} tokens")
+    outs = []
+    with device_arrays() as track:
+        w = track(eng.array(raw))
+        xd = track(eng.array(x))
+        out = track(eng.array((n_tok, rows)))
+        try:
+            for tiles in (0, 1, 2):
+                eng.set_option(tla.OPT_STREAM_TILES, tiles)
+                eng.matmul_batch(out.ptr, w.ptr, xd.ptr, rows, cols, n_tok, t)
+                outs.append(out.download())
+        finally:
+            eng.set_option(tla.OPT_STREAM_TILES, 0)
+    for i in range(n_tok):
+        check_rows(outs[0][i], O.matmul(raw, x[i], rows, cols, t), raw, x[i], t, rows, cols,
+                   f"{name} {rows}x{cols} token {i}")
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+
+
+def test_stream_tiles_option(tla, engines):
+    """TLA_OPT_STREAM_TILES takes 0 (per shape), 1 or 2."""
+    eng = engines(1, 64)
+    for bad in (-1, 3):
+        with pytest.raises(tla.TlaError) as e:
+            eng.set_option(tla.OPT_STREAM_TILES, bad)
+        assert e.value.code == tla.TLA_ERR_INVALID_ARGUMENT
+    eng.set_option(tla.OPT_STREAM_TILES, 2)
+    eng.set_option(tla.OPT_STREAM_TILES, 0)
 
 
 def test_matmul_batch_many_shapes(O, W, engines):

@@ -9,7 +9,7 @@
 // rmsnorm_rows_kernel, swiglu_rows_kernel: rmsnorm and SwiGLU over every
 //   token row of the batch (src/forward.cpp:180-184, 215-225).
 #include "row_math.h"
-#include "tla_internal.h"
+#include "batch.h"
 
 namespace tla {
 namespace {
@@ -119,7 +119,167 @@ __global__ __launch_bounds__(kThreads) void dequant_rows_kernel(const unsigned c
     *reinterpret_cast<float4*>(out + static_cast<long long>(row) * cols + col) = v;
 }
 
+
+// ---- stream_product_kernel --------------------------------------------------
+// The projections of a batch of a few tokens with the weights dequantised in
+// registers (no fp32 copy of the matrix): out[t][row] (+)= sum_k W[row][k]
+// x[t][k] for 16 weight rows and 16 kNT tokens per workgroup (blockIdx.y
+// selects the token chunk).  v_mfma_f32_16x16x4f32 with the tokens as the A
+// operand and the weight rows as the B operand, so that lane l = 16 g + c
+// supplies token c's and row c's value of k slot g, and holds the result of
+// tokens 4 g .. 4 g + 3 for row c.  The k order inside a 32-value block is
+// free as long as A and B follow it: slot g of MFMA step s (s = 0..7) takes
+// value 8 g + s, except for Q4_0, where it takes (g / 2) 16 + (g % 2) 8 + s
+// -- bytes (g % 2) 8 .. + 7 of the block, low nibbles for g < 2, high for
+// g >= 2 -- so that every lane reads 8 contiguous weights and 8 contiguous x
+// values per block.  The four waves take every fourth block of the rows and
+// add their sums in LDS in wave order, so the result is the same from run
+// to run.
+constexpr int kStreamWaves = 4;
+
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Weights (g, s = 0..7) of block `blk` of a weight row in the order above,
+// each the reference's dequantised value (F16 converted, Q8_0 q * d, Q4_0
+// (q - 8) * d); quantised blocks start at even byte offsets and are read as
+// 16-bit halves.
+template <int kType>
+__device__ __forceinline__ void stream_weights(const unsigned char* wrow, int blk, int g, float (&w)[8])
+{
+    if constexpr (kType == kF32) {
+        const float4* q = reinterpret_cast<const float4*>(wrow + 4LL * (32 * blk + 8 * g));
+        const float4 a = q[0], b = q[1];
+        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
+        w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+    } else if constexpr (kType == kF16) {
+        const uint4 h = *reinterpret_cast<const uint4*>(wrow + 2LL * (32 * blk + 8 * g));
+        const unsigned u[4] = {h.x, h.y, h.z, h.w};
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w[2 * i] = half_to_float(u[i] & 0xFFFFu);
+            w[2 * i + 1] = half_to_float(u[i] >> 16);
+        }
+    } else {
+        constexpr int kBlock = kType == kQ8_0 ? 34 : 18;
+        const unsigned short* hw =
+            reinterpret_cast<const unsigned short*>(wrow + static_cast<long long>(kBlock) * blk);
+        const int h = kType == kQ8_0 ? g : (g & 1);  // which 8 bytes of qs
+        const float d = half_to_float(hw[0]);
+        const unsigned q[2] = {hw[1 + 4 * h] | (static_cast<unsigned>(hw[2 + 4 * h]) << 16),
+                               hw[3 + 4 * h] | (static_cast<unsigned>(hw[4 + 4 * h]) << 16)};
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            const unsigned byte = (q[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+            if constexpr (kType == kQ8_0)
+                w[i] = static_cast<float>(static_cast<signed char>(byte)) * d;
+            else
+                w[i] = static_cast<float>(static_cast<int>((byte >> ((g >> 1) * 4)) & 0xFu) - 8) * d;
+        }
+    }
+}
+
+template <int kType, int kNT>
+__global__ __launch_bounds__(kStreamWaves * 64) void stream_product_kernel(const StreamParams p)
+{
+    __shared__ float s_red[kStreamWaves][kNT][4][64];
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int c = lane & 15, g = lane >> 4;
+    const int row = blockIdx.x * 16 + c;
+    // this lane's weight row (the last one for rows past the end) and its segment
+    int seg = 0, r = min(row, p.total_rows - 1);
+    while (seg + 1 < p.n_seg && r >= p.seg[seg].rows) r -= p.seg[seg++].rows;
+    const unsigned char* const wrow = p.seg[seg].w + static_cast<long long>(r) * p.row_bytes;
+    const int t0 = blockIdx.y * 16 * kNT;
+    const int xoff = kType == kQ4_0 ? (g >> 1) * 16 + (g & 1) * 8 : 8 * g;
+    const float* xr[kNT];
+#pragma unroll
+    for (int ti = 0; ti < kNT; ++ti)
+        xr[ti] = p.x + static_cast<long long>(min(t0 + 16 * ti + c, p.n - 1)) * p.x_stride + xoff;
+    floatx4 acc[kNT];
+#pragma unroll
+    for (int ti = 0; ti < kNT; ++ti) acc[ti] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    const int n_blk = p.cols >> 5;
+    for (int b = wave; b < n_blk; b += kStreamWaves) {
+        float w[8];
+        stream_weights<kType>(wrow, b, g, w);
+#pragma unroll
+        for (int ti = 0; ti < kNT; ++ti) {
+            const float4 xa = *reinterpret_cast<const float4*>(xr[ti] + 32 * b);
+            const float4 xb = *reinterpret_cast<const float4*>(xr[ti] + 32 * b + 4);
+            acc[ti] = mfma16(xa.x, w[0], acc[ti]);
+            acc[ti] = mfma16(xa.y, w[1], acc[ti]);
+            acc[ti] = mfma16(xa.z, w[2], acc[ti]);
+            acc[ti] = mfma16(xa.w, w[3], acc[ti]);
+            acc[ti] = mfma16(xb.x, w[4], acc[ti]);
+            acc[ti] = mfma16(xb.y, w[5], acc[ti]);
+            acc[ti] = mfma16(xb.z, w[6], acc[ti]);
+            acc[ti] = mfma16(xb.w, w[7], acc[ti]);
+        }
+    }
+#pragma unroll
+    for (int ti = 0; ti < kNT; ++ti)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) s_red[wave][ti][v][lane] = acc[ti][v];
+    __syncthreads();
+    // thread (wave, lane) writes token 4 g + wave of every tile for row c
+    if (row >= p.total_rows) return;
+    float* const out = p.seg[seg].out + r;
+    const long long stride = p.seg[seg].out_stride;
+#pragma unroll
+    for (int ti = 0; ti < kNT; ++ti) {
+        const int t = t0 + 16 * ti + 4 * g + wave;
+        if (t >= p.n) continue;
+        float sum = s_red[0][ti][wave][lane];
+#pragma unroll
+        for (int w2 = 1; w2 < kStreamWaves; ++w2) sum += s_red[w2][ti][wave][lane];
+        float* const o = out + static_cast<long long>(t) * stride;
+        *o = p.add ? *o + sum : sum;
+    }
+}
+
+template <int kType>
+hipError_t launch_stream_typed(const StreamParams& p, hipStream_t s)
+{
+    const int nt = (p.n + 15) / 16;
+    const dim3 grid(static_cast<unsigned>((p.total_rows + 15) / 16),
+                    static_cast<unsigned>((nt + p.tiles - 1) / p.tiles));
+    const dim3 block(kStreamWaves * 64);
+    if (p.tiles == 1)
+        hipLaunchKernelGGL((stream_product_kernel<kType, 1>), grid, block, 0, s, p);
+    else
+        hipLaunchKernelGGL((stream_product_kernel<kType, 2>), grid, block, 0, s, p);
+    return hipGetLastError();
+}
+
 }  // namespace
+
+bool stream_supported(int type) { return type == kF32 || type == kF16 || type == kQ8_0 || type == kQ4_0; }
+
+hipError_t launch_stream_product(int type, const StreamParams& p, hipStream_t s)
+{
+    if (!stream_supported(type) || p.tiles < 1 || p.tiles > kStreamMaxTiles || p.n < 1 || p.total_rows < 1 || p.cols < 32 || p.cols % 32 != 0 ||
+        p.n_seg < 1 || p.n_seg > kGemvMaxSeg || p.x_stride % 4 != 0 ||
+        reinterpret_cast<uintptr_t>(p.x) % 16 != 0 || p.row_bytes != weight_row_bytes(type, p.cols))
+        return hipErrorInvalidValue;
+    int rows = 0;
+    for (int i = 0; i < p.n_seg; ++i) {
+        const uintptr_t align = type == kF32 || type == kF16 ? 16 : 2;
+        if (p.seg[i].rows < 1 || reinterpret_cast<uintptr_t>(p.seg[i].w) % align != 0) return hipErrorInvalidValue;
+        rows += p.seg[i].rows;
+    }
+    if (rows != p.total_rows) return hipErrorInvalidValue;
+    switch (type) {
+    case kF32: return launch_stream_typed<kF32>(p, s);
+    case kF16: return launch_stream_typed<kF16>(p, s);
+    case kQ8_0: return launch_stream_typed<kQ8_0>(p, s);
+    default: return launch_stream_typed<kQ4_0>(p, s);
+    }
+}
 
 hipError_t launch_dequant_rows(int type, const unsigned char* w, long long row_bytes, int rows, int cols,
                                float* out, hipStream_t s)

@@ -15,6 +15,7 @@
 
 #include <hipblaslt/hipblaslt.h>
 
+#include "batch.h"
 #include "tla_internal.h"
 
 using namespace tla;
@@ -166,6 +167,7 @@ struct tla_engine {
     long long opt_split = 0;
     int opt_plan = TLA_PLAN_AUTO;
     int opt_group = 0;  // kv heads per aligned-plan workgroup, 0 = per launch
+    int opt_stream_tiles = 0;  // streamed product: token tiles per workgroup, 0 = per shape
     int n_cu = 256;          // compute units: decode workgroups per launch
 
     bool prof = false;
@@ -1335,11 +1337,53 @@ int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int 
 
 // out_s[t][row] (+)= W_s[row] . x[t] for the n_seg matrices of `segs`, one
 // type, over n tokens (x rows x_stride floats apart).
+// Batches of kStreamMinTokens .. kStreamMaxTokens vectors multiply F32 / F16
+// / Q8_0 / Q4_0 weights where they lie, dequantised in registers by
+// stream_product_kernel; the library product pays for an fp32 copy of the
+// weights and runs far below the MFMA rate at these widths.  (Past 32
+// vectors the streamed product loses: each CU reads all of x for every 16
+// rows, and a CU streams only a few tens of GB/s.)
+constexpr int kStreamMinTokens = 16;
+constexpr int kStreamMaxTokens = 32;
+
+bool use_stream(int type, int cols, int n, long long x_stride)
+{
+    return stream_supported(type) && n >= kStreamMinTokens && n <= kStreamMaxTokens && cols % 32 == 0 &&
+           x_stride % 4 == 0;
+}
+
+int stream_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int total, int cols,
+                 const float* x, long long x_stride, int n, int add)
+{
+    StreamParams p{};
+    for (int i = 0; i < n_seg; ++i) p.seg[i] = segs[i];
+    p.n_seg = n_seg;
+    p.total_rows = total;
+    p.cols = cols;
+    p.row_bytes = weight_row_bytes(type, cols);
+    p.x = x;
+    p.x_stride = x_stride;
+    p.n = n;
+    p.add = add;
+    // token tiles of 16 per workgroup: one for matrices of at most 128 row
+    // tiles (their workgroups are too few to fill the CUs otherwise; W_o and
+    // W_down at TinyLlama's shapes, 32 tokens: 11.6 against 15.2 us and 22.4
+    // against 30.1 us), else all of them (W_qkv, gate + up: 15.4 against
+    // 19.7 us, 40.6 against 52.7 us)
+    const int nt = (n + 15) / 16;
+    p.tiles = e->opt_stream_tiles > 0 ? e->opt_stream_tiles
+              : (total + 15) / 16 <= 128 ? 1
+                                         : std::min(nt, kStreamMaxTiles);
+    return launch(e, TLA_KERNEL_GEMV, "streamed product",
+                  [&]() -> hipError_t { return launch_stream_product(type, p, e->stream); });
+}
+
 int matrix_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int cols, const float* x,
                  long long x_stride, int n, int add)
 {
     int total = 0;
     for (int i = 0; i < n_seg; ++i) total += segs[i].rows;
+    if (use_stream(type, cols, n, x_stride)) return stream_batch(e, type, segs, n_seg, total, cols, x, x_stride, n, add);
     if (n >= kBatchMinTokens && cols % 32 == 0 && (type != kQ6_K || cols % 256 == 0) &&
         static_cast<long long>(total) * cols < (1LL << 31) && x_stride < (1LL << 31))
         return blas_batch(e, type, segs, n_seg, total, cols, x, x_stride, n, add);
@@ -1391,6 +1435,18 @@ bool layers_expandable(const tla_model* m, int n_layers, int embd, int ff)
             if (t == kQ6_K && (embd % 256 || ff % 256)) return false;
     }
     return embd % 32 == 0 && ff % 32 == 0;
+}
+
+// Whether every matrix of every layer takes the streamed product for a
+// prompt of n_tok tokens (nothing to expand then).
+bool layers_stream(const tla_model* m, int n_layers, int embd, int ff, int n_tok)
+{
+    for (int l = 0; l < n_layers; ++l) {
+        const tla_layer_weights& L = m->layers[l];
+        for (int t : {L.type_q, L.type_k, L.type_v, L.type_o, L.type_ffn})
+            if (!use_stream(t, embd, n_tok, embd) || !use_stream(t, ff, n_tok, 2LL * ff)) return false;
+    }
+    return true;
 }
 
 int ensure_layer_bufs(tla_engine* e, size_t bytes)
@@ -1476,8 +1532,8 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
     const auto U = [](const void* w) { return static_cast<const unsigned char*>(w); };
     const int n_layers = e->cfg.n_layers;
     const LayerLayout lay(embd, kv, ff);
-    const bool ahead =
-        n_tok >= kBatchMinTokens && n_tok < kAheadMaxTokens && layers_expandable(m, n_layers, embd, ff);
+    const bool ahead = n_tok >= kBatchMinTokens && n_tok < kAheadMaxTokens &&
+                       layers_expandable(m, n_layers, embd, ff) && !layers_stream(m, n_layers, embd, ff, n_tok);
     if (ahead) {
         if (int rc = ensure_lt(e)) return rc;
         if (int rc = ensure_layer_bufs(e, static_cast<size_t>(lay.total) * sizeof(float))) return rc;
@@ -1880,6 +1936,11 @@ int tla_set_option(tla_engine* e, int option, long long value)
             value != kDecodeKvGroupLarge)
             return fail(TLA_ERR_INVALID_ARGUMENT, "decode kv group %lld not 0, 1, 2 or 4", value);
         e->opt_group = static_cast<int>(value);
+        return ok();
+    case TLA_OPT_STREAM_TILES:
+        if (value < 0 || value > kStreamMaxTiles)
+            return fail(TLA_ERR_INVALID_ARGUMENT, "stream tiles %lld not in [0, %d]", value, kStreamMaxTiles);
+        e->opt_stream_tiles = static_cast<int>(value);
         return ok();
     default:
         return fail(TLA_ERR_INVALID_ARGUMENT, "unknown option %d", option);
