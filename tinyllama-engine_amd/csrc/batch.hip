@@ -132,9 +132,9 @@ __global__ __launch_bounds__(kThreads) void dequant_rows_kernel(const unsigned c
 // value 8 g + s, except for Q4_0, where it takes (g / 2) 16 + (g % 2) 8 + s
 // -- bytes (g % 2) 8 .. + 7 of the block, low nibbles for g < 2, high for
 // g >= 2 -- so that every lane reads 8 contiguous weights and 8 contiguous x
-// values per block.  The four waves take every fourth block of the rows and
-// add their sums in LDS in wave order, so the result is the same from run
-// to run.
+// values per block.  The four waves take every fourth block of the rows,
+// each keeping the loads of its next blocks in flight, and add their sums in
+// LDS in wave order, so the result is the same from run to run.
 constexpr int kStreamWaves = 4;
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
@@ -144,50 +144,92 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c)
     return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Weights (g, s = 0..7) of block `blk` of a weight row in the order above,
-// each the reference's dequantised value (F16 converted, Q8_0 q * d, Q4_0
-// (q - 8) * d); quantised blocks start at even byte offsets and are read as
-// 16-bit halves.
-template <int kType>
-__device__ __forceinline__ void stream_weights(const unsigned char* wrow, int blk, int g, float (&w)[8])
+// One block's operands for one lane as loaded: the weights' raw bits (F32 8
+// floats, F16 8 halves, Q8_0 / Q4_0 the scale and 8 bytes of qs, read as
+// 16-bit halves since blocks start at even byte offsets) and 8 x values per
+// token tile.  Nothing is computed from them until the block's turn comes,
+// so that the loads of the blocks ahead stay in flight.
+template <int kType, int kNT>
+struct StreamStage {
+    static constexpr int kWords = kType == kF32 ? 8 : kType == kF16 ? 4 : 3;
+    unsigned u[kWords];
+    float4 xa[kNT], xb[kNT];
+};
+
+template <int kType, int kNT>
+__device__ __forceinline__ void stream_load(StreamStage<kType, kNT>& st, const unsigned char* wrow,
+                                            const float* const (&xr)[kNT], int blk, int g)
 {
     if constexpr (kType == kF32) {
-        const float4* q = reinterpret_cast<const float4*>(wrow + 4LL * (32 * blk + 8 * g));
-        const float4 a = q[0], b = q[1];
-        w[0] = a.x; w[1] = a.y; w[2] = a.z; w[3] = a.w;
-        w[4] = b.x; w[5] = b.y; w[6] = b.z; w[7] = b.w;
+        const uint4* q = reinterpret_cast<const uint4*>(wrow + 4LL * (32 * blk + 8 * g));
+        const uint4 a = q[0], b = q[1];
+        st.u[0] = a.x; st.u[1] = a.y; st.u[2] = a.z; st.u[3] = a.w;
+        st.u[4] = b.x; st.u[5] = b.y; st.u[6] = b.z; st.u[7] = b.w;
     } else if constexpr (kType == kF16) {
         const uint4 h = *reinterpret_cast<const uint4*>(wrow + 2LL * (32 * blk + 8 * g));
-        const unsigned u[4] = {h.x, h.y, h.z, h.w};
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            w[2 * i] = half_to_float(u[i] & 0xFFFFu);
-            w[2 * i + 1] = half_to_float(u[i] >> 16);
-        }
+        st.u[0] = h.x; st.u[1] = h.y; st.u[2] = h.z; st.u[3] = h.w;
     } else {
         constexpr int kBlock = kType == kQ8_0 ? 34 : 18;
         const unsigned short* hw =
             reinterpret_cast<const unsigned short*>(wrow + static_cast<long long>(kBlock) * blk);
         const int h = kType == kQ8_0 ? g : (g & 1);  // which 8 bytes of qs
-        const float d = half_to_float(hw[0]);
-        const unsigned q[2] = {hw[1 + 4 * h] | (static_cast<unsigned>(hw[2 + 4 * h]) << 16),
-                               hw[3 + 4 * h] | (static_cast<unsigned>(hw[4 + 4 * h]) << 16)};
+        st.u[0] = hw[0];
+        st.u[1] = hw[1 + 4 * h] | (static_cast<unsigned>(hw[2 + 4 * h]) << 16);
+        st.u[2] = hw[3 + 4 * h] | (static_cast<unsigned>(hw[4 + 4 * h]) << 16);
+    }
+#pragma unroll
+    for (int ti = 0; ti < kNT; ++ti) {
+        st.xa[ti] = *reinterpret_cast<const float4*>(xr[ti] + 32 * blk);
+        st.xb[ti] = *reinterpret_cast<const float4*>(xr[ti] + 32 * blk + 4);
+    }
+}
+
+// The block's products: each weight the reference's dequantised value (F16
+// converted, Q8_0 q * d, Q4_0 (q - 8) * d), 8 MFMA steps per token tile.
+template <int kType, int kNT>
+__device__ __forceinline__ void stream_mfma(const StreamStage<kType, kNT>& st, int g, floatx4 (&acc)[kNT])
+{
+    float w[8];
+    if constexpr (kType == kF32) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) w[i] = __builtin_bit_cast(float, st.u[i]);
+    } else if constexpr (kType == kF16) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            w[2 * i] = half_to_float(st.u[i] & 0xFFFFu);
+            w[2 * i + 1] = half_to_float(st.u[i] >> 16);
+        }
+    } else {
+        const float d = half_to_float(st.u[0]);
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const unsigned byte = (q[i >> 2] >> (8 * (i & 3))) & 0xFFu;
+            const unsigned byte = (st.u[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFFu;
             if constexpr (kType == kQ8_0)
                 w[i] = static_cast<float>(static_cast<signed char>(byte)) * d;
             else
                 w[i] = static_cast<float>(static_cast<int>((byte >> ((g >> 1) * 4)) & 0xFu) - 8) * d;
         }
     }
+#pragma unroll
+    for (int ti = 0; ti < kNT; ++ti) {
+        acc[ti] = mfma16(st.xa[ti].x, w[0], acc[ti]);
+        acc[ti] = mfma16(st.xa[ti].y, w[1], acc[ti]);
+        acc[ti] = mfma16(st.xa[ti].z, w[2], acc[ti]);
+        acc[ti] = mfma16(st.xa[ti].w, w[3], acc[ti]);
+        acc[ti] = mfma16(st.xb[ti].x, w[4], acc[ti]);
+        acc[ti] = mfma16(st.xb[ti].y, w[5], acc[ti]);
+        acc[ti] = mfma16(st.xb[ti].z, w[6], acc[ti]);
+        acc[ti] = mfma16(st.xb[ti].w, w[7], acc[ti]);
+    }
 }
 
 template <int kType, int kNT>
 __global__ __launch_bounds__(kStreamWaves * 64) void stream_product_kernel(const StreamParams p)
 {
+    constexpr int kDepth = 4;  // blocks whose loads a wave has issued
     __shared__ float s_red[kStreamWaves][kNT][4][64];
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    // the wave index as a scalar, so that the block loop's branches are uniform
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int c = lane & 15, g = lane >> 4;
     const int row = blockIdx.x * 16 + c;
     // this lane's weight row (the last one for rows past the end) and its segment
@@ -203,22 +245,27 @@ __global__ __launch_bounds__(kStreamWaves * 64) void stream_product_kernel(const
     floatx4 acc[kNT];
 #pragma unroll
     for (int ti = 0; ti < kNT; ++ti) acc[ti] = floatx4{0.0f, 0.0f, 0.0f, 0.0f};
+    // blocks wave + kStreamWaves i for i < nb, the loads of the next kDepth - 1
+    // in flight while one is multiplied (the weights come from HBM, one round
+    // trip per block otherwise); loads past the wave's last block re-read its
+    // first one, or the row's last block for a wave with none (never used)
     const int n_blk = p.cols >> 5;
-    for (int b = wave; b < n_blk; b += kStreamWaves) {
-        float w[8];
-        stream_weights<kType>(wrow, b, g, w);
+    const int nb = wave < n_blk ? (n_blk - wave + kStreamWaves - 1) / kStreamWaves : 0;
+    const auto block_of = [&](int i) { return min(wave + kStreamWaves * (i < nb ? i : 0), n_blk - 1); };
+    StreamStage<kType, kNT> st[kDepth];
 #pragma unroll
-        for (int ti = 0; ti < kNT; ++ti) {
-            const float4 xa = *reinterpret_cast<const float4*>(xr[ti] + 32 * b);
-            const float4 xb = *reinterpret_cast<const float4*>(xr[ti] + 32 * b + 4);
-            acc[ti] = mfma16(xa.x, w[0], acc[ti]);
-            acc[ti] = mfma16(xa.y, w[1], acc[ti]);
-            acc[ti] = mfma16(xa.z, w[2], acc[ti]);
-            acc[ti] = mfma16(xa.w, w[3], acc[ti]);
-            acc[ti] = mfma16(xb.x, w[4], acc[ti]);
-            acc[ti] = mfma16(xb.y, w[5], acc[ti]);
-            acc[ti] = mfma16(xb.z, w[6], acc[ti]);
-            acc[ti] = mfma16(xb.w, w[7], acc[ti]);
+    for (int d = 0; d < kDepth; ++d) {
+        stream_load(st[d], wrow, xr, block_of(d), g);
+        __builtin_amdgcn_sched_barrier(0);  // the stages' loads in issue order
+    }
+    for (int i0 = 0; i0 < nb; i0 += kDepth) {
+#pragma unroll
+        for (int d = 0; d < kDepth; ++d) {
+            const int i = i0 + d;
+            if (i < nb) stream_mfma(st[d], g, acc);
+            __builtin_amdgcn_sched_barrier(0);
+            stream_load(st[d], wrow, xr, block_of(i + kDepth), g);
+            __builtin_amdgcn_sched_barrier(0);
         }
     }
 #pragma unroll

@@ -1340,13 +1340,12 @@ int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int 
 // Batches of kStreamMinTokens .. kStreamMaxTokens vectors multiply F32 / F16
 // / Q8_0 / Q4_0 weights where they lie, dequantised in registers by
 // stream_product_kernel; the library product pays for an fp32 copy of the
-// weights and runs far below the MFMA rate at these widths.  (Past 40
-// vectors the streamed product loses on Q4_0 prompts -- 48 tokens 3.73
-// against 3.67-3.72 ms, 64 tokens 4.00 against 3.67-3.72 -- while it wins
-// at 33 / 40 tokens, 3.41 / 3.56 against 3.62 / 3.68 ms: each CU reads all
-// of x for every 16 rows, and a CU streams only a few tens of GB/s.)
+// weights and runs far below the MFMA rate at these widths.  (Past 32
+// vectors the streamed product loses on Q4_0 prompts -- 40 tokens 3.96
+// against 3.57-3.68 ms: each CU reads all of x for every 16 rows, and a CU
+// streams only a few tens of GB/s.)
 constexpr int kStreamMinTokens = 16;
-constexpr int kStreamMaxTokens = 40;
+constexpr int kStreamMaxTokens = 32;
 
 bool use_stream(int type, int cols, int n, long long x_stride)
 {
