@@ -226,7 +226,11 @@ __device__ __forceinline__ void stream_mfma(const StreamStage<kType, kNT>& st, i
 template <int kType, int kNT>
 __global__ __launch_bounds__(kStreamWaves * 64) void stream_product_kernel(const StreamParams p)
 {
-    constexpr int kDepth = 4;  // blocks whose loads a wave has issued
+    // blocks whose loads a wave has issued: 4 for one token tile, 2 for two,
+    // whose larger stages (and 704-workgroup gate | up grid) gain less from
+    // depth than they lose in occupancy (32-token Q4_0 prompts 2.53 ms
+    // against 2.66 with 4, 2.72 with 3)
+    constexpr int kDepth = kNT == 1 ? 4 : 2;
     __shared__ float s_red[kStreamWaves][kNT][4][64];
     // the wave index as a scalar, so that the block loop's branches are uniform
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
