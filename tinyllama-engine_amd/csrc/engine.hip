@@ -1340,11 +1340,14 @@ int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int 
 // Batches of kStreamMinTokens .. kStreamMaxTokens vectors multiply F32 / F16
 // / Q8_0 / Q4_0 weights where they lie, dequantised in registers by
 // stream_product_kernel; the library product pays for an fp32 copy of the
-// weights and runs far below the MFMA rate at these widths.  (Past 32
+// weights and runs far below the MFMA rate at these widths, and the
+// multi-vector GEMVs read the weights once per 2-6 vectors (Q4_0 prompts of
+// 4 / 8 / 15 tokens 1.83 / 1.97 / 2.21 ms streamed against 2.34 / 4.21 /
+// 7.25 ms; at 2 tokens the GEMVs win, 1.53 against 1.77 ms).  (Past 32
 // vectors the streamed product loses on Q4_0 prompts -- 40 tokens 3.96
 // against 3.57-3.68 ms: each CU reads all of x for every 16 rows, and a CU
 // streams only a few tens of GB/s.)
-constexpr int kStreamMinTokens = 16;
+constexpr int kStreamMinTokens = 4;
 constexpr int kStreamMaxTokens = 32;
 
 bool use_stream(int type, int cols, int n, long long x_stride)
