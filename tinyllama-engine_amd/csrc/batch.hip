@@ -145,9 +145,9 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c)
 }
 
 // One block's operands for one lane as loaded: the weights' raw bits (F32 8
-// floats, F16 8 halves, Q8_0 / Q4_0 the scale and 8 bytes of qs, read as
-// 16-bit halves since blocks start at even byte offsets) and 8 x values per
-// token tile.  Nothing is computed from them until the block's turn comes,
+// floats, F16 8 halves, Q8_0 / Q4_0 12 bytes holding the lane's 8 bytes of
+// qs, and the scale for the lanes that read from the block's start) and 8 x
+// values per token tile.  Nothing is computed from them until the block's turn comes,
 // so that the loads of the blocks ahead stay in flight.
 template <int kType, int kNT>
 struct StreamStage {
@@ -169,13 +169,18 @@ __device__ __forceinline__ void stream_load(StreamStage<kType, kNT>& st, const u
         const uint4 h = *reinterpret_cast<const uint4*>(wrow + 2LL * (32 * blk + 8 * g));
         st.u[0] = h.x; st.u[1] = h.y; st.u[2] = h.z; st.u[3] = h.w;
     } else {
+        // One 12-byte load per lane: lanes that take qs[0..7] read bytes 0..11
+        // of the block (the scale, then their 8 bytes at 2..9); the others
+        // read the 12 bytes ending with their 8 (at 4..11 of the load) and
+        // take the scale from their row's first lane (stream_mfma).  Blocks
+        // start at even byte offsets: the loads are 2-byte aligned.
         constexpr int kBlock = kType == kQ8_0 ? 34 : 18;
-        const unsigned short* hw =
-            reinterpret_cast<const unsigned short*>(wrow + static_cast<long long>(kBlock) * blk);
         const int h = kType == kQ8_0 ? g : (g & 1);  // which 8 bytes of qs
-        st.u[0] = hw[0];
-        st.u[1] = hw[1 + 4 * h] | (static_cast<unsigned>(hw[2 + 4 * h]) << 16);
-        st.u[2] = hw[3 + 4 * h] | (static_cast<unsigned>(hw[4 + 4 * h]) << 16);
+        const unsigned char* p = wrow + static_cast<long long>(kBlock) * blk + (h ? 8 * h - 2 : 0);
+        const uint3 q = *reinterpret_cast<const uint3*>(p);
+        st.u[0] = q.x;
+        st.u[1] = q.y;
+        st.u[2] = q.z;
     }
 #pragma unroll
     for (int ti = 0; ti < kNT; ++ti) {
@@ -200,10 +205,15 @@ __device__ __forceinline__ void stream_mfma(const StreamStage<kType, kNT>& st, i
             w[2 * i + 1] = half_to_float(st.u[i] >> 16);
         }
     } else {
-        const float d = half_to_float(st.u[0]);
+        // the scale from lane c (g = 0, which loaded the block's first bytes);
+        // this lane's 8 bytes at bytes 2..9 of its load (h = 0) or 4..11
+        const int h = kType == kQ8_0 ? g : (g & 1);
+        const float d = half_to_float(__shfl(st.u[0], threadIdx.x & 15) & 0xFFFFu);
+        const unsigned q[2] = {h ? st.u[1] : (st.u[0] >> 16) | (st.u[1] << 16),
+                               h ? st.u[2] : (st.u[1] >> 16) | (st.u[2] << 16)};
 #pragma unroll
         for (int i = 0; i < 8; ++i) {
-            const unsigned byte = (st.u[1 + (i >> 2)] >> (8 * (i & 3))) & 0xFFu;
+            const unsigned byte = (q[i >> 2] >> (8 * (i & 3))) & 0xFFu;
             if constexpr (kType == kQ8_0)
                 w[i] = static_cast<float>(static_cast<signed char>(byte)) * d;
             else
