@@ -214,15 +214,17 @@ def test_projection_errors(tla, W, engines):
 
 
 BATCH_SHAPES = [(32, 256, 16), (2560, 2048, 33), (64, 5632, 128), (5632, 2048, 130), (96, 512, 300),
-                (2048, 2048, 256), (40, 5632, 257), (48, 256, 7), (40, 512, 20), (48, 256, 3)]
-# (48, 256, 3): GEMV groups; (48, 256, 7), (32, 256, 16), (40, 512, 20): streamed products
+                (2048, 2048, 256), (40, 5632, 257), (48, 256, 7), (40, 512, 20), (48, 256, 2)]
+# (48, 256, 2): GEMV groups (streamed for F16 / F32); (48, 256, 7), (32, 256, 16), (40, 512, 20):
+# streamed products
 
 
 @pytest.mark.parametrize("t,name", TYPES)
 @pytest.mark.parametrize("rows,cols,n_tok", BATCH_SHAPES)
 def test_matmul_batch(O, W, engines, t, name, rows, cols, n_tok):
-    """tla_matmul_batch: groups of GEMVs (< 4 tokens, and Q6_K under 16),
-    the streamed product (4-32 tokens, weights dequantised in registers) or
+    """tla_matmul_batch: groups of GEMVs (under 3 tokens, F16 / F32 under 2,
+    Q6_K under 16), the streamed product (up to 32 tokens, weights
+    dequantised in registers) or
     weights expanded to fp32 and hipBLASLt products, per token against the
     oracle's matmul."""
     if t == Q.Q6_K and cols % 256:
@@ -243,13 +245,13 @@ def test_matmul_batch(O, W, engines, t, name, rows, cols, n_tok):
 
 
 STREAM_SHAPES = [(2560, 2048, 16), (2048, 5632, 32), (40, 64, 17), (200, 128, 31), (96, 256, 40), (72, 512, 4),
-                 (2048, 2048, 9)]
+                 (2048, 2048, 9), (64, 256, 3), (48, 512, 2)]
 
 
 @pytest.mark.parametrize("t,name", TYPES)
 @pytest.mark.parametrize("rows,cols,n_tok", STREAM_SHAPES)
 def test_matmul_batch_streamed(tla, O, W, engines, t, name, rows, cols, n_tok):
-    """The streamed product (4-32 tokens): rows not a multiple of its 16-row
+    """The streamed product (2 or 3 to 32 tokens): rows not a multiple of its 16-row
     tiles, rows of 2 blocks (two of its four waves idle), token counts not a
     multiple of 16, and 40 tokens (the library product past the bound); every token against the oracle's matmul, and the same
     bits with one or two token tiles per workgroup (Q6_K takes the library

@@ -1337,22 +1337,25 @@ int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int 
 
 // out_s[t][row] (+)= W_s[row] . x[t] for the n_seg matrices of `segs`, one
 // type, over n tokens (x rows x_stride floats apart).
-// Batches of kStreamMinTokens .. kStreamMaxTokens vectors multiply F32 / F16
-// / Q8_0 / Q4_0 weights where they lie, dequantised in registers by
+// Batches of stream_min_tokens(type) .. kStreamMaxTokens vectors multiply F32
+// / F16 / Q8_0 / Q4_0 weights where they lie, dequantised in registers by
 // stream_product_kernel; the library product pays for an fp32 copy of the
 // weights and runs far below the MFMA rate at these widths, and the
 // multi-vector GEMVs read the weights once per 2-6 vectors (Q4_0 prompts of
-// 4 / 8 / 15 tokens 1.83 / 1.97 / 2.21 ms streamed against 2.34 / 4.21 /
-// 7.25 ms; at 2 tokens the GEMVs win, 1.53 against 1.77 ms).  (Past 32
+// 3 / 8 / 15 tokens 1.67 / 1.82 / ~2.0 ms streamed against 1.89 / 4.21 /
+// 7.25 ms).  At 2 tokens the GEMVs keep the quantised formats (Q4_0 1.53
+// against 1.63 ms, Q8_0 1.59 against 1.62) but not F16 / F32 (1.69 / 1.93
+// against 1.41 / 1.72 ms).  (Past 32
 // vectors the streamed product loses on Q4_0 prompts -- 40 tokens 3.96
 // against 3.57-3.68 ms: each CU reads all of x for every 16 rows, and a CU
 // streams only a few tens of GB/s.)
-constexpr int kStreamMinTokens = 4;
 constexpr int kStreamMaxTokens = 32;
+
+int stream_min_tokens(int type) { return type == kF16 || type == kF32 ? 2 : 3; }
 
 bool use_stream(int type, int cols, int n, long long x_stride)
 {
-    return stream_supported(type) && n >= kStreamMinTokens && n <= kStreamMaxTokens && cols % 32 == 0 &&
+    return stream_supported(type) && n >= stream_min_tokens(type) && n <= kStreamMaxTokens && cols % 32 == 0 &&
            x_stride % 4 == 0;
 }
 
