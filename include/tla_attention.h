@@ -204,8 +204,8 @@ int tla_matmul(tla_engine* e, float* out_dev, const void* w_dev, const float* x_
                int cols, int type);
 
 /* matmul() over a batch of n_tok vectors: out[t][rows] = W . x[t] (x
- * [n_tok][cols]).  3-32 vectors (F32, F16, Q8_0, Q4_0; F16 and F32 from
- * 2) run as one product that dequantises the weights in registers; from 33
+ * [n_tok][cols]).  3-64 vectors (F32, F16, Q8_0, Q4_0; F16 and F32 from
+ * 2) run as one product that dequantises the weights in registers; from 65
  * vectors on (Q6_K from 16) the weights are expanded to fp32 in an engine
  * workspace (rows x cols floats; F32 weights are used as they are) and
  * multiplied by hipBLASLt's fp32 product; fewer vectors (Q6_K: under 16)
@@ -317,8 +317,8 @@ int tla_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* 
  * token's logits (the ones generate() samples from).  The KV cache ends as
  * after n_tok forward() calls (to fp32 rounding: the attention sums are
  * grouped differently).  Engine memory it keeps for later calls: prompts of
- * 33-255 tokens two layers' weights in fp32 (about 350 MB at TinyLlama's
- * shapes), longer ones the largest matrix in fp32; prompts of 2-32 tokens
+ * 65-255 tokens two layers' weights in fp32 (about 350 MB at TinyLlama's
+ * shapes), longer ones the largest matrix in fp32; prompts of 2-64 tokens
  * none (as long as no layer holds a Q6_K matrix). */
 int tla_prefill_forward(tla_engine* e, const tla_model* m, float* key_cache_dev,
                         float* value_cache_dev, const int* tokens_host, int n_tok, int pos0,
@@ -384,8 +384,8 @@ enum tla_option {
     TLA_OPT_DECODE_GROUP = 2, /* kv heads per decode workgroup in the plan of one split
                                  length: 1, 2 or 4 (the other plan always takes 4);
                                  results do not depend on it */
-    TLA_OPT_STREAM_TILES = 3  /* batched products of 2-32 vectors: vectors per
-                                 workgroup in tiles of 16, 1 or 2; results do not
+    TLA_OPT_STREAM_TILES = 3  /* batched products of 2-64 vectors: vectors per
+                                 workgroup in tiles of 16, 1 to 4; results do not
                                  depend on it */
 };
 enum tla_decode_plan { TLA_PLAN_AUTO = 0, TLA_PLAN_ALIGNED = 1, TLA_PLAN_BALANCED = 2 };

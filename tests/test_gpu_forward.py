@@ -412,9 +412,9 @@ def test_prefill_forward_errors(tla, W, engines):
 
 @pytest.mark.parametrize("name", ["q8_0", "f16_tied", "q4_0", "mixed"])
 def test_prefill_forward_long_prompt(tla, O, W, engines, name):
-    """A 48-token prompt: the batched projections as fp32 weights +
-    hipBLASLt products (>= 16 tokens, every format).  Last token's logits
-    against the oracle's token loop."""
+    """A 48-token prompt: the batched projections as streamed products with
+    three token tiles (Q6_K matrices as fp32 weights + hipBLASLt products).
+    Last token's logits against the oracle's token loop."""
     g = golden("forward.npz")
     spec, t = model_from_golden(W, g, name)
     eng = spec_engine(engines, spec)

@@ -223,7 +223,7 @@ BATCH_SHAPES = [(32, 256, 16), (2560, 2048, 33), (64, 5632, 128), (5632, 2048, 1
 @pytest.mark.parametrize("rows,cols,n_tok", BATCH_SHAPES)
 def test_matmul_batch(O, W, engines, t, name, rows, cols, n_tok):
     """tla_matmul_batch: groups of GEMVs (under 3 tokens, F16 / F32 under 2,
-    Q6_K under 16), the streamed product (up to 32 tokens, weights
+    Q6_K under 16), the streamed product (up to 64 tokens, weights
     dequantised in registers) or
     weights expanded to fp32 and hipBLASLt products, per token against the
     oracle's matmul."""
@@ -245,7 +245,7 @@ def test_matmul_batch(O, W, engines, t, name, rows, cols, n_tok):
 
 
 STREAM_SHAPES = [(2560, 2048, 16), (2048, 5632, 32), (40, 64, 17), (200, 128, 31), (96, 256, 40), (72, 512, 4),
-                 (2048, 2048, 9), (64, 256, 3), (48, 512, 2)]
+                 (2048, 2048, 9), (64, 256, 3), (48, 512, 2), (300, 256, 64), (32, 128, 65), (2048, 2048, 57)]
 
 
 @pytest.mark.parametrize("t,name", TYPES)
@@ -268,7 +268,7 @@ def test_matmul_batch_streamed(tla, O, W, engines, t, name, rows, cols, n_tok):
         xd = track(eng.array(x))
         out = track(eng.array((n_tok, rows)))
         try:
-            for tiles in (0, 1, 2):
+            for tiles in (0, 1, 2, 3, 4):
                 eng.set_option(tla.OPT_STREAM_TILES, tiles)
                 eng.matmul_batch(out.ptr, w.ptr, xd.ptr, rows, cols, n_tok, t)
                 outs.append(out.download())
@@ -282,9 +282,9 @@ def test_matmul_batch_streamed(tla, O, W, engines, t, name, rows, cols, n_tok):
 
 
 def test_stream_tiles_option(tla, engines):
-    """TLA_OPT_STREAM_TILES takes 0 (per shape), 1 or 2."""
+    """TLA_OPT_STREAM_TILES takes 0 (per shape) to 4."""
     eng = engines(1, 64)
-    for bad in (-1, 3):
+    for bad in (-1, 5):
         with pytest.raises(tla.TlaError) as e:
             eng.set_option(tla.OPT_STREAM_TILES, bad)
         assert e.value.code == tla.TLA_ERR_INVALID_ARGUMENT

@@ -11,7 +11,7 @@ namespace tla {
 // workgroup; more tokens take further token chunks, each reading the weights
 // again.  F32 / F16 / Q8_0 / Q4_0 rows of cols % 32 == 0 columns; x rows
 // 16-byte aligned (x_stride % 4 == 0), F32 / F16 weights 16-byte aligned.
-constexpr int kStreamMaxTiles = 2;
+constexpr int kStreamMaxTiles = 4;
 struct StreamParams {
     GemvSegment seg[kGemvMaxSeg];
     int n_seg;

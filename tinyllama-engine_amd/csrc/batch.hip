@@ -236,7 +236,7 @@ __device__ __forceinline__ void stream_mfma(const StreamStage<kType, kNT>& st, i
 template <int kType, int kNT>
 __global__ __launch_bounds__(kStreamWaves * 64) void stream_product_kernel(const StreamParams p)
 {
-    // blocks whose loads a wave has issued: 4 for one token tile, 2 for two,
+    // blocks whose loads a wave has issued: 4 for one token tile, 2 for more,
     // whose larger stages (and 704-workgroup gate | up grid) gain less from
     // depth than they lose in occupancy (32-token Q4_0 prompts 2.53 ms
     // against 2.66 with 4, 2.72 with 3)
@@ -310,10 +310,12 @@ hipError_t launch_stream_typed(const StreamParams& p, hipStream_t s)
     const dim3 grid(static_cast<unsigned>((p.total_rows + 15) / 16),
                     static_cast<unsigned>((nt + p.tiles - 1) / p.tiles));
     const dim3 block(kStreamWaves * 64);
-    if (p.tiles == 1)
-        hipLaunchKernelGGL((stream_product_kernel<kType, 1>), grid, block, 0, s, p);
-    else
-        hipLaunchKernelGGL((stream_product_kernel<kType, 2>), grid, block, 0, s, p);
+    switch (p.tiles) {
+    case 1: hipLaunchKernelGGL((stream_product_kernel<kType, 1>), grid, block, 0, s, p); break;
+    case 2: hipLaunchKernelGGL((stream_product_kernel<kType, 2>), grid, block, 0, s, p); break;
+    case 3: hipLaunchKernelGGL((stream_product_kernel<kType, 3>), grid, block, 0, s, p); break;
+    default: hipLaunchKernelGGL((stream_product_kernel<kType, 4>), grid, block, 0, s, p); break;
+    }
     return hipGetLastError();
 }
 

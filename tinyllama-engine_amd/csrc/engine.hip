@@ -1340,16 +1340,16 @@ int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int 
 // Batches of stream_min_tokens(type) .. kStreamMaxTokens vectors multiply F32
 // / F16 / Q8_0 / Q4_0 weights where they lie, dequantised in registers by
 // stream_product_kernel; the library product pays for an fp32 copy of the
-// weights and runs far below the MFMA rate at these widths, and the
+// weights and runs far below the MFMA rate at these widths (Q4_0 prompts of
+// 33 / 48 / 64 tokens 2.79 / 3.22 / 3.60 ms streamed against 3.60 / 3.64 /
+// 3.65 ms), and the
 // multi-vector GEMVs read the weights once per 2-6 vectors (Q4_0 prompts of
 // 3 / 8 / 15 tokens 1.67 / 1.82 / ~2.0 ms streamed against 1.89 / 4.21 /
 // 7.25 ms).  At 2 tokens the GEMVs keep the quantised formats (Q4_0 1.53
 // against 1.63 ms, Q8_0 1.59 against 1.62) but not F16 / F32 (1.69 / 1.93
-// against 1.41 / 1.72 ms).  (Past 32
-// vectors the streamed product loses on Q4_0 prompts -- 40 tokens 3.96
-// against 3.57-3.68 ms: each CU reads all of x for every 16 rows, and a CU
-// streams only a few tens of GB/s.)
-constexpr int kStreamMaxTokens = 32;
+// against 1.41 / 1.72 ms).  Past 64 vectors the library product wins: each
+// 16-row workgroup loads all of x itself.
+constexpr int kStreamMaxTokens = 64;
 
 int stream_min_tokens(int type) { return type == kF16 || type == kF32 ? 2 : 3; }
 
@@ -1375,8 +1375,8 @@ int stream_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, in
     // token tiles of 16 per workgroup: one for matrices of at most 128 row
     // tiles (their workgroups are too few to fill the CUs otherwise; W_o and
     // W_down at TinyLlama's shapes, 32 tokens: 11.6 against 15.2 us and 22.4
-    // against 30.1 us), else all of them (W_qkv, gate + up: 15.4 against
-    // 19.7 us, 40.6 against 52.7 us)
+    // against 30.1 us), else as many as kStreamMaxTiles allows (W_qkv,
+    // gate + up: 15.4 against 19.7 us, 40.6 against 52.7 us)
     const int nt = (n + 15) / 16;
     p.tiles = e->opt_stream_tiles > 0 ? e->opt_stream_tiles
               : (total + 15) / 16 <= 128 ? 1
