@@ -121,8 +121,8 @@ __global__ __launch_bounds__(kThreads) void dequant_rows_kernel(const unsigned c
 
 
 // ---- stream_product_kernel --------------------------------------------------
-// The projections of a batch of a few tokens with the weights dequantised in
-// registers (no fp32 copy of the matrix): out[t][row] (+)= sum_k W[row][k]
+// The projections of a batch of up to 64 tokens with the weights dequantised
+// in registers (no fp32 copy of the matrix): out[t][row] (+)= sum_k W[row][k]
 // x[t][k] for 16 weight rows and 16 kNT tokens per workgroup (blockIdx.y
 // selects the token chunk).  v_mfma_f32_16x16x4f32 with the tokens as the A
 // operand and the weight rows as the B operand, so that lane l = 16 g + c
@@ -147,8 +147,8 @@ __device__ __forceinline__ floatx4 mfma16(float a, float b, floatx4 c)
 // One block's operands for one lane as loaded: the weights' raw bits (F32 8
 // floats, F16 8 halves, Q8_0 / Q4_0 12 bytes holding the lane's 8 bytes of
 // qs, and the scale for the lanes that read from the block's start) and 8 x
-// values per token tile.  Nothing is computed from them until the block's turn comes,
-// so that the loads of the blocks ahead stay in flight.
+// values per token tile.  Nothing is computed from them until the block's
+// turn comes, so that the loads of the blocks ahead stay in flight.
 template <int kType, int kNT>
 struct StreamStage {
     static constexpr int kWords = kType == kF32 ? 8 : kType == kF16 ? 4 : 3;
