@@ -296,12 +296,22 @@ __global__ __launch_bounds__(64 * kSub * kKvWaves) void decode_split_kernel(
     // issues them after the first batch has arrived: one more round trip).
     asm volatile("" ::"s"(p.q), "s"(p.k), "s"(p.v), "s"(p.out), "s"(p.kc), "s"(p.vc), "s"(p.rope),
                  "s"(p.part));
+    // Likewise every scalar field the first loads depend on (the compiler
+    // fetches the ones it needs later in a second batch, after the first has
+    // arrived: one more round trip before the first tile is requested), and
+    // for one sequence its position and offsets.
+    asm volatile("" ::"s"(p.counters), "s"(p.seq_stride), "s"(p.layer_stride), "s"(p.wg_tiles),
+                 "s"(p.total_tiles), "s"(p.aligned), "s"(p.in_cache), "s"(p.rotate), "s"(p.n_lb),
+                 "s"(p.layer0));
+    if constexpr (kMaxSeq == 1)
+        asm volatile("" ::"s"(b.pos[0]), "s"(b.seq_id[0]), "s"(b.tile_prefix[0]));
     const int lane = threadIdx.x & 63;
     // wave index made explicitly scalar so cache bases stay in SGPRs
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int slot = wave % kKvWaves;  // kv head within the workgroup
     const int sub = wave / kKvWaves;   // which half of the split's positions
-    const int kvh = blockIdx.y * kKvWaves + slot;
+    const int group = blockIdx.y;  // kv group
+    const int kvh = group * kKvWaves + slot;
     const bool active = kvh < p.n_head_kv;  // uniform per wave
 
     // Workgroup w takes the flat tiles [w * wg_tiles, (w + 1) * wg_tiles).
@@ -626,7 +636,7 @@ __global__ __launch_bounds__(64 * kSub * kKvWaves) void decode_split_kernel(
             __syncthreads();
             if (threadIdx.x < n_pend) {
                 const int2 pu = s_pend[threadIdx.x];
-                int* const counter = p.counters + (long long)pu.x * gridDim.y + blockIdx.y;
+                int* const counter = p.counters + (long long)pu.x * p.n_groups + group;
                 const bool last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED,
                                                          __HIP_MEMORY_SCOPE_AGENT) == pu.y - 1;
                 if (last)  // every split has arrived: ready for the next launch
@@ -650,7 +660,7 @@ __global__ __launch_bounds__(64 * kSub * kKvWaves) void decode_split_kernel(
             __atomic_signal_fence(__ATOMIC_SEQ_CST);
             __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
-            int* const counter = p.counters + (long long)unit * gridDim.y + blockIdx.y;
+            int* const counter = p.counters + (long long)unit * p.n_groups + group;
             if (threadIdx.x == 0)
                 s_last = __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED,
                                                 __HIP_MEMORY_SCOPE_AGENT) == nsplit - 1;
@@ -696,10 +706,16 @@ hipError_t launch_decode(const DecodeParams& p, const DecodeSeqs<kMaxSeqPerLaunc
          p.kv_group != kDecodeKvGroupLarge) ||
         (!p.aligned && p.kv_group != kDecodeKvGroupLarge))
         return hipErrorInvalidValue;
-    const dim3 grid((p.total_tiles + p.wg_tiles - 1) / p.wg_tiles,
-                    (p.n_head_kv + p.kv_group - 1) / p.kv_group);
+    const dim3 grid((p.total_tiles + p.wg_tiles - 1) / p.wg_tiles, p.n_groups);
     const dim3 block(64 * kSub * p.kv_group);
-    if (p.n_seq <= 8) {
+    if (p.n_seq == 1) {
+        DecodeSeqs<1> one{};
+        one.pos[0] = seqs.pos[0];
+        one.seq_id[0] = seqs.seq_id[0];
+        one.tile_prefix[0] = seqs.tile_prefix[0];
+        one.tile_prefix[1] = seqs.tile_prefix[1];
+        launch_shape(p, one, grid, block, s);
+    } else if (p.n_seq <= 8) {
         DecodeSeqs<8> small{};
         for (int i = 0; i < p.n_seq; ++i) {
             small.pos[i] = seqs.pos[i];

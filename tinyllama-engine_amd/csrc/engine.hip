@@ -840,11 +840,11 @@ int decode_impl(tla_engine* e, bool fixed_scratch, int n_seq, const int* pos_hos
                          : wg * kDecodeTile <= 256    ? kDecodeKvGroupSmall
                                                       : kDecodeKvGroupLarge;
     const long long units = static_cast<long long>(n_seq) * n_step_layers;
+    const int n_groups = (c.n_head_kv + kv_group - 1) / kv_group;
     if (max_splits > 1) {
         // per (unit, split, kv head): 64 output floats + max + sum for each real head
         const size_t bytes = decode_part_bytes(units, max_splits, c.n_head_kv, e->gqa);
-        const long long groups = (c.n_head_kv + kv_group - 1) / kv_group;
-        const size_t n_counters = static_cast<size_t>(units * groups);
+        const size_t n_counters = static_cast<size_t>(units * n_groups);
         if (fixed_scratch) {
             if (!e->scratch)
                 return fail(TLA_ERR_UNSUPPORTED, "device %d has no static split scratch", e->device);
@@ -886,6 +886,7 @@ int decode_impl(tla_engine* e, bool fixed_scratch, int n_seq, const int* pos_hos
     p.in_cache = in_cache ? 1 : 0;
     p.kv_group = kv_group;
     p.scale_log2 = scale_log2(e->head_dim);
+    p.n_groups = n_groups;
 
     if (int rc = launch(e, TLA_KERNEL_DECODE, "decode",
                         [&] { return launch_decode(p, seqs, e->stream); }))

@@ -55,6 +55,7 @@ struct DecodeParams {
     int kv_group;      // kv heads per workgroup: kDecodeKvGroupSmall / Large
     int rotate;
     float scale_log2;  // log2(e) / sqrt(head_dim)
+    int n_groups;      // kv groups = ceil(n_head_kv / kv_group) (grid y)
 };
 
 // Per-sequence positions and tile offsets of one launch, passed by value in
