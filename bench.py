@@ -689,39 +689,62 @@ def cpu_generate_baseline(spec, tensors, prompt, wname, n_prompt=8, n_decode=8):
             **cpu_host()}
 
 
-READ_FLOOR_GRIDS = (256, 512, 1024, 2048, 4096, 8192)
+READ_FLOOR_GRIDS = (256, 512, 1024, 2048, 4096, 8192, 16384)
+READ_FLOOR_KINDS = {"global": 0, "global_nt": 1, "buffer": 2, "buffer_nt": 3}
+READ_FLOOR_DEPTHS = (8, 16, 32)
+# the 8-sequence x 16384-position x 22-layer step (decode_long)'s algorithmic bytes
+DECODE_LONG_BYTES = 8 * 22 * (2048 * 16384 + 20480)
 
 
-def run_read_floor(steps, warmup, contexts=(2048, 4096, 8192, 16384), n_layers=22):
+def read_floor_sizes(contexts=(2048, 4096, 8192, 16384), n_layers=22, long=True):
+    sizes = [(f"ctx {ctx}", ctx, W.decode_bytes(ctx) * n_layers) for ctx in contexts]
+    if long:
+        sizes.append(("decode_long", 16384, DECODE_LONG_BYTES))
+    return sizes
+
+
+def run_read_floor(steps, warmup, sizes=None, kinds=None, depths=READ_FLOOR_DEPTHS,
+                   grids=READ_FLOOR_GRIDS):
     """The hand-written streaming read (tla_read_floor) over exactly the bytes
-    a batch-1 decode step moves at each context (22 layers, 2048*L + 20480
-    per layer), launches rotating over copies past the Infinity Cache and
-    queued back to back; the best of a few grid sizes.  What one launch can
-    read in the time it takes: the bar for the decode kernel at that size."""
+    a decode step moves: batch 1 x 22 layers at each context (2048*L + 20480
+    per layer) and the 8 x 16384 x 22 step, launches rotating over copies past
+    the Infinity Cache and queued back to back; the best of every load form,
+    depth and grid size.  What one launch can read in the time it takes: the
+    bar for the decode kernel at that size."""
+    sizes = read_floor_sizes() if sizes is None else sizes
+    kinds = READ_FLOOR_KINDS if kinds is None else kinds
     eng = tla.Engine(tla.Config.tinyllama(n_layers=1, n_ctx=16))
-    sink = eng.array((max(READ_FLOOR_GRIDS),))
+    sink = eng.array((max(grids),))
     out = []
-    for ctx in contexts:
-        nbytes = W.decode_bytes(ctx) * n_layers
+    for label, ctx, nbytes in sizes:
         span = (nbytes + 255) // 256 * 256
-        copies = max(2, -(-3 * MALL_BYTES // 2 // nbytes))
+        copies = max(1 if nbytes > 4 * MALL_BYTES else 2, -(-3 * MALL_BYTES // 2 // nbytes))
         buf = tla.DeviceArray(eng, (span * copies,), np.uint8)
-        best = None
-        for grid in READ_FLOOR_GRIDS:
-            def one(i, grid=grid):
-                eng.read_floor(buf.ptr + (i % copies) * span, nbytes, grid, sink.ptr)
-            for i in range(warmup):
-                one(i)
-            ms = back_to_back_ms(eng, one, steps)
-            if best is None or ms < best[0]:
-                best = (ms, grid)
-        ms, grid = best
+        best, by_kind = None, {}
+        for kname, kind in kinds.items():
+            for depth in depths:
+                for grid in grids:
+                    def one(i, grid=grid, kind=kind, depth=depth):
+                        eng.read_floor(buf.ptr + (i % copies) * span, nbytes, grid, sink.ptr, kind, depth)
+                    for i in range(warmup):
+                        one(i)
+                    ms = back_to_back_ms(eng, one, steps)
+                    cand = (ms, kname, depth, grid)
+                    if best is None or ms < best[0]:
+                        best = cand
+                    if kname not in by_kind or ms < by_kind[kname][0]:
+                        by_kind[kname] = cand
+        ms, kname, depth, grid = best
         gbs = nbytes / (ms * 1e-3) / 1e9
-        log(f"[bench] read floor {nbytes / 1e6:.1f} MB (decode batch 1 x {n_layers} layers, ctx {ctx}): "
-            f"{ms * 1e3:.2f} us with {grid} workgroups -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), "
-            f"{copies} rotated copies")
-        out.append({"ctx": ctx, "bytes": nbytes, "us": round(ms * 1e3, 2), "GB_s": round(gbs, 1),
-                    "frac": round(gbs / HBM_PEAK_GBS, 4), "workgroups": grid, "copies": copies})
+        log(f"[bench] read floor {nbytes / 1e6:.1f} MB ({label}): {ms * 1e3:.2f} us with {grid} workgroups, "
+            f"{kname} loads, {depth} per thread in flight -> {gbs:.0f} GB/s ({gbs / HBM_PEAK_GBS:.1%}), "
+            f"{copies} rotated copies; best per load form: "
+            + ", ".join(f"{k} {v[0] * 1e3:.2f} us ({v[2]} deep, {v[3]} wg)" for k, v in by_kind.items()))
+        out.append({"size": label, "ctx": ctx, "bytes": nbytes, "us": round(ms * 1e3, 2),
+                    "GB_s": round(gbs, 1), "frac": round(gbs / HBM_PEAK_GBS, 4), "workgroups": grid,
+                    "load": kname, "depth": depth, "copies": copies,
+                    "best_by_load": {k: {"us": round(v[0] * 1e3, 2), "depth": v[2], "workgroups": v[3]}
+                                     for k, v in by_kind.items()}})
         buf.free()
     sink.free()
     eng.close()
@@ -844,8 +867,9 @@ def main():
                           "unit": "GB/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                           "ms_per_step": r[0]["us"] / 1e3, "higher_is_better": True, "scaling": "weak",
                           "vs_baseline": None, "dtype": "f32", "data": "synthetic",
-                          "config": {"workload": "read_floor", "bytes": "decode batch 1 x 22 layers",
-                                     "contexts": [x["ctx"] for x in r], "parallelism": "none"},
+                          "config": {"workload": "read_floor",
+                                     "bytes": "decode batch 1 x 22 layers; decode_long",
+                                     "sizes": [x["size"] for x in r], "parallelism": "none"},
                           "sweep": r}))
         return
     if args.workload == "mfma_floor":
@@ -999,8 +1023,11 @@ def main():
         # ceiling at batch 1), and the decode kernel's rate over it at 2048
         floor = run_read_floor(args.steps, args.warmup)
         line["extra"]["read_floor"] = floor
-        f2k = next(x for x in floor if x["ctx"] == 2048)
+        f2k = next(x for x in floor if x["size"] == "ctx 2048")
         line["extra"]["decode_model_over_read_floor"] = round(f2k["us"] / (d["ms_per_step"] * 1e3), 4)
+        flong = next(x for x in floor if x["size"] == "decode_long")
+        line["extra"]["decode_long_over_read_floor"] = round(
+            flong["us"] / (line["extra"]["decode_long"]["ms_per_step"] * 1e3), 4)
     print(json.dumps(line))
 
 

@@ -360,12 +360,20 @@ int tla_event_elapsed(tla_engine* e, int slot_begin, int slot_end, float* ms);
 
 /* Streaming-read floor: read `bytes` at src_dev (16-byte aligned, a multiple
  * of 16) with n_workgroups workgroups of 256 threads, each summing one
- * contiguous chunk, on the engine's stream; sink_dev [n_workgroups] floats is
- * never written in practice (the sums are kept only so the loads stay).  What
- * one launch can read from HBM in the time it takes -- the bar the decode
- * kernel's byte rate is set against.  No reference counterpart. */
-int tla_read_floor(tla_engine* e, const void* src_dev, size_t bytes, int n_workgroups,
-                   float* sink_dev);
+ * contiguous chunk with `depth` (8, 16 or 32) 16-byte loads in flight per
+ * thread, in the load form `load_kind` (below), on the engine's stream;
+ * sink_dev [n_workgroups] floats is never written in practice (the sums are
+ * kept only so the loads stay).  The buffer forms need chunks under 2 GiB.
+ * What one launch can read from HBM in the time it takes -- the bar the
+ * decode kernel's byte rate is set against.  No reference counterpart. */
+enum tla_read_kind {
+    TLA_READ_GLOBAL = 0,       /* global_load_dwordx4 */
+    TLA_READ_GLOBAL_NT = 1,    /* the same, non-temporal */
+    TLA_READ_BUFFER = 2,       /* buffer_load_dwordx4, loads past the chunk return zeros */
+    TLA_READ_BUFFER_NT = 3     /* the same, non-temporal */
+};
+int tla_read_floor(tla_engine* e, const void* src_dev, size_t bytes, int n_workgroups, int load_kind,
+                   int depth, float* sink_dev);
 
 /* fp32 MFMA floor: n_workgroups workgroups of 4 waves on the engine's stream,
  * each wave `iters` rounds of 16 v_mfma_f32_32x32x2f32 (2 x 32 x 32 x 2 flops

@@ -149,17 +149,23 @@ def test_mfma_floor_runs_and_leaves_the_sink(tla, engines):
 
 
 def test_read_floor_reads_and_leaves_the_sink(tla, engines):
-    """The streaming-read hook: runs over an odd byte count and grid, never
-    writes its sink for ordinary data, and validates its arguments before
-    launching."""
+    """The streaming-read hook: every load form and depth runs over an odd
+    byte count with grids whose chunks end mid-round (777 workgroups: 1.3
+    rounds of 256 loads per thread; 3: many full rounds and a remainder),
+    never writes its sink for ordinary data, and validates its arguments
+    before launching."""
     eng = engines(1, 64)
     with device_arrays() as track:
         src = track(eng.array(np.arange(1 << 20, dtype=np.float32)))
         sink = track(eng.array(np.full(777, 7.0, np.float32)))
-        eng.read_floor(src.ptr, (1 << 22) - 48, 777, sink.ptr)
+        for kind in (tla.READ_GLOBAL, tla.READ_GLOBAL_NT, tla.READ_BUFFER, tla.READ_BUFFER_NT):
+            for depth in (8, 16, 32):
+                for grid in (777, 3):
+                    eng.read_floor(src.ptr, (1 << 22) - 48, grid, sink.ptr, kind, depth)
         eng.synchronize()
         assert np.all(sink.download() == 7.0)
-        for nbytes, grid in ((15, 4), (1 << 22, 0), (40, 4)):
+        for nbytes, grid, kind, depth in ((15, 4, 0, 8), (1 << 22, 0, 0, 8), (40, 4, 0, 8),
+                                          (1 << 22, 4, 4, 8), (1 << 22, 4, -1, 8), (1 << 22, 4, 2, 12)):
             with pytest.raises(tla.TlaError) as e:
-                eng.read_floor(src.ptr, nbytes, grid, sink.ptr)
+                eng.read_floor(src.ptr, nbytes, grid, sink.ptr, kind, depth)
             assert e.value.code == tla.TLA_ERR_INVALID_ARGUMENT

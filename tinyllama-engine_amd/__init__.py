@@ -51,6 +51,7 @@ W_F32, W_F16, W_Q4_0, W_Q8_0, W_Q6_K = 0, 1, 2, 8, 14
 OPT_DECODE_SPLIT, OPT_DECODE_PLAN, OPT_DECODE_GROUP = 0, 1, 2
 OPT_STREAM_TILES = 3
 PLAN_AUTO, PLAN_ALIGNED, PLAN_BALANCED = 0, 1, 2
+READ_GLOBAL, READ_GLOBAL_NT, READ_BUFFER, READ_BUFFER_NT = 0, 1, 2, 3
 
 
 class TlaError(RuntimeError):
@@ -147,7 +148,7 @@ SIGNATURES = {
     "tla_event_record": (C.c_int, [_vp, C.c_int]),
     "tla_event_elapsed": (C.c_int, [_vp, C.c_int, C.c_int, C.POINTER(C.c_float)]),
     "tla_set_option": (C.c_int, [_vp, C.c_int, C.c_longlong]),
-    "tla_read_floor": (C.c_int, [_vp, _vp, C.c_size_t, C.c_int, _vp]),
+    "tla_read_floor": (C.c_int, [_vp, _vp, C.c_size_t, C.c_int, C.c_int, C.c_int, _vp]),
     "tla_mfma_floor": (C.c_int, [_vp, C.c_int, C.c_int, _vp]),
 }
 
@@ -365,8 +366,10 @@ class Engine:
                "tla_profile_read")
         return ms.value, n.value
 
-    def read_floor(self, src: int, nbytes: int, n_workgroups: int, sink: int):
-        _check(lib().tla_read_floor(self.h, src, nbytes, n_workgroups, sink), "tla_read_floor")
+    def read_floor(self, src: int, nbytes: int, n_workgroups: int, sink: int,
+                   kind: int = READ_GLOBAL, depth: int = 8):
+        _check(lib().tla_read_floor(self.h, src, nbytes, n_workgroups, kind, depth, sink),
+               "tla_read_floor")
 
     def mfma_floor(self, n_workgroups: int, iters: int, sink: int):
         _check(lib().tla_mfma_floor(self.h, n_workgroups, iters, sink), "tla_mfma_floor")

@@ -135,12 +135,17 @@ __device__ __forceinline__ floatx4 ld_dev4(__amdgpu_buffer_rsrc_t rs, int byte_o
 }
 
 // Bounded cache reads: a raw buffer load whose offset is past the
-// resource's byte count returns zeros without a memory request.
+// resource's byte count returns zeros without a memory request.  The cache
+// rows are read once per launch, so the loads are non-temporal: a streaming
+// read of the same bytes runs ~10 % faster with the nt bit than without
+// (tla_read_floor, 185 MB-5.9 GB).
 constexpr unsigned kOutOfRange = 0x80000000u;  // > any slice (engine: < 2^31 - 256 B)
+constexpr int kNonTemporal = 2;                // cache-policy bit NT (gfx940 family)
 
 __device__ __forceinline__ float4 ld_rows4(__amdgpu_buffer_rsrc_t rs, unsigned byte_off)
 {
-    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, 0));
+    return __builtin_bit_cast(float4,
+                              __builtin_amdgcn_raw_buffer_load_b128(rs, byte_off, 0, kNonTemporal));
 }
 
 __device__ __forceinline__ float ld_dev1(__amdgpu_buffer_rsrc_t rs, int byte_off)

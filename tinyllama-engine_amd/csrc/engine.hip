@@ -1897,7 +1897,8 @@ int tla_event_elapsed(tla_engine* e, int slot_begin, int slot_end, float* ms)
     return ok();
 }
 
-int tla_read_floor(tla_engine* e, const void* src_dev, size_t bytes, int n_workgroups, float* sink_dev)
+int tla_read_floor(tla_engine* e, const void* src_dev, size_t bytes, int n_workgroups, int load_kind,
+                   int depth, float* sink_dev)
 {
     if (int rc = check_engine(e)) return rc;
     if (!src_dev || !sink_dev) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
@@ -1906,8 +1907,16 @@ int tla_read_floor(tla_engine* e, const void* src_dev, size_t bytes, int n_workg
                     bytes);
     if (n_workgroups < 1 || n_workgroups > (1 << 20))
         return fail(TLA_ERR_INVALID_ARGUMENT, "n_workgroups %d not in [1, 2^20]", n_workgroups);
+    if (load_kind < TLA_READ_GLOBAL || load_kind > TLA_READ_BUFFER_NT)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "load_kind %d not in [0, 3]", load_kind);
+    if (depth != 8 && depth != 16 && depth != 32)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "depth %d not 8, 16 or 32", depth);
+    if (load_kind >= TLA_READ_BUFFER &&
+        (bytes / 16 / n_workgroups + 1 + 32 * 256) * 16 >= (1ull << 31))
+        return fail(TLA_ERR_INVALID_ARGUMENT, "buffer loads: %zu bytes over %d workgroups is 2 GiB or more each",
+                    bytes, n_workgroups);
     if (int rc = set_device(e)) return rc;
-    const hipError_t err = launch_read_floor(src_dev, bytes, n_workgroups, sink_dev, e->stream);
+    const hipError_t err = launch_read_floor(src_dev, bytes, n_workgroups, load_kind, depth, sink_dev, e->stream);
     if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "read floor launch: %s", hipGetErrorString(err));
     return ok();
 }

@@ -99,29 +99,68 @@ __global__ __launch_bounds__(256) void zero1_kernel(unsigned char* __restrict__ 
 }
 
 // Streaming read floor: workgroup w sums the 16-byte words [w * per_wg,
-// (w + 1) * per_wg) of src, each thread eight loads in flight (unrolled), and
-// writes its sum only if it equals a value no sum of these inputs takes, so
-// that the loads stay but nothing is written.  The fastest a single launch
-// can move a given number of bytes from HBM.
-constexpr int kReadUnroll = 8;
+// (w + 1) * per_wg) of src, each thread kDepth 16-byte loads in flight
+// (unrolled), and writes its sum only if it equals a value no sum of these
+// inputs takes, so that the loads stay but nothing is written.  The fastest
+// a single launch can move a given number of bytes from HBM, over the load
+// forms a kernel can use:
+//   kKind 0  global_load_dwordx4
+//   kKind 1  global_load_dwordx4 nt (__builtin_nontemporal_load)
+//   kKind 2  buffer_load_dwordx4 through a resource covering the chunk: the
+//            loads past its end return zeros without a request, so every
+//            round issues all kDepth loads (no remainder loop)
+//   kKind 3  the same with the nt bit
+constexpr int kRawBufferWord3 = 0x00020000;  // untyped 32-bit buffer (gfx9 family)
+constexpr int kCachePolicyNt = 2;            // buffer cache-policy bit NT (gfx940 family)
 
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+template <int kKind>
+__device__ __forceinline__ float4 floor_load(const float4* p)
+{
+    if constexpr (kKind == 1) {
+        const floatx4_t v = __builtin_nontemporal_load(reinterpret_cast<const floatx4_t*>(p));
+        return make_float4(v.x, v.y, v.z, v.w);
+    } else {
+        return *p;
+    }
+}
+
+template <int kKind, int kDepth>
 __global__ __launch_bounds__(256) void read_floor_kernel(const float4* __restrict__ src, long long n16,
                                                          long long per_wg, float* __restrict__ sink)
 {
     const long long lo = (long long)blockIdx.x * per_wg;
     const long long hi = lo + per_wg < n16 ? lo + per_wg : n16;
     float acc = 0.f;
-    long long i = lo + threadIdx.x;
-    for (; i + (kReadUnroll - 1) * 256 < hi; i += kReadUnroll * 256) {
-        float4 v[kReadUnroll];
+    if constexpr (kKind >= 2) {
+        // chunk bytes < 2^31 (host check): 32-bit offsets
+        const unsigned n = (unsigned)(hi > lo ? hi - lo : 0);
+        const auto rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<float4*>(src + lo), 0, n * 16u,
+                                                          kRawBufferWord3);
+        for (unsigned i = threadIdx.x; i < n; i += kDepth * 256) {
+            float4 v[kDepth];
 #pragma unroll
-        for (int u = 0; u < kReadUnroll; ++u) v[u] = src[i + u * 256];
+            for (int u = 0; u < kDepth; ++u)
+                v[u] = __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                      rs, (i + u * 256u) * 16u, 0, kKind == 3 ? kCachePolicyNt : 0));
 #pragma unroll
-        for (int u = 0; u < kReadUnroll; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
-    }
-    for (; i < hi; i += 256) {
-        const float4 v = src[i];
-        acc += (v.x + v.y) + (v.z + v.w);
+            for (int u = 0; u < kDepth; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+        }
+    } else {
+        long long i = lo + threadIdx.x;
+        for (; i + (kDepth - 1) * 256 < hi; i += kDepth * 256) {
+            float4 v[kDepth];
+#pragma unroll
+            for (int u = 0; u < kDepth; ++u)
+                v[u] = floor_load<kKind>(&src[i + u * 256]);
+#pragma unroll
+            for (int u = 0; u < kDepth; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
+        }
+        for (; i < hi; i += 256) {
+            const float4 v = floor_load<kKind>(&src[i]);
+            acc += (v.x + v.y) + (v.z + v.w);
+        }
     }
     if (acc == -1234.5f) sink[blockIdx.x] = acc;
 }
@@ -170,13 +209,26 @@ hipError_t launch_mfma_floor(int n_wg, int iters, float* sink, hipStream_t s)
     return hipGetLastError();
 }
 
-hipError_t launch_read_floor(const void* src, size_t bytes, int n_wg, float* sink, hipStream_t s)
+hipError_t launch_read_floor(const void* src, size_t bytes, int n_wg, int kind, int depth, float* sink,
+                             hipStream_t s)
 {
     const long long n16 = (long long)(bytes / 16);
-    if (n16 == 0 || n_wg < 1) return hipErrorInvalidValue;
+    if (n16 == 0 || n_wg < 1 || kind < 0 || kind > 3 || (depth != 8 && depth != 16 && depth != 32))
+        return hipErrorInvalidValue;
     const long long per_wg = (n16 + n_wg - 1) / n_wg;
-    hipLaunchKernelGGL(read_floor_kernel, dim3((unsigned)n_wg), dim3(256), 0, s,
-                       static_cast<const float4*>(src), n16, per_wg, sink);
+    if (kind >= 2 && (per_wg + 32 * 256) * 16 >= (1ll << 31)) return hipErrorInvalidValue;
+    const dim3 grid((unsigned)n_wg), block(256);
+    const float4* p = static_cast<const float4*>(src);
+    auto go = [&](auto kernel) { hipLaunchKernelGGL(kernel, grid, block, 0, s, p, n16, per_wg, sink); };
+#define TLA_READ_FLOOR_DEPTHS(K)                        \
+    if (depth == 8) go(read_floor_kernel<K, 8>);        \
+    else if (depth == 16) go(read_floor_kernel<K, 16>); \
+    else go(read_floor_kernel<K, 32>);
+    if (kind == 0) { TLA_READ_FLOOR_DEPTHS(0) }
+    else if (kind == 1) { TLA_READ_FLOOR_DEPTHS(1) }
+    else if (kind == 2) { TLA_READ_FLOOR_DEPTHS(2) }
+    else { TLA_READ_FLOOR_DEPTHS(3) }
+#undef TLA_READ_FLOOR_DEPTHS
     return hipGetLastError();
 }
 

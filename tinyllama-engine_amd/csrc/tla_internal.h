@@ -181,8 +181,11 @@ hipError_t launch_rope(const RopeParams& p, hipStream_t s);
 hipError_t launch_softmax(float* x, int size, hipStream_t s);
 hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
 // Streaming read of `bytes` (16-byte aligned, whole 16-byte words) by n_wg
-// workgroups, each a contiguous chunk; sink [n_wg] is never written in practice.
-hipError_t launch_read_floor(const void* src, size_t bytes, int n_wg, float* sink, hipStream_t s);
+// workgroups, each a contiguous chunk, with load form `kind` (0 global, 1
+// global nt, 2 buffer, 3 buffer nt) and `depth` (8, 16 or 32) loads in flight
+// per thread; sink [n_wg] is never written in practice.
+hipError_t launch_read_floor(const void* src, size_t bytes, int n_wg, int kind, int depth, float* sink,
+                             hipStream_t s);
 // fp32 MFMA floor: n_wg workgroups of 4 waves, each wave iters x 16
 // v_mfma_f32_32x32x2f32; sink [n_wg] is never written in practice.
 hipError_t launch_mfma_floor(int n_wg, int iters, float* sink, hipStream_t s);
