@@ -672,7 +672,7 @@ def cpu_generate_baseline(spec, tensors, prompt, wname, n_prompt=8, n_decode=8):
     import oracle as O
     if not O.ref_forward_available():
         return None
-    from oracle.gguf_writer import write_gguf
+    write_gguf = importlib.import_module("tinyllama-engine_amd.gguf_writer").write_gguf
     threads = cpu_threads()
     with tempfile.TemporaryDirectory() as d:
         path = os.path.join(d, "model.gguf")
@@ -687,6 +687,122 @@ def cpu_generate_baseline(spec, tensors, prompt, wname, n_prompt=8, n_decode=8):
                       f"{threads} threads; 1 thread: 4 decode tokens",
             "ms_per_token": round(ms_n, 2), "single_thread_ms_per_token": round(ms_1, 2),
             **cpu_host()}
+
+
+DROPIN_DIR = os.path.join(ROOT, "tinyllama-engine_amd", "_dropin")
+# one token per byte with the model's byte vocabulary (no spaces: each would
+# be three bytes of U+2581)
+DROPIN_PROMPT = "attentionblocksonthedevice" * 15
+
+
+def run_benchmark_program(prog, model, threads, trials, warmup, decode_tokens, prompt):
+    """One run of the reference's benchmark program (src/benchmark.cpp:265-401)
+    in its CSV mode; returns its row as a dict."""
+    import subprocess
+    cmd = [prog, model, "--threads", str(threads), "--trials", str(trials), "--warmup", str(warmup),
+           "--decode-tokens", str(decode_tokens), "--prompt", prompt, "--csv"]
+    r = subprocess.run(cmd, capture_output=True, text=True, timeout=900)
+    if r.returncode != 0:
+        raise RuntimeError(f"{os.path.basename(prog)} failed ({r.returncode}): {r.stderr[-2000:]}")
+    row = r.stdout.strip().splitlines()[-1].split(",")
+    # label, backend, threads, quant, prompt tokens, decode tokens, prefill ms,
+    # prefill tok/s, decode ms/token, decode tok/s (src/benchmark.cpp:188-203)
+    return {"threads": int(row[2]), "prompt_tokens": int(row[4]), "decode_tokens": int(row[5]),
+            "prefill_ms": float(row[6]), "prefill_tok_s": float(row[7]), "decode_ms_per_token": float(row[8]),
+            "decode_tok_s": float(row[9])}
+
+
+def attention_block_cost(n_ctx, pos, reps=2000):
+    """What one attention block of the drop-in costs the reference's
+    forward() at position `pos`, as tla_host::attention_block makes it:
+    tla_rope_attention_host from RunState's pinned host buffers (the 10 KiB
+    upload of q|k|v, the fused RoPE + append + attention launch, the 8 KiB
+    download of the output, one synchronization), called here through the
+    C ABI from Python, against the launch alone queued back to back."""
+    import ctypes as C
+    eng = tla.Engine(tla.Config.tinyllama(n_layers=1, n_ctx=n_ctx))
+    cfg = eng.cfg
+    kc, vc = eng.kv_cache(1)
+    n_qkv = cfg.n_embd + 2 * cfg.kv_dim
+    qkv_host = eng.host_alloc(4 * n_qkv)
+    out_host = eng.host_alloc(4 * cfg.n_embd)
+    vals = np.random.default_rng(9).standard_normal(n_qkv).astype(np.float32)
+    C.memmove(qkv_host, vals.ctypes.data, vals.nbytes)
+    qkv = eng.array((n_qkv,))
+    out = eng.array((cfg.n_embd,))
+    dq, dk, dv = qkv.ptr, qkv.ptr + 4 * cfg.n_embd, qkv.ptr + 4 * (cfg.n_embd + cfg.kv_dim)
+    lib = tla.lib()
+
+    def block():
+        lib.tla_rope_attention_host(eng.h, out_host, qkv_host, qkv.ptr, out.ptr, kc.ptr, vc.ptr, 0, pos)
+
+    for _ in range(50):
+        block()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        block()
+    block_us = (time.perf_counter() - t0) / reps * 1e6
+    kernel_us = back_to_back_ms(eng, lambda i: eng.rope_attention(out.ptr, dq, dk, dv, kc.ptr, vc.ptr, 0, pos),
+                                reps) * 1e3
+    for a in (kc, vc, qkv, out):
+        a.free()
+    eng.host_free(qkv_host)
+    eng.host_free(out_host)
+    eng.close()
+    return {"block_us": round(block_us, 2), "kernel_us": round(kernel_us, 2),
+            "staging_us": round(block_us - kernel_us, 2)}
+
+
+def run_dropin(trials=1, warmup=0, decode_tokens=16, cpu=True):
+    """The reference's own benchmark program (run_trial,
+    src/benchmark.cpp:113-165: the prompt token by token through forward(),
+    then greedy decode steps) built on the drop-in attention path
+    (tinyllama-engine_amd/_dropin/benchmark_dropin: run_state.h and the block
+    of src/forward.cpp:192-208 replaced, every token's RoPE, cache append
+    and attention on the GPU, everything else the reference's on the host
+    cores), on TinyLlama's shapes with seeded random weights in the
+    TinyLlama Q4_0 file's layout; the reference's unmodified build
+    (benchmark_ref) on the same file and host threads is the CPU baseline."""
+    import tempfile
+    gw = importlib.import_module("tinyllama-engine_amd.gguf_writer")
+    prog = os.path.join(DROPIN_DIR, "benchmark_dropin")
+    if not os.access(prog, os.X_OK):
+        raise RuntimeError("benchmark_dropin is not built (build() builds it where the reference's "
+                           "sources are)")
+    threads = cpu_threads()
+    wt, ot = GEN_FORMATS["q4_0"]
+    spec = W.tinyllama_spec(n_ctx=2048)
+    t = W.make_model(spec, wt, salt=5, output_type=ot)
+    res = {}
+    with tempfile.TemporaryDirectory() as d:
+        model = os.path.join(d, "model.gguf")
+        gw.write_gguf(model, spec, t, vocab=gw.byte_vocab(spec.n_vocab))
+        del t
+        r = run_benchmark_program(prog, model, threads, trials, warmup, decode_tokens, DROPIN_PROMPT)
+        log(f"[bench] dropin: reference benchmark on the drop-in, {threads} threads, Q4_0 TinyLlama shapes: "
+            f"prompt {r['prompt_tokens']} tokens {r['prefill_ms']:.0f} ms ({r['prefill_tok_s']:.1f} tok/s), "
+            f"decode {r['decode_ms_per_token']:.2f} ms/token ({r['decode_tok_s']:.1f} tok/s)")
+        res.update(r)
+        if cpu:
+            import oracle as O
+            ref = os.path.join(O.HERE, "_ref", "benchmark_ref")
+            if os.access(ref, os.X_OK):
+                c = run_benchmark_program(ref, model, threads, trials, warmup, decode_tokens, DROPIN_PROMPT)
+                log(f"[bench] dropin cpu reference: prompt {c['prefill_ms']:.0f} ms "
+                    f"({c['prefill_tok_s']:.1f} tok/s), decode {c['decode_ms_per_token']:.2f} ms/token "
+                    f"({c['decode_tok_s']:.1f} tok/s)")
+                res["cpu_baseline"] = {"value": c["decode_tok_s"], "unit": "tok/s", "cores": threads,
+                                       "kind": "reference",
+                                       "sample": f"the reference's benchmark program unmodified, same model and "
+                                                 f"prompt, {trials} trial(s), {decode_tokens} decode tokens",
+                                       **c, **cpu_host()}
+    pos = res["prompt_tokens"] + decode_tokens // 2
+    res["attention_block"] = {"pos": pos, **attention_block_cost(2048, pos)}
+    b = res["attention_block"]
+    log(f"[bench] dropin: one attention block at position {pos}: {b['block_us']:.1f} us with its host "
+        f"copies, {b['kernel_us']:.1f} us for the launch alone -> {b['staging_us']:.1f} us of staging per "
+        f"layer, {b['staging_us'] * spec.n_layers / 1e3:.2f} ms per token over {spec.n_layers} layers")
+    return res
 
 
 READ_FLOOR_GRIDS = (256, 512, 1024, 2048, 4096, 8192, 16384)
@@ -830,7 +946,7 @@ def main():
     ap.add_argument("--workload", default="decode_model",
                     choices=["decode_model", "decode_long", "decode_ragged", "decode_single",
                              "prefill", "proj", "matmul", "generate", "decode_sweep",
-                             "prefill_sweep", "copy", "read", "read_floor", "mfma_floor"])
+                             "prefill_sweep", "copy", "read", "read_floor", "mfma_floor", "dropin"])
     ap.add_argument("--wtype", default=None, choices=["f32", "f16", "q8_0", "q4_0", "q6_k"],
                     help="weight format of the matmul (default q8_0) or generate (q4_0) workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -860,6 +976,20 @@ def main():
         return
     if args.workload == "read":
         print(json.dumps(run_read(args.steps, args.warmup)))
+        return
+    if args.workload == "dropin":
+        r = run_dropin(cpu=cpu)
+        print(json.dumps({"metric": "decode tok/s of the reference's benchmark program on the drop-in",
+                          "value": r["decode_tok_s"], "unit": "tok/s", "n_gpus": 1, "steps": r["decode_tokens"],
+                          "warmup": 0, "ms_per_step": r["decode_ms_per_token"], "higher_is_better": True,
+                          "scaling": "weak", "vs_baseline": None, "dtype": "q4_0 weights, f32 compute",
+                          "data": "synthetic (seeded random weights)",
+                          "config": {"workload": "dropin", "model": "TinyLlama-1.1B shapes", "weights": "q4_0",
+                                     "prompt_tokens": r["prompt_tokens"], "threads": r["threads"],
+                                     "parallelism": "none"},
+                          "prefill_ms": r["prefill_ms"], "prefill_tok_s": r["prefill_tok_s"],
+                          "attention_block": r["attention_block"],
+                          "cpu_baseline": r.get("cpu_baseline")}))
         return
     if args.workload == "read_floor":
         r = run_read_floor(args.steps, args.warmup)

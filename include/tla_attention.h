@@ -100,6 +100,10 @@ int tla_kv_cache_alloc(tla_engine* e, int n_seq, float** key_cache_dev,
                        float** value_cache_dev);
 /* Blocking copies host<->device and a device copy kernel (device->device,
  * used e.g. to clone a sequence's cache).  Ordered after queued work. */
+/* Pinned (page-locked) host memory, zero-filled, for buffers that cross to
+ * the device every step (RunState's q|k|v and attention output). */
+int tla_host_alloc(tla_engine* e, size_t bytes, void** out_host);
+int tla_host_free(tla_engine* e, void* host);
 int tla_memcpy_h2d(tla_engine* e, void* dst_dev, const void* src_host, size_t bytes);
 int tla_memcpy_d2h(tla_engine* e, void* dst_host, const void* src_dev, size_t bytes);
 int tla_memcpy_d2d(tla_engine* e, void* dst_dev, const void* src_dev, size_t bytes);
@@ -134,6 +138,18 @@ int tla_rope_attention(tla_engine* e, float* out_dev, const float* q_dev, const 
                        const float* v_dev, float* key_cache_dev, float* value_cache_dev,
                        int layer, int pos);
 
+/* The same block for a caller whose q, k, v and output live in host memory,
+ * as forward()'s RunState scratch does (src/forward.cpp:192-208 reads
+ * state.q/k/v and writes state.xb2): qkv_host holds q [n_head*head_dim],
+ * k and v [n_head_kv*head_dim] back to back; they are uploaded to qkv_dev
+ * (same layout), the fused RoPE + append + attention runs, the output is
+ * downloaded from out_dev to out_host, all queued on the engine's stream
+ * with one synchronization at the end.  Pinned host buffers
+ * (tla_host_alloc) make the two copies direct transfers. */
+int tla_rope_attention_host(tla_engine* e, float* out_host, const float* qkv_host, float* qkv_dev,
+                            float* out_dev, float* key_cache_dev, float* value_cache_dev, int layer,
+                            int pos);
+
 /* Batched decode: one new token for each of n_seq sequences, for each of the
  * n_step_layers layers layer0 .. layer0+n_step_layers-1.  Equivalent to
  * calling attention() (or rope()+attention() with TLA_ROTATE) once per
@@ -154,9 +170,9 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
 /* tla_decode without any allocation: same arguments, same kernels and the
  * same results bit for bit, but the split partials and arrival counters live
  * in a fixed per-device static array (32 MiB of partials, 65,536 counters)
- * instead of the engine's workspace, so the call never allocates device or
- * host memory (tla_decode grows its workspace with hipMalloc on first use of
- * a larger shape).  No counterpart in the reference: it is for callers that
+ * instead of the engine's workspace, so the call never allocates device
+ * memory (tla_decode grows its workspace with hipMalloc on first use of a
+ * larger shape), nor host memory unless profiling is on (below).  No counterpart in the reference: it is for callers that
  * cannot allocate -- code under HIP graph capture, tight serving loops,
  * harnesses that forbid allocation.  A launch whose partials or counters
  * exceed the array returns TLA_ERR_UNSUPPORTED and launches nothing (e.g. 22
@@ -164,7 +180,9 @@ int tla_decode(tla_engine* e, int n_seq, const int* pos_host, int layer0, int n_
  * The array is shared by every engine on the device and keeps the last
  * call's contents: calls that overlap on one device (other streams, other
  * host threads) race.  The counters are zeroed when the first engine is
- * created on the device, and every launch returns the ones it uses to zero. */
+ * created on the device, and every launch returns the ones it uses to zero.
+ * With profiling on (tla_profile), the call records a pair of HIP events
+ * around its launch, and the event pool may grow on the host. */
 int tla_decode_noalloc(tla_engine* e, int n_seq, const int* pos_host, int layer0,
                        int n_step_layers, int flags, float* out_dev, const float* q_dev,
                        const float* k_dev, const float* v_dev, float* key_cache_dev,

@@ -13,14 +13,16 @@ import subprocess
 
 import pytest
 
-from oracle import dropin
+from oracle import dropin as ref_programs
 
-pytestmark = pytest.mark.skipif(not os.path.isdir(dropin.REF_SRC), reason="no reference sources here")
+dropin = ref_programs.PACKAGE_DROPIN  # tinyllama-engine_amd/host/dropin.py
+REF_SRC = ref_programs.REF_SRC
+pytestmark = pytest.mark.skipif(not os.path.isdir(REF_SRC), reason="no reference sources here")
 
 
 def test_reference_engine_and_benchmark_build_against_the_dropin(tmp_path):
-    src = dropin.dropin_tree(str(tmp_path))
-    for sources, name in ((dropin.ENGINE, "engine"), (dropin.BENCHMARK, "benchmark")):
+    src = dropin.dropin_tree(REF_SRC, str(tmp_path))
+    for sources, name in dropin.PROGRAMS:
         out = os.path.join(str(tmp_path), name)
         dropin.build_dropin(src, sources, out)
         syms = subprocess.run(["nm", "-C", "--undefined-only", out], capture_output=True,
@@ -34,11 +36,11 @@ def test_dropin_changes_only_run_state_and_forward(tmp_path):
     """The drop-in needs no other change to the reference: the built tree
     differs from the reference's sources in run_state.h (replaced) and
     forward.cpp (the one block) alone."""
-    src = dropin.dropin_tree(str(tmp_path))
+    src = dropin.dropin_tree(REF_SRC, str(tmp_path))
     changed = []
     for name in sorted(os.listdir(src)):
         a = open(os.path.join(src, name), "rb").read()
-        b = open(os.path.join(dropin.REF_SRC, name), "rb").read()
+        b = open(os.path.join(REF_SRC, name), "rb").read()
         if a != b:
             changed.append(name)
     assert changed == ["forward.cpp", "run_state.h"]

@@ -43,6 +43,59 @@ def test_decode_single_golden(tla, W, engines):
         assert np.array_equal(dq.download(), q[127])
 
 
+def test_rope_attention_host_golden(tla, W, engines):
+    """tla_rope_attention_host (the drop-in block with host-resident q|k|v
+    and output, one synchronization) on the golden case: from pinned host
+    buffers (tla_host_alloc) and from ordinary ones, the output within the
+    decode bound of the reference's and bit-identical to the device-pointer
+    entry point, the caches bit-exact."""
+    import ctypes as C
+    g = golden("decode_single.npz")
+    eng = engines(1, 128)
+    rg = W.rng("decode_single", 7)
+    q, k, v = W.normal(rg, (128, 2048)), W.normal(rg, (128, 256)), W.normal(rg, (128, 256))
+    qkv = np.concatenate([q[127], k[127], v[127]]).astype(np.float32)
+    kc_host = g["kc"].reshape(128, 256).copy()
+    vc_host = g["vc"].reshape(128, 256).copy()
+    kc_host[127] = 0
+    vc_host[127] = 0
+    pinned_in = eng.host_alloc(qkv.nbytes)
+    pinned_out = eng.host_alloc(2048 * 4)
+    try:
+        C.memmove(pinned_in, qkv.ctypes.data, qkv.nbytes)
+        with device_arrays() as track:
+            dqkv, dout = track(eng.array((qkv.size,))), track(eng.array((2048,)))
+            got = {}
+            for label in ("device pointers", "pinned", "pageable"):
+                kc, vc = eng.kv_cache(1)
+                track(kc), track(vc)
+                kc.upload(kc_host)
+                vc.upload(vc_host)
+                if label == "device pointers":
+                    dqkv.upload(qkv)
+                    eng.rope_attention(dout.ptr, dqkv.ptr, dqkv.ptr + 4 * 2048, dqkv.ptr + 4 * 2304, kc.ptr,
+                                       vc.ptr, 0, 127)
+                    out = dout.download()
+                elif label == "pinned":
+                    eng.rope_attention_host(pinned_out, pinned_in, dqkv.ptr, dout.ptr, kc.ptr, vc.ptr, 0, 127)
+                    out = np.ctypeslib.as_array((C.c_float * 2048).from_address(pinned_out)).copy()
+                else:
+                    out = np.zeros(2048, np.float32)
+                    eng.rope_attention_host(out.ctypes.data, qkv.ctypes.data, dqkv.ptr, dout.ptr, kc.ptr,
+                                            vc.ptr, 0, 127)
+                got[label] = out
+                err = max_err(out, g["out"])
+                log(f"  {label}: max-abs {err:.3e} vs the reference")
+                assert err <= DECODE_TOL
+                assert np.array_equal(bits(kc.download().reshape(-1)), bits(g["kc"])), label
+                assert np.array_equal(bits(vc.download().reshape(-1)), bits(g["vc"])), label
+            for label in ("pinned", "pageable"):
+                assert np.array_equal(bits(got[label]), bits(got["device pointers"])), label
+    finally:
+        eng.host_free(pinned_in)
+        eng.host_free(pinned_out)
+
+
 def test_decode_peaked_golden(tla, W, engines):
     g = golden("decode_peaked.npz")
     case = W.make_decode("decode_long", 1, 1, 1024, 1023, kv_std=0.5, peaked_frac=0.01, salt=7)

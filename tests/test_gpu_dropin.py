@@ -1,12 +1,14 @@
 """The reference's own programs running on the drop-in.  These are its
 `engine` (main.cpp: prompt, greedy generation, text out) and its `benchmark`
-(benchmark.cpp: run_trial's prefill and decode loops), built by
-oracle/dropin.py from its sources.  In the *_dropin builds, run_state.h is
+(benchmark.cpp: run_trial's prefill and decode loops), built from its
+sources: as they are by oracle/dropin.py (*_ref, in oracle/_ref), and on
+the drop-in by tinyllama-engine_amd/host/dropin.py (*_dropin, in
+tinyllama-engine_amd/_dropin).  In the *_dropin builds, run_state.h is
 this repository's, the block of src/forward.cpp:192-208 is
 tla_host::attention_block, and the RoPE, KV-cache append and attention of
 every token and layer run on the GPU.  In the *_ref builds everything is the
 reference's, on the CPU.  Both read one seeded GGUF model (2 layers, 4 / 2
-heads, Q8_0, a byte-level vocabulary) written by oracle/gguf_writer.py.
+heads, Q8_0, a byte-level vocabulary) written by the package's gguf_writer.
 
 Greedy generation must print the same text, token for token (the default
 prompt is 115 tokens, then 24 are generated): attention on the GPU is within
@@ -23,8 +25,9 @@ from helpers import log
 pytestmark = pytest.mark.gpu
 
 REF_DIR = os.path.join(ROOT, "oracle", "_ref")
-PROGS = {n: os.path.join(REF_DIR, n) for n in ("engine_ref", "engine_dropin", "benchmark_ref",
-                                               "benchmark_dropin")}
+DROPIN_DIR = os.path.join(ROOT, "tinyllama-engine_amd", "_dropin")
+PROGS = {n: os.path.join(DROPIN_DIR if n.endswith("_dropin") else REF_DIR, n)
+         for n in ("engine_ref", "engine_dropin", "benchmark_ref", "benchmark_dropin")}
 needs_programs = pytest.mark.skipif(
     not all(os.access(p, os.X_OK) for p in PROGS.values()),
     reason="oracle/_ref programs not built (building them needs the reference's sources)")
@@ -32,7 +35,9 @@ needs_programs = pytest.mark.skipif(
 
 @pytest.fixture(scope="module")
 def model_path(tmp_path_factory, W):
-    from oracle.gguf_writer import byte_vocab, write_gguf
+    from importlib import import_module
+    gw = import_module("tinyllama-engine_amd.gguf_writer")
+    byte_vocab, write_gguf = gw.byte_vocab, gw.write_gguf
     spec = W.ModelSpec(2, 256, 4, 2, 512, 384, 256)
     path = str(tmp_path_factory.mktemp("dropin") / "model.gguf")
     write_gguf(path, spec, W.make_model(spec, W.W_Q8_0, salt=44), vocab=byte_vocab(spec.n_vocab))

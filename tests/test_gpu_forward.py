@@ -521,3 +521,43 @@ def test_prefill_forward_library_prompt(tla, O, W, engines, name):
     ok = om.kc.reshape(spec.n_layers, spec.n_ctx, spec.kv_dim)
     for kd in (k_dev, k_dev2):
         assert np.abs(kd[0, :, :n] - ok[:, :n]).max() <= 1e-4 * np.abs(ok[:, :n]).max()
+
+
+def test_prefill_forward_after_queued_weight_writes(tla, O, W, engines):
+    """Weights written on the engine's stream and not yet synchronized when a
+    prompt starts: the prompt's layer expansions, which run one layer ahead
+    on a second stream, must still see them.  Layers 0 and 1 (the two
+    expansions queued before any product) are overwritten with garbage,
+    then restored with tla_memcpy_d2d, and a 100-token prompt follows at
+    once; its last logits against the oracle's token loop."""
+    g = golden("forward.npz")
+    base = W.ModelSpec(*[int(v) for v in g["spec"]])
+    spec = W.ModelSpec(base.n_layers, base.n_embd, base.n_head, base.n_head_kv, base.n_ff, base.n_vocab,
+                       128)
+    salt, wt, et, ot = [int(v) for v in g["q8_0_case"]]
+    ov = dict(ast.literal_eval(str(g["q8_0_overrides"])))
+    t = W.make_model(spec, wt, salt=salt, embd_type=None if et < 0 else et,
+                     output_type=None if ot < 0 else ot, overrides=ov)
+    eng = spec_engine(engines, spec)
+    toks = np.random.default_rng(100).integers(0, spec.n_vocab, 100).tolist()
+    want = O.Model(spec, t).tokens(toks)[-1]
+    names = [f"blk.{l}.{w}.weight" for l in (0, 1)
+             for w in ("attn_q", "attn_k", "attn_v", "attn_output", "ffn_gate", "ffn_up", "ffn_down")]
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    try:
+        with device_arrays() as track:
+            saved = {n: track(eng.array(np.ascontiguousarray(t[n][2], np.uint8))) for n in names}
+            junk = np.random.default_rng(7).integers(0, 256, max(a.nbytes for a in saved.values()), np.uint8)
+            for n in names:
+                dm.arrays[n].upload(junk[:dm.arrays[n].nbytes])
+            eng.synchronize()
+            kc, vc = eng.kv_cache(1)
+            track(kc), track(vc)
+            lg = track(eng.array((spec.n_vocab,)))
+            for n in names:
+                eng.copy(dm.arrays[n].ptr, saved[n].ptr, saved[n].nbytes)
+            eng.prefill_forward(dm, kc.ptr, vc.ptr, toks, 0, lg.ptr)
+            got = lg.download()
+    finally:
+        dm.free()
+    check_logits(got[None], want[None], "100-token prompt after queued weight writes vs oracle")

@@ -251,11 +251,12 @@ STREAM_SHAPES = [(2560, 2048, 16), (2048, 5632, 32), (40, 64, 17), (200, 128, 31
 @pytest.mark.parametrize("t,name", TYPES)
 @pytest.mark.parametrize("rows,cols,n_tok", STREAM_SHAPES)
 def test_matmul_batch_streamed(tla, O, W, engines, t, name, rows, cols, n_tok):
-    """The streamed product (2 or 3 to 32 tokens): rows not a multiple of its 16-row
-    tiles, rows of 2 blocks (two of its four waves idle), token counts not a
-    multiple of 16, and 40 tokens (the library product past the bound); every token against the oracle's matmul, and the same
-    bits with one or two token tiles per workgroup (Q6_K takes the library
-    product)."""
+    """The streamed product (2 or 3 to 64 tokens): rows not a multiple of its
+    16-row tiles, rows of 2 blocks (two of its four waves idle), token counts
+    not a multiple of 16, 57 and 64 tokens (four token tiles) and 65 tokens
+    (the library product past the bound); every token against the oracle's
+    matmul, and the same bits with one to four token tiles per workgroup
+    (Q6_K takes the GEMVs under 16 tokens, the library product from 16)."""
     if t == Q.Q6_K and cols % 256:
         pytest.skip("Q6_K rows are whole 256-weight super-blocks")
     eng = engines(1, 64)
@@ -293,12 +294,13 @@ def test_stream_tiles_option(tla, engines):
 
 
 def test_matmul_batch_many_shapes(O, W, engines):
-    """260 batch sizes in a row: every size is a new library product shape
-    (descriptors and algorithm cached per shape, the cache starting over
-    past 256 shapes); products before, across and after the reset against
-    the oracle's matmul."""
-    eng = engines(1, 64)
-    rows, cols, t = 32, 64, Q.Q8_0
+    """260 batch sizes in a row on an engine of its own: Q6_K takes the
+    library product from 16 vectors, so every size from 16 to 275 is a new
+    library product shape (descriptors and algorithm cached per shape, the
+    cache starting over past 256 shapes); products before, across and after
+    the reset against the oracle's matmul."""
+    eng = engines(1, 96)  # a key no other test uses: the plan cache starts empty
+    rows, cols, t = 32, 256, Q.Q6_K
     raw = W.make_weights(t, rows, cols, salt=11)
     x = np.random.default_rng(260).standard_normal((300, cols)).astype(np.float32)
     with device_arrays() as track:

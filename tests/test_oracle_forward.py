@@ -4,13 +4,14 @@ loop (src/generate.cpp:56-100) before the GPU is compared with it:
 
   1. golden logits and greedy tokens from the reference's own forward() and
      GGUF loader (tests/golden/forward.npz, written from GGUF files that
-     oracle/gguf_writer.py produced), bit for bit, five weight layouts
+     tinyllama-engine_amd/gguf_writer.py produced), bit for bit, five weight layouts
      including tied embeddings and mixed per-tensor types;
   2. the compiled reference itself, live, where oracle/_ref was built;
   3. an fp64 forward written from the model's definition
      (tests/forward_ref.py), and exact dequantisation for embed_token;
   4. planted mistakes (oracle_fault 10-12) -- each must trip a pin.
 """
+import importlib
 import os
 import tempfile
 
@@ -44,7 +45,7 @@ def test_gguf_bytes_match_golden(W):
     """The writer reproduces the exact files the golden vectors came from."""
     import hashlib
 
-    from oracle.gguf_writer import write_gguf
+    write_gguf = importlib.import_module("tinyllama-engine_amd.gguf_writer").write_gguf
     g = golden("forward.npz")
     for name in CASES:
         spec, t = model_from_golden(W, g, name)
@@ -70,7 +71,7 @@ def test_silu_and_ffn_golden(O, W):
 @pytest.mark.parametrize("wtype", [8, 1, 2, 0, 14])
 def test_forward_live_reference(O, W, wtype):
     """40 positions of a fresh model (different salt), every format."""
-    from oracle.gguf_writer import write_gguf
+    write_gguf = importlib.import_module("tinyllama-engine_amd.gguf_writer").write_gguf
     spec = W.ModelSpec(2, 256, 4, 1, 768, 300, 48)
     t = W.make_model(spec, wtype, salt=50 + wtype, output_type=None)
     toks = np.random.default_rng(wtype).integers(0, spec.n_vocab, 40)

@@ -15,10 +15,26 @@ from helpers import DECODE_TOL, bits, device_arrays, log, max_err, oracle_decode
 pytestmark = pytest.mark.gpu
 
 
-def run_entry(tla, eng, case, entry):
+def device_free_bytes():
+    """Free device memory as the HIP runtime reports it (hipMemGetInfo)."""
+    for name in ("libamdhip64.so", "libamdhip64.so.7", "/opt/rocm/lib/libamdhip64.so"):
+        try:
+            hip = C.CDLL(name)
+            break
+        except OSError:
+            continue
+    else:
+        pytest.fail("the HIP runtime library is not loadable")
+    free, total = C.c_size_t(), C.c_size_t()
+    assert hip.hipMemGetInfo(C.byref(free), C.byref(total)) == 0
+    return free.value
+
+
+def run_entry(tla, eng, case, entry, check_free=False):
     """One call of `entry` (tla_decode or tla_decode_noalloc) over every
     (sequence, layer) of `case`, on fresh copies of its caches; returns the
-    output and both whole caches."""
+    output and both whole caches.  With check_free, the device's free memory
+    must be the same before and after the call (inputs allocated before)."""
     cfg = eng.cfg
     with device_arrays() as track:
         kc, vc = eng.kv_cache(case.n_seq)
@@ -30,24 +46,43 @@ def run_entry(tla, eng, case, entry):
         pos = np.ascontiguousarray(case.pos, np.int32)
         stride = cfg.n_layers * cfg.n_ctx * cfg.kv_dim
         log(f"  {entry}: n_seq={case.n_seq} layers={case.n_layers} pos={pos.tolist()[:4]}")
+        eng.synchronize()
+        before = device_free_bytes()
         rc = getattr(tla.lib(), entry)(eng.h, int(pos.size), pos.ctypes.data_as(C.POINTER(C.c_int)),
                                        0, case.n_layers, tla.TLA_ROTATE, out.ptr, q.ptr, k.ptr, v.ptr,
                                        kc.ptr, vc.ptr, stride)
         assert rc == tla.TLA_OK, tla.last_error()
+        eng.synchronize()
+        after = device_free_bytes()
+        log(f"    device free memory {before} -> {after} bytes")
+        if check_free:
+            assert after == before, f"{entry} changed free device memory by {before - after} bytes"
         return out.download(), kc.download(), vc.download()
 
 
-def test_noalloc_equals_decode_on_two_calls(tla, O, W, engines):
-    eng = engines(22, 2048)
+def test_noalloc_equals_decode_on_two_calls(tla, O, W):
+    """On an engine of its own that has never decoded (no workspace yet),
+    tla_decode_noalloc runs first with the device's free memory unchanged,
+    then tla_decode (which allocates its workspace: the free memory drops)
+    on the same inputs.  Run alone in a fresh process, this is also the
+    process's first decode launch: the decode kernels' code object must
+    already be loaded (at engine creation), since its load allocates."""
+    eng = tla.Engine(tla.Config.tinyllama(n_layers=22, n_ctx=2048))
     cases = [
         # 22 layers x 2048 positions, one sequence: 11 splits per unit merged
         W.decode_model(n_layers=22, n_ctx=2048),
         # smaller: two ragged sequences, fewer splits, fewer units
         W.make_decode(41, 2, 22, 2048, [700, 64], salt=3),
     ]
-    for case in cases:
-        want, wk, wv = run_entry(tla, eng, case, "tla_decode")
-        got, gk, gv = run_entry(tla, eng, case, "tla_decode_noalloc")
+    try:
+        results = []
+        for case in cases:
+            got, gk, gv = run_entry(tla, eng, case, "tla_decode_noalloc", check_free=True)
+            want, wk, wv = run_entry(tla, eng, case, "tla_decode")
+            results.append((case, got, gk, gv, want, wk, wv))
+    finally:
+        eng.close()
+    for case, got, gk, gv, want, wk, wv in results:
         assert np.array_equal(bits(got), bits(want)), "outputs differ from tla_decode"
         assert np.array_equal(bits(gk), bits(wk)) and np.array_equal(bits(gv), bits(wv)), "caches differ"
         ref, _, _ = oracle_decode(O, case)

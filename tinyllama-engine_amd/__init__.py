@@ -136,6 +136,9 @@ SIGNATURES = {
                                       C.c_int, C.c_int, C.POINTER(C.c_int)]),
     "tla_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
     "tla_rope_attention": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
+    "tla_rope_attention_host": (C.c_int, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, C.c_int, C.c_int]),
+    "tla_host_alloc": (C.c_int, [_vp, C.c_size_t, C.POINTER(_vp)]),
+    "tla_host_free": (C.c_int, [_vp, _vp]),
     "tla_decode": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int,
                              _vp, _vp, _vp, _vp, _vp, _vp, C.c_size_t]),
     "tla_decode_noalloc": (C.c_int, [_vp, C.c_int, C.POINTER(C.c_int), C.c_int, C.c_int, C.c_int,
@@ -269,6 +272,19 @@ class Engine:
                   layer: int, pos: int, att: int = 0):
         _check(lib().tla_attention(self.h, out, q, k, v, key_cache, value_cache, att or None,
                                    layer, pos), "tla_attention")
+
+    def rope_attention_host(self, out_host: int, qkv_host: int, qkv_dev: int, out_dev: int,
+                            key_cache: int, value_cache: int, layer: int, pos: int):
+        _check(lib().tla_rope_attention_host(self.h, out_host, qkv_host, qkv_dev, out_dev, key_cache,
+                                             value_cache, layer, pos), "tla_rope_attention_host")
+
+    def host_alloc(self, nbytes: int) -> int:
+        p = _vp()
+        _check(lib().tla_host_alloc(self.h, nbytes, C.byref(p)), "tla_host_alloc")
+        return p.value
+
+    def host_free(self, ptr: int):
+        _check(lib().tla_host_free(self.h, ptr), "tla_host_free")
 
     def rope_attention(self, out: int, q: int, k: int, v: int, key_cache: int,
                        value_cache: int, layer: int, pos: int):

@@ -177,10 +177,14 @@ __device__ __forceinline__ void stream_load(StreamStage<kType, kNT>& st, const u
         constexpr int kBlock = kType == kQ8_0 ? 34 : 18;
         const int h = kType == kQ8_0 ? g : (g & 1);  // which 8 bytes of qs
         const unsigned char* p = wrow + static_cast<long long>(kBlock) * blk + (h ? 8 * h - 2 : 0);
-        const uint3 q = *reinterpret_cast<const uint3*>(p);
-        st.u[0] = q.x;
-        st.u[1] = q.y;
-        st.u[2] = q.z;
+        // p is only 2-byte aligned: copy the bytes (the compiler, told the
+        // true alignment, still emits one dwordx3 load, since gfx950 runs
+        // global memory in unaligned-access mode).
+        unsigned q[3];
+        __builtin_memcpy(q, p, 12);
+        st.u[0] = q[0];
+        st.u[1] = q[1];
+        st.u[2] = q[2];
     }
 #pragma unroll
     for (int ti = 0; ti < kNT; ++ti) {
@@ -320,6 +324,12 @@ hipError_t launch_stream_typed(const StreamParams& p, hipStream_t s)
 }
 
 }  // namespace
+
+hipError_t load_batch_code()
+{
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&swiglu_rows_kernel));
+}
 
 bool stream_supported(int type) { return type == kF32 || type == kF16 || type == kQ8_0 || type == kQ4_0; }
 

@@ -699,6 +699,12 @@ void launch_shape(const DecodeParams& p, const DecodeSeqs<kMaxSeq>& b, dim3 grid
 
 }  // namespace
 
+hipError_t load_decode_code()
+{
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&decode_split_kernel<1, false, kDecodeKvGroupSmall>));
+}
+
 size_t decode_part_bytes(long long units, int max_splits, int n_head_kv, int gqa)
 {
     return static_cast<size_t>(units) * max_splits * n_head_kv * 66 * gqa * sizeof(float);

@@ -160,6 +160,7 @@ struct tla_engine {
     float* layer_buf[2] = {};
     size_t layer_buf_bytes = 0;
     hipEvent_t layer_ready[2] = {}, layer_done[2] = {};
+    hipEvent_t side_start = nullptr;  // recorded on `stream` before a prompt's first expansion
     hipblasLtHandle_t lt = nullptr;  // created at the first library product
     void* lt_ws = nullptr;           // its workspace (kLtWorkspace bytes)
     std::deque<LtPlan> lt_plans;     // per product shape (a deque: plans stay put as it grows)
@@ -431,6 +432,14 @@ int tla_engine_create(const tla_config* cfg, int device, tla_engine** out)
         return bail(fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE,
                          "rope table: %s", hipGetErrorString(err)));
     if (int rc = scratch_setup(e)) return bail(rc);
+    // Every kernel's code object is loaded now, not at its first launch (a
+    // load allocates device memory: tla_decode_noalloc's first call would).
+    for (hipError_t (*load)() : {load_decode_code, load_prefill_code, load_gemv_code, load_batch_code,
+                                 load_small_ops_code}) {
+        const hipError_t lerr = load();
+        if (lerr != hipSuccess)
+            return bail(fail(TLA_ERR_DEVICE, "loading kernel code: %s", hipGetErrorString(lerr)));
+    }
     *out = e;
     return ok();
 }
@@ -458,6 +467,7 @@ int tla_engine_destroy(tla_engine* e)
         if (e->layer_ready[i]) (void)hipEventDestroy(e->layer_ready[i]);
         if (e->layer_done[i]) (void)hipEventDestroy(e->layer_done[i]);
     }
+    if (e->side_start) (void)hipEventDestroy(e->side_start);
     if (e->side) (void)hipStreamDestroy(e->side);
     for (LtPlan& pl : e->lt_plans) lt_plan_destroy(pl);
     if (e->lt_ws) (void)hipFree(e->lt_ws);
@@ -493,6 +503,33 @@ int tla_alloc(tla_engine* e, size_t bytes, void** out_dev)
         return fail(TLA_ERR_DEVICE, "zero fill: %s", hipGetErrorString(err));
     }
     *out_dev = p;
+    return ok();
+}
+
+int tla_host_alloc(tla_engine* e, size_t bytes, void** out_host)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!out_host) return fail(TLA_ERR_INVALID_ARGUMENT, "out_host is NULL");
+    *out_host = nullptr;
+    if (bytes == 0) return fail(TLA_ERR_INVALID_ARGUMENT, "zero-byte allocation");
+    if (int rc = set_device(e)) return rc;
+    void* p = nullptr;
+    const hipError_t err = hipHostMalloc(&p, bytes, hipHostMallocDefault);
+    if (err != hipSuccess)
+        return fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE,
+                    "pinned host allocation of %zu bytes: %s", bytes, hipGetErrorString(err));
+    std::memset(p, 0, bytes);
+    *out_host = p;
+    return ok();
+}
+
+int tla_host_free(tla_engine* e, void* host)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!host) return TLA_OK;
+    if (int rc = set_device(e)) return rc;
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    TLA_HIP(hipHostFree(host));
     return ok();
 }
 
@@ -931,6 +968,31 @@ int tla_rope_attention(tla_engine* e, float* out_dev, const float* q_dev, const 
 {
     return tla_decode(e, 1, &pos, layer, 1, TLA_ROTATE, out_dev, q_dev, k_dev, v_dev,
                       key_cache_dev, value_cache_dev, 0);
+}
+
+int tla_rope_attention_host(tla_engine* e, float* out_host, const float* qkv_host, float* qkv_dev,
+                            float* out_dev, float* key_cache_dev, float* value_cache_dev, int layer,
+                            int pos)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!out_host || !qkv_host) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL host pointer");
+    if (!qkv_dev || !out_dev || !key_cache_dev || !value_cache_dev)
+        return fail(TLA_ERR_INVALID_ARGUMENT, "NULL device pointer");
+    if (int rc = set_device(e)) return rc;
+    const size_t q_floats = static_cast<size_t>(e->cfg.n_head) * e->head_dim;
+    const size_t qkv_bytes = (q_floats + 2 * static_cast<size_t>(e->kv_dim)) * sizeof(float);
+    TLA_HIP(hipMemcpyAsync(qkv_dev, qkv_host, qkv_bytes, hipMemcpyHostToDevice, e->stream));
+    const float* dq = qkv_dev;
+    const float* dk = dq + q_floats;
+    const float* dv = dk + e->kv_dim;
+    if (int rc = tla_decode(e, 1, &pos, layer, 1, TLA_ROTATE, out_dev, dq, dk, dv, key_cache_dev,
+                            value_cache_dev, 0)) {
+        (void)hipStreamSynchronize(e->stream);  // the upload may still read qkv_host
+        return rc;
+    }
+    TLA_HIP(hipMemcpyAsync(out_host, out_dev, q_floats * sizeof(float), hipMemcpyDeviceToHost, e->stream));
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    return ok();
 }
 
 int tla_prefill(tla_engine* e, int pos0, int n_tok, int layer0, int n_step_layers, int flags,
@@ -1465,6 +1527,7 @@ int ensure_layer_bufs(tla_engine* e, size_t bytes)
             TLA_HIP(hipEventCreateWithFlags(&e->layer_ready[i], hipEventDisableTiming));
             TLA_HIP(hipEventCreateWithFlags(&e->layer_done[i], hipEventDisableTiming));
         }
+        TLA_HIP(hipEventCreateWithFlags(&e->side_start, hipEventDisableTiming));
     }
     if (bytes <= e->layer_buf_bytes) return TLA_OK;
     TLA_HIP(hipStreamSynchronize(e->stream));
@@ -1545,6 +1608,11 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
     if (ahead) {
         if (int rc = ensure_lt(e)) return rc;
         if (int rc = ensure_layer_bufs(e, static_cast<size_t>(lay.total) * sizeof(float))) return rc;
+        // The side stream starts after everything already queued on the
+        // engine stream (the weights may have been written there, e.g. by
+        // tla_memcpy_d2d); layer_done orders only the buffers' reuse.
+        TLA_HIP(hipEventRecord(e->side_start, e->stream));
+        TLA_HIP(hipStreamWaitEvent(e->side, e->side_start, 0));
         if (int rc = expand_layer(e, m, 0, 0, lay)) return rc;
     }
     for (int l = 0; l < n_layers; ++l) {

@@ -1005,6 +1005,12 @@ hipError_t launch_typed(const GemvParams& p, hipStream_t s)
 
 }  // namespace
 
+hipError_t load_gemv_code()
+{
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&vec_add_kernel));
+}
+
 long long weight_row_bytes(int type, int cols)
 {
     switch (type) {

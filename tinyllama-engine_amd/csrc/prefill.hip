@@ -350,6 +350,12 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
 
 }  // namespace
 
+hipError_t load_prefill_code()
+{
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&prefill_append_kernel));
+}
+
 hipError_t launch_prefill_append(const PrefillParams& p, hipStream_t s)
 {
     const long long threads = (long long)p.n_lb * p.n_tok * p.n_head_kv * 16;

@@ -202,6 +202,12 @@ __global__ __launch_bounds__(256) void mfma_floor_kernel(int iters, float* __res
 
 }  // namespace
 
+hipError_t load_small_ops_code()
+{
+    hipFuncAttributes a;
+    return hipFuncGetAttributes(&a, reinterpret_cast<const void*>(&copy16_kernel));
+}
+
 hipError_t launch_mfma_floor(int n_wg, int iters, float* sink, hipStream_t s)
 {
     if (n_wg < 1 || iters < 1) return hipErrorInvalidValue;

@@ -192,4 +192,14 @@ hipError_t launch_mfma_floor(int n_wg, int iters, float* sink, hipStream_t s);
 // Zero fill by a kernel (no memset node: safe under stream capture).
 hipError_t launch_zero(void* dst, size_t bytes, hipStream_t s);
 
+// Each source file's kernels are one code object, which the runtime loads
+// (allocating device memory) on first use unless something asks for it
+// earlier; the engine asks for all of them when it is created, so that no
+// later call allocates for it.
+hipError_t load_decode_code();
+hipError_t load_prefill_code();
+hipError_t load_gemv_code();
+hipError_t load_batch_code();
+hipError_t load_small_ops_code();
+
 }  // namespace tla

@@ -4,10 +4,11 @@ magic "GGUF", u32 version, u64 tensor count, u64 kv count; strings are u64
 length + bytes; tensor info = name, u32 n_dims, u64 dims (ne0 first), u32
 ggml type, u64 offset from the aligned start of the data section).
 
-TEST INFRASTRUCTURE ONLY (with the rest of oracle/): used by the tests and
-bench.py's cpu_baseline leg to hand a seeded random model to the reference's own GGUF
-loader and forward pass (oracle/_ref/libref_forward.so); the GPU path takes
-the same tensors as device pointers."""
+Synthetic model files: the seeded random models of workloads.make_model
+written in the layout the reference's GGUF loader reads (src/gguf_model.cpp),
+so that the reference's own programs -- its forward pass, its `engine` and
+`benchmark`, and those programs built on the drop-in attention path -- can
+load the same weights the device path takes as pointers.  No compute."""
 import struct
 
 import numpy as np

@@ -110,8 +110,11 @@ void allocate_state(::RunState& st, const Config& cfg, Engine& eng)
     try {
         st.x = new float[cfg.n_embd]();
         st.xb = new float[cfg.n_embd]();
-        st.xb2 = new float[cfg.n_embd]();
-        st.qkv_host = new float[cfg.n_embd + 2 * st.kv_dim]();
+        void* h = nullptr;  // the two buffers the attention block moves: pinned
+        check(tla_host_alloc(eng.get(), sizeof(float) * cfg.n_embd, &h), "output host buffer");
+        st.xb2 = static_cast<float*>(h);
+        check(tla_host_alloc(eng.get(), sizeof(float) * (cfg.n_embd + 2 * st.kv_dim), &h), "q|k|v host buffer");
+        st.qkv_host = static_cast<float*>(h);
         st.q = st.qkv_host;
         st.k = st.q + cfg.n_embd;
         st.v = st.k + st.kv_dim;
@@ -140,8 +143,10 @@ void free_state(::RunState& st) noexcept
 {
     delete[] st.x;
     delete[] st.xb;
-    delete[] st.xb2;
-    delete[] st.qkv_host;
+    if (st.engine) {
+        tla_host_free(st.engine->get(), st.xb2);
+        tla_host_free(st.engine->get(), st.qkv_host);
+    }
     delete[] st.att;
     delete[] st.hb;
     delete[] st.hb2;
@@ -166,16 +171,11 @@ void attention_block(::RunState& state, int layer, int pos)
 {
     if (!state.engine) throw std::runtime_error("attention_block: RunState not allocated");
     tla_engine* e = state.engine->get();
-    const std::size_t n = state.n_embd + 2 * static_cast<std::size_t>(state.kv_dim);
-    check(tla_memcpy_h2d(e, state.d_qkv, state.q, sizeof(float) * n), "q|k|v upload");
-    const float* dq = state.d_qkv;
-    const float* dk = dq + state.n_embd;
-    const float* dv = dk + state.kv_dim;
-    check(tla_rope_attention(e, state.d_out, dq, dk, dv, state.key_cache, state.value_cache, layer,
-                             pos),
-          "rope+attention");
-    check(tla_memcpy_d2h(e, state.xb2, state.d_out, sizeof(float) * state.n_embd),
-          "attention output download");
+    // q | k | v (contiguous in qkv_host) up, RoPE + append + attention, the
+    // output down into xb2: one queue, one synchronization
+    check(tla_rope_attention_host(e, state.xb2, state.qkv_host, state.d_qkv, state.d_out, state.key_cache,
+                                  state.value_cache, layer, pos),
+          "attention block");
 }
 
 void matmul(Engine& eng, float* out, const void* w, const float* x, int rows, int cols, int type)
