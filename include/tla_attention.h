@@ -223,12 +223,15 @@ int tla_matmul(tla_engine* e, float* out_dev, const void* w_dev, const float* x_
 
 /* matmul() over a batch of n_tok vectors: out[t][rows] = W . x[t] (x
  * [n_tok][cols]).  3-64 vectors (F32, F16, Q8_0, Q4_0; F16 and F32 from
- * 2) run as one product that dequantises the weights in registers; from 65
- * vectors on (Q6_K from 16) the weights are expanded to fp32 in an engine
- * workspace (rows x cols floats; F32 weights are used as they are) and
- * multiplied by hipBLASLt's fp32 product; fewer vectors (Q6_K: under 16)
- * run as groups of matrix-vector products.  fp32 accumulation throughout.
- * Used for the prompt's projections. */
+ * 2) run as one product that dequantises the weights in registers on the
+ * fp32 matrix cores; from 65 vectors on (Q6_K from 16) as the split product:
+ * x split into three bf16 pieces (an engine workspace of 6 bytes per
+ * element, tokens padded to 64), weights dequantised in registers into exact
+ * bf16 pieces, every product of pieces exact in the fp32 accumulator of the
+ * bf16 matrix cores (K cut into ranges for small grids, their sums added in
+ * order from a second workspace); fewer vectors (Q6_K: under 16) run as
+ * groups of matrix-vector products.  fp32 accumulation throughout: equal to
+ * the reference to fp32 rounding.  Used for the prompt's projections. */
 int tla_matmul_batch(tla_engine* e, float* out_dev, const void* w_dev, const float* x_dev, int rows,
                      int cols, int n_tok, int type);
 
@@ -334,10 +337,11 @@ int tla_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* 
  * [n_vocab] receives the last
  * token's logits (the ones generate() samples from).  The KV cache ends as
  * after n_tok forward() calls (to fp32 rounding: the attention sums are
- * grouped differently).  Engine memory it keeps for later calls: prompts of
- * 65-255 tokens two layers' weights in fp32 (about 350 MB at TinyLlama's
- * shapes), longer ones the largest matrix in fp32; prompts of 2-64 tokens
- * none (as long as no layer holds a Q6_K matrix). */
+ * grouped differently).  Engine memory it keeps for later calls: the split
+ * product's workspaces, for prompts past 64 tokens (or with a Q6_K layer
+ * matrix past 15): 6 bytes per token (padded to 64) and column of the
+ * widest product input (TinyLlama, 512 tokens: 17 MB), and partial sums of
+ * at most a few MB. */
 int tla_prefill_forward(tla_engine* e, const tla_model* m, float* key_cache_dev,
                         float* value_cache_dev, const int* tokens_host, int n_tok, int pos0,
                         float* logits_dev);
@@ -410,9 +414,15 @@ enum tla_option {
     TLA_OPT_DECODE_GROUP = 2, /* kv heads per decode workgroup in the plan of one split
                                  length: 1, 2 or 4 (the other plan always takes 4);
                                  results do not depend on it */
-    TLA_OPT_STREAM_TILES = 3  /* batched products of 2-64 vectors: vectors per
+    TLA_OPT_STREAM_TILES = 3, /* batched products of 2-64 vectors: vectors per
                                  workgroup in tiles of 16, 1 to 4; results do not
                                  depend on it */
+    TLA_OPT_SPLIT_ROWS = 4,   /* batched products past 64 vectors (Q6_K: from 16):
+                                 16-row subtiles per wave, 1, 2 or 4 (0: per
+                                 shape); results do not depend on it */
+    TLA_OPT_SPLIT_K = 5       /* the same products: ranges K is cut into, 1 to 64
+                                 (0: per shape; at most one per 32-column block);
+                                 results change by fp32 rounding only */
 };
 enum tla_decode_plan { TLA_PLAN_AUTO = 0, TLA_PLAN_ALIGNED = 1, TLA_PLAN_BALANCED = 2 };
 int tla_set_option(tla_engine* e, int option, long long value);

@@ -413,7 +413,7 @@ def test_prefill_forward_errors(tla, W, engines):
 @pytest.mark.parametrize("name", ["q8_0", "f16_tied", "q4_0", "mixed"])
 def test_prefill_forward_long_prompt(tla, O, W, engines, name):
     """A 48-token prompt: the batched projections as streamed products with
-    three token tiles (Q6_K matrices as fp32 weights + hipBLASLt products).
+    three token tiles (Q6_K matrices as split products).
     Last token's logits against the oracle's token loop."""
     g = golden("forward.npz")
     spec, t = model_from_golden(W, g, name)
@@ -477,13 +477,13 @@ def test_prefill_forward_streamed_prompt(tla, O, W, engines, name):
 
 
 @pytest.mark.parametrize("name", ["q8_0", "f16_tied", "q4_0", "f32", "mixed"])
-def test_prefill_forward_library_prompt(tla, O, W, engines, name):
-    """A 300-token prompt: every batched projection as weights expanded to
-    fp32 and hipBLASLt products, Q/K/V as three products and gate | up as
-    one (F32 weights multiplied where they lie, one product per matrix).  The golden case's weights on a
-    320-position context, in one call and as two calls of 150 tokens (the
-    second at pos0 = 150); last token's logits and the whole K cache against
-    the oracle's token loop."""
+def test_prefill_forward_split_prompt(tla, O, W, engines, name):
+    """A 300-token prompt: every batched projection as the split product (bf16
+    pieces on the matrix cores, fp32 sums), Q/K/V as one launch of three
+    segments where their formats agree and gate | up as one of two.  The
+    golden case's weights on a 320-position context, in one call and as two
+    calls of 150 tokens (the second at pos0 = 150); last token's logits and
+    the whole K cache against the oracle's token loop."""
     g = golden("forward.npz")
     base = W.ModelSpec(*[int(v) for v in g["spec"]])
     spec = W.ModelSpec(base.n_layers, base.n_embd, base.n_head, base.n_head_kv, base.n_ff, base.n_vocab,
@@ -497,7 +497,7 @@ def test_prefill_forward_library_prompt(tla, O, W, engines, name):
     toks = np.random.default_rng(300).integers(0, spec.n_vocab, n).tolist()
     om = O.Model(spec, t)
     want = om.tokens(toks)[-1]
-    log(f"  {name}: {n}-token prompt through the library products")
+    log(f"  {name}: {n}-token prompt through the split products")
     dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
     try:
         with device_arrays() as track:
@@ -525,11 +525,10 @@ def test_prefill_forward_library_prompt(tla, O, W, engines, name):
 
 def test_prefill_forward_after_queued_weight_writes(tla, O, W, engines):
     """Weights written on the engine's stream and not yet synchronized when a
-    prompt starts: the prompt's layer expansions, which run one layer ahead
-    on a second stream, must still see them.  Layers 0 and 1 (the two
-    expansions queued before any product) are overwritten with garbage,
-    then restored with tla_memcpy_d2d, and a 100-token prompt follows at
-    once; its last logits against the oracle's token loop."""
+    prompt starts: every product of the prompt must see them.  Layers 0 and
+    1 are overwritten with garbage, then restored with tla_memcpy_d2d, and a
+    100-token prompt follows at once; its last logits against the oracle's
+    token loop."""
     g = golden("forward.npz")
     base = W.ModelSpec(*[int(v) for v in g["spec"]])
     spec = W.ModelSpec(base.n_layers, base.n_embd, base.n_head, base.n_head_kv, base.n_ff, base.n_vocab,

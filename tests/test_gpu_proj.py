@@ -224,8 +224,8 @@ BATCH_SHAPES = [(32, 256, 16), (2560, 2048, 33), (64, 5632, 128), (5632, 2048, 1
 def test_matmul_batch(O, W, engines, t, name, rows, cols, n_tok):
     """tla_matmul_batch: groups of GEMVs (under 3 tokens, F16 / F32 under 2,
     Q6_K under 16), the streamed product (up to 64 tokens, weights
-    dequantised in registers) or
-    weights expanded to fp32 and hipBLASLt products, per token against the
+    dequantised in registers) or the split product (bf16 pieces of x and of
+    the weights on the matrix cores, fp32 sums), per token against the
     oracle's matmul."""
     if t == Q.Q6_K and cols % 256:
         pytest.skip("Q6_K rows are whole 256-weight super-blocks")
@@ -254,9 +254,9 @@ def test_matmul_batch_streamed(tla, O, W, engines, t, name, rows, cols, n_tok):
     """The streamed product (2 or 3 to 64 tokens): rows not a multiple of its
     16-row tiles, rows of 2 blocks (two of its four waves idle), token counts
     not a multiple of 16, 57 and 64 tokens (four token tiles) and 65 tokens
-    (the library product past the bound); every token against the oracle's
+    (the split product past the bound); every token against the oracle's
     matmul, and the same bits with one to four token tiles per workgroup
-    (Q6_K takes the GEMVs under 16 tokens, the library product from 16)."""
+    (Q6_K takes the GEMVs under 16 tokens, the split product from 16)."""
     if t == Q.Q6_K and cols % 256:
         pytest.skip("Q6_K rows are whole 256-weight super-blocks")
     eng = engines(1, 64)
@@ -294,12 +294,11 @@ def test_stream_tiles_option(tla, engines):
 
 
 def test_matmul_batch_many_shapes(O, W, engines):
-    """260 batch sizes in a row on an engine of its own: Q6_K takes the
-    library product from 16 vectors, so every size from 16 to 275 is a new
-    library product shape (descriptors and algorithm cached per shape, the
-    cache starting over past 256 shapes); products before, across and after
-    the reset against the oracle's matmul."""
-    eng = engines(1, 96)  # a key no other test uses: the plan cache starts empty
+    """Q6_K products of every batch size from 16 to 275 in a row on an engine
+    of its own (the split product from 16 vectors), so that the split-x and
+    partial-sum workspaces grow while products are queued; products at
+    several sizes against the oracle's matmul."""
+    eng = engines(1, 96)  # a key no other test uses: the workspaces start empty
     rows, cols, t = 32, 256, Q.Q6_K
     raw = W.make_weights(t, rows, cols, salt=11)
     x = np.random.default_rng(260).standard_normal((300, cols)).astype(np.float32)
@@ -309,18 +308,73 @@ def test_matmul_batch_many_shapes(O, W, engines):
         out = track(eng.array((300, rows)))
         for n_tok in range(16, 276):
             eng.matmul_batch(out.ptr, w.ptr, xd.ptr, rows, cols, n_tok, t)
-            if n_tok in (16, 200, 271, 275):
+            if n_tok in (16, 65, 200, 275):
                 got = out.download()
                 for i in (0, n_tok - 1):
                     check_rows(got[i], O.matmul(raw, x[i], rows, cols, t), raw, x[i], t, rows, cols,
                                f"{n_tok} tokens, token {i}")
 
 
+SPLIT_SHAPES = [(2048, 5632, 130), (2560, 2048, 65), (11264, 2048, 100), (40, 512, 70), (300, 256, 128)]
+
+
+@pytest.mark.parametrize("t,name", TYPES)
+@pytest.mark.parametrize("rows,cols,n_tok", SPLIT_SHAPES)
+def test_split_product_tilings(tla, O, W, engines, t, name, rows, cols, n_tok):
+    """The split product with 1, 2 and 4 row subtiles per wave (K in 3
+    ranges) gives the same bits: every output is one wave's sums in the same
+    order.  K cut into 1, 3 and 7 ranges (sums added in range order by the
+    second launch), and the per-shape choice, each within the oracle bound
+    for every token checked."""
+    if t == Q.Q6_K and cols % 256:
+        pytest.skip("Q6_K rows are whole 256-weight super-blocks")
+    eng = engines(1, 64)
+    raw = W.make_weights(t, rows, cols, salt=rows + 7 * cols)
+    x = np.random.default_rng(n_tok + 3).standard_normal((n_tok, cols)).astype(np.float32)
+    outs = {}
+    with device_arrays() as track:
+        w = track(eng.array(raw))
+        xd = track(eng.array(x))
+        out = track(eng.array((n_tok, rows)))
+        try:
+            # row tilings with K fixed (the per-shape K split follows the tiling)
+            eng.set_option(tla.OPT_SPLIT_K, 3)
+            for v in (1, 2, 4):
+                eng.set_option(tla.OPT_SPLIT_ROWS, v)
+                eng.matmul_batch(out.ptr, w.ptr, xd.ptr, rows, cols, n_tok, t)
+                outs[(tla.OPT_SPLIT_ROWS, v)] = out.download()
+            eng.set_option(tla.OPT_SPLIT_ROWS, 0)
+            for v in (0, 1, 3, 7):
+                eng.set_option(tla.OPT_SPLIT_K, v)
+                eng.matmul_batch(out.ptr, w.ptr, xd.ptr, rows, cols, n_tok, t)
+                outs[(tla.OPT_SPLIT_K, v)] = out.download()
+        finally:
+            eng.set_option(tla.OPT_SPLIT_ROWS, 0)
+            eng.set_option(tla.OPT_SPLIT_K, 0)
+    base = outs[(tla.OPT_SPLIT_ROWS, 1)]
+    for v in (2, 4):
+        assert np.array_equal(outs[(tla.OPT_SPLIT_ROWS, v)].view(np.uint32), base.view(np.uint32)), v
+    for (opt, v), got in outs.items():
+        for i in sorted({0, n_tok // 3, n_tok - 1}):
+            check_rows(got[i], O.matmul(raw, x[i], rows, cols, t), raw, x[i], t, rows, cols,
+                       f"{name} {rows}x{cols} opt {opt}={v} token {i}")
+
+
+def test_split_options(tla, engines):
+    """TLA_OPT_SPLIT_ROWS takes 0, 1, 2, 4; TLA_OPT_SPLIT_K 0 to 64."""
+    eng = engines(1, 64)
+    for opt, bad in ((tla.OPT_SPLIT_ROWS, (-1, 3, 8)), (tla.OPT_SPLIT_K, (-1, 65))):
+        for b in bad:
+            with pytest.raises(tla.TlaError) as e:
+                eng.set_option(opt, b)
+            assert e.value.code == tla.TLA_ERR_INVALID_ARGUMENT
+        eng.set_option(opt, 0)
+
+
 @pytest.mark.parametrize("rows,cols,n_tok", [(2048, 5632, 16), (256, 2048, 300), (11264, 2048, 512)])
 def test_matmul_batch_is_reproducible(W, engines, rows, cols, n_tok):
-    """The library product gives the same bits when repeated (its algorithm
-    is chosen once per shape; a split-K algorithm would have to sum in a
-    fixed order)."""
+    """The split product gives the same bits when repeated (fixed tiling and
+    K ranges per shape, the ranges' sums added in a fixed order)."""
     eng = engines(1, 64)
     raw = W.make_weights(Q.Q4_0, rows, cols, salt=5)
     x = np.random.default_rng(7).standard_normal((n_tok, cols)).astype(np.float32)

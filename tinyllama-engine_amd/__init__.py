@@ -50,6 +50,8 @@ KERNEL_DECODE, KERNEL_PREFILL, KERNEL_APPEND, KERNEL_GEMV = range(4)
 W_F32, W_F16, W_Q4_0, W_Q8_0, W_Q6_K = 0, 1, 2, 8, 14
 OPT_DECODE_SPLIT, OPT_DECODE_PLAN, OPT_DECODE_GROUP = 0, 1, 2
 OPT_STREAM_TILES = 3
+OPT_SPLIT_ROWS = 4
+OPT_SPLIT_K = 5
 PLAN_AUTO, PLAN_ALIGNED, PLAN_BALANCED = 0, 1, 2
 READ_GLOBAL, READ_GLOBAL_NT, READ_BUFFER, READ_BUFFER_NT = 0, 1, 2, 3
 

@@ -27,6 +27,34 @@ struct StreamParams {
 bool stream_supported(int type);
 hipError_t launch_stream_product(int type, const StreamParams& p, hipStream_t s);
 
+// Products of many tokens on the bf16 matrix cores with fp32 accuracy
+// (split_product.hip): x is first split into three bf16 planes
+// (launch_split_rows, split_x_bytes(n, cols) bytes at xs), then
+// out[t][row] (+)= W[row] . x[t] for every format of the reference
+// (F32 / F16 16-byte aligned, Q8_0 / Q4_0 / Q6_K 2-byte aligned), 64 x
+// rows_per_wave rows x 64 tokens per workgroup, K in k_splits ranges.
+struct SplitParams {
+    GemvSegment seg[kGemvMaxSeg];
+    int n_seg;
+    int total_rows;            // sum of seg[].rows
+    int cols;                  // multiple of 32 (of 256 for Q6_K)
+    long long row_bytes;
+    const unsigned char* xs;   // the planes of launch_split_rows
+    int n;                     // tokens
+    int n_sub;                 // split_tokens(n) / 16
+    int add;                   // 1: out += W.x, 0: out = W.x
+    int rows_per_wave;         // 16-row subtiles per wave: 1, 2 or 4
+    int k_splits;              // K cut into this many ranges of blk_per_split 32-column
+    int blk_per_split;         // blocks (grid z); each split's sums go to part, and a
+    float* part;               // second launch adds them in split order: [k_splits][n][total_rows]
+};
+size_t split_part_bytes(int n, int total_rows, int k_splits);
+int split_tokens(int n);                  // tokens padded to the 64-token tile
+size_t split_x_bytes(int n, int cols);    // bytes of the planes
+hipError_t launch_split_rows(const float* x, long long x_stride, int n, int cols, unsigned char* xs,
+                             hipStream_t s);
+hipError_t launch_split_product(int type, const SplitParams& p, hipStream_t s);
+
 }  // namespace tla
 
 #endif  // TLA_BATCH_H

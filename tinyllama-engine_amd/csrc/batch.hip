@@ -1,11 +1,10 @@
 // Batched-prompt helpers (tla_prefill_forward, tla_matmul_batch):
 //
-// dequant_rows_kernel: weights in the reference's formats (matmul(),
-//   src/ops.cpp:959-983, block layouts src/gguf.h:56-135) expanded to fp32
-//   rows, which the engine multiplies with hipBLASLt's fp32 product
-//   (engine.hip): the batched form of the projections forward() makes per
-//   token (src/forward.cpp:180-228) when the prompt runs through the model
-//   at once.
+// stream_product_kernel: the projections of a batch of up to 64 tokens with
+//   the weights dequantised in registers (matmul(), src/ops.cpp:959-983,
+//   block layouts src/gguf.h:56-135): the batched form of the projections
+//   forward() makes per token (src/forward.cpp:180-228) when the prompt runs
+//   through the model at once.  Longer batches: split_product.hip.
 // rmsnorm_rows_kernel, swiglu_rows_kernel: rmsnorm and SwiGLU over every
 //   token row of the batch (src/forward.cpp:180-184, 215-225).
 #include "row_math.h"
@@ -15,7 +14,6 @@ namespace tla {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kChunk = 32;  // columns per quantisation block (Q8_0 / Q4_0)
 
 __device__ __forceinline__ float half_to_float(unsigned h)
 {
@@ -47,78 +45,6 @@ __global__ __launch_bounds__(kThreads) void swiglu_rows_kernel(float* h, int n_f
         g[c] = (v * sigmoid) * g[n_ff + c];
     }
 }
-
-// Q6_K super-block (ql[128] qh[64] scales[16] d; 210 bytes, 256 values):
-// value r = d * scales[8h + 2k + l / 16] * q with h = r / 128, k = (r % 128)
-// / 32, l = r % 32, q = (4 bits of ql[64h + 32(k % 2) + l], low for k < 2)
-// | (2 bits 2k of qh[32h + l]) << 4, minus 32 (src/gguf.h layout; the
-// reference's embed_token() order of products).
-__device__ float q6k_value(const unsigned char* blk, int r)
-{
-    const int h = r >> 7, k = (r & 127) >> 5, l = r & 31;
-    const unsigned char* ql = blk + 64 * h;
-    const unsigned char* qh = blk + 128 + 32 * h;
-    const signed char* sc = reinterpret_cast<const signed char*>(blk + 192) + 8 * h;
-    const float d = half_to_float(blk[208] | (blk[209] << 8));
-    const int lo = (k & 1) ? ql[l + 32] : ql[l];
-    const int q = ((k < 2 ? (lo & 0x0F) : (lo >> 4)) | (((qh[l] >> (2 * k)) & 3) << 4)) - 32;
-    return d * static_cast<float>(sc[(l >> 4) + 2 * k]) * static_cast<float>(q);
-}
-
-// out[row][4j .. 4j + 3] = the fp32 values of columns 4j .. 4j + 3 of a
-// weight row, one thread per float4 of output, so the threads of a wave
-// store 1 KiB contiguously.  Each value is the reference's dequantised
-// weight (F16 converted, Q8_0 q * d, Q4_0 (q - 8) * d, Q6_K by
-// q6k_value).  Blocks start at even byte offsets, so the quantised bytes are
-// read as 16-bit halves.
-template <int kType>
-__global__ __launch_bounds__(kThreads) void dequant_rows_kernel(const unsigned char* __restrict__ w,
-                                                                long long row_bytes, int rows, int cols,
-                                                                float* __restrict__ out)
-{
-    const int n4 = cols / 4;
-    const long long g = static_cast<long long>(blockIdx.x) * kThreads + threadIdx.x;
-    if (g >= static_cast<long long>(rows) * n4) return;
-    const int row = static_cast<int>(g / n4);
-    const int col = 4 * static_cast<int>(g - static_cast<long long>(row) * n4);
-    const unsigned char* wrow = w + row * row_bytes;
-    float4 v;
-    if constexpr (kType == kF32) {
-        v = *reinterpret_cast<const float4*>(wrow + 4LL * col);
-    } else if constexpr (kType == kF16) {
-        const uint2 h = *reinterpret_cast<const uint2*>(wrow + 2LL * col);
-        v = make_float4(half_to_float(h.x & 0xFFFFu), half_to_float(h.x >> 16), half_to_float(h.y & 0xFFFFu),
-                        half_to_float(h.y >> 16));
-    } else if constexpr (kType == kQ6_K) {
-        const unsigned char* blk = wrow + 210LL * (col >> 8);
-        const int r = col & 255;
-        v = make_float4(q6k_value(blk, r), q6k_value(blk, r + 1), q6k_value(blk, r + 2), q6k_value(blk, r + 3));
-    } else {
-        constexpr int kBlock = kType == kQ8_0 ? 34 : 18;
-        const unsigned char* blk = wrow + static_cast<long long>(kBlock) * (col >> 5);
-        const unsigned short* hw = reinterpret_cast<const unsigned short*>(blk);
-        const float d = half_to_float(hw[0]);
-        const int cb = col & 31;
-        if constexpr (kType == kQ8_0) {
-            // columns cb .. cb + 3 are qs[cb .. cb + 3]
-            const unsigned q = hw[1 + cb / 2] | (static_cast<unsigned>(hw[2 + cb / 2]) << 16);
-            v = make_float4(static_cast<float>(static_cast<signed char>(q & 0xFFu)) * d,
-                            static_cast<float>(static_cast<signed char>((q >> 8) & 0xFFu)) * d,
-                            static_cast<float>(static_cast<signed char>((q >> 16) & 0xFFu)) * d,
-                            static_cast<float>(static_cast<signed char>(q >> 24)) * d);
-        } else {
-            // column e < 16 is the low nibble of qs[e], e >= 16 the high nibble of qs[e - 16]
-            const int b = cb & 15, shift = (cb >> 4) * 4;
-            const unsigned q = hw[1 + b / 2] | (static_cast<unsigned>(hw[2 + b / 2]) << 16);
-            v = make_float4(static_cast<float>(static_cast<int>((q >> shift) & 0xFu) - 8) * d,
-                            static_cast<float>(static_cast<int>((q >> (8 + shift)) & 0xFu) - 8) * d,
-                            static_cast<float>(static_cast<int>((q >> (16 + shift)) & 0xFu) - 8) * d,
-                            static_cast<float>(static_cast<int>((q >> (24 + shift)) & 0xFu) - 8) * d);
-        }
-    }
-    *reinterpret_cast<float4*>(out + static_cast<long long>(row) * cols + col) = v;
-}
-
 
 // ---- stream_product_kernel --------------------------------------------------
 // The projections of a batch of up to 64 tokens with the weights dequantised
@@ -352,24 +278,6 @@ hipError_t launch_stream_product(int type, const StreamParams& p, hipStream_t s)
     case kQ8_0: return launch_stream_typed<kQ8_0>(p, s);
     default: return launch_stream_typed<kQ4_0>(p, s);
     }
-}
-
-hipError_t launch_dequant_rows(int type, const unsigned char* w, long long row_bytes, int rows, int cols,
-                               float* out, hipStream_t s)
-{
-    if (rows < 1 || cols < kChunk || cols % kChunk != 0 || (type == kQ6_K && cols % 256 != 0))
-        return hipErrorInvalidValue;
-    const long long n = static_cast<long long>(rows) * (cols / 4);
-    const dim3 grid(static_cast<unsigned>((n + kThreads - 1) / kThreads));
-    switch (type) {
-    case kF32: hipLaunchKernelGGL(dequant_rows_kernel<kF32>, grid, dim3(kThreads), 0, s, w, row_bytes, rows, cols, out); break;
-    case kF16: hipLaunchKernelGGL(dequant_rows_kernel<kF16>, grid, dim3(kThreads), 0, s, w, row_bytes, rows, cols, out); break;
-    case kQ8_0: hipLaunchKernelGGL(dequant_rows_kernel<kQ8_0>, grid, dim3(kThreads), 0, s, w, row_bytes, rows, cols, out); break;
-    case kQ4_0: hipLaunchKernelGGL(dequant_rows_kernel<kQ4_0>, grid, dim3(kThreads), 0, s, w, row_bytes, rows, cols, out); break;
-    case kQ6_K: hipLaunchKernelGGL(dequant_rows_kernel<kQ6_K>, grid, dim3(kThreads), 0, s, w, row_bytes, rows, cols, out); break;
-    default: return hipErrorInvalidValue;
-    }
-    return hipGetLastError();
 }
 
 hipError_t launch_rmsnorm_rows(float* out, const float* x, const float* w, int n_rows, int size, float eps,

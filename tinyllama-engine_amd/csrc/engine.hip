@@ -13,7 +13,6 @@
 #include <utility>
 #include <vector>
 
-#include <hipblaslt/hipblaslt.h>
 
 #include "batch.h"
 #include "tla_internal.h"
@@ -108,30 +107,6 @@ namespace {
 std::mutex g_scratch_mu;
 void* g_scratch_ptr[kScratchDevices] = {};  // device address of `scratch`, per device
 
-// One library product shape, C (m x n, ldc) = op(A) (A stored k x m, lda,
-// transposed) x B (k x n, ldb), fp32 in and out, fp32 compute: its
-// descriptors and the first algorithm the library's heuristic returns.
-struct LtPlan {
-    int m = 0, n = 0, k = 0;
-    long long lda = 0, ldb = 0, ldc = 0;
-    hipblasLtMatmulDesc_t desc = nullptr;
-    hipblasLtMatrixLayout_t a = nullptr, b = nullptr, c = nullptr;
-    hipblasLtMatmulAlgo_t algo{};
-};
-
-void lt_plan_destroy(LtPlan& pl)
-{
-    if (pl.a) (void)hipblasLtMatrixLayoutDestroy(pl.a);
-    if (pl.b) (void)hipblasLtMatrixLayoutDestroy(pl.b);
-    if (pl.c) (void)hipblasLtMatrixLayoutDestroy(pl.c);
-    if (pl.desc) (void)hipblasLtMatmulDescDestroy(pl.desc);
-    pl = LtPlan{};
-}
-
-constexpr size_t kLtWorkspace = 32u << 20;
-// Product shapes kept: every prompt length brings up to four (Q/K/V, W_o,
-// gate | up, down); past this many the cache starts over.
-constexpr size_t kLtMaxPlans = 256;
 }  // namespace
 
 struct tla_engine {
@@ -149,26 +124,17 @@ struct tla_engine {
     size_t n_counters = 0;
     void* fwd = nullptr;     // forward(): residual stream, q|k|v, attention out, FFN, tokens
     size_t fwd_bytes = 0;
-    float* wf = nullptr;       // weights expanded to fp32 for the library product
-    size_t wf_bytes = 0;
-    // A prompt's layers, expanded to fp32 one layer ahead on a second
-    // stream while the current layer's products run: two layer buffers,
-    // `layer_ready[i]` recorded on `side` once buffer i holds its layer,
-    // `layer_done[i]` on `stream` once the products reading buffer i are
-    // queued behind it.
-    hipStream_t side = nullptr;
-    float* layer_buf[2] = {};
-    size_t layer_buf_bytes = 0;
-    hipEvent_t layer_ready[2] = {}, layer_done[2] = {};
-    hipEvent_t side_start = nullptr;  // recorded on `stream` before a prompt's first expansion
-    hipblasLtHandle_t lt = nullptr;  // created at the first library product
-    void* lt_ws = nullptr;           // its workspace (kLtWorkspace bytes)
-    std::deque<LtPlan> lt_plans;     // per product shape (a deque: plans stay put as it grows)
+    unsigned char* xs = nullptr;  // batched products: x split into bf16 planes
+    size_t xs_bytes = 0;
+    float* part = nullptr;        // and their K splits' partial sums
+    size_t part_bytes = 0;
     int* argmax_slot = nullptr;
     long long opt_split = 0;
     int opt_plan = TLA_PLAN_AUTO;
     int opt_group = 0;  // kv heads per aligned-plan workgroup, 0 = per launch
     int opt_stream_tiles = 0;  // streamed product: token tiles per workgroup, 0 = per shape
+    int opt_split_rows = 0;    // split product: 16-row subtiles per wave, 0 = per shape
+    int opt_split_k = 0;       // split product: K ranges, 0 = per shape
     int n_cu = 256;          // compute units: decode workgroups per launch
 
     bool prof = false;
@@ -460,18 +426,8 @@ int tla_engine_destroy(tla_engine* e)
     if (e->ws) (void)hipFree(e->ws);
     if (e->counters) (void)hipFree(e->counters);
     if (e->fwd) (void)hipFree(e->fwd);
-    if (e->wf) (void)hipFree(e->wf);
-    if (e->side) (void)hipStreamSynchronize(e->side);
-    for (int i = 0; i < 2; ++i) {
-        if (e->layer_buf[i]) (void)hipFree(e->layer_buf[i]);
-        if (e->layer_ready[i]) (void)hipEventDestroy(e->layer_ready[i]);
-        if (e->layer_done[i]) (void)hipEventDestroy(e->layer_done[i]);
-    }
-    if (e->side_start) (void)hipEventDestroy(e->side_start);
-    if (e->side) (void)hipStreamDestroy(e->side);
-    for (LtPlan& pl : e->lt_plans) lt_plan_destroy(pl);
-    if (e->lt_ws) (void)hipFree(e->lt_ws);
-    if (e->lt) (void)hipblasLtDestroy(e->lt);
+    if (e->xs) (void)hipFree(e->xs);
+    if (e->part) (void)hipFree(e->part);
     if (e->argmax_slot) (void)hipFree(e->argmax_slot);
     if (e->rope) (void)hipFree(e->rope);
     if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -1255,163 +1211,89 @@ int gemv_rows(tla_engine* e, int type, const void* w, float* out, int rows, int 
     return TLA_OK;
 }
 
-// Token batches at least this long take the library product below; shorter
-// ones the multi-vector GEMV (weights read once per group of up to 8
-// tokens).
+// Token batches at least this long (and past the streamed product's range)
+// take the split product below; shorter ones the multi-vector GEMV (weights
+// read once per group of up to 8 tokens).
 constexpr int kBatchMinTokens = 16;
 
-int ensure_wf(tla_engine* e, size_t bytes)
+// Grows a workspace of the split product to `bytes` (after the stream's
+// queued work, which may still read it).
+int ensure_buf(tla_engine* e, void** buf, size_t& have, size_t bytes, const char* what)
 {
-    if (bytes <= e->wf_bytes) return TLA_OK;
+    if (bytes <= have) return TLA_OK;
     TLA_HIP(hipStreamSynchronize(e->stream));
-    if (e->wf) TLA_HIP(hipFree(e->wf));
-    e->wf = nullptr;
-    e->wf_bytes = 0;
-    const hipError_t err = hipMalloc(&e->wf, bytes);
+    if (*buf) TLA_HIP(hipFree(*buf));
+    *buf = nullptr;
+    have = 0;
+    const hipError_t err = hipMalloc(buf, bytes);
     if (err != hipSuccess)
-        return fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE,
-                    "fp32 weight workspace (%zu bytes): %s", bytes, hipGetErrorString(err));
-    e->wf_bytes = bytes;
+        return fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE, "%s (%zu bytes): %s",
+                    what, bytes, hipGetErrorString(err));
+    have = bytes;
     return TLA_OK;
 }
 
-int ensure_lt(tla_engine* e)
+// out_s[t][row] (+)= W_s[row] . x[t] as the split product (split_product.hip):
+// x split into three bf16 planes, then one launch over all segments, the
+// weights dequantised in registers.  16-row subtiles per wave: 4 for matrices
+// with enough rows to give every CU a workgroup at that size (F32 weights:
+// 2, for their registers), else 2, else 1.  A grid still short of two
+// workgroups per CU cuts K into ranges of at least 8 blocks (each a
+// workgroup walking its range, the ranges' sums added in order by a second
+// launch): a workgroup's blocks follow one another at a memory round trip
+// each, so fewer blocks per workgroup is what shortens a small product.
+int split_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int total, int cols, const float* x,
+                long long x_stride, int n, int add)
 {
-    if (e->lt) return TLA_OK;
-    hipblasLtHandle_t h = nullptr;
-    if (hipblasLtCreate(&h) != HIPBLAS_STATUS_SUCCESS) return fail(TLA_ERR_DEVICE, "hipblasLtCreate failed");
-    const hipError_t err = hipMalloc(&e->lt_ws, kLtWorkspace);
-    if (err != hipSuccess) {
-        (void)hipblasLtDestroy(h);
-        e->lt_ws = nullptr;
-        return fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE,
-                    "library product workspace: %s", hipGetErrorString(err));
+    if (int rc = ensure_buf(e, reinterpret_cast<void**>(&e->xs), e->xs_bytes, split_x_bytes(n, cols), "split-x workspace")) return rc;
+    SplitParams p{};
+    for (int i = 0; i < n_seg; ++i) p.seg[i] = segs[i];
+    p.n_seg = n_seg;
+    p.total_rows = total;
+    p.cols = cols;
+    p.row_bytes = weight_row_bytes(type, cols);
+    p.xs = e->xs;
+    p.n = n;
+    p.n_sub = split_tokens(n) / 16;
+    p.add = add;
+    const long long token_tiles = p.n_sub / 4;
+    auto groups = [&](int rw) { return (total + 64LL * rw - 1) / (64LL * rw) * token_tiles; };
+    p.rows_per_wave = type != kF32 && groups(4) >= e->n_cu ? 4 : groups(2) >= e->n_cu ? 2 : 1;
+    if (e->opt_split_rows > 0) p.rows_per_wave = e->opt_split_rows;
+    const int n_blk = cols / 32;
+    const long long g = groups(p.rows_per_wave);
+    int splits = g >= e->n_cu ? 1 : static_cast<int>(std::min<long long>((2LL * e->n_cu + g - 1) / g, n_blk / 8));
+    if (e->opt_split_k > 0) splits = e->opt_split_k;
+    splits = std::max(1, std::min(splits, n_blk));
+    p.blk_per_split = (n_blk + splits - 1) / splits;
+    p.k_splits = (n_blk + p.blk_per_split - 1) / p.blk_per_split;
+    if (p.k_splits > 1) {
+        if (int rc = ensure_buf(e, reinterpret_cast<void**>(&e->part), e->part_bytes, split_part_bytes(n, total, p.k_splits),
+                                "split-product partial sums"))
+            return rc;
+        p.part = e->part;
     }
-    e->lt = h;
-    return TLA_OK;
-}
-
-// The cached plan of a product shape, built (descriptors + the heuristic's
-// first algorithm) at its first use.
-int lt_plan(tla_engine* e, int m, int n, int k, long long lda, long long ldb, long long ldc, const LtPlan** out)
-{
-    for (const LtPlan& pl : e->lt_plans)
-        if (pl.m == m && pl.n == n && pl.k == k && pl.lda == lda && pl.ldb == ldb && pl.ldc == ldc) {
-            *out = &pl;
-            return TLA_OK;
-        }
-    LtPlan pl;
-    pl.m = m, pl.n = n, pl.k = k, pl.lda = lda, pl.ldb = ldb, pl.ldc = ldc;
-    const hipblasOperation_t op_t = HIPBLAS_OP_T, op_n = HIPBLAS_OP_N;
-    hipblasLtMatmulPreference_t pref = nullptr;
-    size_t ws = kLtWorkspace;
-    hipblasLtMatmulHeuristicResult_t res{};
-    int got = 0;
-    const bool ok =
-        hipblasLtMatmulDescCreate(&pl.desc, HIPBLAS_COMPUTE_32F, HIP_R_32F) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSA, &op_t, sizeof(op_t)) ==
-            HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatmulDescSetAttribute(pl.desc, HIPBLASLT_MATMUL_DESC_TRANSB, &op_n, sizeof(op_n)) ==
-            HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatrixLayoutCreate(&pl.a, HIP_R_32F, k, m, lda) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatrixLayoutCreate(&pl.b, HIP_R_32F, k, n, ldb) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatrixLayoutCreate(&pl.c, HIP_R_32F, m, n, ldc) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatmulPreferenceCreate(&pref) == HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatmulPreferenceSetAttribute(pref, HIPBLASLT_MATMUL_PREF_MAX_WORKSPACE_BYTES, &ws, sizeof(ws)) ==
-            HIPBLAS_STATUS_SUCCESS &&
-        hipblasLtMatmulAlgoGetHeuristic(e->lt, pl.desc, pl.a, pl.b, pl.c, pl.c, pref, 1, &res, &got) ==
-            HIPBLAS_STATUS_SUCCESS &&
-        got > 0;
-    if (pref) (void)hipblasLtMatmulPreferenceDestroy(pref);
-    if (!ok) {
-        lt_plan_destroy(pl);
-        return fail(TLA_ERR_DEVICE, "no library product for %d x %d x %d", m, n, k);
-    }
-    pl.algo = res.algo;
-    e->lt_plans.push_back(pl);
-    *out = &e->lt_plans.back();
-    return TLA_OK;
-}
-
-// out_s[t][row] (+)= W_s[row] . x[t] as hipBLASLt fp32 products over the
-// weights expanded to fp32 (launch_dequant_rows): one product per run of
-// segments whose outputs continue each other's columns (gate | up), else
-// one per segment.  In column-major terms C (rows x n, ldc = out_stride) =
-// Wf^T (Wf row-major [rows][cols]) x X (cols x n, ldb = x_stride), beta 1
-// for the residual.
-// `expanded`: the segments' weights already expanded to fp32, segment after
-// segment (the prompt's layer buffers); else F32 weights are multiplied
-// where they lie (one product per segment) and the other formats expanded
-// into the workspace first.
-int blas_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int total, int cols,
-               const float* x, long long x_stride, int n, int add, const float* expanded = nullptr)
-{
-    const bool direct = !expanded && type == kF32;
-    const bool expand = !expanded && !direct;
-    if (int rc = ensure_lt(e)) return rc;
-    if (e->lt_plans.size() + kGemvMaxSeg > kLtMaxPlans) {  // before any plan of this call is taken
-        for (LtPlan& pl : e->lt_plans) lt_plan_destroy(pl);
-        e->lt_plans.clear();
-    }
-    if (expand)
-        if (int rc = ensure_wf(e, static_cast<size_t>(total) * cols * sizeof(float))) return rc;
-    const float* const wbase = expanded ? expanded : e->wf;
-    struct Run {
-        int seg;
-        const float* w;
-        const LtPlan* plan;
-    };
-    Run runs[kGemvMaxSeg];
-    int n_runs = 0;
-    long long r0 = 0;
-    for (int i = 0; i < n_seg;) {
-        int j = i + 1, rows = segs[i].rows;
-        while (!direct && j < n_seg && segs[j].out_stride == segs[i].out_stride &&
-               segs[j].out == segs[i].out + rows)
-            rows += segs[j++].rows;
-        const LtPlan* plan = nullptr;
-        if (int rc = lt_plan(e, rows, n, cols, cols, x_stride, segs[i].out_stride, &plan)) return rc;
-        const float* w = direct ? reinterpret_cast<const float*>(segs[i].w) : wbase + r0 * cols;
-        runs[n_runs++] = {i, w, plan};
-        r0 += rows;
-        i = j;
-    }
-    const long long row_bytes = static_cast<long long>(weight_row_bytes(type, cols));
-    return launch(e, TLA_KERNEL_GEMV, "batched product", [&]() -> hipError_t {
-        long long w0 = 0;
-        for (int i = 0; i < n_seg && expand; ++i) {
-            const hipError_t err = launch_dequant_rows(type, segs[i].w, row_bytes, segs[i].rows, cols,
-                                                       e->wf + w0 * cols, e->stream);
-            if (err != hipSuccess) return err;
-            w0 += segs[i].rows;
-        }
-        const float alpha = 1.0f, beta = add ? 1.0f : 0.0f;
-        for (int r = 0; r < n_runs; ++r) {
-            const Run& ru = runs[r];
-            float* out = segs[ru.seg].out;
-            if (hipblasLtMatmul(e->lt, ru.plan->desc, &alpha, ru.w, ru.plan->a, x, ru.plan->b,
-                                &beta, out, ru.plan->c, out, ru.plan->c, &ru.plan->algo, e->lt_ws, kLtWorkspace,
-                                e->stream) != HIPBLAS_STATUS_SUCCESS)
-                return hipErrorLaunchFailure;
-        }
-        return hipGetLastError();
-    });
+    if (int rc = launch(e, TLA_KERNEL_GEMV, "split rows",
+                        [&]() -> hipError_t { return launch_split_rows(x, x_stride, n, cols, e->xs, e->stream); }))
+        return rc;
+    return launch(e, TLA_KERNEL_GEMV, "split product",
+                  [&]() -> hipError_t { return launch_split_product(type, p, e->stream); });
 }
 
 // out_s[t][row] (+)= W_s[row] . x[t] for the n_seg matrices of `segs`, one
 // type, over n tokens (x rows x_stride floats apart).
 // Batches of stream_min_tokens(type) .. kStreamMaxTokens vectors multiply F32
 // / F16 / Q8_0 / Q4_0 weights where they lie, dequantised in registers by
-// stream_product_kernel; the library product pays for an fp32 copy of the
-// weights and runs far below the MFMA rate at these widths (Q4_0 prompts of
-// 33 / 48 / 64 tokens 2.79 / 3.22 / 3.60 ms streamed against 3.60 / 3.64 /
-// 3.65 ms), and the
+// stream_product_kernel; a library product on an fp32 copy of the weights
+// ran far below the MFMA rate at these widths (Q4_0 prompts of 33 / 48 / 64
+// tokens 2.79 / 3.22 / 3.60 ms streamed against 3.60 / 3.64 / 3.65 ms), and
+// the
 // multi-vector GEMVs read the weights once per 2-6 vectors (Q4_0 prompts of
 // 3 / 8 / 15 tokens 1.67 / 1.82 / ~2.0 ms streamed against 1.89 / 4.21 /
 // 7.25 ms).  At 2 tokens the GEMVs keep the quantised formats (Q4_0 1.53
 // against 1.63 ms, Q8_0 1.59 against 1.62) but not F16 / F32 (1.69 / 1.93
-// against 1.41 / 1.72 ms).  Past 64 vectors the library product wins: each
-// 16-row workgroup loads all of x itself.
+// against 1.41 / 1.72 ms).  Past 64 vectors the split product takes over:
+// each 16-row workgroup of the streamed product loads all of x itself.
 constexpr int kStreamMaxTokens = 64;
 
 int stream_min_tokens(int type) { return type == kF16 || type == kF32 ? 2 : 3; }
@@ -1454,9 +1336,9 @@ int matrix_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, in
     int total = 0;
     for (int i = 0; i < n_seg; ++i) total += segs[i].rows;
     if (use_stream(type, cols, n, x_stride)) return stream_batch(e, type, segs, n_seg, total, cols, x, x_stride, n, add);
-    if (n >= kBatchMinTokens && cols % 32 == 0 && (type != kQ6_K || cols % 256 == 0) &&
-        static_cast<long long>(total) * cols < (1LL << 31) && x_stride < (1LL << 31))
-        return blas_batch(e, type, segs, n_seg, total, cols, x, x_stride, n, add);
+    if (n >= kBatchMinTokens && cols % 32 == 0 && (type != kQ6_K || cols % 256 == 0) && x_stride % 4 == 0 &&
+        reinterpret_cast<std::uintptr_t>(x) % 16 == 0)
+        return split_batch(e, type, segs, n_seg, total, cols, x, x_stride, n, add);
     const int chunk = std::max(1, std::min({n, kGemvMaxVec, kGemvLdsBytes / gemv_lds_per_vec(cols)}));
     for (int t0 = 0; t0 < n; t0 += chunk) {
         GemvParams p{};
@@ -1477,120 +1359,12 @@ int matrix_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, in
     return TLA_OK;
 }
 
-// A layer's seven matrices expanded to fp32, one after another: Wq [embd]
-// [embd], Wk, Wv [kv][embd], Wo [embd][embd], W_gate, W_up [ff][embd],
-// W_down [embd][ff].
-struct LayerLayout {
-    long long q, k, v, o, gate, up, down, total;  // offsets in floats
-    LayerLayout(long long embd, long long kv, long long ff)
-    {
-        q = 0;
-        k = q + embd * embd;
-        v = k + kv * embd;
-        o = v + kv * embd;
-        gate = o + embd * embd;
-        up = gate + ff * embd;
-        down = up + ff * embd;
-        total = down + embd * ff;
-    }
-};
-
-// Whether every matrix of every layer takes the library product (the
-// prompt's layers can then be expanded ahead).
-bool layers_expandable(const tla_model* m, int n_layers, int embd, int ff)
-{
-    for (int l = 0; l < n_layers; ++l) {
-        const tla_layer_weights& L = m->layers[l];
-        for (int t : {L.type_q, L.type_k, L.type_v, L.type_o, L.type_ffn})
-            if (t == kQ6_K && (embd % 256 || ff % 256)) return false;
-    }
-    return embd % 32 == 0 && ff % 32 == 0;
-}
-
-// Whether every matrix of every layer takes the streamed product for a
-// prompt of n_tok tokens (nothing to expand then).
-bool layers_stream(const tla_model* m, int n_layers, int embd, int ff, int n_tok)
-{
-    for (int l = 0; l < n_layers; ++l) {
-        const tla_layer_weights& L = m->layers[l];
-        for (int t : {L.type_q, L.type_k, L.type_v, L.type_o, L.type_ffn})
-            if (!use_stream(t, embd, n_tok, embd) || !use_stream(t, ff, n_tok, 2LL * ff)) return false;
-    }
-    return true;
-}
-
-int ensure_layer_bufs(tla_engine* e, size_t bytes)
-{
-    if (!e->side) {
-        TLA_HIP(hipStreamCreateWithFlags(&e->side, hipStreamNonBlocking));
-        for (int i = 0; i < 2; ++i) {
-            TLA_HIP(hipEventCreateWithFlags(&e->layer_ready[i], hipEventDisableTiming));
-            TLA_HIP(hipEventCreateWithFlags(&e->layer_done[i], hipEventDisableTiming));
-        }
-        TLA_HIP(hipEventCreateWithFlags(&e->side_start, hipEventDisableTiming));
-    }
-    if (bytes <= e->layer_buf_bytes) return TLA_OK;
-    TLA_HIP(hipStreamSynchronize(e->stream));
-    TLA_HIP(hipStreamSynchronize(e->side));
-    for (int i = 0; i < 2; ++i) {
-        if (e->layer_buf[i]) TLA_HIP(hipFree(e->layer_buf[i]));
-        e->layer_buf[i] = nullptr;
-    }
-    e->layer_buf_bytes = 0;
-    for (int i = 0; i < 2; ++i) {
-        const hipError_t err = hipMalloc(&e->layer_buf[i], bytes);
-        if (err != hipSuccess)
-            return fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE,
-                        "fp32 layer buffers (2 x %zu bytes): %s", bytes, hipGetErrorString(err));
-    }
-    e->layer_buf_bytes = bytes;
-    return TLA_OK;
-}
-
-// Prompts shorter than this expand their layers ahead on the side stream.
-// Same box, TinyLlama Q4_0 prompts: 32 tokens 3.28 against 3.88 ms; at 512
-// tokens the expansions slow the products they share the CUs with (10.62
-// against 10.37 ms), and a grid capped at 64 workgroups is too slow to keep
-// ahead (9.4 ms at 32 tokens).
-constexpr int kAheadMaxTokens = 256;
-
-// Layer l's weights expanded into layer buffer `slot` on the side stream,
-// after the products that last read that buffer; layer_ready[slot] marks
-// the end.  (The expansions are not in tla_profile's sums: they run beside
-// the products.)
-int expand_layer(tla_engine* e, const tla_model* m, int l, int slot, const LayerLayout& lay)
-{
-    const int embd = e->cfg.n_embd, kv = e->kv_dim, ff = m->n_ff;
-    const tla_layer_weights& L = m->layers[l];
-    float* const buf = e->layer_buf[slot];
-    TLA_HIP(hipStreamWaitEvent(e->side, e->layer_done[slot], 0));
-    struct M {
-        const void* w;
-        int type, rows, cols;
-        long long at;
-    } const mats[7] = {{L.wq, L.type_q, embd, embd, lay.q},       {L.wk, L.type_k, kv, embd, lay.k},
-                       {L.wv, L.type_v, kv, embd, lay.v},         {L.wo, L.type_o, embd, embd, lay.o},
-                       {L.w_gate, L.type_ffn, ff, embd, lay.gate}, {L.w_up, L.type_ffn, ff, embd, lay.up},
-                       {L.w_down, L.type_ffn, embd, ff, lay.down}};
-    for (const M& mt : mats)
-        if (int rc = check_hip(launch_dequant_rows(mt.type, static_cast<const unsigned char*>(mt.w),
-                                                   weight_row_bytes(mt.type, mt.cols), mt.rows, mt.cols,
-                                                   buf + mt.at, e->side),
-                               "layer expansion"))
-            return rc;
-    TLA_HIP(hipEventRecord(e->layer_ready[slot], e->side));
-    return TLA_OK;
-}
-
 // The prompt as one batch (n_tok tokens at positions pos0..): embeddings,
 // then per layer rmsnorm + Q/K/V over all tokens, the causal prefill
 // attention (RoPE + append in-kernel), W_o + residual and the FFN;
-// logits of the last token only (when `logits` is non-null).  From
-// kBatchMinTokens to kAheadMaxTokens tokens the products are library
-// products whose weights were expanded one layer ahead on the side stream
-// (while the previous layer's products ran); other prompts take
-// matrix_batch (multi-vector GEMVs under kBatchMinTokens, in-stream
-// expansion + library products above).
+// logits of the last token only (when `logits` is non-null).  Every
+// product is a matrix_batch: multi-vector GEMVs, streamed products or
+// split products by the prompt's length.
 int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, float* vc,
                 const int* tokens_dev, int n_tok, int pos0, float* logits)
 {
@@ -1602,42 +1376,19 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
         return rc;
     const auto U = [](const void* w) { return static_cast<const unsigned char*>(w); };
     const int n_layers = e->cfg.n_layers;
-    const LayerLayout lay(embd, kv, ff);
-    const bool ahead = n_tok >= kBatchMinTokens && n_tok < kAheadMaxTokens &&
-                       layers_expandable(m, n_layers, embd, ff) && !layers_stream(m, n_layers, embd, ff, n_tok);
-    if (ahead) {
-        if (int rc = ensure_lt(e)) return rc;
-        if (int rc = ensure_layer_bufs(e, static_cast<size_t>(lay.total) * sizeof(float))) return rc;
-        // The side stream starts after everything already queued on the
-        // engine stream (the weights may have been written there, e.g. by
-        // tla_memcpy_d2d); layer_done orders only the buffers' reuse.
-        TLA_HIP(hipEventRecord(e->side_start, e->stream));
-        TLA_HIP(hipStreamWaitEvent(e->side, e->side_start, 0));
-        if (int rc = expand_layer(e, m, 0, 0, lay)) return rc;
-    }
     for (int l = 0; l < n_layers; ++l) {
         const tla_layer_weights& L = m->layers[l];
-        const float* const wl = ahead ? e->layer_buf[l & 1] : nullptr;
-        if (ahead) {
-            if (l + 1 < n_layers)
-                if (int rc = expand_layer(e, m, l + 1, (l + 1) & 1, lay)) return rc;
-            TLA_HIP(hipStreamWaitEvent(e->stream, e->layer_ready[l & 1], 0));
-        }
-        // one product run: the expanded layer's weights at `at`, or matrix_batch
         auto product = [&](int type, const GemvSegment* segs, int n_seg, int cols, const float* x,
-                           long long x_stride, int add, long long at) -> int {
-            if (!ahead) return matrix_batch(e, type, segs, n_seg, cols, x, x_stride, n_tok, add);
-            int total = 0;
-            for (int i = 0; i < n_seg; ++i) total += segs[i].rows;
-            return blas_batch(e, type, segs, n_seg, total, cols, x, x_stride, n_tok, add, wl + at);
+                           long long x_stride, int add) -> int {
+            return matrix_batch(e, type, segs, n_seg, cols, x, x_stride, n_tok, add);
         };
         // rmsnorm rows, then Q/K/V (src/forward.cpp:180-190)
         if (int rc = check_hip(launch_rmsnorm_rows(b.xb, b.x, L.attn_norm, n_tok, embd, eps, e->stream),
                                "rmsnorm rows"))
             return rc;
-        if (ahead || (L.type_q == L.type_k && L.type_q == L.type_v)) {
+        if (L.type_q == L.type_k && L.type_q == L.type_v) {
             const GemvSegment segs[3] = {{U(L.wq), b.q, embd, embd}, {U(L.wk), b.k, kv, kv}, {U(L.wv), b.v, kv, kv}};
-            if (int rc = product(L.type_q, segs, 3, embd, b.xb, embd, 0, lay.q)) return rc;
+            if (int rc = product(L.type_q, segs, 3, embd, b.xb, embd, 0)) return rc;
         } else {
             const GemvSegment sq{U(L.wq), b.q, embd, embd}, sk{U(L.wk), b.k, kv, kv}, sv{U(L.wv), b.v, kv, kv};
             if (int rc = matrix_batch(e, L.type_q, &sq, 1, embd, b.xb, embd, n_tok, 0)) return rc;
@@ -1649,7 +1400,7 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
         // x += Wo . att (src/forward.cpp:210-213)
         {
             const GemvSegment so{U(L.wo), b.x, embd, embd};
-            if (int rc = product(L.type_o, &so, 1, embd, b.att, embd, 1, lay.o)) return rc;
+            if (int rc = product(L.type_o, &so, 1, embd, b.att, embd, 1)) return rc;
         }
         // FFN (src/forward.cpp:215-228): rmsnorm rows, gate and up into
         // hb [t][gate | up], SiLU x up in place, x += W_down . h
@@ -1658,14 +1409,13 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
             return rc;
         {
             const GemvSegment segs[2] = {{U(L.w_gate), b.hb, ff, 2LL * ff}, {U(L.w_up), b.hb + ff, ff, 2LL * ff}};
-            if (int rc = product(L.type_ffn, segs, 2, embd, b.xb, embd, 0, lay.gate)) return rc;
+            if (int rc = product(L.type_ffn, segs, 2, embd, b.xb, embd, 0)) return rc;
         }
         if (int rc = check_hip(launch_swiglu_rows(b.hb, n_tok, ff, e->stream), "swiglu rows")) return rc;
         {
             const GemvSegment sd{U(L.w_down), b.x, embd, embd};
-            if (int rc = product(L.type_ffn, &sd, 1, ff, b.hb, 2LL * ff, 1, lay.down)) return rc;
+            if (int rc = product(L.type_ffn, &sd, 1, ff, b.hb, 2LL * ff, 1)) return rc;
         }
-        if (ahead) TLA_HIP(hipEventRecord(e->layer_done[l & 1], e->stream));  // buffer l & 1 free after this
     }
     if (logits)
         if (int rc = gemv1(e, m->type_output, m->output, logits, m->n_vocab, embd,
@@ -2026,6 +1776,15 @@ int tla_set_option(tla_engine* e, int option, long long value)
         if (value < 0 || value > kStreamMaxTiles)
             return fail(TLA_ERR_INVALID_ARGUMENT, "stream tiles %lld not in [0, %d]", value, kStreamMaxTiles);
         e->opt_stream_tiles = static_cast<int>(value);
+        return ok();
+    case TLA_OPT_SPLIT_ROWS:
+        if (value != 0 && value != 1 && value != 2 && value != 4)
+            return fail(TLA_ERR_INVALID_ARGUMENT, "split rows %lld not 0, 1, 2 or 4", value);
+        e->opt_split_rows = static_cast<int>(value);
+        return ok();
+    case TLA_OPT_SPLIT_K:
+        if (value < 0 || value > 64) return fail(TLA_ERR_INVALID_ARGUMENT, "split K %lld not in [0, 64]", value);
+        e->opt_split_k = static_cast<int>(value);
         return ok();
     default:
         return fail(TLA_ERR_INVALID_ARGUMENT, "unknown option %d", option);

@@ -157,12 +157,6 @@ hipError_t launch_embed(int type, float* out, const unsigned char* table, int to
 hipError_t launch_argmax(int* out, int* out2, const float* x, int n, hipStream_t s);
 
 // ---- token batches (batch.hip) -------------------------------------------
-// Weights of `rows` rows of `cols` columns in format `type` (row_bytes per
-// row) expanded to fp32 [rows][cols] at out: F32 as is, F16 converted, Q8_0
-// q * d, Q4_0 (q - 8) * d, Q6_K d * scale * q.  cols a multiple of 32 (256
-// for Q6_K).
-hipError_t launch_dequant_rows(int type, const unsigned char* w, long long row_bytes, int rows, int cols,
-                               float* out, hipStream_t s);
 hipError_t launch_rmsnorm_rows(float* out, const float* x, const float* w, int n_rows, int size, float eps,
                                hipStream_t s);
 // h rows of [gate | up] (2 n_ff floats): gate = silu(gate) * up in place.
