@@ -1235,13 +1235,16 @@ int ensure_buf(tla_engine* e, void** buf, size_t& have, size_t bytes, const char
 
 // out_s[t][row] (+)= W_s[row] . x[t] as the split product (split_product.hip):
 // x split into three bf16 planes, then one launch over all segments, the
-// weights dequantised in registers.  16-row subtiles per wave: 4 for matrices
-// with enough rows to give every CU a workgroup at that size (F32 weights:
-// 2, for their registers), else 2, else 1.  A grid still short of two
-// workgroups per CU cuts K into ranges of at least 8 blocks (each a
-// workgroup walking its range, the ranges' sums added in order by a second
-// launch): a workgroup's blocks follow one another at a memory round trip
-// each, so fewer blocks per workgroup is what shortens a small product.
+// weights dequantised in registers.  Two 16-row subtiles per wave where
+// that still gives half the CUs a workgroup, else one; then K cut into
+// ranges of at least 8 blocks until the grid holds about 2.5 workgroups per
+// CU (each a workgroup walking its range, the ranges' sums added in order
+// by a second launch).  A workgroup's blocks follow one another at about a
+// memory round trip each, so shorter ranges and more resident workgroups
+// are what shortens a product.  Same box, TinyLlama's four matrices, Q4_0,
+// rows per wave x K ranges swept: at 512 tokens gate | up 129 us (2 x 1)
+// against 174 us with 4 rows per wave, W_down 73 us (2 x 4-6) against 107
+// (1 x 2); at 128 tokens every matrix within 2 us of its best.
 int split_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int total, int cols, const float* x,
                 long long x_stride, int n, int add)
 {
@@ -1258,11 +1261,11 @@ int split_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int
     p.add = add;
     const long long token_tiles = p.n_sub / 4;
     auto groups = [&](int rw) { return (total + 64LL * rw - 1) / (64LL * rw) * token_tiles; };
-    p.rows_per_wave = type != kF32 && groups(4) >= e->n_cu ? 4 : groups(2) >= e->n_cu ? 2 : 1;
+    p.rows_per_wave = 2 * groups(2) >= e->n_cu ? 2 : 1;
     if (e->opt_split_rows > 0) p.rows_per_wave = e->opt_split_rows;
     const int n_blk = cols / 32;
-    const long long g = groups(p.rows_per_wave);
-    int splits = g >= e->n_cu ? 1 : static_cast<int>(std::min<long long>((2LL * e->n_cu + g - 1) / g, n_blk / 8));
+    const long long g = groups(p.rows_per_wave), target = 5LL * e->n_cu / 2;
+    int splits = static_cast<int>(std::min<long long>((target + g - 1) / g, n_blk / 8));
     if (e->opt_split_k > 0) splits = e->opt_split_k;
     splits = std::max(1, std::min(splits, n_blk));
     p.blk_per_split = (n_blk + splits - 1) / splits;
