@@ -242,12 +242,21 @@ __device__ __forceinline__ void decode_w(const WRaw<kType>& w, int kb, int g, bf
         d = half_to_float(__shfl(w.u[0], threadIdx.x & 15) & 0xFFFFu);
         const unsigned q[2] = {h ? w.u[1] : (w.u[0] >> 16) | (w.u[1] << 16),
                                h ? w.u[2] : (w.u[1] >> 16) | (w.u[2] << 16)};
+        // Each byte u (Q4_0: the nibble masked in place; Q8_0: the byte with
+        // its sign bit flipped, q + 128) becomes the float 2^23 + u by one
+        // byte permute into the mantissa of 2^23 (0x4B000000), and one
+        // subtraction leaves u - 8 (Q4_0) or u - 128 = q (Q8_0): two
+        // operations per weight.  Small integers: the bf16 packing is exact.
+        constexpr float kBase = kType == kQ8_0 ? 8388736.f : 8388616.f;  // 2^23 + 128, 2^23 + 8
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const unsigned byte = (q[e >> 2] >> (8 * (e & 3))) & 0xFFu;
-            const int v = kType == kQ8_0 ? static_cast<int>(static_cast<signed char>(byte))
-                                         : static_cast<int>((byte >> ((g >> 1) * 4)) & 0xFu) - 8;
-            b[0][e] = static_cast<__bf16>(static_cast<float>(v));
+        for (int i = 0; i < 2; ++i) {
+            const unsigned m = kType == kQ8_0 ? q[i] ^ 0x80808080u : (q[i] >> ((g >> 1) * 4)) & 0x0F0F0F0Fu;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                // bytes: [m.byte e, 0, 0, 0x4B] (selector 0x0C reads zero)
+                const unsigned f = __builtin_amdgcn_perm(0x4B000000u, m, 0x070C0C00u + e);
+                b[0][4 * i + e] = static_cast<__bf16>(__builtin_bit_cast(float, f) - kBase);
+            }
         }
     }
 }
