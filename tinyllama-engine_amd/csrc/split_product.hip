@@ -261,29 +261,27 @@ __device__ __forceinline__ void decode_w(const WRaw<kType>& w, int kb, int g, bf
     }
 }
 
-// One block's products for one row subtile: acc[s] (+)= over the 4 token
-// subtiles, pieces (b_i, x_p) with i + p <= 2, smallest terms first.
+// One block's products for one (row subtile, token subtile) tile: acc (+)=
+// the products of pieces (b_i, x_p) with i + p <= 2, smallest terms first,
+// scaled by the block scale where there is one.
 template <int kType>
-__device__ __forceinline__ void block_products(const bf16x8 (&a)[kTW][3], const bf16x8 (&b)[Fmt<kType>::kN],
-                                               float d, floatx4 (&acc)[kTW])
+__device__ __forceinline__ void tile_products(const bf16x8 (&a)[3], const bf16x8 (&b)[Fmt<kType>::kN], float d,
+                                              floatx4& acc)
 {
+    floatx4 t = Fmt<kType>::kScaled ? floatx4{0.f, 0.f, 0.f, 0.f} : acc;
+    if constexpr (Fmt<kType>::kN >= 3) t = mfma(a[0], b[2], t);
+    if constexpr (Fmt<kType>::kN >= 2) {
+        t = mfma(a[1], b[1], t);
+        t = mfma(a[0], b[1], t);
+    }
+    t = mfma(a[2], b[0], t);
+    t = mfma(a[1], b[0], t);
+    t = mfma(a[0], b[0], t);
+    if constexpr (Fmt<kType>::kScaled) {
 #pragma unroll
-    for (int s = 0; s < kTW; ++s) {
-        floatx4 t = Fmt<kType>::kScaled ? floatx4{0.f, 0.f, 0.f, 0.f} : acc[s];
-        if constexpr (Fmt<kType>::kN >= 3) t = mfma(a[s][0], b[2], t);
-        if constexpr (Fmt<kType>::kN >= 2) {
-            t = mfma(a[s][1], b[1], t);
-            t = mfma(a[s][0], b[1], t);
-        }
-        t = mfma(a[s][2], b[0], t);
-        t = mfma(a[s][1], b[0], t);
-        t = mfma(a[s][0], b[0], t);
-        if constexpr (Fmt<kType>::kScaled) {
-#pragma unroll
-            for (int q = 0; q < 4; ++q) acc[s][q] = fmaf(d, t[q], acc[s][q]);
-        } else {
-            acc[s] = t;
-        }
+        for (int q = 0; q < 4; ++q) acc[q] = fmaf(d, t[q], acc[q]);
+    } else {
+        acc = t;
     }
 }
 
@@ -317,10 +315,17 @@ __global__ __launch_bounds__(kThreads) void split_product_kernel(const SplitPara
     __shared__ __align__(16) unsigned char s_x[kRing][kStageBytes];
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int j = lane & 15, g = lane >> 4;
-    const int row0 = (blockIdx.x * kWaves + wave) * 16 * kRW;
-    const int s0 = blockIdx.y * kTW;  // first token subtile
+    // Tiles by linear workgroup id L, token tile fastest (y = L mod the
+    // token tiles): workgroups run on XCD L mod 8, so each XCD's workgroups
+    // share a few token tiles' x planes in its L2 (at 512 tokens one XCD one
+    // tile, 0.8 MB) while the weights stream through.
+    const unsigned L = blockIdx.x + gridDim.x * (blockIdx.y + gridDim.y * blockIdx.z);
+    const unsigned ty = L % gridDim.y, rest = L / gridDim.y;
+    const unsigned tx = rest % gridDim.x, tz = rest / gridDim.x;
+    const int row0 = (tx * kWaves + wave) * 16 * kRW;
+    const int s0 = ty * kTW;  // first token subtile
     // K range of this workgroup: blocks [kb_lo, kb_hi) (grid z splits K)
-    const int kb_lo = blockIdx.z * p.blk_per_split;
+    const int kb_lo = tz * p.blk_per_split;
     const int kb_hi = min(kb_lo + p.blk_per_split, p.cols >> 5);
 
     // this lane's weight row in each row subtile (the last row for rows past
@@ -385,18 +390,20 @@ __global__ __launch_bounds__(kThreads) void split_product_kernel(const SplitPara
         load_x(xr_this, kb + 3);
         __syncthreads();
         if (kb < kb_hi) {  // uniform
-            bf16x8 a[kTW][3];
+            // the row subtiles' weights first, then the token subtiles one
+            // at a time (their x pieces read from LDS just before use)
+            bf16x8 b[kRW][Fmt<kType>::kN];
+            float d[kRW];
 #pragma unroll
-            for (int s = 0; s < kTW; ++s)
+            for (int r = 0; r < kRW; ++r) decode_w<kType>(wr_this[r], kb, g, b[r], d[r]);
+#pragma unroll
+            for (int s = 0; s < kTW; ++s) {
+                bf16x8 a[3];
 #pragma unroll
                 for (int pl = 0; pl < 3; ++pl)
-                    a[s][pl] = *reinterpret_cast<const bf16x8*>(&s_x[u][(pl * kTW + s) * 1024 + 16 * lane]);
+                    a[pl] = *reinterpret_cast<const bf16x8*>(&s_x[u][(pl * kTW + s) * 1024 + 16 * lane]);
 #pragma unroll
-            for (int r = 0; r < kRW; ++r) {
-                bf16x8 b[Fmt<kType>::kN];
-                float d;
-                decode_w<kType>(wr_this[r], kb, g, b, d);
-                block_products<kType>(a, b, d, acc[r]);
+                for (int r = 0; r < kRW; ++r) tile_products<kType>(a, b[r], d[r], acc[r][s]);
             }
         }
         load_ws(wr_this, kb + 3);
@@ -415,7 +422,7 @@ __global__ __launch_bounds__(kThreads) void split_product_kernel(const SplitPara
         const int row = row0 + 16 * r + j;
         if (row >= p.total_rows) continue;
         if (p.part) {
-            float* const o = p.part + static_cast<long long>(blockIdx.z) * p.n * p.total_rows + row;
+            float* const o = p.part + static_cast<long long>(tz) * p.n * p.total_rows + row;
 #pragma unroll
             for (int s = 0; s < kTW; ++s)
 #pragma unroll
