@@ -397,13 +397,13 @@ enum tla_read_kind {
 int tla_read_floor(tla_engine* e, const void* src_dev, size_t bytes, int n_workgroups, int load_kind,
                    int depth, float* sink_dev);
 
-/* fp32 MFMA floor: n_workgroups workgroups of 4 waves on the engine's stream,
- * each wave `iters` rounds of 16 v_mfma_f32_32x32x2f32 (2 x 32 x 32 x 2 flops
- * each) on two independent accumulators with operands that change from lane
- * to lane; sink_dev [n_workgroups] floats is never written in practice.  What
- * one launch can execute of fp32 MFMA work in the time it takes -- the bar
- * the prefill attention kernel's rate is set against.  No reference
- * counterpart. */
+/* MFMA floor: n_workgroups workgroups of 4 waves on the engine's stream,
+ * each wave `iters` rounds of 16 v_mfma_f32_32x32x16_bf16 (2 x 32 x 32 x 16
+ * flops each) on two independent accumulators with operands that change from
+ * lane to lane; sink_dev [n_workgroups] floats is never written in practice.
+ * What one launch can execute of bf16 MFMA work in the time it takes -- the
+ * bar the prefill attention kernel's products are set against.  No
+ * reference counterpart. */
 int tla_mfma_floor(tla_engine* e, int n_workgroups, int iters, float* sink_dev);
 
 /* Tuning knobs (0 = automatic). */

@@ -26,6 +26,7 @@
 //   (workgroup i runs on XCD i % 8) to share that XCD's L2, and each XCD
 //   starts the query tiles with the most key tiles first, across all of its
 //   (layer, kv head) pairs, so the last workgroups to start are short ones.
+#include "bf16_split.h"
 #include "lane_math.h"
 #include "rope_math.h"
 #include "tla_internal.h"
@@ -34,16 +35,13 @@ namespace tla {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx8 __attribute__((ext_vector_type(8)));
 
 constexpr int kQTile = 32;
 constexpr int kKTile = 32;
 constexpr int kWavesP = 4;
 constexpr int kXcds = 8;
-
-__device__ __forceinline__ floatx16 mfma32(float a, float b, floatx16 c)
-{
-    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
-}
 
 __global__ __launch_bounds__(256) void prefill_append_kernel(const PrefillParams p)
 {
@@ -96,14 +94,50 @@ __device__ __forceinline__ unsigned div_magic(unsigned n, unsigned m)
 }
 
 constexpr float kRescaleSlack = 8.f;  // log2 units
-constexpr int kRowPad = 68;  // LDS row stride (floats): 64 + 4 keeps operand reads conflict-free
+constexpr int kPlane = 32 * 64 * 2;  // bytes of one bf16 plane of a 32-key tile
 
-__global__ __launch_bounds__(64 * kWavesP) __attribute__((amdgpu_waves_per_eu(3, 3))) void
+// Products of two split operands on v_mfma_f32_32x32x16_bf16: a . b for
+// a = a0 + a1 + a2 and b = b0 + b1 + b2 (bf16 pieces of fp32 values), the
+// six piece products down to 2^-16 of a b, smallest first.  The three left
+// out (a1 b2, a2 b1, a2 b2) are below 2^-24 of a b.
+__device__ __forceinline__ floatx16 split_products(const bf16x8 (&a)[3], const bf16x8 (&b)[3], floatx16 c)
+{
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[2], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[1], b[0], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[1], c, 0, 0, 0);
+    c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[0], b[0], c, 0, 0, 0);
+    return c;
+}
+
+// The three planes of eight fp32 values.
+__device__ __forceinline__ void split8(floatx8 v, bf16x8 (&o)[3])
+{
+    split3x8(v, o[0], o[1], o[2]);
+}
+
+// Row i of a K tile in LDS holds key kperm(i) of the tile (bits 2 and 3 of
+// the index swapped; its own inverse).  Score register r of lane 32 h + j
+// then holds key 16 (r / 8) + 8 h + r % 8 for query j, which is what lane
+// 32 h + j supplies as the B operand (P^T) of the P.V product at k step
+// r / 8, element r % 8: the scores are that operand as they are.
+__device__ __forceinline__ int kperm(int i)
+{
+    return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
+}
+
+__global__ __launch_bounds__(64 * kWavesP) __attribute__((amdgpu_waves_per_eu(2, 2))) void
 prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
 {
-    // K and V tiles of 32 keys, shared by the 4 waves, double-buffered.
-    __shared__ float sk[2][kKTile][kRowPad];
-    __shared__ float sv[2][kKTile][kRowPad];
+    // K and V tiles of 32 keys as three bf16 planes each, shared by the 4
+    // waves, double-buffered.  Each plane is laid out in the order a wave
+    // reads it as an MFMA operand, 1 KiB per read with lane l at 16 l:
+    //   K: byte 512 c + 16 i = dims 8c .. 8c+7 of row i (key kperm(i));
+    //   V: byte 2048 dt + 1024 s + 512 h + 16 i = keys 16s + 8h .. +7 of
+    //      dim 2i + dt.
+    __shared__ __align__(16) unsigned char sk[2][3][kPlane];
+    __shared__ __align__(16) unsigned char sv[2][3][kPlane];
 
     // ---- XCD-aware, heavy-first mapping of workgroups to tiles ----
     // Workgroup b runs on XCD b % 8 and XCDs start their workgroups in order
@@ -111,8 +145,8 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     // tiles of a pair share one L2; within an XCD, query tiles are handed out
     // longest first (most key tiles) across all its pairs.
     // The quotients are multiply-highs on scalar registers: a workgroup that
-    // starts beside two MFMA-bound waves gets few vector issue slots, and
-    // the compiler's divisions go through the vector unit.
+    // starts beside MFMA-bound waves gets few vector issue slots, and the
+    // compiler's divisions go through the vector unit.
     const int xcd = blockIdx.x % kXcds;
     const int slot = blockIdx.x / kXcds;
     const int xcd_pairs = (g.n_pairs - xcd + kXcds - 1) / kXcds;
@@ -135,7 +169,7 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     const int qh = kvh * p.gqa + (computes ? hq : 0);
 
     const int col = lane & 31;  // query row within the tile
-    const int half = lane >> 5; // which 32 of the 64 dims (Q/K) / key sub-block
+    const int half = lane >> 5; // which 8 of each 16 dims (Q, K) / keys (P, V)
     const int i0 = qt * kQTile;
     const int trow = min(i0 + col, p.n_tok - 1);  // clamped token index
     const int qpos = p.pos0 + i0 + col;           // this row's position
@@ -150,44 +184,73 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     const float* kc = p.kc + layer_off;
     const float* vc = p.vc + layer_off;
 
-    // ---- cooperative tile loads: thread -> rows t/16 and t/16 + 16, float4 t%16.
-    // Keys past last_key are clamped to it (masked in the scores, or never
-    // used).  Byte offsets are 32-bit from a uniform base (one layer's cache
-    // slice is < 4 GiB).
-    const int lrow = threadIdx.x >> 4, lc4 = threadIdx.x & 15;
-    auto gload = [&](const float* base, int tile, float4* dst) {
-#pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            const unsigned key = (unsigned)min(tile * kKTile + lrow + 16 * h, last_key);
-            dst[h] = ldg4_at(base, (key * (unsigned)kv_dim + 4u * lc4) * 4u);
-        }
+    // ---- cooperative tile loads.  Keys past last_key are clamped to it
+    // (masked in the scores, or never used).  Byte offsets are 32-bit from a
+    // uniform base (one layer's cache slice is < 4 GiB).
+    //   K: thread t loads dims 8c .. 8c+7 of key kk (c = t / 32, kk = t % 32)
+    //      and writes them to row kperm(kk): a wave's writes are 1 KiB apiece.
+    //   V: thread t loads dim d of keys 8kg .. 8kg+7 (kg = t / 64, the wave;
+    //      d = 2 (t % 32) + (t / 32) % 2), one 256-byte key row per load
+    //      instruction, and writes the 8 keys of dim d as one piece.
+    const int kk = threadIdx.x & 31, kch = threadIdx.x >> 5;
+    const int vkg = threadIdx.x >> 6, vd = 2 * (threadIdx.x & 31) + ((threadIdx.x >> 5) & 1);
+    const unsigned k_lds = 512u * kch + 16u * kperm(kk);
+    const unsigned v_lds = 2048u * (vd & 1) + 1024u * (vkg >> 1) + 512u * (vkg & 1) + 16u * (vd >> 1);
+    auto kload = [&](int tile) {
+        const unsigned key = (unsigned)min(tile * kKTile + kk, last_key);
+        const unsigned off = (key * (unsigned)kv_dim + 8u * kch) * 4u;
+        const float4 a = ldg4_at(kc, off), b = ldg4_at(kc, off + 16u);
+        return floatx8{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
     };
-    auto lstore = [&](float (*buf)[kRowPad], const float4* src) {
+    auto vload = [&](int tile) {
+        floatx8 v;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) *reinterpret_cast<float4*>(&buf[lrow + 16 * h][4 * lc4]) = src[h];
+        for (int e = 0; e < 8; ++e) {
+            const unsigned key = (unsigned)min(tile * kKTile + 8 * vkg + e, last_key);
+            v[e] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(vc) +
+                                                   (key * (unsigned)kv_dim + (unsigned)vd) * 4u);
+        }
+        return v;
+    };
+    auto lstore = [&](unsigned char (*planes)[kPlane], unsigned off, floatx8 src) {
+        bf16x8 pc[3];
+        split8(src, pc);
+#pragma unroll
+        for (int q = 0; q < 3; ++q) *reinterpret_cast<bf16x8*>(&planes[q][off]) = pc[q];
     };
 
-    // ---- Q^T operand: lane holds q[row][32*half + s] * scale * log2(e) ----
-    float4 qv[8];
+    // ---- Q^T operand: lane 32 h + j holds, for k step s, dims 16s + 8h ..
+    // +7 of query j, times scale * log2(e), as three bf16 planes ----
+    bf16x8 qp[4][3];
     {
-        const float* qrow = p.q + (((long long)lb * p.n_tok + trow) * p.n_head + qh) * kHeadDim + 32 * half;
-        const float* tab = reinterpret_cast<const float*>(p.rope + (long long)(p.pos0 + trow) * kPairs);
+        const float* qrow = p.q + (((long long)lb * p.n_tok + trow) * p.n_head + qh) * kHeadDim + 8 * half;
+        const float* tab = reinterpret_cast<const float*>(p.rope + (long long)(p.pos0 + trow) * kPairs) + 8 * half;
         // All sixteen loads are issued before any is used.
-        float4 cs[8];
+        float4 qv[8], cs[8];
 #pragma unroll
         for (int f = 0; f < 8; ++f) {
-            qv[f] = ldg4(qrow + 4 * f);
-            cs[f] = ldg4(tab + 2 * (16 * half + 2 * f));
+            qv[f] = ldg4(qrow + 16 * (f >> 1) + 4 * (f & 1));
+            cs[f] = ldg4(tab + 16 * (f >> 1) + 4 * (f & 1));  // (cos, sin) pairs of those dims
         }
         // Scaled first, then rotated with fused multiply-adds: q only enters
         // the scores, so it needs the reference's accuracy, not its bits (the
         // cache rows, which must match bit for bit, are rotated by the append
-        // kernel), and the new wave does this with few vector issue slots.
+        // kernel).
 #pragma unroll
-        for (int f = 0; f < 8; ++f) {
-            const float4 x = make_float4(qv[f].x * p.scale_log2, qv[f].y * p.scale_log2,
-                                         qv[f].z * p.scale_log2, qv[f].w * p.scale_log2);
-            qv[f] = p.rotate ? rotate4_fma(x, cs[f]) : x;
+        for (int s = 0; s < 4; ++s) {
+            floatx8 v;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const float4 x0 = qv[2 * s + h2];
+                const float4 x = make_float4(x0.x * p.scale_log2, x0.y * p.scale_log2, x0.z * p.scale_log2,
+                                             x0.w * p.scale_log2);
+                const float4 r = p.rotate ? rotate4_fma(x, cs[2 * s + h2]) : x;
+                v[4 * h2 + 0] = r.x;
+                v[4 * h2 + 1] = r.y;
+                v[4 * h2 + 2] = r.z;
+                v[4 * h2 + 3] = r.w;
+            }
+            split8(v, qp[s]);
         }
     }
 
@@ -197,20 +260,16 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     float m_run = -INFINITY;
     float l_run = 0.f;
 
-    // S^T = K.Q^T for the tile in K buffer b (K operand: lane holds
-    // K[col][32*half + s]).  s[gi] = S[query col][key 8*(gi/4) + 4*half + gi%4].
-    auto scores = [&](int b) {
-        const float* krow = &sk[b][col][32 * half];
-        floatx16 s;
+    // S^T = K.Q^T for the tile in K buffer kb: s[r] = S[query col][key
+    // 16 (r / 8) + 8 half + r % 8 of the tile].
+    auto scores = [&](const unsigned char (*kb)[kPlane]) {
+        floatx16 s = {};
 #pragma unroll
-        for (int i = 0; i < 16; ++i) s[i] = 0.f;
+        for (int ks = 0; ks < 4; ++ks) {
+            bf16x8 a[3];
 #pragma unroll
-        for (int f = 0; f < 8; ++f) {
-            const float4 kk = *reinterpret_cast<const float4*>(krow + 4 * f);
-            s = mfma32(kk.x, qv[f].x, s);
-            s = mfma32(kk.y, qv[f].y, s);
-            s = mfma32(kk.z, qv[f].z, s);
-            s = mfma32(kk.w, qv[f].w, s);
+            for (int q = 0; q < 3; ++q) a[q] = *reinterpret_cast<const bf16x8*>(&kb[q][1024 * ks + 16 * lane]);
+            s = split_products(a, qp[ks], s);
         }
         return s;
     };
@@ -218,14 +277,14 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     auto softmax = [&](floatx16& s, int j0, bool masked) {
         if (masked) {
 #pragma unroll
-            for (int gi = 0; gi < 16; ++gi) {
-                const int key = j0 + 8 * (gi >> 2) + 4 * half + (gi & 3);
-                s[gi] = (key <= qpos && key <= last_key) ? s[gi] : -INFINITY;
+            for (int r = 0; r < 16; ++r) {
+                const int key = j0 + 16 * (r >> 3) + 8 * half + (r & 7);
+                s[r] = (key <= qpos && key <= last_key) ? s[r] : -INFINITY;
             }
         }
         float mx = s[0];
 #pragma unroll
-        for (int gi = 1; gi < 16; ++gi) mx = fmaxf(mx, s[gi]);
+        for (int r = 1; r < 16; ++r) mx = fmaxf(mx, s[r]);
         mx = max_xor32(mx);  // the other half of the keys
         // The running max only moves when some row's tile max exceeds it by
         // more than 2^8: probabilities then stay <= 256 and the sums in fp32
@@ -241,42 +300,31 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
         }
         float lsum = 0.f;
 #pragma unroll
-        for (int gi = 0; gi < 16; ++gi) {
-            s[gi] = __builtin_amdgcn_exp2f(s[gi] - m_run);
-            lsum += s[gi];
+        for (int r = 0; r < 16; ++r) {
+            s[r] = __builtin_amdgcn_exp2f(s[r] - m_run);
+            lsum += s[r];
         }
         l_run += lsum;
     };
-    // O^T += V^T.P^T for the tile in V buffer b (V operand: lane holds
-    // V[8*(gi/4) + 4*half + gi%4][2*col + dt]).  The operands come in four
-    // groups of four gi, two groups in registers: the first two are read at
-    // the top of the step (vread_head, before the next tile's scores and this
-    // tile's softmax), each later one while the group before it is in the
-    // MFMAs, so no MFMA pair waits on an LDS round trip.  The scheduling
-    // barriers keep the compiler from sinking the reads to their uses.
-    float2 vv[2][4];
-    auto vread = [&](int b, int g, float2* dst) {
+    // O^T += V^T.P^T for the tile in V buffer vb: o_dt[r] accumulates dim
+    // 2 (8 (r / 4) + 4 half + r % 4) + dt of query col.  P^T at k step ks is
+    // s[8 ks .. 8 ks + 7], split into planes just before its products.
+    auto accumulate = [&](const floatx16& s, const unsigned char (*vb)[kPlane]) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-            dst[i] = *reinterpret_cast<const float2*>(&sv[b][8 * g + 4 * half + i][2 * col]);
-    };
-    auto vread_head = [&](int b) {
-        vread(b, 0, vv[0]);
-        vread(b, 1, vv[1]);
-        __builtin_amdgcn_sched_barrier(0);
-    };
-    auto accumulate = [&](const floatx16& s, int b) {
+        for (int ks = 0; ks < 2; ++ks) {
+            floatx8 pv;
 #pragma unroll
-        for (int g = 0; g < 4; ++g) {
+            for (int e = 0; e < 8; ++e) pv[e] = s[8 * ks + e];
+            bf16x8 pp[3];
+            split8(pv, pp);
+            bf16x8 a0[3], a1[3];
 #pragma unroll
-            for (int i = 0; i < 4; ++i) {
-                o0 = mfma32(vv[g & 1][i].x, s[4 * g + i], o0);
-                o1 = mfma32(vv[g & 1][i].y, s[4 * g + i], o1);
+            for (int q = 0; q < 3; ++q) {
+                a0[q] = *reinterpret_cast<const bf16x8*>(&vb[q][1024 * ks + 16 * lane]);
+                a1[q] = *reinterpret_cast<const bf16x8*>(&vb[q][2048 + 1024 * ks + 16 * lane]);
             }
-            if (g + 2 < 4) {
-                vread(b, g + 2, vv[g & 1]);
-                __builtin_amdgcn_sched_barrier(0);
-            }
+            o0 = split_products(a0, pp, o0);
+            o1 = split_products(a1, pp, o1);
         }
     };
 
@@ -285,50 +333,46 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     // At the start of step j the LDS holds K[j+1] and V[j]; the step stores
     // K[j+2] and V[j+1], loaded from global memory one step earlier, into the
     // buffers of K[j] and V[j-1], and issues the loads of K[j+3] and V[j+2].
-    float4 ld_k[2], ld_v[2];
-    gload(kc, 0, ld_k);
-    gload(vc, 0, ld_v);
-    lstore(sk[0], ld_k);
-    lstore(sv[0], ld_v);
-    gload(kc, 1, ld_k);
-    gload(vc, 1, ld_v);
-    lstore(sk[1], ld_k);
-    gload(kc, 2, ld_k);
+    floatx8 ld_k = kload(0), ld_v = vload(0);
+    lstore(sk[0], k_lds, ld_k);
+    lstore(sv[0], v_lds, ld_v);
+    ld_k = kload(1);
+    ld_v = vload(1);
+    lstore(sk[1], k_lds, ld_k);
+    ld_k = kload(2);
     __syncthreads();
     floatx16 s_cur;
-    if (computes) s_cur = scores(0);
+    if (computes) s_cur = scores(sk[0]);
     __syncthreads();  // K[0]'s buffer is overwritten in step 0
 
     int j = 0;
     for (; j < n_plain; ++j) {
         if (computes) {
-            vread_head(j & 1);
-            const floatx16 s_next = scores((j + 1) & 1);
+            const floatx16 s_next = scores(sk[(j + 1) & 1]);
             softmax(s_cur, j * kKTile, false);
-            accumulate(s_cur, j & 1);
+            accumulate(s_cur, sv[j & 1]);
             s_cur = s_next;
         }
-        lstore(sk[j & 1], ld_k);
-        lstore(sv[(j + 1) & 1], ld_v);
-        gload(kc, j + 3, ld_k);
-        gload(vc, j + 2, ld_v);
+        lstore(sk[j & 1], k_lds, ld_k);
+        lstore(sv[(j + 1) & 1], v_lds, ld_v);
+        ld_k = kload(j + 3);
+        ld_v = vload(j + 2);
         __syncthreads();
     }
     for (; j < n_kt; ++j) {  // at most two tiles reach the diagonal
         const bool more = j + 1 < n_kt;  // uniform
         if (computes) {
             floatx16 s_next = {};  // unused after the last tile
-            vread_head(j & 1);
-            if (more) s_next = scores((j + 1) & 1);
+            if (more) s_next = scores(sk[(j + 1) & 1]);
             softmax(s_cur, j * kKTile, true);
-            accumulate(s_cur, j & 1);
+            accumulate(s_cur, sv[j & 1]);
             s_cur = s_next;
         }
         if (more) {
-            lstore(sk[j & 1], ld_k);
-            lstore(sv[(j + 1) & 1], ld_v);
-            gload(kc, j + 3, ld_k);
-            gload(vc, j + 2, ld_v);
+            lstore(sk[j & 1], k_lds, ld_k);
+            lstore(sv[(j + 1) & 1], v_lds, ld_v);
+            ld_k = kload(j + 3);
+            ld_v = vload(j + 2);
             __syncthreads();
         }
     }

@@ -165,33 +165,35 @@ __global__ __launch_bounds__(256) void read_floor_kernel(const float4* __restric
     if (acc == -1234.5f) sink[blockIdx.x] = acc;
 }
 
-// fp32 MFMA floor: each wave runs `iters` rounds of 16 v_mfma_f32_32x32x2f32
+// MFMA floor: each wave runs `iters` rounds of 16 v_mfma_f32_32x32x16_bf16
 // on two independent accumulators, operands pseudo-random per lane (so the
 // matrix cores see real bit patterns), and writes its sum only if it equals a
 // value no sum of these operands takes, so that the work stays but nothing is
-// written.  The fastest a single launch can execute a given number of fp32
-// MFMA flops: 2 x 32 x 32 x 2 per instruction.
+// written.  The fastest a single launch can execute a given number of bf16
+// MFMA flops: 2 x 32 x 32 x 16 per instruction, the instruction the prefill
+// attention kernel's products run on.
 typedef float floatx16_t __attribute__((ext_vector_type(16)));
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 
 __global__ __launch_bounds__(256) void mfma_floor_kernel(int iters, float* __restrict__ sink)
 {
-    floatx16_t c0, c1;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { c0[i] = 0.f; c1[i] = 0.f; }
-    float r[16];
+    floatx16_t c0 = {}, c1 = {};
+    bf16x8_t r[4];
     unsigned h = threadIdx.x * 2654435761u + blockIdx.x * 40503u + 12345u;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        h ^= h << 13;
-        h ^= h >> 17;
-        h ^= h << 5;
-        r[i] = (float)(int)(h & 0xffffff) * (1.0f / 8388608.0f) - 1.0f;
-    }
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            h ^= h << 13;
+            h ^= h >> 17;
+            h ^= h << 5;
+            r[i][e] = static_cast<__bf16>((float)(int)(h & 0xffffff) * (1.0f / 8388608.0f) - 1.0f);
+        }
     for (int it = 0; it < iters; ++it) {
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            c0 = __builtin_amdgcn_mfma_f32_32x32x2f32(r[(2 * u) & 15], r[(2 * u + 7) & 15], c0, 0, 0, 0);
-            c1 = __builtin_amdgcn_mfma_f32_32x32x2f32(r[(2 * u + 1) & 15], r[(2 * u + 8) & 15], c1, 0, 0, 0);
+            c0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r[u & 3], r[(u + 1) & 3], c0, 0, 0, 0);
+            c1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(r[(u + 2) & 3], r[(u + 3) & 3], c1, 0, 0, 0);
         }
     }
     float acc = 0.f;

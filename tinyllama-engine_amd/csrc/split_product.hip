@@ -43,6 +43,7 @@
 // Every output is one wave's sum in a fixed order: the same bits on every
 // run and for any grid.
 #include "batch.h"
+#include "bf16_split.h"
 
 namespace tla {
 namespace {
@@ -67,23 +68,6 @@ __device__ __forceinline__ floatx4 mfma(bf16x8 a, bf16x8 b, floatx4 c)
 __device__ __forceinline__ float half_to_float(unsigned h)
 {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(h)));
-}
-
-// v = v0 + v1 + v2 exactly, each a bf16 (round to nearest even at each
-// step; v - v0 has at most 16 significant bits, v - v0 - v1 at most 8).
-__device__ __forceinline__ void split3(float v, __bf16& v0, __bf16& v1, __bf16& v2)
-{
-    v0 = static_cast<__bf16>(v);
-    const float r1 = v - static_cast<float>(v0);
-    v1 = static_cast<__bf16>(r1);
-    v2 = static_cast<__bf16>(r1 - static_cast<float>(v1));
-}
-// v = v0 + v1 exactly for v of at most 16 significant bits (F16 weights,
-// Q6_K's sc * q).
-__device__ __forceinline__ void split2(float v, __bf16& v0, __bf16& v1)
-{
-    v0 = static_cast<__bf16>(v);
-    v1 = static_cast<__bf16>(v - static_cast<float>(v0));
 }
 
 // Byte offset of plane p of block kb, token subtile s, in the split x.
