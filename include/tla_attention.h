@@ -195,7 +195,11 @@ int tla_decode_noalloc(tla_engine* e, int n_seq, const int* pos_host, int layer0
  * attends to positions 0 .. pos0+t.  With TLA_ROTATE, q and k are rotated in
  * the kernel at their own positions.
  *   q_dev/out_dev [n_step_layers][n_tok][n_head][head_dim]
- *   k/v_dev       [n_step_layers][n_tok][n_head_kv][head_dim] */
+ *   k/v_dev       [n_step_layers][n_tok][n_head_kv][head_dim]
+ * Engine memory it keeps for later calls: the keys and values of positions
+ * 0 .. pos0+n_tok-1 as bf16 planes, n_step_layers x n_head_kv x
+ * ceil((pos0 + n_tok) / 32) x 24 KiB, grown (after a stream synchronize) when
+ * a call needs more. */
 int tla_prefill(tla_engine* e, int pos0, int n_tok, int layer0, int n_step_layers, int flags,
                 float* out_dev, const float* q_dev, const float* k_dev, const float* v_dev,
                 float* key_cache_dev, float* value_cache_dev);

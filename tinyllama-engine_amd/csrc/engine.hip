@@ -128,6 +128,8 @@ struct tla_engine {
     size_t xs_bytes = 0;
     float* part = nullptr;        // and their K splits' partial sums
     size_t part_bytes = 0;
+    unsigned char* kvp = nullptr; // prefill: K and V tiles as bf16 planes
+    size_t kvp_bytes = 0;
     int* argmax_slot = nullptr;
     long long opt_split = 0;
     int opt_plan = TLA_PLAN_AUTO;
@@ -428,6 +430,7 @@ int tla_engine_destroy(tla_engine* e)
     if (e->fwd) (void)hipFree(e->fwd);
     if (e->xs) (void)hipFree(e->xs);
     if (e->part) (void)hipFree(e->part);
+    if (e->kvp) (void)hipFree(e->kvp);
     if (e->argmax_slot) (void)hipFree(e->argmax_slot);
     if (e->rope) (void)hipFree(e->rope);
     if (e->stream) (void)hipStreamDestroy(e->stream);
@@ -951,6 +954,27 @@ int tla_rope_attention_host(tla_engine* e, float* out_host, const float* qkv_hos
     return ok();
 }
 
+namespace {
+
+// Grows a workspace to `bytes` (after the stream's queued work, which may
+// still read it).
+int ensure_buf(tla_engine* e, void** buf, size_t& have, size_t bytes, const char* what)
+{
+    if (bytes <= have) return TLA_OK;
+    TLA_HIP(hipStreamSynchronize(e->stream));
+    if (*buf) TLA_HIP(hipFree(*buf));
+    *buf = nullptr;
+    have = 0;
+    const hipError_t err = hipMalloc(buf, bytes);
+    if (err != hipSuccess)
+        return fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE, "%s (%zu bytes): %s",
+                    what, bytes, hipGetErrorString(err));
+    have = bytes;
+    return TLA_OK;
+}
+
+}  // namespace
+
 int tla_prefill(tla_engine* e, int pos0, int n_tok, int layer0, int n_step_layers, int flags,
                 float* out_dev, const float* q_dev, const float* k_dev, const float* v_dev,
                 float* key_cache_dev, float* value_cache_dev)
@@ -987,6 +1011,11 @@ int tla_prefill(tla_engine* e, int pos0, int n_tok, int layer0, int n_step_layer
     p.gqa = e->gqa;
     p.rotate = (flags & TLA_ROTATE) ? 1 : 0;
     p.scale_log2 = scale_log2(e->head_dim);
+    p.n_ptiles = (pos0 + n_tok + 31) / 32;
+    if (int rc = ensure_buf(e, reinterpret_cast<void**>(&e->kvp), e->kvp_bytes,
+                            prefill_planes_bytes(n_step_layers, c.n_head_kv, pos0, n_tok), "prefill K/V planes"))
+        return rc;
+    p.kvp = e->kvp;
     if (int rc = launch(e, TLA_KERNEL_APPEND, "prefill append",
                         [&] { return launch_prefill_append(p, e->stream); }))
         return rc;
@@ -1215,23 +1244,6 @@ int gemv_rows(tla_engine* e, int type, const void* w, float* out, int rows, int 
 // take the split product below; shorter ones the multi-vector GEMV (weights
 // read once per group of up to 8 tokens).
 constexpr int kBatchMinTokens = 16;
-
-// Grows a workspace of the split product to `bytes` (after the stream's
-// queued work, which may still read it).
-int ensure_buf(tla_engine* e, void** buf, size_t& have, size_t bytes, const char* what)
-{
-    if (bytes <= have) return TLA_OK;
-    TLA_HIP(hipStreamSynchronize(e->stream));
-    if (*buf) TLA_HIP(hipFree(*buf));
-    *buf = nullptr;
-    have = 0;
-    const hipError_t err = hipMalloc(buf, bytes);
-    if (err != hipSuccess)
-        return fail(err == hipErrorOutOfMemory ? TLA_ERR_OUT_OF_MEMORY : TLA_ERR_DEVICE, "%s (%zu bytes): %s",
-                    what, bytes, hipGetErrorString(err));
-    have = bytes;
-    return TLA_OK;
-}
 
 // out_s[t][row] (+)= W_s[row] . x[t] as the split product (split_product.hip):
 // x split into three bf16 planes, then one launch over all segments, the

@@ -1,4 +1,5 @@
-// Causal prefill attention for gfx950 (fp32 MFMA, fp32 accumulation).
+// Causal prefill attention for gfx950: products on the bf16 matrix cores
+// with fp32 accuracy, fp32 accumulation.
 //
 // Reference semantics: the prompt is fed token by token (src/generate.cpp:
 // 56-59); for the attention block that is, for t = 0..n_tok-1 at position
@@ -8,18 +9,30 @@
 // 0..P, the whole prompt is one causal (lower-triangular) attention over
 // the cache after all appends -- which is what these kernels compute.
 //
-// prefill_append_kernel: rotates every k row (when asked) and writes k and v
-//   rows to the cache.  Bit-exact with the reference's append.
+// Exact splitting.  Every fp32 operand (q, k, v and the probabilities P) is
+// the sum of three bf16 pieces, x = x0 + x1 + x2 (bf16_split.h); a product
+// of two pieces is exact in fp32, so a . b is computed as the six piece
+// products down to 2^-16 of a b (a0b0, a0b1, a1b0, a0b2, a1b1, a2b0) on
+// v_mfma_f32_32x32x16_bf16, whose rate is 16 times that of fp32 MFMA.  The
+// three left out are below 2^-24 of a b: the reference's accuracy, not its
+// bits.
+//
+// prefill_append_kernel: one workgroup per (layer, kv head, 32-key tile):
+//   rotates the prompt's k rows (when asked) and writes k and v rows to the
+//   cache, bit-exact with the reference's append, and writes every key of
+//   the tile (earlier ones read back from the cache) as K and V planes in
+//   the layout the attention kernel's MFMA operands are read in.
 //
 // prefill_attention_kernel: one workgroup = 4 waves = 4 q heads of one kv
 //   head, over one tile of 32 query tokens.  Each wave:
-//     S^T[32 keys][32 queries] = K[32][64] . Q^T[64][32]   32 x mfma_f32_32x32x2f32
+//     S^T[32 keys][32 queries] = K[32][64] . Q^T[64][32]   24 MFMAs
 //     causal mask, online softmax per query row (the running max moves
 //       only when it grows by more than 2^8, so most tiles skip rescaling O)
-//     O^T[64 d][32 queries]   += V^T[64][32] . P^T[32][32] 32 x mfma_f32_32x32x2f32
-//   The S accumulator layout (lane l: query l%32, keys 8*(g/4)+4*(l/32)+g%4)
-//   is the B operand of the P.V product as is, so P never leaves registers.
-//   Q (rotated in registers with the host-built table) is loaded once.
+//     O^T[64 d][32 queries]   += V^T[64][32] . P^T[32][32] 24 MFMAs
+//   The S accumulator layout is the B operand of the P.V product as is (K
+//   rows are stored permuted, kperm), so P never leaves registers.  Q
+//   (rotated in registers with the host-built table) is split once.  Tiles
+//   come from the planes into LDS with direct global-to-LDS loads.
 //
 // Scheduling: key/value tiles of one (layer, kv head) are read by all its
 //   query tiles and q heads, so those workgroups are placed on one XCD
@@ -35,34 +48,111 @@ namespace tla {
 namespace {
 
 typedef float floatx16 __attribute__((ext_vector_type(16)));
-typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float floatx8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 
 constexpr int kQTile = 32;
 constexpr int kKTile = 32;
 constexpr int kWavesP = 4;
 constexpr int kXcds = 8;
 
+// Planes of one 32-key tile, K then V, three bf16 planes each, each plane
+// in the order the attention kernel's waves read it as an MFMA operand
+// (1 KiB per read, lane l at byte 16 l):
+//   K plane: byte 512 c + 16 i = dims 8c .. 8c+7 of key kperm(i);
+//   V plane: byte 2048 dt + 1024 s + 512 h + 16 i = keys 16s + 8h .. +7
+//            of dim 2i + dt.
+constexpr int kPlane = kKTile * kHeadDim * 2;  // bytes of one bf16 plane of a tile
+constexpr int kHalfTile = 3 * kPlane;          // K (or V) of a tile: 12 KiB
+constexpr int kTileBytes = 2 * kHalfTile;
+
+// Row i of a K tile holds key kperm(i) of the tile (bits 2 and 3 of the
+// index swapped; its own inverse).  Score register r of lane 32 h + j then
+// holds key 16 (r / 8) + 8 h + r % 8 for query j, which is what lane 32 h +
+// j supplies as the B operand (P^T) of the P.V product at k step r / 8,
+// element r % 8.
+__device__ __forceinline__ int kperm(int i)
+{
+    return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
+}
+
+// The three planes of eight fp32 values.
+__device__ __forceinline__ void split8(floatx8 v, bf16x8 (&o)[3])
+{
+    split3x8(v, o[0], o[1], o[2]);
+}
+
+// One workgroup per (layer, kv head, 32-key tile) of positions 0 ..
+// pos0+n_tok-1, tile fastest.  Keys from pos0 on are the prompt's; earlier
+// keys are read from the cache; keys past the last position are zeros.
+//   K: thread t holds dims 8c .. 8c+7 of key kk (c = t / 32, kk = t % 32);
+//   V: thread t holds dim d of keys 8kg .. 8kg+7 (kg = t / 64, d = 2 (t % 32)
+//      + (t / 32) % 2), so each of its plane pieces is one 16-byte store and
+//      each wave's cache store instruction one 256-byte key row.
 __global__ __launch_bounds__(256) void prefill_append_kernel(const PrefillParams p)
 {
-    const long long gid = (long long)blockIdx.x * 256 + threadIdx.x;
-    const int c4 = (int)(gid & 15);  // float4 within the 64-float row
-    const long long row = gid >> 4;  // (lb, t, kvh)
-    const long long n_rows = (long long)p.n_lb * p.n_tok * p.n_head_kv;
-    if (row >= n_rows) return;
-    const int kvh = (int)(row % p.n_head_kv);
-    const long long lt = row / p.n_head_kv;
-    const int t = (int)(lt % p.n_tok);
-    const int lb = (int)(lt / p.n_tok);
-    const int pos = p.pos0 + t;
-    const float* tab = reinterpret_cast<const float*>(p.rope + (long long)pos * kPairs);
-    const float4 k_in = ldg4(p.k + row * kHeadDim + 4 * c4);
-    const float4 cs = ldg4(tab + 4 * c4);  // loaded either way: no branch before the loads
-    const float4 kx = p.rotate ? rotate4(k_in, cs) : k_in;
-    const long long dst = (long long)(p.layer0 + lb) * p.layer_stride +
-                          ((long long)pos * p.n_head_kv + kvh) * kHeadDim + 4 * c4;
-    stg4(p.kc + dst, kx);
-    stg4(p.vc + dst, ldg4(p.v + row * kHeadDim + 4 * c4));
+    const int tile = (int)(blockIdx.x % (unsigned)p.n_ptiles);
+    const int pair = (int)(blockIdx.x / (unsigned)p.n_ptiles);  // lb * n_head_kv + kvh
+    const int kvh = pair % p.n_head_kv, lb = pair / p.n_head_kv;
+    const int n_pos = p.pos0 + p.n_tok;
+    const int kv_dim = p.n_head_kv * kHeadDim;
+    const long long layer_off = (long long)(p.layer0 + lb) * p.layer_stride + (long long)kvh * kHeadDim;
+    float* const kc = p.kc + layer_off;
+    float* const vc = p.vc + layer_off;
+    unsigned char* const planes = p.kvp + ((long long)pair * p.n_ptiles + tile) * kTileBytes;
+
+    // Every load is issued before the first store (one memory round trip).
+    const int kk = threadIdx.x & 31, c = threadIdx.x >> 5;
+    const int kkey = tile * kKTile + kk;
+    const bool k_new = kkey >= p.pos0 && kkey < n_pos;
+    float* const kdst = kc + (long long)kkey * kv_dim + 8 * c;
+    float4 ka = make_float4(0.f, 0.f, 0.f, 0.f), kb = ka, ca = ka, cb = ka;
+    if (k_new) {
+        const float* src = p.k + (((long long)lb * p.n_tok + (kkey - p.pos0)) * p.n_head_kv + kvh) * kHeadDim + 8 * c;
+        const float* tab = reinterpret_cast<const float*>(p.rope + (long long)kkey * kPairs) + 8 * c;
+        ka = ldg4(src);
+        kb = ldg4(src + 4);
+        ca = ldg4(tab);
+        cb = ldg4(tab + 4);
+    } else if (kkey < n_pos) {
+        ka = ldg4(kdst);
+        kb = ldg4(kdst + 4);
+    }
+    const int kg = threadIdx.x >> 6, d = 2 * (threadIdx.x & 31) + ((threadIdx.x >> 5) & 1);
+    floatx8 vx;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int key = tile * kKTile + 8 * kg + e;
+        float val = 0.f;
+        if (key >= p.pos0 && key < n_pos)
+            val = p.v[(((long long)lb * p.n_tok + (key - p.pos0)) * p.n_head_kv + kvh) * kHeadDim + d];
+        else if (key < n_pos)
+            val = vc[(long long)key * kv_dim + d];
+        vx[e] = val;
+    }
+
+    if (k_new) {
+        if (p.rotate) {
+            ka = rotate4(ka, ca);
+            kb = rotate4(kb, cb);
+        }
+        stg4(kdst, ka);
+        stg4(kdst + 4, kb);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int key = tile * kKTile + 8 * kg + e;
+        if (key >= p.pos0 && key < n_pos) vc[(long long)key * kv_dim + d] = vx[e];
+    }
+    bf16x8 pc[3];
+    split8(floatx8{ka.x, ka.y, ka.z, ka.w, kb.x, kb.y, kb.z, kb.w}, pc);
+#pragma unroll
+    for (int q = 0; q < 3; ++q) *reinterpret_cast<bf16x8*>(planes + q * kPlane + 512 * c + 16 * kperm(kk)) = pc[q];
+    split8(vx, pc);
+#pragma unroll
+    for (int q = 0; q < 3; ++q)
+        *reinterpret_cast<bf16x8*>(planes + kHalfTile + q * kPlane + 2048 * (d & 1) + 1024 * (kg >> 1) +
+                                   512 * (kg & 1) + 16 * (d >> 1)) = pc[q];
 }
 
 struct PrefillGrid {
@@ -94,12 +184,10 @@ __device__ __forceinline__ unsigned div_magic(unsigned n, unsigned m)
 }
 
 constexpr float kRescaleSlack = 8.f;  // log2 units
-constexpr int kPlane = 32 * 64 * 2;  // bytes of one bf16 plane of a 32-key tile
 
 // Products of two split operands on v_mfma_f32_32x32x16_bf16: a . b for
-// a = a0 + a1 + a2 and b = b0 + b1 + b2 (bf16 pieces of fp32 values), the
-// six piece products down to 2^-16 of a b, smallest first.  The three left
-// out (a1 b2, a2 b1, a2 b2) are below 2^-24 of a b.
+// a = a0 + a1 + a2 and b = b0 + b1 + b2, the six piece products down to
+// 2^-16 of a b, smallest first.
 __device__ __forceinline__ floatx16 split_products(const bf16x8 (&a)[3], const bf16x8 (&b)[3], floatx16 c)
 {
     c = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a[2], b[0], c, 0, 0, 0);
@@ -111,33 +199,29 @@ __device__ __forceinline__ floatx16 split_products(const bf16x8 (&a)[3], const b
     return c;
 }
 
-// The three planes of eight fp32 values.
-__device__ __forceinline__ void split8(floatx8 v, bf16x8 (&o)[3])
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef __attribute__((address_space(1))) void* global_ptr;
+
+// Copies half a tile (12 KiB, K or V) from the planes into LDS: 12 chunks
+// of 1 KiB, 3 per wave, each one direct global-to-LDS load of 16 bytes per
+// lane (lane l's bytes land at byte 16 l of the chunk).
+__device__ __forceinline__ void copy_half(const unsigned char* src, unsigned char* dst, int wave, int lane)
 {
-    split3x8(v, o[0], o[1], o[2]);
+#pragma unroll
+    for (int c = 0; c < 3; ++c) {
+        const int chunk = 3 * wave + c;
+        __builtin_amdgcn_global_load_lds((global_ptr)(src + 1024 * chunk + 16 * lane), (lds_ptr)(dst + 1024 * chunk),
+                                         16, 0, 0);
+    }
 }
 
-// Row i of a K tile in LDS holds key kperm(i) of the tile (bits 2 and 3 of
-// the index swapped; its own inverse).  Score register r of lane 32 h + j
-// then holds key 16 (r / 8) + 8 h + r % 8 for query j, which is what lane
-// 32 h + j supplies as the B operand (P^T) of the P.V product at k step
-// r / 8, element r % 8: the scores are that operand as they are.
-__device__ __forceinline__ int kperm(int i)
-{
-    return (i & ~12) | ((i & 4) << 1) | ((i & 8) >> 1);
-}
-
-__global__ __launch_bounds__(64 * kWavesP) __attribute__((amdgpu_waves_per_eu(2, 2))) void
+__global__ __launch_bounds__(64 * kWavesP) __attribute__((amdgpu_waves_per_eu(3, 3))) void
 prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
 {
-    // K and V tiles of 32 keys as three bf16 planes each, shared by the 4
-    // waves, double-buffered.  Each plane is laid out in the order a wave
-    // reads it as an MFMA operand, 1 KiB per read with lane l at 16 l:
-    //   K: byte 512 c + 16 i = dims 8c .. 8c+7 of row i (key kperm(i));
-    //   V: byte 2048 dt + 1024 s + 512 h + 16 i = keys 16s + 8h .. +7 of
-    //      dim 2i + dt.
-    __shared__ __align__(16) unsigned char sk[2][3][kPlane];
-    __shared__ __align__(16) unsigned char sv[2][3][kPlane];
+    // K and V tiles (three bf16 planes each, the planes' layout), shared by
+    // the 4 waves, double-buffered.
+    __shared__ __align__(16) unsigned char sk[2][kHalfTile];
+    __shared__ __align__(16) unsigned char sv[2][kHalfTile];
 
     // ---- XCD-aware, heavy-first mapping of workgroups to tiles ----
     // Workgroup b runs on XCD b % 8 and XCDs start their workgroups in order
@@ -165,7 +249,7 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
     const int lane = threadIdx.x & 63;
     const int hq = hg * kWavesP + wave;
-    const bool computes = hq < p.gqa;  // uniform per wave; others only load tiles
+    const bool computes = hq < p.gqa;  // uniform per wave; others only copy tiles
     const int qh = kvh * p.gqa + (computes ? hq : 0);
 
     const int col = lane & 31;  // query row within the tile
@@ -179,44 +263,14 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     // position: no key in them is masked for any row.
     const int n_plain = min((p.pos0 + i0 + 1) / kKTile, n_kt - 1);
 
-    const int kv_dim = p.n_head_kv * kHeadDim;
-    const long long layer_off = (long long)(p.layer0 + lb) * p.layer_stride + (long long)kvh * kHeadDim;
-    const float* kc = p.kc + layer_off;
-    const float* vc = p.vc + layer_off;
-
-    // ---- cooperative tile loads.  Keys past last_key are clamped to it
-    // (masked in the scores, or never used).  Byte offsets are 32-bit from a
-    // uniform base (one layer's cache slice is < 4 GiB).
-    //   K: thread t loads dims 8c .. 8c+7 of key kk (c = t / 32, kk = t % 32)
-    //      and writes them to row kperm(kk): a wave's writes are 1 KiB apiece.
-    //   V: thread t loads dim d of keys 8kg .. 8kg+7 (kg = t / 64, the wave;
-    //      d = 2 (t % 32) + (t / 32) % 2), one 256-byte key row per load
-    //      instruction, and writes the 8 keys of dim d as one piece.
-    const int kk = threadIdx.x & 31, kch = threadIdx.x >> 5;
-    const int vkg = threadIdx.x >> 6, vd = 2 * (threadIdx.x & 31) + ((threadIdx.x >> 5) & 1);
-    const unsigned k_lds = 512u * kch + 16u * kperm(kk);
-    const unsigned v_lds = 2048u * (vd & 1) + 1024u * (vkg >> 1) + 512u * (vkg & 1) + 16u * (vd >> 1);
-    auto kload = [&](int tile) {
-        const unsigned key = (unsigned)min(tile * kKTile + kk, last_key);
-        const unsigned off = (key * (unsigned)kv_dim + 8u * kch) * 4u;
-        const float4 a = ldg4_at(kc, off), b = ldg4_at(kc, off + 16u);
-        return floatx8{a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+    // The pair's tiles in the planes (tile j's K at tiles + j kTileBytes, its
+    // V kHalfTile further).  Past the last tile nothing is copied.
+    const unsigned char* const tiles = p.kvp + ((long long)lb * p.n_head_kv + kvh) * p.n_ptiles * kTileBytes;
+    auto copy_k = [&](int j, int b) {
+        if (j < n_kt) copy_half(tiles + (long long)j * kTileBytes, sk[b], wave, lane);
     };
-    auto vload = [&](int tile) {
-        floatx8 v;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const unsigned key = (unsigned)min(tile * kKTile + 8 * vkg + e, last_key);
-            v[e] = *reinterpret_cast<const float*>(reinterpret_cast<const char*>(vc) +
-                                                   (key * (unsigned)kv_dim + (unsigned)vd) * 4u);
-        }
-        return v;
-    };
-    auto lstore = [&](unsigned char (*planes)[kPlane], unsigned off, floatx8 src) {
-        bf16x8 pc[3];
-        split8(src, pc);
-#pragma unroll
-        for (int q = 0; q < 3; ++q) *reinterpret_cast<bf16x8*>(&planes[q][off]) = pc[q];
+    auto copy_v = [&](int j, int b) {
+        if (j < n_kt) copy_half(tiles + (long long)j * kTileBytes + kHalfTile, sv[b], wave, lane);
     };
 
     // ---- Q^T operand: lane 32 h + j holds, for k step s, dims 16s + 8h ..
@@ -254,21 +308,19 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
         }
     }
 
-    floatx16 o0, o1;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) { o0[i] = 0.f; o1[i] = 0.f; }
+    floatx16 o0 = {}, o1 = {};
     float m_run = -INFINITY;
     float l_run = 0.f;
 
     // S^T = K.Q^T for the tile in K buffer kb: s[r] = S[query col][key
     // 16 (r / 8) + 8 half + r % 8 of the tile].
-    auto scores = [&](const unsigned char (*kb)[kPlane]) {
+    auto scores = [&](const unsigned char* kb) {
         floatx16 s = {};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) {
             bf16x8 a[3];
 #pragma unroll
-            for (int q = 0; q < 3; ++q) a[q] = *reinterpret_cast<const bf16x8*>(&kb[q][1024 * ks + 16 * lane]);
+            for (int q = 0; q < 3; ++q) a[q] = *reinterpret_cast<const bf16x8*>(kb + q * kPlane + 1024 * ks + 16 * lane);
             s = split_products(a, qp[ks], s);
         }
         return s;
@@ -309,7 +361,7 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     // O^T += V^T.P^T for the tile in V buffer vb: o_dt[r] accumulates dim
     // 2 (8 (r / 4) + 4 half + r % 4) + dt of query col.  P^T at k step ks is
     // s[8 ks .. 8 ks + 7], split into planes just before its products.
-    auto accumulate = [&](const floatx16& s, const unsigned char (*vb)[kPlane]) {
+    auto accumulate = [&](const floatx16& s, const unsigned char* vb) {
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
             floatx8 pv;
@@ -320,8 +372,8 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
             bf16x8 a0[3], a1[3];
 #pragma unroll
             for (int q = 0; q < 3; ++q) {
-                a0[q] = *reinterpret_cast<const bf16x8*>(&vb[q][1024 * ks + 16 * lane]);
-                a1[q] = *reinterpret_cast<const bf16x8*>(&vb[q][2048 + 1024 * ks + 16 * lane]);
+                a0[q] = *reinterpret_cast<const bf16x8*>(vb + q * kPlane + 1024 * ks + 16 * lane);
+                a1[q] = *reinterpret_cast<const bf16x8*>(vb + q * kPlane + 2048 + 1024 * ks + 16 * lane);
             }
             o0 = split_products(a0, pp, o0);
             o1 = split_products(a1, pp, o1);
@@ -330,37 +382,49 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
 
     // Software pipeline over key tiles j: step j computes the scores of tile
     // j+1 (MFMA) while the softmax of tile j (VALU) runs, then P.V of tile j.
-    // At the start of step j the LDS holds K[j+1] and V[j]; the step stores
-    // K[j+2] and V[j+1], loaded from global memory one step earlier, into the
-    // buffers of K[j] and V[j-1], and issues the loads of K[j+3] and V[j+2].
-    floatx8 ld_k = kload(0), ld_v = vload(0);
-    lstore(sk[0], k_lds, ld_k);
-    lstore(sv[0], v_lds, ld_v);
-    ld_k = kload(1);
-    ld_v = vload(1);
-    lstore(sk[1], k_lds, ld_k);
-    ld_k = kload(2);
+    // At the start of step j the LDS holds K[j+1] and V[j]; the step copies
+    // K[j+2] and V[j+1] into the buffers of K[j] and V[j-1] (both read in
+    // step j-1), and waits for its copies before the barrier that ends it.
+    copy_k(0, 0);
+    copy_v(0, 0);
+    copy_k(1, 1);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
     floatx16 s_cur;
     if (computes) s_cur = scores(sk[0]);
-    __syncthreads();  // K[0]'s buffer is overwritten in step 0
+    __syncthreads();  // K[0]'s buffer is refilled in step 0
 
-    int j = 0;
-    for (; j < n_plain; ++j) {
+    // A step with no masked key; the scores of tile j in s_this, tile j+1's
+    // into s_next.  Two steps per loop trip, the two accumulators trading
+    // roles, so that no copy of the scores is needed between steps.
+    auto plain_step = [&](int j, floatx16& s_this, floatx16& s_next) {
+        copy_k(j + 2, j & 1);
+        copy_v(j + 1, (j + 1) & 1);
         if (computes) {
-            const floatx16 s_next = scores(sk[(j + 1) & 1]);
-            softmax(s_cur, j * kKTile, false);
-            accumulate(s_cur, sv[j & 1]);
-            s_cur = s_next;
+            s_next = scores(sk[(j + 1) & 1]);
+            softmax(s_this, j * kKTile, false);
+            accumulate(s_this, sv[j & 1]);
         }
-        lstore(sk[j & 1], k_lds, ld_k);
-        lstore(sv[(j + 1) & 1], v_lds, ld_v);
-        ld_k = kload(j + 3);
-        ld_v = vload(j + 2);
+        __builtin_amdgcn_s_waitcnt(0);
         __syncthreads();
+    };
+    int j = 0;
+    floatx16 s_alt;
+    for (; j + 1 < n_plain; j += 2) {
+        plain_step(j, s_cur, s_alt);
+        plain_step(j + 1, s_alt, s_cur);
+    }
+    if (j < n_plain) {
+        plain_step(j, s_cur, s_alt);
+        s_cur = s_alt;
+        ++j;
     }
     for (; j < n_kt; ++j) {  // at most two tiles reach the diagonal
         const bool more = j + 1 < n_kt;  // uniform
+        if (more) {
+            copy_k(j + 2, j & 1);
+            copy_v(j + 1, (j + 1) & 1);
+        }
         if (computes) {
             floatx16 s_next = {};  // unused after the last tile
             if (more) s_next = scores(sk[(j + 1) & 1]);
@@ -369,10 +433,7 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
             s_cur = s_next;
         }
         if (more) {
-            lstore(sk[j & 1], k_lds, ld_k);
-            lstore(sv[(j + 1) & 1], v_lds, ld_v);
-            ld_k = kload(j + 3);
-            ld_v = vload(j + 2);
+            __builtin_amdgcn_s_waitcnt(0);
             __syncthreads();
         }
     }
@@ -394,6 +455,12 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
 
 }  // namespace
 
+size_t prefill_planes_bytes(int n_lb, int n_head_kv, int pos0, int n_tok)
+{
+    const long long tiles = ((long long)pos0 + n_tok + kKTile - 1) / kKTile;
+    return (size_t)n_lb * n_head_kv * tiles * kTileBytes;
+}
+
 hipError_t load_prefill_code()
 {
     hipFuncAttributes a;
@@ -402,14 +469,16 @@ hipError_t load_prefill_code()
 
 hipError_t launch_prefill_append(const PrefillParams& p, hipStream_t s)
 {
-    const long long threads = (long long)p.n_lb * p.n_tok * p.n_head_kv * 16;
-    const long long blocks = (threads + 255) / 256;
+    if (!p.kvp || p.n_ptiles != (p.pos0 + p.n_tok + kKTile - 1) / kKTile) return hipErrorInvalidValue;
+    const long long blocks = (long long)p.n_lb * p.n_head_kv * p.n_ptiles;
+    if (blocks >= (1LL << 31)) return hipErrorInvalidValue;
     hipLaunchKernelGGL(prefill_append_kernel, dim3((unsigned)blocks), dim3(256), 0, s, p);
     return hipGetLastError();
 }
 
 hipError_t launch_prefill_attention(const PrefillParams& p, hipStream_t s)
 {
+    if (!p.kvp || p.n_ptiles != (p.pos0 + p.n_tok + kKTile - 1) / kKTile) return hipErrorInvalidValue;
     PrefillGrid g;
     g.n_qt = (p.n_tok + kQTile - 1) / kQTile;
     g.n_hg = (p.gqa + kWavesP - 1) / kWavesP;

@@ -95,8 +95,14 @@ struct PrefillParams {
     int gqa;
     int rotate;
     float scale_log2;
+    // K and V of every 32-key tile of positions 0 .. pos0+n_tok-1 as bf16
+    // planes, written by the append and read by the attention kernel:
+    // [n_lb][n_head_kv][n_ptiles] tiles of prefill_tile_bytes()
+    unsigned char* kvp;
+    int n_ptiles;
 };
 
+size_t prefill_planes_bytes(int n_lb, int n_head_kv, int pos0, int n_tok);
 hipError_t launch_prefill_append(const PrefillParams& p, hipStream_t s);
 hipError_t launch_prefill_attention(const PrefillParams& p, hipStream_t s);
 
