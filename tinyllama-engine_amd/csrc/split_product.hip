@@ -53,8 +53,11 @@ constexpr int kWaves = kThreads / 64;
 constexpr int kTW = 4;         // token subtiles of 16 per workgroup
 constexpr int kRing = 3;       // LDS stages, x register stages and weight register stages
 constexpr int kStageBytes = 3 * kTW * 1024;
-constexpr int kPieces = kStageBytes / 16 / kThreads;  // 16-byte pieces per thread and stage
-static_assert(kPieces * 16 * kThreads == kStageBytes, "a stage is whole pieces per thread");
+constexpr int kChunksPerWave = kStageBytes / 1024 / kWaves;  // 1 KiB copies per wave and stage
+static_assert(kChunksPerWave * 1024 * kWaves == kStageBytes, "a stage is whole chunks per wave");
+
+typedef __attribute__((address_space(3))) void* lds_ptr;
+typedef __attribute__((address_space(1))) void* global_ptr;
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -142,7 +145,12 @@ struct Fmt {
     static constexpr bool kScaled = kType == kQ4_0 || kType == kQ8_0 || kType == kQ6_K;
 };
 
-// Loads of block kb of one weight row (wrow) for lane group g.
+// Loads of block kb of one weight row (wrow) for lane group g.  kRowLoads:
+// the memory instructions they are at least (separate addresses the
+// compiler cannot merge), which the kernel's wait for its LDS copies counts.
+template <int kType>
+constexpr int kRowLoads = kType == kF32 ? 2 : kType == kQ6_K ? 4 : 1;
+
 template <int kType>
 __device__ __forceinline__ void load_w(WRaw<kType>& w, const unsigned char* wrow, int kb, int g)
 {
@@ -296,7 +304,10 @@ __device__ __forceinline__ RowSeg row_seg(const SplitParams& p, int row)
 template <int kType, int kRW>
 __global__ __launch_bounds__(kThreads) void split_product_kernel(const SplitParams p)
 {
-    __shared__ __align__(16) unsigned char s_x[kRing][kStageBytes];
+    // The ring's stages as separate arrays, so that the compiler sees that a
+    // stage being read is not the one a copy in flight writes.
+    __shared__ __align__(16) unsigned char s_x0[kStageBytes], s_x1[kStageBytes], s_x2[kStageBytes];
+    auto stage_base = [&](int u) __attribute__((always_inline)) { return u == 0 ? s_x0 : u == 1 ? s_x1 : s_x2; };
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6), lane = threadIdx.x & 63;
     const int j = lane & 15, g = lane >> 4;
     // Tiles by linear workgroup id L, token tile fastest (y = L mod the
@@ -321,21 +332,20 @@ __global__ __launch_bounds__(kThreads) void split_product_kernel(const SplitPara
         wrow[r] = rs.w + static_cast<long long>(rs.row) * p.row_bytes;
     }
 
-    // x stage of block kb: plane q / (64 kTW), piece q % (64 kTW) of the
-    // workgroup's kTW subtiles, for the thread's pieces q = tid + 256 m
-    auto load_x = [&](u32x4 (&xr)[kPieces], int kb) __attribute__((always_inline)) {
-        kb = min(kb, kb_hi - 1);  // past the end: a block that exists (never used)
+    // x stage of block kb: 12 chunks of 1 KiB, chunk c = plane c / 4 of
+    // token subtile s0 + c % 4, copied by direct global-to-LDS loads, three
+    // per wave (lane l's 16 bytes land at byte 16 l of the chunk).  Past the
+    // end the last block is copied again (never read), so every iteration
+    // issues the same memory operations.
+    auto copy_x = [&](int kb, int stage) __attribute__((always_inline)) {
+        kb = min(kb, kb_hi - 1);
 #pragma unroll
-        for (int m = 0; m < kPieces; ++m) {
-            const int q = threadIdx.x + kThreads * m;
-            const int pl = q / (64 * kTW), off = q % (64 * kTW);
-            xr[m] = *reinterpret_cast<const u32x4*>(p.xs + plane_chunk(kb, pl, s0, p.n_sub) + 16 * off);
+        for (int i = 0; i < kChunksPerWave; ++i) {
+            const int c = kChunksPerWave * wave + i;
+            __builtin_amdgcn_global_load_lds(
+                (global_ptr)(p.xs + plane_chunk(kb, c / kTW, s0, p.n_sub) + 1024 * (c % kTW) + 16 * lane),
+                (lds_ptr)(stage_base(stage) + 1024 * c), 16, 0, 0);
         }
-    };
-    auto store_x = [&](const u32x4 (&xr)[kPieces], int stage) __attribute__((always_inline)) {
-#pragma unroll
-        for (int m = 0; m < kPieces; ++m)
-            *reinterpret_cast<u32x4*>(&s_x[stage][16 * (threadIdx.x + kThreads * m)]) = xr[m];
     };
     auto load_ws = [&](WRaw<kType> (&wr)[kRW], int kb) __attribute__((always_inline)) {
         kb = min(kb, kb_hi - 1);
@@ -349,30 +359,47 @@ __global__ __launch_bounds__(kThreads) void split_product_kernel(const SplitPara
 #pragma unroll
         for (int s = 0; s < kTW; ++s) acc[r][s] = floatx4{0.f, 0.f, 0.f, 0.f};
 
-    // Block b: x registers xr<b % 3> (loaded two iterations before it is
-    // stored), LDS stage b % 3 (stored one iteration before it is read),
+    // Block b: LDS stage b % 3 (copied two iterations before it is read),
     // weights wr<b % 3> (loaded three iterations before use).  Iteration kb:
-    // store block kb + 1's x, load block kb + 3's x, barrier, multiply block
-    // kb, load block kb + 3's weights.  Loads are unconditional (past the
-    // end they re-read the last block), so every path keeps the same loads
-    // in flight.  Separate arrays per ring slot, chosen at compile time,
-    // stay in registers.
-    u32x4 xr0[kPieces], xr1[kPieces], xr2[kPieces];
+    // wait for block kb's copy, barrier (every wave's copy has landed and
+    // every wave is done with block kb - 1), copy block kb + 2 into block
+    // kb - 1's stage, multiply block kb, load block kb + 3's weights.  The
+    // wait counts memory operations: after block kb's copy this wave issued
+    // block kb + 1's and kb + 2's weights (at least kRowLoads per row each)
+    // and block kb + 1's copy (kChunksPerWave), so waiting until no more than
+    // that many are outstanding means the copy has landed (they complete in
+    // order; a count below the true one only waits longer).  Scheduling
+    // barriers keep that order.  Separate arrays per ring
+    // slot, chosen at compile time, stay in registers.
+    // The prologue issues its operations in the loop's order (weights of
+    // block b + 3 after the copy of block b + 2), as if iterations kb_lo - 3
+    // .. kb_lo - 1 had run.
     WRaw<kType> wr0[kRW], wr1[kRW], wr2[kRW];
-    load_x(xr0, kb_lo);
-    load_x(xr1, kb_lo + 1);
-    load_x(xr2, kb_lo + 2);
     load_ws(wr0, kb_lo);
+    __builtin_amdgcn_sched_barrier(0);
+    copy_x(kb_lo, 0);
+    __builtin_amdgcn_sched_barrier(0);
     load_ws(wr1, kb_lo + 1);
+    __builtin_amdgcn_sched_barrier(0);
+    copy_x(kb_lo + 1, 1);
+    __builtin_amdgcn_sched_barrier(0);
     load_ws(wr2, kb_lo + 2);
-    store_x(xr0, 0);
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
 
-    auto iteration = [&](int kb, auto& xr_this, auto& xr_next, auto& wr_this, const int u,
-                         const int u1) __attribute__((always_inline)) {
-        store_x(xr_next, u1);
-        load_x(xr_this, kb + 3);
-        __syncthreads();
+    constexpr int kAfterCopy = kChunksPerWave + 2 * kRW * kRowLoads<kType>;
+    static_assert(kAfterCopy < 64, "vmcnt holds 6 bits");
+    constexpr int kVmcntWait = (kAfterCopy & 15) | ((kAfterCopy >> 4) << 14) | 0xF70;  // vmcnt(kAfterCopy)
+    auto iteration = [&](int kb, auto& wr_this, const int u, const int u2) __attribute__((always_inline)) {
+        // A bare barrier: __syncthreads' release fence would wait for every
+        // outstanding load (the copies write LDS through the vector memory
+        // path), weights included.  The LDS reads of block kb - 1 were used
+        // before this point, so its stage is free once every wave is here.
+        __builtin_amdgcn_s_waitcnt(kVmcntWait);
+        asm volatile("" ::: "memory");
+        __builtin_amdgcn_s_barrier();
+        asm volatile("" ::: "memory");
+        copy_x(kb + 2, u2);
+        __builtin_amdgcn_sched_barrier(0);
         if (kb < kb_hi) {  // uniform
             // the row subtiles' weights first, then the token subtiles one
             // at a time (their x pieces read from LDS just before use)
@@ -385,19 +412,23 @@ __global__ __launch_bounds__(kThreads) void split_product_kernel(const SplitPara
                 bf16x8 a[3];
 #pragma unroll
                 for (int pl = 0; pl < 3; ++pl)
-                    a[pl] = *reinterpret_cast<const bf16x8*>(&s_x[u][(pl * kTW + s) * 1024 + 16 * lane]);
+                    a[pl] = *reinterpret_cast<const bf16x8*>(stage_base(u) + (pl * kTW + s) * 1024 + 16 * lane);
 #pragma unroll
                 for (int r = 0; r < kRW; ++r) tile_products<kType>(a, b[r], d[r], acc[r][s]);
             }
         }
+        __builtin_amdgcn_sched_barrier(0);
         load_ws(wr_this, kb + 3);
+        __builtin_amdgcn_sched_barrier(0);
     };
 #pragma unroll 1
     for (int kb0 = kb_lo; kb0 < kb_hi; kb0 += kRing) {
-        iteration(kb0, xr0, xr1, wr0, 0, 1);
-        iteration(kb0 + 1, xr1, xr2, wr1, 1, 2);
-        iteration(kb0 + 2, xr2, xr0, wr2, 2, 0);
+        iteration(kb0, wr0, 0, 2);
+        iteration(kb0 + 1, wr1, 1, 0);
+        iteration(kb0 + 2, wr2, 2, 1);
     }
+    // the copies past the end land before the workgroup's LDS is released
+    __builtin_amdgcn_s_waitcnt(0);
 
     // lane (g, j) holds tokens 16 (s0 + s) + 4 g + q of row row0 + 16 r + j;
     // with K split, the sums go to part[z][t][row] for split_reduce_kernel
