@@ -159,12 +159,16 @@ struct PrefillGrid {
     int n_qt;     // query tiles
     int n_hg;     // head groups of 4 waves per kv head
     int n_pairs;  // n_lb * n_head_kv
-    int per_xcd;  // workgroup slots per XCD: ceil(n_pairs / 8) * n_hg * n_qt
+    // Pair groups: 8 (pair i on XCD i % 8) for at least 8 pairs, else 1 (all
+    // query tiles over the whole GPU: one layer has 4 pairs).
+    int n_grp, grp_shift;  // n_grp = 1 << grp_shift
+    int per_grp;           // workgroup slots per group: ceil(n_pairs / n_grp) * n_hg * n_qt
     // Quotients by the launch's divisors as multiply-highs: q = mulhi(n, m)
     // with m = ceil(2^32 / d), exact for n * d < 2^32 (checked at launch); a
-    // divisor of 1 has m = 0 and takes q = n.  The XCDs below n_pairs % 8
-    // (all when it is 0) hold ceil(n_pairs / 8) pairs, the others one fewer.
-    unsigned m_rank_big, m_rank_small;  // pairs per XCD x n_hg
+    // divisor of 1 has m = 0 and takes q = n.  The groups below
+    // n_pairs % n_grp (all when it is 0) hold ceil(n_pairs / n_grp) pairs,
+    // the others one fewer.
+    unsigned m_rank_big, m_rank_small;  // pairs per group x n_hg
     unsigned m_hg;                      // n_hg
     unsigned m_kv;                      // n_head_kv
 };
@@ -203,52 +207,67 @@ typedef __attribute__((address_space(3))) void* lds_ptr;
 typedef __attribute__((address_space(1))) void* global_ptr;
 
 // Copies half a tile (12 KiB, K or V) from the planes into LDS: 12 chunks
-// of 1 KiB, 3 per wave, each one direct global-to-LDS load of 16 bytes per
-// lane (lane l's bytes land at byte 16 l of the chunk).
+// of 1 KiB over kWaves waves, each one direct global-to-LDS load of 16
+// bytes per lane (lane l's bytes land at byte 16 l of the chunk).
+template <int kWaves>
 __device__ __forceinline__ void copy_half(const unsigned char* src, unsigned char* dst, int wave, int lane)
 {
+    constexpr int kPer = 12 / kWaves;
 #pragma unroll
-    for (int c = 0; c < 3; ++c) {
-        const int chunk = 3 * wave + c;
+    for (int c = 0; c < kPer; ++c) {
+        const int chunk = kPer * wave + c;
         __builtin_amdgcn_global_load_lds((global_ptr)(src + 1024 * chunk + 16 * lane), (lds_ptr)(dst + 1024 * chunk),
                                          16, 0, 0);
     }
 }
 
+// kKS key splits: the workgroup's 4 waves are 4 / kKS q heads x kKS key
+// splits; split h walks key tiles h, h + kKS, ... with its own double
+// buffers, and the splits' softmax states are merged in LDS at the end.
+// kKS = 2 halves the longest query tile's walk for grids that do not fill
+// the GPU (one layer per launch, as the batched prompt makes them).
+template <int kKS>
 __global__ __launch_bounds__(64 * kWavesP) __attribute__((amdgpu_waves_per_eu(3, 3))) void
 prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
 {
-    // K and V tiles (three bf16 planes each, the planes' layout), shared by
-    // the 4 waves, double-buffered.
-    __shared__ __align__(16) unsigned char sk[2][kHalfTile];
-    __shared__ __align__(16) unsigned char sv[2][kHalfTile];
+    constexpr int kHeads = kWavesP / kKS;  // q heads per workgroup
+    // K and V tiles (three bf16 planes each, the planes' layout) per key
+    // split, shared by its waves, double-buffered.  (Three buffers per split,
+    // the copies two steps ahead, measured slower for kKS = 2: 144 KiB of
+    // LDS, one workgroup per CU.)
+    constexpr int kNB = 2;
+    __shared__ __align__(16) unsigned char sk[kKS][kNB][kHalfTile];
+    __shared__ __align__(16) unsigned char sv[kKS][kNB][kHalfTile];
 
     // ---- XCD-aware, heavy-first mapping of workgroups to tiles ----
     // Workgroup b runs on XCD b % 8 and XCDs start their workgroups in order
-    // of b / 8.  (layer, kv head) pair i belongs to XCD i % 8, so all query
-    // tiles of a pair share one L2; within an XCD, query tiles are handed out
-    // longest first (most key tiles) across all its pairs.
+    // of b / 8.  With 8 groups, (layer, kv head) pair i belongs to XCD i % 8,
+    // so all query tiles of a pair share one L2; within an XCD, query tiles
+    // are handed out longest first (most key tiles) across all its pairs.
+    // With one group (fewer than 8 pairs: their tiles fit every L2) the same
+    // order runs over the whole GPU.
     // The quotients are multiply-highs on scalar registers: a workgroup that
     // starts beside MFMA-bound waves gets few vector issue slots, and the
     // compiler's divisions go through the vector unit.
-    const int xcd = blockIdx.x % kXcds;
-    const int slot = blockIdx.x / kXcds;
-    const int xcd_pairs = (g.n_pairs - xcd + kXcds - 1) / kXcds;
-    const bool big = xcd_pairs * kXcds >= g.n_pairs;  // this XCD holds ceil(n_pairs / 8) pairs
-    const int per_rank = xcd_pairs * g.n_hg;
+    const int grp = blockIdx.x & (g.n_grp - 1);
+    const int slot = blockIdx.x >> g.grp_shift;
+    const int grp_pairs = (g.n_pairs - grp + g.n_grp - 1) >> g.grp_shift;
+    const bool big = (grp_pairs << g.grp_shift) >= g.n_pairs;  // this group holds ceil(n_pairs / n_grp) pairs
+    const int per_rank = grp_pairs * g.n_hg;
     if (slot >= per_rank * g.n_qt) return;  // whole workgroup
     const int rank = (int)div_magic((unsigned)slot, big ? g.m_rank_big : g.m_rank_small);
     const int qt = g.n_qt - 1 - rank;
     const int rem = slot - rank * per_rank;
     const int pg = (int)div_magic((unsigned)rem, g.m_hg);
-    const int pair = xcd + kXcds * pg;  // (lb, kvh)
+    const int pair = grp + (pg << g.grp_shift);  // (lb, kvh)
     const int hg = rem - pg * g.n_hg;
     const int lb = (int)div_magic((unsigned)pair, g.m_kv);
     const int kvh = pair - lb * p.n_head_kv;
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // scalar
     const int lane = threadIdx.x & 63;
-    const int hq = hg * kWavesP + wave;
+    const int kh = wave / kHeads, hw = wave % kHeads;  // key split, head within the workgroup
+    const int hq = hg * kHeads + hw;
     const bool computes = hq < p.gqa;  // uniform per wave; others only copy tiles
     const int qh = kvh * p.gqa + (computes ? hq : 0);
 
@@ -266,11 +285,13 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
     // The pair's tiles in the planes (tile j's K at tiles + j kTileBytes, its
     // V kHalfTile further).  Past the last tile nothing is copied.
     const unsigned char* const tiles = p.kvp + ((long long)lb * p.n_head_kv + kvh) * p.n_ptiles * kTileBytes;
+    // Past the last tile the last one is copied again (never read), so that
+    // every step issues the same copies and the waits can count them.
     auto copy_k = [&](int j, int b) {
-        if (j < n_kt) copy_half(tiles + (long long)j * kTileBytes, sk[b], wave, lane);
+        copy_half<kHeads>(tiles + (long long)min(j, n_kt - 1) * kTileBytes, sk[kh][b], hw, lane);
     };
     auto copy_v = [&](int j, int b) {
-        if (j < n_kt) copy_half(tiles + (long long)j * kTileBytes + kHalfTile, sv[b], wave, lane);
+        copy_half<kHeads>(tiles + (long long)min(j, n_kt - 1) * kTileBytes + kHalfTile, sv[kh][b], hw, lane);
     };
 
     // ---- Q^T operand: lane 32 h + j holds, for k step s, dims 16s + 8h ..
@@ -342,18 +363,22 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
         // more than 2^8: probabilities then stay <= 256 and the sums in fp32
         // range, and most tiles skip the rescale of O.  The result is the
         // same softmax: O and l share whatever max they were scaled by.
+        // A row whose keys have all been masked so far keeps m_run = -inf
+        // (a key split's first tile can lie past some rows' positions): its
+        // probabilities are 0, and nothing is rescaled.
         if (__any(mx > m_run + kRescaleSlack)) {
             const float m_new = fmaxf(m_run, mx);
-            const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
+            const float alpha = m_new == -INFINITY ? 1.f : __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the first tile
             m_run = m_new;
             l_run *= alpha;
             o0 *= alpha;
             o1 *= alpha;
         }
+        const float m_use = m_run == -INFINITY ? 0.f : m_run;
         float lsum = 0.f;
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-            s[r] = __builtin_amdgcn_exp2f(s[r] - m_run);
+            s[r] = __builtin_amdgcn_exp2f(s[r] - m_use);
             lsum += s[r];
         }
         l_run += lsum;
@@ -380,61 +405,91 @@ prefill_attention_kernel(const PrefillParams p, const PrefillGrid g)
         }
     };
 
-    // Software pipeline over key tiles j: step j computes the scores of tile
-    // j+1 (MFMA) while the softmax of tile j (VALU) runs, then P.V of tile j.
-    // At the start of step j the LDS holds K[j+1] and V[j]; the step copies
-    // K[j+2] and V[j+1] into the buffers of K[j] and V[j-1] (both read in
-    // step j-1), and waits for its copies before the barrier that ends it.
-    copy_k(0, 0);
-    copy_v(0, 0);
-    copy_k(1, 1);
+    // Software pipeline over this split's key tiles j_m = kh + m kKS: step m
+    // computes the scores of tile j_{m+1} (MFMA) while the softmax of tile
+    // j_m (VALU) runs, then P.V of tile j_m.  Tile j_m's K and V sit in
+    // buffer m % kNB.  Step m copies K[j_{m+kNB}] and V[j_{m+kNB-1}] into the
+    // buffers of K[j_m] and V[j_{m-1}] (both read in step m - 1), and before
+    // the barrier that ends it waits for the copies step m + 1 reads, issued
+    // kNB - 2 steps earlier: the copies of the last kNB - 2 steps may stay in
+    // flight.  Every split runs the same number of steps (barriers); a split
+    // past its last tile only copies and waits.
+    constexpr int kCopies = 2 * (12 / kHeads);  // copy instructions per wave and step
+    constexpr int kInFlight = (kNB - 2) * kCopies;
+    static_assert(kInFlight < 64, "vmcnt holds 6 bits");
+    constexpr int kWaitCopies = (kInFlight & 15) | ((kInFlight >> 4) << 14) | 0xF70;  // vmcnt(kInFlight)
+    const int n_steps = (n_kt + kKS - 1) / kKS;
+    auto tile_of = [&](int m) { return kh + m * kKS; };
+#pragma unroll
+    for (int b = 0; b < kNB; ++b) copy_k(tile_of(b), b);
+#pragma unroll
+    for (int b = 0; b + 1 < kNB; ++b) copy_v(tile_of(b), b);
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    floatx16 s_cur;
-    if (computes) s_cur = scores(sk[0]);
-    __syncthreads();  // K[0]'s buffer is refilled in step 0
+    floatx16 s_cur = {};
+    if (computes && tile_of(0) < n_kt) s_cur = scores(sk[kh][0]);
+    __syncthreads();  // K[j_0]'s buffer is refilled in step 0
 
-    // A step with no masked key; the scores of tile j in s_this, tile j+1's
-    // into s_next.  Two steps per loop trip, the two accumulators trading
-    // roles, so that no copy of the scores is needed between steps.
-    auto plain_step = [&](int j, floatx16& s_this, floatx16& s_next) {
-        copy_k(j + 2, j & 1);
-        copy_v(j + 1, (j + 1) & 1);
-        if (computes) {
-            s_next = scores(sk[(j + 1) & 1]);
-            softmax(s_this, j * kKTile, false);
-            accumulate(s_this, sv[j & 1]);
+    // The scores of tile j_m in s_this, tile j_{m+1}'s into s_next.  Two
+    // steps per loop trip, the two accumulators trading roles, so that no
+    // copy of the scores is needed between steps.  Only the last one or two
+    // tiles reach the diagonal (masked).
+    auto step = [&](int m, floatx16& s_this, floatx16& s_next) {
+        const int j = tile_of(m), jn = tile_of(m + 1);
+        const bool last = m + 1 == n_steps;  // uniform
+        copy_k(tile_of(m + kNB), m % kNB);
+        copy_v(tile_of(m + kNB - 1), (m + kNB - 1) % kNB);
+        if (computes && j < n_kt) {
+            if (jn < n_kt) s_next = scores(sk[kh][(m + 1) % kNB]);
+            softmax(s_this, j * kKTile, j >= n_plain);
+            accumulate(s_this, sv[kh][m % kNB]);
         }
-        __builtin_amdgcn_s_waitcnt(0);
-        __syncthreads();
+        if (!last) {
+            // A bare barrier: __syncthreads' release fence would wait for
+            // every copy in flight (they write LDS through the vector memory
+            // path).  This step's LDS reads were used before this point.
+            __builtin_amdgcn_s_waitcnt(kWaitCopies);
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        }
     };
-    int j = 0;
-    floatx16 s_alt;
-    for (; j + 1 < n_plain; j += 2) {
-        plain_step(j, s_cur, s_alt);
-        plain_step(j + 1, s_alt, s_cur);
+    floatx16 s_alt = {};
+    int m = 0;
+    for (; m + 1 < n_steps; m += 2) {
+        step(m, s_cur, s_alt);
+        step(m + 1, s_alt, s_cur);
     }
-    if (j < n_plain) {
-        plain_step(j, s_cur, s_alt);
-        s_cur = s_alt;
-        ++j;
-    }
-    for (; j < n_kt; ++j) {  // at most two tiles reach the diagonal
-        const bool more = j + 1 < n_kt;  // uniform
-        if (more) {
-            copy_k(j + 2, j & 1);
-            copy_v(j + 1, (j + 1) & 1);
+    if (m < n_steps) step(m, s_cur, s_alt);
+    __builtin_amdgcn_s_waitcnt(0);  // the copies past the end land before the LDS is reused or released
+
+    if constexpr (kKS == 2) {
+        // Split 1 hands its softmax state (running max, partial sum, O) to
+        // split 0 through LDS (the tile buffers, free now); split 0 merges:
+        // both scaled to the larger max.  Split 0 always had a tile.
+        __syncthreads();
+        float* const xch = reinterpret_cast<float*>(&sk[0][0][0]) + hw * 34 * 64 + lane;
+        if (kh == 1 && computes) {
+            xch[0] = m_run;
+            xch[64] = l_run;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                xch[64 * (2 + i)] = o0[i];
+                xch[64 * (18 + i)] = o1[i];
+            }
         }
+        __syncthreads();
+        if (kh == 1) return;
         if (computes) {
-            floatx16 s_next = {};  // unused after the last tile
-            if (more) s_next = scores(sk[(j + 1) & 1]);
-            softmax(s_cur, j * kKTile, true);
-            accumulate(s_cur, sv[j & 1]);
-            s_cur = s_next;
-        }
-        if (more) {
-            __builtin_amdgcn_s_waitcnt(0);
-            __syncthreads();
+            const float m_b = xch[0];
+            const float m_new = fmaxf(m_run, m_b);
+            const float fa = __builtin_amdgcn_exp2f(m_run - m_new), fb = __builtin_amdgcn_exp2f(m_b - m_new);
+            l_run = l_run * fa + xch[64] * fb;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) {
+                o0[i] = o0[i] * fa + xch[64 * (2 + i)] * fb;
+                o1[i] = o1[i] * fa + xch[64 * (18 + i)] * fb;
+            }
         }
     }
 
@@ -476,30 +531,63 @@ hipError_t launch_prefill_append(const PrefillParams& p, hipStream_t s)
     return hipGetLastError();
 }
 
-hipError_t launch_prefill_attention(const PrefillParams& p, hipStream_t s)
+namespace {
+
+// Compute units of the current device (cached per device).
+int device_cus()
 {
-    if (!p.kvp || p.n_ptiles != (p.pos0 + p.n_tok + kKTile - 1) / kKTile) return hipErrorInvalidValue;
+    static int cus[64] = {};
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) {
+        int n = 0;
+        if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n < 1) n = 256;
+        cus[dev] = n;
+    }
+    return cus[dev];
+}
+
+template <int kKS>
+hipError_t launch_attention(const PrefillParams& p, hipStream_t s)
+{
+    constexpr int kHeads = kWavesP / kKS;
     PrefillGrid g;
     g.n_qt = (p.n_tok + kQTile - 1) / kQTile;
-    g.n_hg = (p.gqa + kWavesP - 1) / kWavesP;
+    g.n_hg = (p.gqa + kHeads - 1) / kHeads;
     g.n_pairs = p.n_lb * p.n_head_kv;
-    g.per_xcd = (g.n_pairs + kXcds - 1) / kXcds * g.n_hg * g.n_qt;
+    g.n_grp = g.n_pairs >= kXcds ? kXcds : 1;
+    g.grp_shift = g.n_grp == kXcds ? 3 : 0;
+    static_assert(kXcds == 8, "grp_shift");
+    g.per_grp = (g.n_pairs + g.n_grp - 1) / g.n_grp * g.n_hg * g.n_qt;
     // m = ceil(2^32 / d) (0 for d <= 1); mulhi(n, m) = n / d whenever n * d < 2^32.
     auto magic = [](long long d) -> unsigned {
         return d <= 1 ? 0u : (unsigned)(((1ULL << 32) + (unsigned long long)d - 1) / (unsigned long long)d);
     };
-    const long long rank_big = (long long)((g.n_pairs + kXcds - 1) / kXcds) * g.n_hg;
-    const long long rank_small = (long long)(g.n_pairs / kXcds) * g.n_hg;
-    if ((long long)g.per_xcd * rank_big >= (1LL << 32) || (long long)rank_big * g.n_hg >= (1LL << 32) ||
+    const long long rank_big = (long long)((g.n_pairs + g.n_grp - 1) / g.n_grp) * g.n_hg;
+    const long long rank_small = (long long)(g.n_pairs / g.n_grp) * g.n_hg;
+    if ((long long)g.per_grp * rank_big >= (1LL << 32) || (long long)rank_big * g.n_hg >= (1LL << 32) ||
         (long long)g.n_pairs * p.n_head_kv >= (1LL << 32))
         return hipErrorInvalidValue;  // quotients by multiply-high would not be exact
     g.m_rank_big = magic(rank_big);
     g.m_rank_small = magic(rank_small);
     g.m_hg = magic(g.n_hg);
     g.m_kv = magic(p.n_head_kv);
-    hipLaunchKernelGGL(prefill_attention_kernel, dim3(g.per_xcd * kXcds), dim3(64 * kWavesP), 0, s,
-                       p, g);
+    hipLaunchKernelGGL((prefill_attention_kernel<kKS>), dim3(g.per_grp * g.n_grp), dim3(64 * kWavesP), 0, s, p, g);
     return hipGetLastError();
+}
+
+}  // namespace
+
+// Two key splits per workgroup where one split per workgroup would give at
+// most one workgroup per CU (one layer per launch up to 1024 tokens: 512
+// tokens 128 workgroups), else one.  (At 2048 tokens, 512 workgroups of one
+// split run faster than 1024 of two.)
+hipError_t launch_prefill_attention(const PrefillParams& p, hipStream_t s)
+{
+    if (!p.kvp || p.n_ptiles != (p.pos0 + p.n_tok + kKTile - 1) / kKTile) return hipErrorInvalidValue;
+    const long long pairs = (long long)p.n_lb * p.n_head_kv;
+    const long long wg1 = pairs * ((p.gqa + kWavesP - 1) / kWavesP) * ((p.n_tok + kQTile - 1) / kQTile);
+    return wg1 <= device_cus() ? launch_attention<2>(p, s) : launch_attention<1>(p, s);
 }
 
 }  // namespace tla
