@@ -285,6 +285,30 @@ def test_forward_wide_embedding(tla, O, W, engines):
     check_logits(got, want, "n_embd 3072 q4_0 vs oracle")
 
 
+@pytest.mark.parametrize("n_embd,n_head,n_head_kv,wtype,wo_type", [
+    (256, 4, 4, "W_Q8_0", "W_F32"),   # gqa 1
+    (512, 8, 2, "W_Q4_0", "W_Q6_K"),  # gqa 4: W_o column groups of one Q6_K super-block
+    (1024, 16, 2, "W_F16", "W_Q4_0"),  # gqa 8
+    (512, 8, 1, "W_Q8_0", "W_F16"),   # gqa 8, one kv head
+    (512, 8, 8, "W_Q4_0", "W_Q8_0"),  # 8 kv heads: no fused launch at any position
+])
+def test_forward_short_context_fusion(tla, O, W, engines, n_embd, n_head, n_head_kv, wtype, wo_type):
+    """A decode step over at most 64 positions runs attention and W_o as one
+    launch (each workgroup recomputes one kv head's attention; the W_o
+    partials per kv head reach x through the FFN launches); from position
+    64 on, the attention launch and the W_o GEMV.  70 tokens one at a time
+    against the oracle, every step's logits (the last 6 past the switch)."""
+    spec = W.ModelSpec(2, n_embd, n_head, n_head_kv, 512, 384, 72)
+    t = W.make_model(spec, getattr(W, wtype), salt=91 + n_head,
+                     overrides={"attn_output.weight": getattr(W, wo_type)})
+    toks = [(37 * i + 11) % spec.n_vocab for i in range(70)]
+    om = O.Model(spec, t)
+    want = np.stack([om.forward(tk, i) for i, tk in enumerate(toks)])
+    eng = spec_engine(engines, spec)
+    got = run_forward(tla, eng, spec, t, toks)
+    check_logits(got, want, f"gqa {n_head // n_head_kv} x {n_head_kv} kv heads, W_o {wo_type} vs oracle")
+
+
 def test_forward_errors(tla, W, engines):
     spec = W.ModelSpec(2, 256, 4, 2, 512, 384, 64)
     t = W.make_model(spec, W.W_Q8_0, salt=3)

@@ -1101,6 +1101,7 @@ int check_model(const tla_engine* e, const tla_model* m)
 // logits [n_vocab] floats, then n_ints ints.
 struct FwdBufs {
     float *x, *xb, *q, *k, *v, *att, *hb, *hb2, *logits;
+    float* parts;  // [kAttnOutMaxParts][n_embd]: the fused attention + W_o launch's partials
     int* tokens;
 };
 
@@ -1108,7 +1109,8 @@ int fwd_bufs(tla_engine* e, const tla_model* m, int rows, int n_ints, FwdBufs* b
 {
     const size_t embd = e->cfg.n_embd, kv = e->kv_dim, ff = m->n_ff, nv = m->n_vocab;
     const size_t r = static_cast<size_t>(rows);
-    const size_t floats = r * (4 * embd + 2 * kv + 2 * ff) + nv;
+    const size_t parts_at = (r * (4 * embd + 2 * kv + 2 * ff) + nv + 63) / 64 * 64;  // 256-byte aligned
+    const size_t floats = parts_at + kAttnOutMaxParts * embd;
     const size_t bytes = (floats * sizeof(float) + 255) / 256 * 256 + (n_ints + 1) * sizeof(int);
     if (bytes > e->fwd_bytes) {
         TLA_HIP(hipStreamSynchronize(e->stream));
@@ -1130,6 +1132,7 @@ int fwd_bufs(tla_engine* e, const tla_model* m, int rows, int n_ints, FwdBufs* b
     b->hb = b->v + r * kv;
     b->hb2 = b->hb + ff;  // row 0's up projection; row t's gate at hb + 2*n_ff*t
     b->logits = b->hb + r * 2 * ff;
+    b->parts = f + parts_at;
     b->tokens = reinterpret_cast<int*>(static_cast<char*>(e->fwd) + (floats * sizeof(float) + 255) / 256 * 256);
     return TLA_OK;
 }
@@ -1181,12 +1184,37 @@ int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc,
             if (int rc = gemv1(e, L.type_k, L.wk, b.k, kv, embd, b.xb, nullptr, nullptr, 0.f, 0)) return rc;
             if (int rc = gemv1(e, L.type_v, L.wv, b.v, kv, embd, b.xb, nullptr, nullptr, 0.f, 0)) return rc;
         }
-        // RoPE + append + attention (src/forward.cpp:192-208)
-        if (int rc = tla_decode(e, 1, &pos, l, 1, rope_in_gemv ? TLA_KV_IN_CACHE : TLA_ROTATE, b.att, b.q,
-                                b.k, b.v, kc, vc, 0))
-            return rc;
-        // x += Wo . att (src/forward.cpp:210-213)
-        if (int rc = gemv1(e, L.type_o, L.wo, b.x, embd, embd, b.att, nullptr, nullptr, 0.f, 1)) return rc;
+        // Attention and x += Wo . att (src/forward.cpp:198-213).  Over a
+        // short context, one launch: the partials of W_o per kv head, which
+        // the FFN launches add to x (x itself is not written here).
+        const int gqa = e->cfg.n_head / e->cfg.n_head_kv;
+        const bool fused_out = rope_in_gemv && gemv_can_add_parts(ff) &&
+                               attn_out_supported(L.type_o, gqa, e->cfg.n_head_kv, pos + 1);
+        if (fused_out) {
+            const long long layer = static_cast<long long>(l) * e->cfg.n_ctx * kv;
+            AttnOutParams a{};
+            a.q = b.q;
+            a.kc = kc + layer;
+            a.vc = vc + layer;
+            a.n_pos = pos + 1;
+            a.kv_dim = kv;
+            a.gqa = gqa;
+            a.n_head_kv = e->cfg.n_head_kv;
+            a.w = static_cast<const unsigned char*>(L.wo);
+            a.row_bytes = weight_row_bytes(L.type_o, embd);
+            a.group_bytes = weight_row_bytes(L.type_o, 64 * gqa);
+            a.rows = embd;
+            a.parts = b.parts;
+            if (int rc = launch(e, TLA_KERNEL_DECODE, "attention + W_o",
+                                [&] { return launch_attn_out(L.type_o, a, e->stream); }))
+                return rc;
+        } else {
+            // RoPE + append + attention
+            if (int rc = tla_decode(e, 1, &pos, l, 1, rope_in_gemv ? TLA_KV_IN_CACHE : TLA_ROTATE, b.att, b.q,
+                                    b.k, b.v, kc, vc, 0))
+                return rc;
+            if (int rc = gemv1(e, L.type_o, L.wo, b.x, embd, embd, b.att, nullptr, nullptr, 0.f, 1)) return rc;
+        }
         // rmsnorm + gate and up projections, then SiLU x up, W_down and the
         // residual (src/forward.cpp:215-228, src/ops.cpp:1535-1564).  SiLU x
         // up is the gate/up launch's epilogue where the format pairs rows
@@ -1206,11 +1234,30 @@ int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc,
             p.norm_w = L.ffn_norm;
             p.eps = eps;
             p.pair = paired ? 1 : 0;
+            if (fused_out) {
+                p.xparts = b.parts;
+                p.n_parts = e->cfg.n_head_kv;
+            }
             if (int rc = run_gemv(e, L.type_ffn, p)) return rc;
         }
-        if (int rc = gemv1(e, L.type_ffn, L.w_down, b.x, embd, ff, b.hb, paired ? nullptr : b.hb2,
-                           nullptr, 0.f, 1))
-            return rc;
+        {
+            GemvParams p{};
+            p.seg[0] = {static_cast<const unsigned char*>(L.w_down), b.x, embd, embd};
+            p.n_seg = 1;
+            p.total_rows = embd;
+            p.cols = ff;
+            p.row_bytes = static_cast<int>(weight_row_bytes(L.type_ffn, ff));
+            p.n_vec = 1;
+            p.x = b.hb;
+            p.x_stride = ff;
+            p.x2 = paired ? nullptr : b.hb2;
+            p.add = 1;
+            if (fused_out) {
+                p.rparts = b.parts;
+                p.n_parts = e->cfg.n_head_kv;
+            }
+            if (int rc = run_gemv(e, L.type_ffn, p)) return rc;
+        }
     }
     // final rmsnorm + classifier (src/forward.cpp:241-265)
     if (logits)

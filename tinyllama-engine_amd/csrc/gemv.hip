@@ -76,6 +76,21 @@ __device__ __forceinline__ void lds_x(const float* xs, int c0, float* o)
     }
 }
 
+// Sum of the fused attention + W_o launch's partials at index i: the n
+// (<= kAttnOutMaxParts) loads issued together (an index past n reloads
+// partial 0), then added in order ((p0 + p1) + p2) + p3.
+__device__ __forceinline__ float part_sum(const float* parts, int n, long long stride, long long i)
+{
+    float v[kAttnOutMaxParts];
+#pragma unroll
+    for (int g = 0; g < kAttnOutMaxParts; ++g) v[g] = parts[(g < n ? g : 0) * stride + i];
+    float s = v[0];
+#pragma unroll
+    for (int g = 1; g < kAttnOutMaxParts; ++g)
+        if (g < n) s += v[g];
+    return s;
+}
+
 // F32 and F16 weights are read once per launch, each load instruction of a
 // row's lanes one contiguous stretch, so those loads are non-temporal (nt
 // bit): 32000 x 2048 F16 20.9 against 22.8 us, as a streaming read runs ~10 %
@@ -445,12 +460,12 @@ struct SegRegs {
 // Epilogue of a one-vector launch, a template parameter so that plain
 // launches carry none of the others' code: kPlain (y (+)= W.x), kPairEpi
 // (gate and up rows paired, SwiGLU written), kRopeEpi (q and k row pairs
-// rotated).
-constexpr int kPlain = 0, kPairEpi = 1, kRopeEpi = 2;
+// rotated), kPartsEpi (y += W.x with the residual partials: rparts).
+constexpr int kPlain = 0, kPairEpi = 1, kRopeEpi = 2, kPartsEpi = 3;
 
 // kSteps: unit steps of a row held at once (a row of up to kSteps x lanes
 // units is requested whole); rows with more units load the rest step by step.
-template <int kType, int kRows, int kSteps>
+template <int kType, int kRows, int kSteps, bool kParts = false>
 struct RowGroup {
     Unit<kType> un[kSteps][kRows];
     const unsigned char* w[kRows];
@@ -515,6 +530,28 @@ struct RowGroup {
             old[k] = *out[k];
             if constexpr (kEpi == kRopeEpi) cs[k] = p.rope[(row[k] & 63) >> 1];
         }
+        if constexpr (kParts) {
+#pragma unroll
+            for (int k = 0; k < kRows; ++k) {
+                const float* pr = p.rparts + (out[k] - p.seg[0].out);
+#pragma unroll
+                for (int g = 0; g < kAttnOutMaxParts; ++g)
+                    pv[k][g] = pr[static_cast<long long>(g < p.n_parts ? g : 0) * p.seg[0].rows];
+            }
+        }
+    }
+    // The residual's old value of row k: with residual partials, old + ((p0
+    // + p1) + ...), summed here, where it is used, so that their loads stay
+    // in flight behind the pass's weights until then.
+    float pv[kParts ? kRows : 1][kParts ? kAttnOutMaxParts : 1];
+    __device__ float residual(const GemvParams& p, int k) const
+    {
+        if constexpr (!kParts) return old[k];
+        float a = pv[k][0];
+#pragma unroll
+        for (int g = 1; g < kAttnOutMaxParts; ++g)
+            if (g < p.n_parts) a += pv[k][g];
+        return old[k] + a;
     }
 };
 
@@ -532,7 +569,7 @@ template <int kType, int kLanesPerRow, int kRows, int kSteps, bool kMulti, int k
 __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
 {
     static_assert(!kMulti || kRows == 1, "several vectors take one row per lane group");
-    static_assert(kEpi == kPlain || (!kMulti && kSteps == 1), "special epilogues: one vector");
+    static_assert(kEpi == kPlain || (!kMulti && (kSteps == 1 || kEpi == kPartsEpi)), "special epilogues: one vector");
     static_assert(kEpi != kPairEpi || kRows == 2, "paired rows: two per lane group");
     static_assert(kEpi != kRopeEpi || (kRows == 1 && kLanesPerRow == 32), "RoPE: pairs in one wave");
     constexpr bool kZeroOffsets = kType == kQ8_0 || kType == kQ4_0 || kType == kQ6_K;
@@ -565,8 +602,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
     constexpr int kXRegs = kLanesPerRow * kSteps * kUnit / kThreads;
     constexpr int kX4 = (kXRegs + 3) / 4;
     const float* const nw = p.norm_w ? p.norm_w : p.x2 ? p.x2 : p.x;
+    // The attention + W_o partials are added here only where x is at most 2
+    // float4 per thread (their loads, issued together, would otherwise take
+    // the registers of the weights in flight); elsewhere the staging below
+    // adds them.
+    constexpr bool kPartsEarly = kX4 <= 2;
     const bool x_early = !kMulti && p.cols <= kXRegs * kThreads && !(p.norm_w && p.x2) &&
-                         aligned16(p.x) && aligned16(nw);
+                         (kPartsEarly || !p.xparts) && aligned16(p.x) && aligned16(nw);
     const int cols4 = p.cols / 4;
     float4 xr[kX4], nr[kX4];
     if (x_early) {
@@ -578,11 +620,27 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
             nr[i] = ldg4(nw + cc);
         }
     }
+    // The fused attention + W_o launch's partials for x, requested with x;
+    // added once the weights are requested too (a use here would hold the
+    // weights' request back until they arrive).
+    float4 pp[kPartsEarly ? kX4 : 1][kAttnOutMaxParts];
+    const bool parts_early = kPartsEarly && x_early && p.xparts;
+    if (parts_early) {
+#pragma unroll
+        for (int i = 0; i < (kPartsEarly ? kX4 : 1); ++i) {
+            const int c4 = threadIdx.x + i * kThreads;
+            const int cc = c4 < cols4 ? 4 * c4 : 0;
+#pragma unroll
+            for (int g = 0; g < kAttnOutMaxParts; ++g)
+                pp[i][g] = ldg4(p.xparts + static_cast<long long>(g < p.n_parts ? g : 0) * p.cols + cc);
+        }
+    }
 
     const SegRegs sr(p);
     int ps = wave;
-    RowGroup<kType, kRows, kSteps> ga;
-    [[maybe_unused]] RowGroup<kType, kRows, kSteps> gb;
+    constexpr bool kParts = kEpi == kPartsEpi;
+    RowGroup<kType, kRows, kSteps, kParts> ga;
+    [[maybe_unused]] RowGroup<kType, kRows, kSteps, kParts> gb;
     if constexpr (kMulti) {
         ga.locate(p, sr, ps * kPassRows + sub, kRowsPerWave);
         ga.load_head(units, kLanesPerRow, l);
@@ -601,6 +659,18 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
         // registers, in the orders of row_math.h (the rmsnorm kernels' and
         // the staging below's): the 4 threads of a run sit in consecutive
         // lanes.
+        if (parts_early) {
+            // x + ((p0 + p1) + ...)
+#pragma unroll
+            for (int i = 0; i < (kPartsEarly ? kX4 : 1); ++i) {
+                float4 a = pp[i][0];
+#pragma unroll
+                for (int g = 1; g < kAttnOutMaxParts; ++g)
+                    if (g < p.n_parts)
+                        a = make_float4(a.x + pp[i][g].x, a.y + pp[i][g].y, a.z + pp[i][g].z, a.w + pp[i][g].w);
+                xr[i] = make_float4(xr[i].x + a.x, xr[i].y + a.y, xr[i].z + a.z, xr[i].w + a.w);
+            }
+        }
         float4 t[kX4];
         float ss = 0.f;
 #pragma unroll
@@ -638,7 +708,8 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
         {
             const float* x2v = p.x2 ? p.x2 + v * p.x_stride : nullptr;
             for (int c = threadIdx.x; c < p.cols; c += kThreads) {
-                const float t = x2v ? silu(xv[c]) * x2v[c] : xv[c];
+                float t = x2v ? silu(xv[c]) * x2v[c] : xv[c];
+                if (p.xparts) t = t + part_sum(p.xparts, p.n_parts, p.cols, c);  // one vector, no x2
                 xs[xpad(c)] = t;
                 ss += t * t;
             }
@@ -670,7 +741,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
     }
 
     // One pass over the rows in g (its first kSteps unit steps loaded).
-    auto run_pass = [&](RowGroup<kType, kRows, kSteps>& g) {
+    auto run_pass = [&](RowGroup<kType, kRows, kSteps, kParts>& g) {
         const float* xs_base = xs_all;
         float acc[kRows][kGemvMaxVec];
 #pragma unroll
@@ -751,7 +822,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
                 if (v >= n_vec) break;
                 const float t = row_sum<kLanesPerRow>(acc[k][v]);
                 float* o = g.out[k] + v * g.out_stride[k];
-                const float old = kMulti ? *o : g.old[k];
+                const float old = kMulti ? *o : g.residual(p, k);
                 if (g.valid[k] && l == kLanesPerRow - 1) *o = p.add ? old + t : t;
             }
         }
@@ -783,6 +854,166 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
         run_pass(gb);
         ps += n_waves;
     }
+}
+
+// ---- decode attention over a short context fused with W_o --------------------
+//
+// One launch in place of a decode step's attention launch and its W_o
+// product (src/forward.cpp:198-213) when the context has at most
+// kAttnOutMaxPos positions.  Workgroup (b, g) takes W_o rows 32b .. 32b+31
+// restricted to the columns of kv head g's q heads, a row-major sub-matrix
+// (the row stride of W_o, its base gqa * 64 columns in), recomputes those
+// heads' attention (src/ops.cpp:1377-1511) over the cached positions, and
+// writes its rows' partial products parts[g][row].  The launches after it
+// add the partials to the residual (the gate/up launch's x staging, the
+// W_down launch's residual base, both in the order of part_sum), so no
+// workgroup waits for another: each kv head's attention is recomputed by
+// the rows / 32 workgroups that need it, from cache rows that sit in L2
+// after the first of them.
+//
+// The W_o weights of a lane (one 64-column unit of one row: 8 lanes per
+// row, 8 rows per wave) are requested first; q, the K tile and the V tile
+// of the wave follow.  Wave w takes positions 16w .. 16w+15, with the
+// decode kernel's MFMA layouts:
+//   S^T[16 pos][16 heads] = K[16 pos][64] . Q^T[64][16 heads]   16 x v_mfma_f32_16x16x4f32
+//   O^T[64 d][16 heads]   = V^T[64 d][16 pos] . P^T[16 pos][16 heads]
+// (heads gqa .. 15 zero; lane 16k + i holds dims 16k .. 16k+15 of key i and
+// of q head i, and the S accumulator is the P.V B operand).  The waves meet
+// in LDS twice: for the heads' maxima, then for the sums and O, combined in
+// wave order.  The output is the x of the W_o sub-matrix, staged as the
+// GEMV stages x (padded, with the 16-column sums).
+typedef float attn_f4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ attn_f4 mfma16x4(float a, float b, attn_f4 c)
+{
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+constexpr int kAttnOutRows = 32;  // W_o rows per workgroup: 4 waves x 8 rows of 8 lanes
+constexpr int kAttnOutCols = kAttnOutMaxGqa * 64;
+
+template <int kType>
+__global__ __launch_bounds__(kThreads) void attn_out_kernel(const AttnOutParams p)
+{
+    static_assert(kThreads == 256 && kAttnOutMaxPos == 64, "4 waves of 16 positions");
+    __shared__ __align__(16) float xs[xs_floats(kAttnOutCols)];
+    __shared__ float s16[kAttnOutCols / 16];
+    __shared__ float s_max[4][16], s_sum[4][16];
+    __shared__ float s_o[4][16 * 65];  // O of each wave, [head][dim], rows padded to 65
+
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = blockIdx.y;
+    const int units = p.gqa;  // 64-column units of a row's group
+
+    // ---- W_o: lane l of row group `sub` holds unit l of its row ----
+    const int sub = lane >> 3, l = lane & 7;
+    const int lu = l < units ? l : 0;  // lanes past the row's units load unit 0 (not used)
+    const int row = blockIdx.x * kAttnOutRows + wave * 8 + sub;
+    const bool valid = row < p.rows;
+    const unsigned char* wrow = p.w + static_cast<long long>(valid ? row : 0) * p.row_bytes +
+                                static_cast<long long>(g) * p.group_bytes;
+    Unit<kType> un;
+    un.load(wrow, 0, units, lu);
+
+    // ---- q, K and V of this wave's 16 positions (rows past n_pos read row
+    // 0, masked below; V rows there are weighted by 0) ----
+    const int i = lane & 15, k4 = lane >> 4;
+    const bool head = i < p.gqa;
+    const int pk = 16 * wave + i;
+    const float4* kr4 = reinterpret_cast<const float4*>(p.kc + static_cast<long long>(pk < p.n_pos ? pk : 0) * p.kv_dim +
+                                                        64 * g + 16 * k4);
+    const float4* qr4 = reinterpret_cast<const float4*>(p.q + static_cast<long long>(g * p.gqa + (head ? i : 0)) * 64 +
+                                                        16 * k4);
+    float4 kr[4], qr[4], vr[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        kr[s] = kr4[s];
+        qr[s] = qr4[s];
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const int pv = 16 * wave + 4 * k4 + s;
+        vr[s] = *reinterpret_cast<const float4*>(p.vc + static_cast<long long>(pv < p.n_pos ? pv : 0) * p.kv_dim +
+                                                 64 * g + 4 * i);
+    }
+
+    // scores in log2 units: q.k / sqrt(64) * log2(e)
+    attn_f4 sacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const float qv[4] = {head ? qr[s].x : 0.f, head ? qr[s].y : 0.f, head ? qr[s].z : 0.f, head ? qr[s].w : 0.f};
+        const float kv[4] = {kr[s].x, kr[s].y, kr[s].z, kr[s].w};
+#pragma unroll
+        for (int c = 0; c < 4; ++c) sacc = mfma16x4(kv[c], qv[c], sacc);
+    }
+    constexpr float kScale = 0.125f * 1.4426950408889634f;
+    float t[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) t[r] = 16 * wave + 4 * k4 + r < p.n_pos ? sacc[r] * kScale : -__builtin_huge_valf();
+    float m = fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]));
+    m = fmaxf(m, __shfl_xor(m, 16));
+    m = fmaxf(m, __shfl_xor(m, 32));
+    if (k4 == 0) s_max[wave][i] = m;
+    __syncthreads();
+    // position 0 is in wave 0's tile: every head's maximum is finite
+    const float mg = fmaxf(fmaxf(s_max[0][i], s_max[1][i]), fmaxf(s_max[2][i], s_max[3][i]));
+    float pr[4], lsum = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        pr[r] = __builtin_amdgcn_exp2f(t[r] - mg);  // exp2(-inf) = 0 for masked positions
+        lsum += pr[r];
+    }
+    lsum += __shfl_xor(lsum, 16);
+    lsum += __shfl_xor(lsum, 32);
+    if (k4 == 0) s_sum[wave][i] = lsum;
+
+    // O^T block b, rows 4 k4 + r: dim 4 (4 k4 + r) + b of head i
+    attn_f4 o[4] = {};
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+        const float vv[4] = {vr[s].x, vr[s].y, vr[s].z, vr[s].w};
+#pragma unroll
+        for (int b = 0; b < 4; ++b) o[b] = mfma16x4(vv[b], pr[s], o[b]);
+    }
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) s_o[wave][65 * i + 4 * (4 * k4 + r) + b] = o[b][r];
+    __syncthreads();
+
+    // attention output of the group's heads = x of the W_o sub-matrix
+    const int ncols = 64 * p.gqa;
+    for (int c = threadIdx.x; c < ncols; c += kThreads) {
+        const int h = c >> 6, d = c & 63;
+        const float num = ((s_o[0][65 * h + d] + s_o[1][65 * h + d]) + s_o[2][65 * h + d]) + s_o[3][65 * h + d];
+        const float den = ((s_sum[0][h] + s_sum[1][h]) + s_sum[2][h]) + s_sum[3][h];
+        xs[xpad(c)] = num / den;
+    }
+    __syncthreads();
+    constexpr bool kZeroOffsets = kType == kQ8_0 || kType == kQ4_0 || kType == kQ6_K;
+    if constexpr (kZeroOffsets) {
+        for (int b = threadIdx.x; b < ncols / 16; b += kThreads) {
+            const float4* xb = reinterpret_cast<const float4*>(xs + xpad(16 * b));
+            s16[b] = (sum4(xb[0]) + sum4(xb[1])) + (sum4(xb[2]) + sum4(xb[3]));
+        }
+        __syncthreads();
+    }
+
+    // ---- the rows' partial products ----
+    float pt[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+        constexpr int kW = Unit<kType>::kW;
+        float xv[16];
+#pragma unroll
+        for (int j = 0; j < 16 / kW; ++j) lds_x<kW>(xs, Unit<kType>::xcol(0, units, lu, q, j), xv + kW * j);
+        pt[q] = un.part(q, xv);
+    }
+    float f = l < units ? un.finish(pt, s16) : 0.f;
+    f += __shfl_xor(f, 1);
+    f += __shfl_xor(f, 2);
+    f += __shfl_xor(f, 4);
+    if (valid && l == 0) p.parts[static_cast<long long>(g) * p.rows + row] = f;
 }
 
 __global__ __launch_bounds__(kThreads) void rmsnorm_kernel(float* out, const float* x,
@@ -980,6 +1211,12 @@ hipError_t launch_typed(const GemvParams& p, hipStream_t s)
 {
     const int units = p.cols / kUnit;
     if (p.rope_rows > 0) return launch_shaped<kType, 32, 1, 1, false, kRopeEpi>(p, s);  // gemv_can_rope
+    if (p.rparts) {  // gemv_can_add_parts: one vector, one segment, rows of <= 128 units
+        if (p.n_vec != 1 || p.n_seg != 1 || units > 128 || p.pair) return hipErrorInvalidValue;
+        return units <= 32   ? launch_shaped<kType, 32, 1, 1, false, kPartsEpi>(p, s)
+               : units <= 64 ? launch_shaped<kType, 64, 1, 1, false, kPartsEpi>(p, s)
+                             : launch_shaped<kType, 64, 1, 2, false, kPartsEpi>(p, s);
+    }
     if (p.pair) {  // gemv_can_pair: one vector, a two-row format, rows of <= 64 units
         if constexpr (Unit<kType>::kRows == 2)
             return units <= 32 ? launch_shaped<kType, 32, 2, 1, false, kPairEpi>(p, s)
@@ -1023,6 +1260,11 @@ long long weight_row_bytes(int type, int cols)
     }
 }
 
+bool gemv_can_add_parts(int cols)
+{
+    return cols / kUnit <= 128;
+}
+
 bool gemv_can_rope(int cols)
 {
     return cols / kUnit <= 32;
@@ -1033,6 +1275,38 @@ bool gemv_can_pair(int type, int rows, int cols)
     const int units = cols / kUnit;
     const bool two_rows = type == kQ8_0 || type == kQ4_0 || type == kQ6_K;
     return two_rows && units <= 64 && rows % (units <= 32 ? 2 : 1) == 0;
+}
+
+bool attn_out_supported(int type, int gqa, int n_head_kv, int n_pos)
+{
+    if (gqa < 1 || gqa > kAttnOutMaxGqa || n_head_kv < 1 || n_head_kv > kAttnOutMaxParts || n_pos < 1 ||
+        n_pos > kAttnOutMaxPos)
+        return false;
+    switch (type) {
+    case kF32:
+    case kF16:
+    case kQ8_0:
+    case kQ4_0: return true;
+    case kQ6_K: return (64 * gqa) % 256 == 0;  // the group's columns are whole super-blocks
+    default: return false;
+    }
+}
+
+hipError_t launch_attn_out(int type, const AttnOutParams& p, hipStream_t s)
+{
+    if (!attn_out_supported(type, p.gqa, p.n_head_kv, p.n_pos) || p.rows < 1 || !p.q || !p.kc || !p.vc ||
+        !p.w || !p.parts || p.kv_dim != 64 * p.n_head_kv)
+        return hipErrorInvalidValue;
+    const dim3 grid((p.rows + kAttnOutRows - 1) / kAttnOutRows, p.n_head_kv);
+    switch (type) {
+    case kF32: hipLaunchKernelGGL(attn_out_kernel<kF32>, grid, dim3(kThreads), 0, s, p); break;
+    case kF16: hipLaunchKernelGGL(attn_out_kernel<kF16>, grid, dim3(kThreads), 0, s, p); break;
+    case kQ8_0: hipLaunchKernelGGL(attn_out_kernel<kQ8_0>, grid, dim3(kThreads), 0, s, p); break;
+    case kQ4_0: hipLaunchKernelGGL(attn_out_kernel<kQ4_0>, grid, dim3(kThreads), 0, s, p); break;
+    case kQ6_K: hipLaunchKernelGGL(attn_out_kernel<kQ6_K>, grid, dim3(kThreads), 0, s, p); break;
+    default: return hipErrorInvalidValue;
+    }
+    return hipGetLastError();
 }
 
 hipError_t launch_gemv(int type, const GemvParams& p, hipStream_t s)

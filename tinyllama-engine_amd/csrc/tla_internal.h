@@ -111,6 +111,9 @@ hipError_t launch_prefill_attention(const PrefillParams& p, hipStream_t s);
 enum WeightType { kF32 = 0, kF16 = 1, kQ4_0 = 2, kQ8_0 = 8, kQ6_K = 14 };
 constexpr int kGemvMaxVec = 8;    // vectors per launch (x staged in LDS)
 constexpr int kGemvMaxSeg = 3;    // matrices per launch (Wq, Wk, Wv)
+constexpr int kAttnOutMaxParts = 4;   // kv heads of a fused attention + W_o launch
+constexpr int kAttnOutMaxGqa = 8;     // q heads per kv head there
+constexpr int kAttnOutMaxPos = 64;    // context positions there
 
 struct GemvSegment {
     const unsigned char* w;  // [rows][row_bytes]
@@ -139,10 +142,41 @@ struct GemvParams {
                              // non-null in every launch (read whether or not used)
     int rope_rows;           // rows [0, rope_rows) are rotated in pairs (2i, 2i+1) of each
                              // 64-row head (RoPE of the q and k projections); 0: none
+    // Partial sums of the fused attention + W_o launch (launch_attn_out),
+    // n_parts vectors of cols (xparts) or rows (rparts) floats each, added
+    // to x in the order ((x + (p0 + p1 + ...)), partials summed first, in
+    // order):
+    const float* xparts;     // non-null: x is replaced by that sum before anything else (no x2)
+    const float* rparts;     // non-null (one segment, add = 1): the residual's old out[r] is
+    int n_parts;             // replaced by that sum; 1..kAttnOutMaxParts
 };
+
+// Decode attention of one token over a short context fused with the W_o
+// product (launch_attn_out): parts[g][r] = W_o[r][cols of kv head g's q
+// heads] . attention output of those heads, for g < n_head_kv.
+struct AttnOutParams {
+    const float* q;          // [n_head][64], rotated
+    const float* kc;         // the layer's key cache [n_ctx][kv_dim] (position n_pos - 1 appended)
+    const float* vc;         // the layer's value cache
+    int n_pos;               // positions 0 .. n_pos - 1, 1..kAttnOutMaxPos
+    int kv_dim;              // n_head_kv * 64
+    int gqa;                 // q heads per kv head, 1..kAttnOutMaxGqa
+    int n_head_kv;           // 1..kAttnOutMaxParts
+    const unsigned char* w;  // W_o [rows][row_bytes], rows x (n_head_kv * gqa * 64)
+    long long row_bytes;
+    long long group_bytes;   // bytes of gqa * 64 columns of a row
+    int rows;
+    float* parts;            // [n_head_kv][rows]
+};
+// Whether launch_attn_out takes this shape.
+bool attn_out_supported(int type, int gqa, int n_head_kv, int n_pos);
+hipError_t launch_attn_out(int type, const AttnOutParams& p, hipStream_t s);
 
 // Whether launch_gemv can pair gate and up rows (pair = 1) for this shape.
 bool gemv_can_pair(int type, int rows, int cols);
+// Whether a one-vector launch_gemv over rows of `cols` columns takes
+// residual partials (rparts): rows of at most 128 units (cols <= 8192).
+bool gemv_can_add_parts(int cols);
 // Whether launch_gemv can rotate row pairs in its epilogue (rope_rows > 0):
 // one vector, rows of at most 32 units (cols <= 2048).
 bool gemv_can_rope(int cols);
@@ -186,8 +220,8 @@ hipError_t launch_copy(void* dst, const void* src, size_t bytes, hipStream_t s);
 // per thread; sink [n_wg] is never written in practice.
 hipError_t launch_read_floor(const void* src, size_t bytes, int n_wg, int kind, int depth, float* sink,
                              hipStream_t s);
-// fp32 MFMA floor: n_wg workgroups of 4 waves, each wave iters x 16
-// v_mfma_f32_32x32x2f32; sink [n_wg] is never written in practice.
+// bf16 MFMA floor: n_wg workgroups of 4 waves, each wave iters x 16
+// v_mfma_f32_32x32x16_bf16; sink [n_wg] is never written in practice.
 hipError_t launch_mfma_floor(int n_wg, int iters, float* sink, hipStream_t s);
 // Zero fill by a kernel (no memset node: safe under stream capture).
 hipError_t launch_zero(void* dst, size_t bytes, hipStream_t s);
