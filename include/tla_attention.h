@@ -301,6 +301,16 @@ int tla_embed(tla_engine* e, float* out_dev, const void* table_dev, int token, i
 /* sample_argmax() src/ops.h:249: the first index of the largest logit. */
 int tla_argmax(tla_engine* e, const float* logits_dev, int n_vocab, int* token_host);
 
+/* matmul() then sample_argmax() (src/ops.cpp:959-983, 1587-1597), the last
+ * two steps of a greedy decode step (src/generate.cpp:84-90): out = W . x
+ * as tla_matmul (rows of at most 4096 columns), and *token_host = the first
+ * index of the largest out, from argmax keys each workgroup of the product
+ * posts with one atomic (a NaN never wins, except at index 0; -0 ties with
+ * +0), read by a one-wave launch.  tla_generate_greedy takes every token
+ * after its first this way. */
+int tla_matmul_argmax(tla_engine* e, float* out_dev, const void* w_dev, const float* x_dev, int rows,
+                      int cols, int type, int* token_host);
+
 /* The weights forward() reads from the GGUF file (src/forward.cpp:167-266),
  * as device pointers to the tensors' unchanged bytes (16-byte aligned) and
  * their ggml_type ids.  `output` is token_embd when the file has no

@@ -190,6 +190,54 @@ def test_argmax(O, engines):
         assert got == want, (got, want)
 
 
+def test_matmul_argmax(O, W, engines):
+    """matmul then sample_argmax with the argmax keys that the product's
+    workgroups post (the path tla_generate_greedy takes for every token
+    after its first): against the oracle's argmax of the same launch's
+    logits, over ties (identical rows: the first wins), NaN rows (never
+    win), a NaN at row 0 (index 0), +0 ties with everything else negative,
+    and random Q8_0 / Q6_K / F16 products with 512 workgroups (8 per key
+    slot)."""
+    eng = engines(1, 64)
+    lib = O.oracle()
+    from oracle import fptr
+    rg = np.random.default_rng(12)
+    rows, cols = 32000, 256
+    x = np.abs(rg.standard_normal(cols)).astype(np.float32) + 0.1  # positive
+    base = rg.standard_normal((rows, cols)).astype(np.float32)
+    cases = []
+    w = base.copy()
+    w[[5, 900, 31999]] = 1.0  # the largest logit, three times, bit-equal
+    cases.append(("ties", w, 5))
+    w = base.copy()
+    w[[3, 77]] = np.nan
+    cases.append(("nan rows", w, None))
+    w = base.copy()
+    w[0, 17] = np.nan
+    cases.append(("nan at 0", w, 0))
+    w = -np.abs(base) - 0.01  # every logit negative ...
+    w[[7, 10]] = 0.0          # ... but two exact zeros
+    cases.append(("zero ties", w, 7))
+    cases.append(("random f32", base, None))
+    with device_arrays() as track:
+        dx = track(eng.array(x))
+        out = track(eng.array((rows,)))
+        for name, wf, want_idx in cases:
+            dw = track(eng.array(np.ascontiguousarray(wf, np.float32)))
+            got = eng.matmul_argmax(out.ptr, dw.ptr, dx.ptr, rows, cols, Q.F32)
+            lg = out.download()
+            want = lib.oracle_argmax(fptr(lg), rows)
+            assert got == want, (name, got, want)
+            if want_idx is not None:
+                assert got == want_idx, (name, got, want_idx)
+        for t in (Q.Q8_0, Q.Q6_K, Q.F16):
+            raw = W.make_weights(t, rows, cols, salt=40 + t)
+            dw = track(eng.array(raw))
+            got = eng.matmul_argmax(out.ptr, dw.ptr, dx.ptr, rows, cols, t)
+            lg = out.download()
+            assert got == lib.oracle_argmax(fptr(lg), rows), t
+
+
 def run_forward(tla, eng, spec, t, tokens):
     dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
     try:

@@ -131,6 +131,7 @@ SIGNATURES = {
                                 C.c_int, _vp]),
     "tla_embed": (C.c_int, [_vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.c_int]),
     "tla_argmax": (C.c_int, [_vp, _vp, C.c_int, C.POINTER(C.c_int)]),
+    "tla_matmul_argmax": (C.c_int, [_vp, _vp, _vp, _vp, C.c_int, C.c_int, C.c_int, C.POINTER(C.c_int)]),
     "tla_forward": (C.c_int, [_vp, C.POINTER(Model), _vp, _vp, C.c_int, C.c_int, _vp]),
     "tla_prefill_forward": (C.c_int, [_vp, C.POINTER(Model), _vp, _vp, C.POINTER(C.c_int), C.c_int,
                                       C.c_int, _vp]),
@@ -351,6 +352,12 @@ class Engine:
     def argmax(self, logits: int, n_vocab: int) -> int:
         t = C.c_int()
         _check(lib().tla_argmax(self.h, logits, n_vocab, C.byref(t)), "tla_argmax")
+        return t.value
+
+    def matmul_argmax(self, out: int, w: int, x: int, rows: int, cols: int, wtype: int) -> int:
+        t = C.c_int()
+        _check(lib().tla_matmul_argmax(self.h, out, w, x, rows, cols, wtype, C.byref(t)),
+               "tla_matmul_argmax")
         return t.value
 
     def forward(self, model: "DeviceModel", kc: int, vc: int, token: int, pos: int, logits: int):

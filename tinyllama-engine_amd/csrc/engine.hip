@@ -131,6 +131,7 @@ struct tla_engine {
     unsigned char* kvp = nullptr; // prefill: K and V tiles as bf16 planes
     size_t kvp_bytes = 0;
     int* argmax_slot = nullptr;
+    unsigned long long* amax_keys = nullptr;  // kAmaxSlots keys (tla_matmul_argmax)
     long long opt_split = 0;
     int opt_plan = TLA_PLAN_AUTO;
     int opt_group = 0;  // kv heads per aligned-plan workgroup, 0 = per launch
@@ -432,6 +433,7 @@ int tla_engine_destroy(tla_engine* e)
     if (e->part) (void)hipFree(e->part);
     if (e->kvp) (void)hipFree(e->kvp);
     if (e->argmax_slot) (void)hipFree(e->argmax_slot);
+    if (e->amax_keys) (void)hipFree(e->amax_keys);
     if (e->rope) (void)hipFree(e->rope);
     if (e->stream) (void)hipStreamDestroy(e->stream);
     delete e;
@@ -1103,15 +1105,18 @@ struct FwdBufs {
     float *x, *xb, *q, *k, *v, *att, *hb, *hb2, *logits;
     float* parts;  // [kAttnOutMaxParts][n_embd]: the fused attention + W_o launch's partials
     int* tokens;
+    unsigned long long* amax;  // [n_amax rows][kAmaxSlots]: argmax keys of generated tokens
 };
 
-int fwd_bufs(tla_engine* e, const tla_model* m, int rows, int n_ints, FwdBufs* b)
+int fwd_bufs(tla_engine* e, const tla_model* m, int rows, int n_ints, FwdBufs* b, int n_amax = 0)
 {
     const size_t embd = e->cfg.n_embd, kv = e->kv_dim, ff = m->n_ff, nv = m->n_vocab;
     const size_t r = static_cast<size_t>(rows);
     const size_t parts_at = (r * (4 * embd + 2 * kv + 2 * ff) + nv + 63) / 64 * 64;  // 256-byte aligned
     const size_t floats = parts_at + kAttnOutMaxParts * embd;
-    const size_t bytes = (floats * sizeof(float) + 255) / 256 * 256 + (n_ints + 1) * sizeof(int);
+    const size_t ints_at = (floats * sizeof(float) + 255) / 256 * 256;
+    const size_t amax_at = (ints_at + (n_ints + 1) * sizeof(int) + 255) / 256 * 256;
+    const size_t bytes = amax_at + static_cast<size_t>(n_amax) * kAmaxSlots * sizeof(unsigned long long);
     if (bytes > e->fwd_bytes) {
         TLA_HIP(hipStreamSynchronize(e->stream));
         if (e->fwd) TLA_HIP(hipFree(e->fwd));
@@ -1133,19 +1138,25 @@ int fwd_bufs(tla_engine* e, const tla_model* m, int rows, int n_ints, FwdBufs* b
     b->hb2 = b->hb + ff;  // row 0's up projection; row t's gate at hb + 2*n_ff*t
     b->logits = b->hb + r * 2 * ff;
     b->parts = f + parts_at;
-    b->tokens = reinterpret_cast<int*>(static_cast<char*>(e->fwd) + (floats * sizeof(float) + 255) / 256 * 256);
+    b->tokens = reinterpret_cast<int*>(static_cast<char*>(e->fwd) + ints_at);
+    b->amax = reinterpret_cast<unsigned long long*>(static_cast<char*>(e->fwd) + amax_at);
     return TLA_OK;
 }
 
-// One forward() step: the token from `token`, or from token_dev when that is
-// non-null; logits written when `logits` is non-null.
+// One forward() step: the token from `token`, from token_dev when that is
+// non-null, or from the argmax keys at token_amax when that is non-null
+// (then also stored at token_out); logits written when `logits` is
+// non-null, with their argmax keys posted to logits_amax (kAmaxSlots keys,
+// zero before) when that is non-null.
 int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, float* vc,
-                 int token, const int* token_dev, int pos, float* logits)
+                 int token, const int* token_dev, int pos, float* logits,
+                 const unsigned long long* token_amax = nullptr, int* token_out = nullptr,
+                 unsigned long long* logits_amax = nullptr)
 {
     const int embd = e->cfg.n_embd, kv = e->kv_dim, ff = m->n_ff;
     const float eps = m->rms_norm_eps;
     if (int rc = check_hip(launch_embed(m->type_embd, b.x, static_cast<const unsigned char*>(m->token_embd),
-                                        token, token_dev, 1, embd, e->stream),
+                                        token, token_dev, 1, embd, e->stream, token_amax, token_out),
                            "embed"))
         return rc;
     for (int l = 0; l < e->cfg.n_layers; ++l) {
@@ -1259,11 +1270,23 @@ int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc,
             if (int rc = run_gemv(e, L.type_ffn, p)) return rc;
         }
     }
-    // final rmsnorm + classifier (src/forward.cpp:241-265)
-    if (logits)
-        if (int rc = gemv1(e, m->type_output, m->output, logits, m->n_vocab, embd, b.x, nullptr,
-                           m->output_norm, eps, 0))
-            return rc;
+    // final rmsnorm + classifier (src/forward.cpp:241-265), with the
+    // logits' argmax keys where asked (sample_argmax, src/ops.cpp:1587-1597)
+    if (logits) {
+        GemvParams p{};
+        p.seg[0] = {static_cast<const unsigned char*>(m->output), logits, m->n_vocab, m->n_vocab};
+        p.n_seg = 1;
+        p.total_rows = m->n_vocab;
+        p.cols = embd;
+        p.row_bytes = static_cast<int>(weight_row_bytes(m->type_output, embd));
+        p.n_vec = 1;
+        p.x = b.x;
+        p.x_stride = embd;
+        p.norm_w = m->output_norm;
+        p.eps = eps;
+        p.amax = logits_amax;
+        if (int rc = run_gemv(e, m->type_output, p)) return rc;
+    }
     return TLA_OK;
 }
 
@@ -1636,6 +1659,38 @@ int tla_argmax(tla_engine* e, const float* logits_dev, int n_vocab, int* token_h
     return ok();
 }
 
+int tla_matmul_argmax(tla_engine* e, float* out_dev, const void* w_dev, const float* x_dev, int rows,
+                      int cols, int type, int* token_host)
+{
+    if (int rc = check_engine(e)) return rc;
+    if (!out_dev || !w_dev || !x_dev || !token_host) return fail(TLA_ERR_INVALID_ARGUMENT, "NULL pointer");
+    if (rows < 1) return fail(TLA_ERR_INVALID_ARGUMENT, "rows %d < 1", rows);
+    if (int rc = check_gemv(type, cols, 1, w_dev)) return rc;
+    if (!gemv_can_amax(cols)) return fail(TLA_ERR_UNSUPPORTED, "argmax keys: rows of %d > 4096 columns", cols);
+    if (int rc = set_device(e)) return rc;
+    if (!e->argmax_slot) TLA_HIP(hipMalloc(reinterpret_cast<void**>(&e->argmax_slot), sizeof(int)));
+    if (!e->amax_keys)
+        TLA_HIP(hipMalloc(reinterpret_cast<void**>(&e->amax_keys), kAmaxSlots * sizeof(unsigned long long)));
+    TLA_HIP(launch_zero(e->amax_keys, kAmaxSlots * sizeof(unsigned long long), e->stream));
+    GemvParams p{};
+    p.seg[0] = {static_cast<const unsigned char*>(w_dev), out_dev, rows, 0};
+    p.n_seg = 1;
+    p.total_rows = rows;
+    p.cols = cols;
+    p.row_bytes = static_cast<int>(weight_row_bytes(type, cols));
+    p.n_vec = 1;
+    p.x = x_dev;
+    p.x_stride = cols;
+    p.amax = e->amax_keys;
+    if (int rc = run_gemv(e, type, p)) return rc;
+    hipError_t err = launch_amax_token(e->amax_keys, e->argmax_slot, e->stream);
+    if (err == hipSuccess)
+        err = hipMemcpyAsync(token_host, e->argmax_slot, sizeof(int), hipMemcpyDeviceToHost, e->stream);
+    if (err == hipSuccess) err = hipStreamSynchronize(e->stream);
+    if (err != hipSuccess) return fail(TLA_ERR_DEVICE, "matmul_argmax: %s", hipGetErrorString(err));
+    return ok();
+}
+
 int tla_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* value_cache_dev,
                 int token, int pos, float* logits_dev)
 {
@@ -1696,8 +1751,13 @@ int tla_generate_greedy(tla_engine* e, const tla_model* m, float* key_cache_dev,
             return fail(TLA_ERR_OUT_OF_RANGE, "prompt[%d] = %d outside [0, n_vocab)", i, prompt_host[i]);
     if (int rc = set_device(e)) return rc;
     const bool batch = (flags & TLA_BATCH_PROMPT) != 0;
+    // argmax keys by the classifier launch: rows of generated tokens 1 ..
+    // n_gen - 1 (n_gen rows, row 0 unused), zeroed by a fill kernel
+    const bool keys = gemv_can_amax(e->cfg.n_embd);
     FwdBufs b{};
-    if (int rc = fwd_bufs(e, m, batch ? n_prompt : 1, n_gen + n_prompt, &b)) return rc;
+    if (int rc = fwd_bufs(e, m, batch ? n_prompt : 1, n_gen + n_prompt, &b, keys ? n_gen : 0)) return rc;
+    if (keys && n_gen > 1)
+        TLA_HIP(launch_zero(b.amax, static_cast<size_t>(n_gen) * kAmaxSlots * sizeof(unsigned long long), e->stream));
     int pos = 0;
     if (batch) {
         int* prompt_dev = b.tokens + 1 + n_gen;
@@ -1714,15 +1774,34 @@ int tla_generate_greedy(tla_engine* e, const tla_model* m, float* key_cache_dev,
                                       i + 1 == n_prompt ? b.logits : nullptr))
                 return rc;
     }
-    // b.tokens[0]: the current token; b.tokens[1 + i]: generated token i
-    for (int i = 0; i < n_gen; ++i) {
-        if (int rc = check_hip(launch_argmax(b.tokens, b.tokens + 1 + i, b.logits, m->n_vocab, e->stream),
-                               "argmax"))
-            return rc;
-        if (i + 1 == n_gen) break;
-        if (int rc = forward_step(e, m, b, key_cache_dev, value_cache_dev, 0, b.tokens, pos++, b.logits))
-            return rc;
+    // b.tokens[0]: the current token; b.tokens[1 + i]: generated token i.
+    // Token 0 from the prompt's logits by the argmax launch; with keys, each
+    // later token i from the keys its step's classifier posted to row i,
+    // read by the next step's embedding launch (which stores it) or, for
+    // the last, by a one-wave launch.
+    if (int rc = check_hip(launch_argmax(b.tokens, b.tokens + 1, b.logits, m->n_vocab, e->stream), "argmax"))
+        return rc;
+    for (int i = 1; i < n_gen; ++i) {
+        unsigned long long* row = b.amax + static_cast<size_t>(i) * kAmaxSlots;
+        if (keys) {
+            const bool from_keys = i >= 2;  // token i - 1
+            if (int rc = forward_step(e, m, b, key_cache_dev, value_cache_dev, 0, from_keys ? nullptr : b.tokens,
+                                      pos++, b.logits, from_keys ? row - kAmaxSlots : nullptr,
+                                      from_keys ? b.tokens + i : nullptr, row))
+                return rc;
+        } else {
+            if (int rc = forward_step(e, m, b, key_cache_dev, value_cache_dev, 0, b.tokens, pos++, b.logits))
+                return rc;
+            if (int rc = check_hip(launch_argmax(b.tokens, b.tokens + 1 + i, b.logits, m->n_vocab, e->stream),
+                                   "argmax"))
+                return rc;
+        }
     }
+    if (keys && n_gen > 1)
+        if (int rc = check_hip(launch_amax_token(b.amax + static_cast<size_t>(n_gen - 1) * kAmaxSlots,
+                                                 b.tokens + n_gen, e->stream),
+                               "argmax keys"))
+            return rc;
     TLA_HIP(hipMemcpyAsync(tokens_host, b.tokens + 1, sizeof(int) * n_gen, hipMemcpyDeviceToHost, e->stream));
     TLA_HIP(hipStreamSynchronize(e->stream));
     return ok();

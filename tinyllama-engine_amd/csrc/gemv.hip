@@ -461,7 +461,44 @@ struct SegRegs {
 // launches carry none of the others' code: kPlain (y (+)= W.x), kPairEpi
 // (gate and up rows paired, SwiGLU written), kRopeEpi (q and k row pairs
 // rotated), kPartsEpi (y += W.x with the residual partials: rparts).
-constexpr int kPlain = 0, kPairEpi = 1, kRopeEpi = 2, kPartsEpi = 3;
+constexpr int kPlain = 0, kPairEpi = 1, kRopeEpi = 2, kPartsEpi = 3, kAmaxEpi = 4;
+
+// Argmax keys: the larger key is the larger value, or the equal value at the
+// smaller index (the reference's strict '>' scan from index 0,
+// src/ops.cpp:1587-1597).  Values map to unsigned integers in their order
+// (sign bit set: complemented, else the sign bit added), -0 taken as +0 so
+// that it ties with +0 as the comparison does; the index goes in the low
+// word, complemented.  A NaN never wins, except at index 0, where the scan
+// never leaves it: the largest key.  Every real key is above 0, the empty
+// slot.
+__device__ __forceinline__ unsigned long long amax_key(float v, int i)
+{
+    if (v != v) return i == 0 ? ~0ULL : 0ULL;
+    const unsigned u = __builtin_bit_cast(unsigned, v + 0.0f);
+    const unsigned ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+    return (static_cast<unsigned long long>(ord) << 32) | (0xFFFFFFFFu - static_cast<unsigned>(i));
+}
+
+__device__ __forceinline__ unsigned long long wave_max_u64(unsigned long long v)
+{
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) {
+        const unsigned lo = __shfl_xor(static_cast<unsigned>(v), o);
+        const unsigned hi = __shfl_xor(static_cast<unsigned>(v >> 32), o);
+        const unsigned long long w = (static_cast<unsigned long long>(hi) << 32) | lo;
+        v = w > v ? w : v;
+    }
+    return v;
+}
+
+// The token the kAmaxSlots keys give (every lane of the wave): the largest
+// key's index; 0 if no key was posted.
+__device__ __forceinline__ int amax_token(const unsigned long long* amax)
+{
+    static_assert(kAmaxSlots == 64, "one slot per lane");
+    const unsigned long long k = wave_max_u64(amax[threadIdx.x & 63]);
+    return k ? static_cast<int>(0xFFFFFFFFu - static_cast<unsigned>(k)) : 0;
+}
 
 // kSteps: unit steps of a row held at once (a row of up to kSteps x lanes
 // units is requested whole); rows with more units load the rest step by step.
@@ -570,6 +607,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
 {
     static_assert(!kMulti || kRows == 1, "several vectors take one row per lane group");
     static_assert(kEpi == kPlain || (!kMulti && (kSteps == 1 || kEpi == kPartsEpi)), "special epilogues: one vector");
+    [[maybe_unused]] unsigned long long best = 0;  // kAmaxEpi: this lane's largest argmax key
     static_assert(kEpi != kPairEpi || kRows == 2, "paired rows: two per lane group");
     static_assert(kEpi != kRopeEpi || (kRows == 1 && kLanesPerRow == 32), "RoPE: pairs in one wave");
     constexpr bool kZeroOffsets = kType == kQ8_0 || kType == kQ4_0 || kType == kQ6_K;
@@ -824,6 +862,12 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
                 float* o = g.out[k] + v * g.out_stride[k];
                 const float old = kMulti ? *o : g.residual(p, k);
                 if (g.valid[k] && l == kLanesPerRow - 1) *o = p.add ? old + t : t;
+                if constexpr (kEpi == kAmaxEpi) {
+                    if (g.valid[k] && l == kLanesPerRow - 1) {
+                        const unsigned long long key = amax_key(t, g.row[k]);
+                        best = key > best ? key : best;
+                    }
+                }
             }
         }
     };
@@ -853,6 +897,19 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
         __builtin_amdgcn_sched_barrier(0);
         run_pass(gb);
         ps += n_waves;
+    }
+    if constexpr (kEpi == kAmaxEpi) {
+        // the workgroup's largest key: over the wave, then over the waves;
+        // one atomic per workgroup
+        __shared__ unsigned long long s_best[kThreads / 64];
+        best = wave_max_u64(best);
+        if (lane == 0) s_best[threadIdx.x >> 6] = best;
+        __syncthreads();
+        if (threadIdx.x == 0) {
+#pragma unroll
+            for (int w = 1; w < kThreads / 64; ++w) best = s_best[w] > best ? s_best[w] : best;
+            if (best) atomicMax(p.amax + blockIdx.x % kAmaxSlots, best);
+        }
     }
 }
 
@@ -1078,11 +1135,15 @@ __device__ float embed_elem(int type, const unsigned char* row, int i)
 
 // Row blockIdx.y of out [n_tok][n] = table row tokens_dev[blockIdx.y] (or
 // `token` when tokens_dev is null).
+// With amax (one row): the token the argmax keys there give; token_out
+// (non-null) receives it from workgroup 0.
 __global__ __launch_bounds__(kThreads) void embed_kernel(int type, float* out,
                                                          const unsigned char* table, long long row_bytes,
-                                                         int token, const int* tokens_dev, int n)
+                                                         int token, const int* tokens_dev,
+                                                         const unsigned long long* amax, int* token_out, int n)
 {
-    const int t = tokens_dev ? tokens_dev[blockIdx.y] : token;
+    const int t = amax ? amax_token(amax) : tokens_dev ? tokens_dev[blockIdx.y] : token;
+    if (token_out && blockIdx.x == 0 && threadIdx.x == 0) token_out[blockIdx.y] = t;
     const unsigned char* row = table + row_bytes * t;
     float* o = out + static_cast<long long>(blockIdx.y) * n;
     for (int i = blockIdx.x * kThreads + threadIdx.x; i < n; i += gridDim.x * kThreads)
@@ -1211,6 +1272,12 @@ hipError_t launch_typed(const GemvParams& p, hipStream_t s)
 {
     const int units = p.cols / kUnit;
     if (p.rope_rows > 0) return launch_shaped<kType, 32, 1, 1, false, kRopeEpi>(p, s);  // gemv_can_rope
+    if (p.amax) {  // one vector, one segment, rows of <= 64 units, no residual
+        if (p.n_vec != 1 || p.n_seg != 1 || units > 64 || p.pair || p.add || p.rparts) return hipErrorInvalidValue;
+        constexpr int kR = Unit<kType>::kRows;
+        return units <= 32 ? launch_shaped<kType, 32, kR, 1, false, kAmaxEpi>(p, s)
+                           : launch_shaped<kType, 64, kR, 1, false, kAmaxEpi>(p, s);
+    }
     if (p.rparts) {  // gemv_can_add_parts: one vector, one segment, rows of <= 128 units
         if (p.n_vec != 1 || p.n_seg != 1 || units > 128 || p.pair) return hipErrorInvalidValue;
         return units <= 32   ? launch_shaped<kType, 32, 1, 1, false, kPartsEpi>(p, s)
@@ -1263,6 +1330,11 @@ long long weight_row_bytes(int type, int cols)
 bool gemv_can_add_parts(int cols)
 {
     return cols / kUnit <= 128;
+}
+
+bool gemv_can_amax(int cols)
+{
+    return cols / kUnit <= 64;
 }
 
 bool gemv_can_rope(int cols)
@@ -1342,11 +1414,25 @@ hipError_t launch_elementwise_mul(float* a, const float* b, int size, hipStream_
 }
 
 hipError_t launch_embed(int type, float* out, const unsigned char* table, int token,
-                        const int* tokens_dev, int n_tok, int n, hipStream_t s)
+                        const int* tokens_dev, int n_tok, int n, hipStream_t s,
+                        const unsigned long long* amax, int* token_out)
 {
+    if (amax && n_tok != 1) return hipErrorInvalidValue;
     const int blocks = std::min(64, (n + kThreads - 1) / kThreads);
     hipLaunchKernelGGL(embed_kernel, dim3(blocks, n_tok), dim3(kThreads), 0, s, type, out, table,
-                       weight_row_bytes(type, n), token, tokens_dev, n);
+                       weight_row_bytes(type, n), token, tokens_dev, amax, token_out, n);
+    return hipGetLastError();
+}
+
+__global__ __launch_bounds__(64) void amax_token_kernel(const unsigned long long* amax, int* out)
+{
+    const int t = amax_token(amax);
+    if (threadIdx.x == 0) *out = t;
+}
+
+hipError_t launch_amax_token(const unsigned long long* amax, int* out, hipStream_t s)
+{
+    hipLaunchKernelGGL(amax_token_kernel, dim3(1), dim3(64), 0, s, amax, out);
     return hipGetLastError();
 }
 

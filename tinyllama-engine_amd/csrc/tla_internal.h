@@ -114,6 +114,7 @@ constexpr int kGemvMaxSeg = 3;    // matrices per launch (Wq, Wk, Wv)
 constexpr int kAttnOutMaxParts = 4;   // kv heads of a fused attention + W_o launch
 constexpr int kAttnOutMaxGqa = 8;     // q heads per kv head there
 constexpr int kAttnOutMaxPos = 64;    // context positions there
+constexpr int kAmaxSlots = 64;        // argmax key slots of a GEMV launch (GemvParams::amax)
 
 struct GemvSegment {
     const unsigned char* w;  // [rows][row_bytes]
@@ -149,6 +150,12 @@ struct GemvParams {
     const float* xparts;     // non-null: x is replaced by that sum before anything else (no x2)
     const float* rparts;     // non-null (one segment, add = 1): the residual's old out[r] is
     int n_parts;             // replaced by that sum; 1..kAttnOutMaxParts
+    // Non-null (one vector, one segment, add = 0, rows of <= 64 units): each
+    // workgroup also posts the largest (value, first index) of its outputs,
+    // as an argmax key, with an atomic max into amax[blockIdx % kAmaxSlots]
+    // (which start at zero).  The largest key of the slots is the argmax of
+    // all outputs, by the rule of launch_argmax.
+    unsigned long long* amax;
 };
 
 // Decode attention of one token over a short context fused with the W_o
@@ -177,6 +184,9 @@ bool gemv_can_pair(int type, int rows, int cols);
 // Whether a one-vector launch_gemv over rows of `cols` columns takes
 // residual partials (rparts): rows of at most 128 units (cols <= 8192).
 bool gemv_can_add_parts(int cols);
+// Whether a one-vector launch_gemv over rows of `cols` columns posts argmax
+// keys (amax): rows of at most 64 units (cols <= 4096).
+bool gemv_can_amax(int cols);
 // Whether launch_gemv can rotate row pairs in its epilogue (rope_rows > 0):
 // one vector, rows of at most 32 units (cols <= 2048).
 bool gemv_can_rope(int cols);
@@ -190,8 +200,13 @@ hipError_t launch_silu(float* x, int size, hipStream_t s);
 hipError_t launch_elementwise_mul(float* a, const float* b, int size, hipStream_t s);
 // out[t][n] = table row tokens_dev[t] for t < n_tok (tokens_dev null: one
 // row, `token`).
+// With amax non-null (one row): the token is the argmax the kAmaxSlots keys
+// there give, also stored at token_out when that is non-null.
 hipError_t launch_embed(int type, float* out, const unsigned char* table, int token,
-                        const int* tokens_dev, int n_tok, int n, hipStream_t s);
+                        const int* tokens_dev, int n_tok, int n, hipStream_t s,
+                        const unsigned long long* amax = nullptr, int* token_out = nullptr);
+// *out = the argmax the kAmaxSlots keys at amax give.
+hipError_t launch_amax_token(const unsigned long long* amax, int* out, hipStream_t s);
 // *out = first index of the largest value (NaN never wins; a NaN at 0 gives 0),
 // also stored at out2 when non-null.
 hipError_t launch_argmax(int* out, int* out2, const float* x, int n, hipStream_t s);
