@@ -341,15 +341,16 @@ def test_forward_wide_embedding(tla, O, W, engines):
     (512, 8, 8, "W_Q4_0", "W_Q8_0"),  # 8 kv heads: no fused launch at any position
 ])
 def test_forward_short_context_fusion(tla, O, W, engines, n_embd, n_head, n_head_kv, wtype, wo_type):
-    """A decode step over at most 64 positions runs attention and W_o as one
-    launch (each workgroup recomputes one kv head's attention; the W_o
-    partials per kv head reach x through the FFN launches); from position
-    64 on, the attention launch and the W_o GEMV.  70 tokens one at a time
-    against the oracle, every step's logits (the last 6 past the switch)."""
-    spec = W.ModelSpec(2, n_embd, n_head, n_head_kv, 512, 384, 72)
+    """A decode step over at most 192 positions runs attention and W_o as
+    one launch (each workgroup recomputes one kv head's attention, waves
+    taking 1-3 tiles of 16 positions; the W_o partials per kv head reach x
+    through the FFN launches); from position 192 on, the attention launch
+    and the W_o GEMV.  200 tokens one at a time against the oracle, every
+    step's logits (the last 8 past the switch)."""
+    spec = W.ModelSpec(2, n_embd, n_head, n_head_kv, 512, 384, 208)
     t = W.make_model(spec, getattr(W, wtype), salt=91 + n_head,
                      overrides={"attn_output.weight": getattr(W, wo_type)})
-    toks = [(37 * i + 11) % spec.n_vocab for i in range(70)]
+    toks = [(37 * i + 11) % spec.n_vocab for i in range(200)]
     om = O.Model(spec, t)
     want = np.stack([om.forward(tk, i) for i, tk in enumerate(toks)])
     eng = spec_engine(engines, spec)

@@ -1196,8 +1196,9 @@ int forward_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc,
             if (int rc = gemv1(e, L.type_v, L.wv, b.v, kv, embd, b.xb, nullptr, nullptr, 0.f, 0)) return rc;
         }
         // Attention and x += Wo . att (src/forward.cpp:198-213).  Over a
-        // short context, one launch: the partials of W_o per kv head, which
-        // the FFN launches add to x (x itself is not written here).
+        // context of at most kAttnOutMaxPos positions, one launch: the
+        // partials of W_o per kv head, which the FFN launches add to x (x
+        // itself is not written here).
         const int gqa = e->cfg.n_head / e->cfg.n_head_kv;
         const bool fused_out = rope_in_gemv && gemv_can_add_parts(ff) &&
                                attn_out_supported(L.type_o, gqa, e->cfg.n_head_kv, pos + 1);

@@ -929,16 +929,24 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
 // after the first of them.
 //
 // The W_o weights of a lane (one 64-column unit of one row: 8 lanes per
-// row, 8 rows per wave) are requested first; q, the K tile and the V tile
-// of the wave follow.  Wave w takes positions 16w .. 16w+15, with the
-// decode kernel's MFMA layouts:
+// row, 8 rows per wave) are requested first; q and the wave's first K and V
+// tile follow.  Wave w takes the 16-position tiles w, w + 4, w + 8 (each
+// tile's successor requested before it is computed), with the decode
+// kernel's MFMA layouts:
 //   S^T[16 pos][16 heads] = K[16 pos][64] . Q^T[64][16 heads]   16 x v_mfma_f32_16x16x4f32
-//   O^T[64 d][16 heads]   = V^T[64 d][16 pos] . P^T[16 pos][16 heads]
+//   O^T[64 d][16 heads]  += V^T[64 d][16 pos] . P^T[16 pos][16 heads]
 // (heads gqa .. 15 zero; lane 16k + i holds dims 16k .. 16k+15 of key i and
-// of q head i, and the S accumulator is the P.V B operand).  The waves meet
-// in LDS twice: for the heads' maxima, then for the sums and O, combined in
-// wave order.  The output is the x of the W_o sub-matrix, staged as the
-// GEMV stages x (padded, with the 16-column sums).
+// of q head i, and the S accumulator is the P.V B operand), and a running
+// maximum and sum per head.  The waves meet in LDS twice: for the heads'
+// maxima, then for the sums and O scaled to them, added in wave order.  The
+// output is the x of the W_o sub-matrix, staged as the GEMV stages x
+// (padded, with the 16-column sums).
+//
+// Against the attention launch and the W_o GEMV it replaces (MI355X, Q4_0
+// TinyLlama, 20 greedy tokens after prompts of 32-200 tokens): 534 against
+// 580 us per token at positions 32-51, 576 against 612 at 100-119, 610
+// against 632 at 140-159, 614 against 631 at 170-189 (three tiles per
+// wave), 644 against 635 at 200-219 (a fourth tile): hence 192 positions.
 typedef float attn_f4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ attn_f4 mfma16x4(float a, float b, attn_f4 c)
@@ -952,7 +960,7 @@ constexpr int kAttnOutCols = kAttnOutMaxGqa * 64;
 template <int kType>
 __global__ __launch_bounds__(kThreads) void attn_out_kernel(const AttnOutParams p)
 {
-    static_assert(kThreads == 256 && kAttnOutMaxPos == 64, "4 waves of 16 positions");
+    static_assert(kThreads == 256 && kAttnOutMaxPos % 64 == 0, "4 waves of 16-position tiles");
     __shared__ __align__(16) float xs[xs_floats(kAttnOutCols)];
     __shared__ float s16[kAttnOutCols / 16];
     __shared__ float s_max[4][16], s_sum[4][16];
@@ -972,70 +980,95 @@ __global__ __launch_bounds__(kThreads) void attn_out_kernel(const AttnOutParams 
     Unit<kType> un;
     un.load(wrow, 0, units, lu);
 
-    // ---- q, K and V of this wave's 16 positions (rows past n_pos read row
-    // 0, masked below; V rows there are weighted by 0) ----
+    // ---- attention of the group's heads: wave w takes the 16-position
+    // tiles w, w + 4, ... (rows past n_pos read row 0, masked; V rows there
+    // are weighted by 0), with a running maximum, sum and O per head, the
+    // next tile's K and V requested before the current one is computed ----
     const int i = lane & 15, k4 = lane >> 4;
     const bool head = i < p.gqa;
-    const int pk = 16 * wave + i;
-    const float4* kr4 = reinterpret_cast<const float4*>(p.kc + static_cast<long long>(pk < p.n_pos ? pk : 0) * p.kv_dim +
-                                                        64 * g + 16 * k4);
-    const float4* qr4 = reinterpret_cast<const float4*>(p.q + static_cast<long long>(g * p.gqa + (head ? i : 0)) * 64 +
-                                                        16 * k4);
-    float4 kr[4], qr[4], vr[4];
+    const int n_tiles = (p.n_pos + 15) >> 4;
+    const float* kg = p.kc + 64 * g + 16 * k4;  // this lane's K dims of position 0
+    const float* vg = p.vc + 64 * g + 4 * i;    // this lane's V dims of position 0
+    auto load_tile = [&](int j, float4 (&kr)[4], float4 (&vr)[4]) {
+        const int pk = 16 * j + i;
+        const float4* k4p = reinterpret_cast<const float4*>(kg + static_cast<long long>(pk < p.n_pos ? pk : 0) * p.kv_dim);
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        kr[s] = kr4[s];
-        qr[s] = qr4[s];
+        for (int s = 0; s < 4; ++s) kr[s] = k4p[s];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const int pv = 16 * j + 4 * k4 + s;
+            vr[s] = *reinterpret_cast<const float4*>(vg + static_cast<long long>(pv < p.n_pos ? pv : 0) * p.kv_dim);
+        }
+    };
+    float4 qr[4];
+    {
+        const float4* qr4 = reinterpret_cast<const float4*>(p.q + static_cast<long long>(g * p.gqa + (head ? i : 0)) * 64 +
+                                                            16 * k4);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) qr[s] = qr4[s];
     }
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const int pv = 16 * wave + 4 * k4 + s;
-        vr[s] = *reinterpret_cast<const float4*>(p.vc + static_cast<long long>(pv < p.n_pos ? pv : 0) * p.kv_dim +
-                                                 64 * g + 4 * i);
-    }
-
-    // scores in log2 units: q.k / sqrt(64) * log2(e)
-    attn_f4 sacc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const float qv[4] = {head ? qr[s].x : 0.f, head ? qr[s].y : 0.f, head ? qr[s].z : 0.f, head ? qr[s].w : 0.f};
-        const float kv[4] = {kr[s].x, kr[s].y, kr[s].z, kr[s].w};
-#pragma unroll
-        for (int c = 0; c < 4; ++c) sacc = mfma16x4(kv[c], qv[c], sacc);
-    }
-    constexpr float kScale = 0.125f * 1.4426950408889634f;
-    float t[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) t[r] = 16 * wave + 4 * k4 + r < p.n_pos ? sacc[r] * kScale : -__builtin_huge_valf();
-    float m = fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]));
-    m = fmaxf(m, __shfl_xor(m, 16));
-    m = fmaxf(m, __shfl_xor(m, 32));
-    if (k4 == 0) s_max[wave][i] = m;
-    __syncthreads();
-    // position 0 is in wave 0's tile: every head's maximum is finite
-    const float mg = fmaxf(fmaxf(s_max[0][i], s_max[1][i]), fmaxf(s_max[2][i], s_max[3][i]));
-    float pr[4], lsum = 0.f;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-        pr[r] = __builtin_amdgcn_exp2f(t[r] - mg);  // exp2(-inf) = 0 for masked positions
-        lsum += pr[r];
-    }
-    lsum += __shfl_xor(lsum, 16);
-    lsum += __shfl_xor(lsum, 32);
-    if (k4 == 0) s_sum[wave][i] = lsum;
-
-    // O^T block b, rows 4 k4 + r: dim 4 (4 k4 + r) + b of head i
+    float4 kb[2][4], vb[2][4];
+    if (wave < n_tiles) load_tile(wave, kb[0], vb[0]);
+    constexpr float kScale = 0.125f * 1.4426950408889634f;  // 1 / sqrt(64) in log2 units
+    float m_run = -__builtin_huge_valf(), l_run = 0.f;
     attn_f4 o[4] = {};
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-        const float vv[4] = {vr[s].x, vr[s].y, vr[s].z, vr[s].w};
+    for (int it = 0; it < kAttnOutMaxPos / 64; ++it) {
+        const int j = wave + 4 * it;
+        if (j >= n_tiles) break;  // uniform per wave
+        float4 (&kr)[4] = kb[it & 1];
+        float4 (&vr)[4] = vb[it & 1];
+        if (it + 1 < kAttnOutMaxPos / 64 && j + 4 < n_tiles) load_tile(j + 4, kb[(it + 1) & 1], vb[(it + 1) & 1]);
+        // S^T: lane 16 k4 + i holds positions 16 j + 4 k4 + r of head i
+        attn_f4 sacc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int b = 0; b < 4; ++b) o[b] = mfma16x4(vv[b], pr[s], o[b]);
+        for (int s = 0; s < 4; ++s) {
+            const float qv[4] = {head ? qr[s].x : 0.f, head ? qr[s].y : 0.f, head ? qr[s].z : 0.f,
+                                 head ? qr[s].w : 0.f};
+            const float kv[4] = {kr[s].x, kr[s].y, kr[s].z, kr[s].w};
+#pragma unroll
+            for (int c = 0; c < 4; ++c) sacc = mfma16x4(kv[c], qv[c], sacc);
+        }
+        float t[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+            t[r] = 16 * j + 4 * k4 + r < p.n_pos ? sacc[r] * kScale : -__builtin_huge_valf();
+        float m = fmaxf(fmaxf(t[0], t[1]), fmaxf(t[2], t[3]));
+        m = fmaxf(m, __shfl_xor(m, 16));
+        m = fmaxf(m, __shfl_xor(m, 32));
+        const float m_new = fmaxf(m_run, m);  // finite: position 16 j is in the context
+        const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);  // 0 on the wave's first tile
+        float pr[4], lsum = 0.f;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            pr[r] = __builtin_amdgcn_exp2f(t[r] - m_new);  // exp2(-inf) = 0 for masked positions
+            lsum += pr[r];
+        }
+        lsum += __shfl_xor(lsum, 16);
+        lsum += __shfl_xor(lsum, 32);
+        l_run = l_run * alpha + lsum;
+        m_run = m_new;
+        // O^T block b, rows 4 k4 + r: dim 4 (4 k4 + r) + b of head i
+#pragma unroll
+        for (int b = 0; b < 4; ++b) o[b] *= alpha;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+            const float vv[4] = {vr[s].x, vr[s].y, vr[s].z, vr[s].w};
+#pragma unroll
+            for (int b = 0; b < 4; ++b) o[b] = mfma16x4(vv[b], pr[s], o[b]);
+        }
     }
+    // the waves' states scaled to the heads' common maximum (position 0 is
+    // wave 0's: finite); a wave without tiles contributes 0
+    if (k4 == 0) s_max[wave][i] = m_run;
+    __syncthreads();
+    const float mg = fmaxf(fmaxf(s_max[0][i], s_max[1][i]), fmaxf(s_max[2][i], s_max[3][i]));
+    const float sw = __builtin_amdgcn_exp2f(m_run - mg);
+    if (k4 == 0) s_sum[wave][i] = l_run * sw;
 #pragma unroll
     for (int b = 0; b < 4; ++b)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) s_o[wave][65 * i + 4 * (4 * k4 + r) + b] = o[b][r];
+        for (int r = 0; r < 4; ++r) s_o[wave][65 * i + 4 * (4 * k4 + r) + b] = o[b][r] * sw;
     __syncthreads();
 
     // attention output of the group's heads = x of the W_o sub-matrix

@@ -113,7 +113,7 @@ constexpr int kGemvMaxVec = 8;    // vectors per launch (x staged in LDS)
 constexpr int kGemvMaxSeg = 3;    // matrices per launch (Wq, Wk, Wv)
 constexpr int kAttnOutMaxParts = 4;   // kv heads of a fused attention + W_o launch
 constexpr int kAttnOutMaxGqa = 8;     // q heads per kv head there
-constexpr int kAttnOutMaxPos = 64;    // context positions there
+constexpr int kAttnOutMaxPos = 192;   // context positions there (3 tiles of 16 per wave)
 constexpr int kAmaxSlots = 64;        // argmax key slots of a GEMV launch (GemvParams::amax)
 
 struct GemvSegment {
