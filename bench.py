@@ -28,7 +28,8 @@ Other workloads (--workload): decode_long (16384 context, batch 8, 22 layers),
 decode_ragged (64 sequences, L in [256, 2048], 22 layers), prefill,
 decode_single (one layer, position 127: reported as latency), decode_sweep
 (batch 1, 22 layers, contexts 2K-16K), prefill_sweep (one prompt of 512 to
-4096 tokens, 22 layers), proj (the
+4096 tokens, 22 layers), prefill_layer_sweep (one layer per launch, 128 to
+2048 tokens: the launches a batched prompt makes), proj (the
 attention block's projections for a 22-layer decode step, and the GEMV kernel
 on a 32000 x 2048 matrix in every weight format), matmul (that GEMV alone in
 one format, --wtype), copy (the
@@ -391,11 +392,13 @@ def run_prefill(steps, warmup, cpu, n_layers=22, n_tok=512, label="prefill"):
 
 
 def run_prefill_sweep(steps, warmup, lengths=(512, 1024, 2048, 4096), n_layers=22):
-    """Causal prefill of one prompt of each length over 22 layers (Q/K/V
-    N(0,1), seeded): the attention kernel's TFLOP/s as the prompt grows."""
+    """Causal prefill of one prompt of each length over n_layers layers in
+    one launch (Q/K/V N(0,1), seeded): the attention kernel's TFLOP/s as the
+    prompt grows."""
     out = []
     for n_tok in lengths:
-        r = run_prefill(steps, warmup, False, n_layers, n_tok, label=f"prefill {n_tok} tokens")
+        r = run_prefill(steps, warmup, False, n_layers, n_tok,
+                        label=f"prefill {n_tok} tokens" + ("" if n_layers == 22 else f", {n_layers} layer(s)"))
         out.append({"n_tok": n_tok, "us": round(r["prefill_kernel_ms"] * 1e3, 2),
                     "flops": r["algorithmic_flops"], "TFLOP_s": r["roofline"]["achieved"],
                     "frac": r["roofline"]["frac"]})
@@ -967,7 +970,8 @@ def main():
     ap.add_argument("--workload", default="decode_model",
                     choices=["decode_model", "decode_long", "decode_ragged", "decode_single",
                              "prefill", "proj", "matmul", "generate", "decode_sweep",
-                             "prefill_sweep", "copy", "read", "read_floor", "mfma_floor", "dropin"])
+                             "prefill_sweep", "prefill_layer_sweep", "copy", "read", "read_floor", "mfma_floor",
+                             "dropin"])
     ap.add_argument("--wtype", default=None, choices=["f32", "f16", "q8_0", "q4_0", "q6_k"],
                     help="weight format of the matmul (default q8_0) or generate (q4_0) workload")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
@@ -1049,15 +1053,18 @@ def main():
                                      "contexts": [x["ctx"] for x in r], "parallelism": "none"},
                           "sweep": r}))
         return
-    if args.workload == "prefill_sweep":
-        r = run_prefill_sweep(args.steps, args.warmup)
+    if args.workload in ("prefill_sweep", "prefill_layer_sweep"):
+        one = args.workload == "prefill_layer_sweep"
+        n_layers = 1 if one else 22
+        r = run_prefill_sweep(args.steps, args.warmup, (128, 256, 512, 1024, 2048) if one else
+                              (512, 1024, 2048, 4096), n_layers)
         last = r[-1]
         print(json.dumps({"metric": HEADLINE_METRIC, "value": last["TFLOP_s"], "unit": "TFLOP/s",
                           "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                           "ms_per_step": last["us"] / 1e3, "higher_is_better": True,
                           "scaling": "weak", "vs_baseline": None, "dtype": "f32",
                           "data": "synthetic",
-                          "config": {"workload": "prefill_sweep", "batch": 1, "n_layers": 22,
+                          "config": {"workload": args.workload, "batch": 1, "n_layers": n_layers,
                                      "lengths": [x["n_tok"] for x in r], "parallelism": "none"},
                           "sweep": r}))
         return
