@@ -339,8 +339,14 @@ typedef struct tla_model {
  * embedding, every layer (rmsnorm + Q/K/V, RoPE + append + attention, W_o +
  * residual, rmsnorm + SwiGLU FFN + residual) and the classifier, on the
  * device: logits_dev [n_vocab].  Caches as from tla_kv_cache_alloc (one
- * sequence); the residual stream and scratch are the engine's.  5 launches
- * per layer + 2. */
+ * sequence); the residual stream and scratch are the engine's.  4 launches
+ * per layer + 2 where the layer's Q/K/V launch can rotate and append (one
+ * weight type for the three, n_embd <= 2048), pos < 192, n_head_kv <= 4,
+ * n_head / n_head_kv <= 8 (a multiple of 4 for a Q6_K W_o) and n_ff <=
+ * 8192: attention and W_o are then one
+ * launch whose workgroups each recompute one kv head's attention and write
+ * W_o's partial products for that head's columns, which the FFN launches
+ * add to the residual; else 5 per layer + 2. */
 int tla_forward(tla_engine* e, const tla_model* m, float* key_cache_dev, float* value_cache_dev,
                 int token, int pos, float* logits_dev);
 
@@ -364,9 +370,12 @@ int tla_prefill_forward(tla_engine* e, const tla_model* m, float* key_cache_dev,
  * temperature 0, without the tokenizer): forward() over the prompt at
  * positions 0..n_prompt-1 (token by token, or as one batch with
  * TLA_BATCH_PROMPT), then n_gen tokens each from the argmax of the
- * previous logits.  The sampled token stays on the device between steps,
- * so every launch is queued without waiting; tokens_host [n_gen] is
- * written at the end.  The caller stops at its EOS token, as the reference
+ * previous logits: the first by an argmax launch, the later ones (n_embd
+ * <= 4096) from the argmax keys the classifier's workgroups post, as
+ * tla_matmul_argmax, read by the next step's embedding launch (engine
+ * memory: 512 bytes per generated token).  The sampled token stays on the
+ * device between steps, so every launch is queued without waiting;
+ * tokens_host [n_gen] is written at the end.  The caller stops at its EOS token, as the reference
  * does (tokens after it are computed but not used).  Needs n_prompt >= 1
  * and n_prompt + n_gen - 1 <= n_ctx. */
 int tla_generate_greedy(tla_engine* e, const tla_model* m, float* key_cache_dev,
@@ -375,7 +384,8 @@ int tla_generate_greedy(tla_engine* e, const tla_model* m, float* key_cache_dev,
 
 /* ---- measurement hooks (no reference counterpart) ------------------- */
 enum tla_kernel_id {
-    TLA_KERNEL_DECODE = 0,  /* split-KV decode attention: RoPE + append +
+    TLA_KERNEL_DECODE = 0,  /* split-KV decode attention (and forward()'s
+                               short-context attention + W_o): RoPE + append +
                                attention + split merge, one launch           */
     TLA_KERNEL_PREFILL = 1, /* causal MFMA prefill attention                 */
     TLA_KERNEL_APPEND = 2,  /* prefill RoPE + cache append                   */
