@@ -303,6 +303,30 @@ def test_generate_greedy_matches_reference(tla, O, W, engines, name):
     assert got == g[f"{name}_greedy"].tolist()
 
 
+@pytest.mark.parametrize("name", ["q8_0", "f32"])
+def test_generate_greedy_short_runs(tla, O, W, engines, name):
+    """1, 2 and 3 generated tokens are the first tokens of the golden run:
+    the first comes from the argmax launch alone, the second from the keys
+    the classifier posts read by the one-wave launch at the end, the third
+    also through the embedding launch's read of the keys."""
+    g = golden("forward.npz")
+    spec, t = model_from_golden(W, g, name)
+    eng = spec_engine(engines, spec)
+    prompt, want = g["prompt"].tolist(), g[f"{name}_greedy"].tolist()
+    assert len(want) >= 3
+    dm = tla.DeviceModel(eng, t, spec.n_ff, spec.n_vocab, spec.rms_norm_eps)
+    try:
+        with device_arrays() as track:
+            kc, vc = eng.kv_cache(1)
+            track(kc), track(vc)
+            for n in (1, 2, 3):
+                for batch in (False, True):
+                    got = eng.generate_greedy(dm, kc.ptr, vc.ptr, prompt, n, batch_prompt=batch)
+                    assert got == want[:n], (n, batch, got)
+    finally:
+        dm.free()
+
+
 def test_forward_tinyllama_shape(tla, O, W, engines):
     """TinyLlama's shapes (22 layers, n_embd 2048, 32/4 heads, n_ff 5632,
     vocabulary 32000), Q8_0 weights with a Q6_K classifier, against the
