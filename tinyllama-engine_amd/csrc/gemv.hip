@@ -928,11 +928,13 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const GemvParams p)
 // the rows / 32 workgroups that need it, from cache rows that sit in L2
 // after the first of them.
 //
-// The W_o weights of a lane (one 64-column unit of one row: 8 lanes per
-// row, 8 rows per wave) are requested first; q and the wave's first K and V
-// tile follow.  Wave w takes the 16-position tiles w, w + 4, w + 8 (each
-// tile's successor requested before it is computed), with the decode
-// kernel's MFMA layouts:
+// q and the wave's first K and V tile are requested first, then the W_o
+// weights of the lane (one 64-column unit of one row: 8 lanes per row, 8
+// rows per wave), which are used last: loads complete in order, and the
+// attention waiting behind the weights measured 532-535 against 515-516 us
+// per token (Q4_0, 20 tokens after a 32-token prompt).  Wave w takes the
+// 16-position tiles w, w + 4, w + 8 (each tile's successor requested before
+// it is computed), with the decode kernel's MFMA layouts:
 //   S^T[16 pos][16 heads] = K[16 pos][64] . Q^T[64][16 heads]   16 x v_mfma_f32_16x16x4f32
 //   O^T[64 d][16 heads]  += V^T[64 d][16 pos] . P^T[16 pos][16 heads]
 // (heads gqa .. 15 zero; lane 16k + i holds dims 16k .. 16k+15 of key i and
@@ -970,7 +972,8 @@ __global__ __launch_bounds__(kThreads) void attn_out_kernel(const AttnOutParams 
     const int g = blockIdx.y;
     const int units = p.gqa;  // 64-column units of a row's group
 
-    // ---- W_o: lane l of row group `sub` holds unit l of its row ----
+    // ---- W_o: lane l of row group `sub` holds unit l of its row (loaded
+    // after the attention's operands) ----
     const int sub = lane >> 3, l = lane & 7;
     const int lu = l < units ? l : 0;  // lanes past the row's units load unit 0 (not used)
     const int row = blockIdx.x * kAttnOutRows + wave * 8 + sub;
@@ -978,7 +981,6 @@ __global__ __launch_bounds__(kThreads) void attn_out_kernel(const AttnOutParams 
     const unsigned char* wrow = p.w + static_cast<long long>(valid ? row : 0) * p.row_bytes +
                                 static_cast<long long>(g) * p.group_bytes;
     Unit<kType> un;
-    un.load(wrow, 0, units, lu);
 
     // ---- attention of the group's heads: wave w takes the 16-position
     // tiles w, w + 4, ... (rows past n_pos read row 0, masked; V rows there
@@ -1009,6 +1011,7 @@ __global__ __launch_bounds__(kThreads) void attn_out_kernel(const AttnOutParams 
     }
     float4 kb[2][4], vb[2][4];
     if (wave < n_tiles) load_tile(wave, kb[0], vb[0]);
+    un.load(wrow, 0, units, lu);  // the weights after q, K and V: used last
     constexpr float kScale = 0.125f * 1.4426950408889634f;  // 1 / sqrt(64) in log2 units
     float m_run = -__builtin_huge_valf(), l_run = 0.f;
     attn_f4 o[4] = {};
