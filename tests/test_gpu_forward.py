@@ -363,6 +363,8 @@ def test_forward_wide_embedding(tla, O, W, engines):
     (1024, 16, 2, "W_F16", "W_Q4_0"),  # gqa 8
     (512, 8, 1, "W_Q8_0", "W_F16"),   # gqa 8, one kv head
     (512, 8, 8, "W_Q4_0", "W_Q8_0"),  # 8 kv heads: no fused launch at any position
+    (768, 12, 4, "W_Q4_0", "W_Q8_0"),  # gqa 3: column groups of 192 (6 blocks, 108 / 204 B)
+    (384, 6, 3, "W_F16", "W_F16"),     # 3 kv heads: three partials
 ])
 def test_forward_short_context_fusion(tla, O, W, engines, n_embd, n_head, n_head_kv, wtype, wo_type):
     """A decode step over at most 192 positions runs attention and W_o as
@@ -373,6 +375,7 @@ def test_forward_short_context_fusion(tla, O, W, engines, n_embd, n_head, n_head
     step's logits (the last 8 past the switch)."""
     spec = W.ModelSpec(2, n_embd, n_head, n_head_kv, 512, 384, 208)
     t = W.make_model(spec, getattr(W, wtype), salt=91 + n_head,
+                     output_type=W.W_Q6_K if n_embd % 256 == 0 else W.W_Q8_0,
                      overrides={"attn_output.weight": getattr(W, wo_type)})
     toks = [(37 * i + 11) % spec.n_vocab for i in range(200)]
     om = O.Model(spec, t)
