@@ -196,8 +196,8 @@ def test_matmul_argmax(O, W, engines):
     after its first): against the oracle's argmax of the same launch's
     logits, over ties (identical rows: the first wins), NaN rows (never
     win), a NaN at row 0 (index 0), +0 ties with everything else negative,
-    and random Q8_0 / Q6_K / F16 products with 512 workgroups (8 per key
-    slot)."""
+    and random Q8_0 / Q6_K / F16 / Q4_0 products with 512 workgroups (8 per
+    key slot)."""
     eng = engines(1, 64)
     lib = O.oracle()
     from oracle import fptr
@@ -230,7 +230,7 @@ def test_matmul_argmax(O, W, engines):
             assert got == want, (name, got, want)
             if want_idx is not None:
                 assert got == want_idx, (name, got, want_idx)
-        for t in (Q.Q8_0, Q.Q6_K, Q.F16):
+        for t in (Q.Q8_0, Q.Q6_K, Q.F16, Q.Q4_0):
             raw = W.make_weights(t, rows, cols, salt=40 + t)
             dw = track(eng.array(raw))
             got = eng.matmul_argmax(out.ptr, dw.ptr, dx.ptr, rows, cols, t)
