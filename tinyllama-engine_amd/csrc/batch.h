@@ -47,7 +47,14 @@ struct SplitParams {
     int k_splits;              // K cut into this many ranges of blk_per_split 32-column
     int blk_per_split;         // blocks (grid z); each split's sums go to part, and a
     float* part;               // second launch adds them in split order: [k_splits][n][total_rows]
+    int defer_reduce;          // 1: that launch is left to the caller (launch_reduce_rmsnorm_rows)
 };
+// x[t][c] += the K ranges' sums part[z][t][c] (z in order, as the split
+// product's own second launch adds them), then out[t] = rmsnorm(x[t]) * w
+// (the rmsnorm rows' arithmetic): n_tok rows of size floats, one workgroup
+// per row.  x, part, out 16-byte aligned, size a multiple of 4.
+hipError_t launch_reduce_rmsnorm_rows(float* x, const float* part, int k_splits, float* out, const float* w,
+                                      int n_tok, int size, float eps, hipStream_t s);
 size_t split_part_bytes(int n, int total_rows, int k_splits);
 int split_tokens(int n);                  // tokens padded to the 64-token tile
 size_t split_x_bytes(int n, int cols);    // bytes of the planes

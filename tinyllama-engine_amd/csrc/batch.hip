@@ -33,6 +33,39 @@ __global__ __launch_bounds__(kThreads) void rmsnorm_rows_kernel(float* out, cons
     for (int c = threadIdx.x; c < size; c += kThreads) o[c] = xr[c] * rms * w[c];
 }
 
+// x[t] += the split product's K-range sums, then rmsnorm of the row into
+// out: the product's reduce launch and the rmsnorm launch after it as one.
+// Sums in the reduce launch's order (ranges in order, then added to x), the
+// rmsnorm's in row_sum_squares' (16-byte pieces t, t + kThreads, ...).
+__global__ __launch_bounds__(kThreads) void reduce_rmsnorm_rows_kernel(float* x, const float* part, int k_splits,
+                                                                       long long plane, float* out, const float* w,
+                                                                       int size, float eps)
+{
+    __shared__ float s_red[kThreads / 64];
+    const long long row = static_cast<long long>(blockIdx.x) * size;
+    float4* const xr = reinterpret_cast<float4*>(x + row);
+    const float4* const pr = reinterpret_cast<const float4*>(part + row);
+    const long long plane4 = plane / 4;
+    float ss = 0.f;
+    for (int c4 = threadIdx.x; c4 < size / 4; c4 += kThreads) {
+        float4 a = pr[c4];
+        for (int z = 1; z < k_splits; ++z) {
+            const float4 b = pr[z * plane4 + c4];
+            a = make_float4(a.x + b.x, a.y + b.y, a.z + b.z, a.w + b.w);
+        }
+        const float4 o = xr[c4];
+        const float4 v = make_float4(o.x + a.x, o.y + a.y, o.z + a.z, o.w + a.w);
+        xr[c4] = v;
+        ss += sum_sq4(v);
+    }
+    ss = block_sum<kThreads>(ss, s_red);
+    const float rms = 1.0f / sqrtf(ss / static_cast<float>(size) + eps);
+    float* const o = out + row;
+    const float* const xs = x + row;  // this thread's own stores, read back
+    for (int c4 = threadIdx.x; c4 < size / 4; c4 += kThreads)
+        for (int e = 0; e < 4; ++e) o[4 * c4 + e] = xs[4 * c4 + e] * rms * w[4 * c4 + e];
+}
+
 // h[t][c] = silu(h[t][c]) * h[t][n_ff + c] in place, rows of 2 n_ff floats
 // (gate then up), with the reference's operation order (src/ops.cpp:1107-1148).
 __global__ __launch_bounds__(kThreads) void swiglu_rows_kernel(float* h, int n_ff)
@@ -284,6 +317,17 @@ hipError_t launch_rmsnorm_rows(float* out, const float* x, const float* w, int n
                                hipStream_t s)
 {
     hipLaunchKernelGGL(rmsnorm_rows_kernel, dim3(n_rows), dim3(kThreads), 0, s, out, x, w, size, eps);
+    return hipGetLastError();
+}
+
+hipError_t launch_reduce_rmsnorm_rows(float* x, const float* part, int k_splits, float* out, const float* w,
+                                      int n_tok, int size, float eps, hipStream_t s)
+{
+    const auto a16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+    if (n_tok < 1 || size < 4 || size % 4 != 0 || k_splits < 1 || !a16(x) || !a16(part) || !a16(out))
+        return hipErrorInvalidValue;
+    hipLaunchKernelGGL(reduce_rmsnorm_rows_kernel, dim3(n_tok), dim3(kThreads), 0, s, x, part, k_splits,
+                       static_cast<long long>(n_tok) * size, out, w, size, eps);
     return hipGetLastError();
 }
 

@@ -1329,8 +1329,9 @@ constexpr int kBatchMinTokens = 16;
 // against 174 us with 4 rows per wave, W_down 73 us (2 x 4-6) against 107
 // (1 x 2); at 128 tokens every matrix within 2 us of its best.
 int split_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int total, int cols, const float* x,
-                long long x_stride, int n, int add)
+                long long x_stride, int n, int add, int* deferred = nullptr)
 {
+    if (deferred) *deferred = 0;
     if (int rc = ensure_buf(e, reinterpret_cast<void**>(&e->xs), e->xs_bytes, split_x_bytes(n, cols), "split-x workspace")) return rc;
     SplitParams p{};
     for (int i = 0; i < n_seg; ++i) p.seg[i] = segs[i];
@@ -1358,6 +1359,13 @@ int split_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int
                                 "split-product partial sums"))
             return rc;
         p.part = e->part;
+        // one segment added to rows of its own width: the caller may add the
+        // ranges' sums itself, with the rmsnorm that follows
+        // (launch_reduce_rmsnorm_rows), instead of a launch of their own
+        if (deferred && n_seg == 1 && add && segs[0].out_stride == total) {
+            p.defer_reduce = 1;
+            *deferred = p.k_splits;
+        }
     }
     if (int rc = launch(e, TLA_KERNEL_GEMV, "split rows",
                         [&]() -> hipError_t { return launch_split_rows(x, x_stride, n, cols, e->xs, e->stream); }))
@@ -1416,15 +1424,18 @@ int stream_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, in
                   [&]() -> hipError_t { return launch_stream_product(type, p, e->stream); });
 }
 
+// deferred (when non-null): the K ranges whose sums a split product left in
+// e->part for the caller to add (launch_reduce_rmsnorm_rows), else 0.
 int matrix_batch(tla_engine* e, int type, const GemvSegment* segs, int n_seg, int cols, const float* x,
-                 long long x_stride, int n, int add)
+                 long long x_stride, int n, int add, int* deferred = nullptr)
 {
+    if (deferred) *deferred = 0;
     int total = 0;
     for (int i = 0; i < n_seg; ++i) total += segs[i].rows;
     if (use_stream(type, cols, n, x_stride)) return stream_batch(e, type, segs, n_seg, total, cols, x, x_stride, n, add);
     if (n >= kBatchMinTokens && cols % 32 == 0 && (type != kQ6_K || cols % 256 == 0) && x_stride % 4 == 0 &&
         reinterpret_cast<std::uintptr_t>(x) % 16 == 0)
-        return split_batch(e, type, segs, n_seg, total, cols, x, x_stride, n, add);
+        return split_batch(e, type, segs, n_seg, total, cols, x, x_stride, n, add, deferred);
     const int chunk = std::max(1, std::min({n, kGemvMaxVec, kGemvLdsBytes / gemv_lds_per_vec(cols)}));
     for (int t0 = 0; t0 < n; t0 += chunk) {
         GemvParams p{};
@@ -1462,6 +1473,18 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
         return rc;
     const auto U = [](const void* w) { return static_cast<const unsigned char*>(w); };
     const int n_layers = e->cfg.n_layers;
+    // The W_o and W_down products add to x; where their K ranges' sums are
+    // left in e->part (pending), the rmsnorm rows launch after them adds
+    // them first (one launch for both), before any other product reuses
+    // e->part.  After the last layer x is added to by the product itself.
+    int pending = 0;
+    auto norm_rows = [&](const float* w) -> int {
+        const hipError_t err = pending ? launch_reduce_rmsnorm_rows(b.x, e->part, pending, b.xb, w, n_tok, embd,
+                                                                    eps, e->stream)
+                                       : launch_rmsnorm_rows(b.xb, b.x, w, n_tok, embd, eps, e->stream);
+        pending = 0;
+        return check_hip(err, "rmsnorm rows");
+    };
     for (int l = 0; l < n_layers; ++l) {
         const tla_layer_weights& L = m->layers[l];
         auto product = [&](int type, const GemvSegment* segs, int n_seg, int cols, const float* x,
@@ -1469,9 +1492,7 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
             return matrix_batch(e, type, segs, n_seg, cols, x, x_stride, n_tok, add);
         };
         // rmsnorm rows, then Q/K/V (src/forward.cpp:180-190)
-        if (int rc = check_hip(launch_rmsnorm_rows(b.xb, b.x, L.attn_norm, n_tok, embd, eps, e->stream),
-                               "rmsnorm rows"))
-            return rc;
+        if (int rc = norm_rows(L.attn_norm)) return rc;
         if (L.type_q == L.type_k && L.type_q == L.type_v) {
             const GemvSegment segs[3] = {{U(L.wq), b.q, embd, embd}, {U(L.wk), b.k, kv, kv}, {U(L.wv), b.v, kv, kv}};
             if (int rc = product(L.type_q, segs, 3, embd, b.xb, embd, 0)) return rc;
@@ -1486,13 +1507,11 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
         // x += Wo . att (src/forward.cpp:210-213)
         {
             const GemvSegment so{U(L.wo), b.x, embd, embd};
-            if (int rc = product(L.type_o, &so, 1, embd, b.att, embd, 1)) return rc;
+            if (int rc = matrix_batch(e, L.type_o, &so, 1, embd, b.att, embd, n_tok, 1, &pending)) return rc;
         }
         // FFN (src/forward.cpp:215-228): rmsnorm rows, gate and up into
         // hb [t][gate | up], SiLU x up in place, x += W_down . h
-        if (int rc = check_hip(launch_rmsnorm_rows(b.xb, b.x, L.ffn_norm, n_tok, embd, eps, e->stream),
-                               "rmsnorm rows"))
-            return rc;
+        if (int rc = norm_rows(L.ffn_norm)) return rc;
         {
             const GemvSegment segs[2] = {{U(L.w_gate), b.hb, ff, 2LL * ff}, {U(L.w_up), b.hb + ff, ff, 2LL * ff}};
             if (int rc = product(L.type_ffn, segs, 2, embd, b.xb, embd, 0)) return rc;
@@ -1500,7 +1519,9 @@ int prompt_step(tla_engine* e, const tla_model* m, const FwdBufs& b, float* kc, 
         if (int rc = check_hip(launch_swiglu_rows(b.hb, n_tok, ff, e->stream), "swiglu rows")) return rc;
         {
             const GemvSegment sd{U(L.w_down), b.x, embd, embd};
-            if (int rc = product(L.type_ffn, &sd, 1, ff, b.hb, 2LL * ff, 1)) return rc;
+            if (int rc = matrix_batch(e, L.type_ffn, &sd, 1, ff, b.hb, 2LL * ff, n_tok, 1,
+                                      l + 1 < n_layers ? &pending : nullptr))
+                return rc;
         }
     }
     if (logits)

@@ -495,7 +495,7 @@ hipError_t launch_typed(const SplitParams& p, hipStream_t s)
     case 2: err = launch_product<kType, 2>(p, s); break;
     default: err = launch_product<kType, 4>(p, s); break;
     }
-    if (err != hipSuccess || !p.part) return err;
+    if (err != hipSuccess || !p.part || p.defer_reduce) return err;
     const long long n = static_cast<long long>(p.n) * p.total_rows;
     hipLaunchKernelGGL(split_reduce_kernel, dim3(static_cast<unsigned>((n + kThreads - 1) / kThreads)),
                        dim3(kThreads), 0, s, p);
