@@ -190,7 +190,7 @@ def test_argmax(O, engines):
         assert got == want, (got, want)
 
 
-def test_matmul_argmax(O, W, engines):
+def test_matmul_argmax(tla, O, W, engines):
     """matmul then sample_argmax with the argmax keys that the product's
     workgroups post (the path tla_generate_greedy takes for every token
     after its first): against the oracle's argmax of the same launch's
@@ -236,6 +236,12 @@ def test_matmul_argmax(O, W, engines):
             got = eng.matmul_argmax(out.ptr, dw.ptr, dx.ptr, rows, cols, t)
             lg = out.download()
             assert got == lib.oracle_argmax(fptr(lg), rows), t
+        # rows past 64 units (4096 columns) take no argmax keys: refused
+        wide = track(eng.array(np.zeros((8, 4160), np.float32)))
+        xw = track(eng.array(np.zeros(4160, np.float32)))
+        with pytest.raises(tla.TlaError) as e:
+            eng.matmul_argmax(out.ptr, wide.ptr, xw.ptr, 8, 4160, Q.F32)
+        assert e.value.code == tla.TLA_ERR_UNSUPPORTED
 
 
 def run_forward(tla, eng, spec, t, tokens):
